@@ -1,0 +1,163 @@
+"""Benchmark: batch-1 greedy decode of a BitNet-b1.58-2B4T-shaped model on one
+MI355X (30 layers, hidden 2560, FFN 6912 ReLU^2-gated,
+20/5 heads, head_dim 128, vocab 128256 bf16 tied head, random-init weights,
+64-token uniform-random prompt, then greedy decode).
+
+A step is one decode token (one pass of the whole token loop).  Prints one
+JSON line: decode tok/s, the roofline of the dominant kernel class (the
+ternary decode GEMV, HBM-bound) measured with HIP events on the library's
+stream, and the CPU baseline (the SIMD restatement of the reference's CPU
+path, timed on this host).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO / "lemonade-burn_amd"))
+
+HBM_PEAK_GBS = 8000.0
+SEED = 2026
+PROMPT_LEN = 64
+
+
+def cpu_baseline(budget_s: float = 15.0) -> dict:
+    """Reference CPU path restated (VNNI/AVX-512BW/AVX2 ternary GEMV +
+    AVX-512 bf16 LM head, OpenMP over rows), same model shape and seed,
+    greedy decode on this host's cores for about `budget_s` seconds."""
+    sys.path.insert(0, str(REPO / "oracle"))
+    import lbt_oracle as orc
+
+    old = orc.set_fast(2)
+    try:
+        t0 = time.perf_counter()
+        om = orc.OracleModel(orc.config(), SEED)
+        build_s = time.perf_counter() - t0
+        prompt = np.random.default_rng(64).integers(0, 128256, 8).astype(np.uint32)
+        tok = int(om.forward(prompt)[0].argmax())
+        n, t0 = 0, time.perf_counter()
+        while True:
+            tok = int(om.forward([tok])[0].argmax())
+            n += 1
+            el = time.perf_counter() - t0
+            if el > budget_s or n >= 256:
+                break
+        om.free()
+    finally:
+        orc.set_fast(old)
+    return {
+        "value": round(n / el, 3),
+        "unit": "tok/s",
+        "cores": int(orc.lib().port_threads()),
+        "kind": "port",
+        "sample": f"2B-shaped synthetic model (seed {SEED}), 8-token prompt then {n} greedy decode steps in "
+                  f"{el:.1f}s; ternary {orc.lib().port_isa().decode()} + AVX-512 bf16 head (model build {build_s:.1f}s)",
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=128)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--prof-steps", type=int, default=32)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build runs on one GPU; a multi-GPU figure is not part of it "
+              "(rows of the ternary GEMVs would shard across GPUs with no exchange).", file=sys.stderr)
+        return 2
+
+    import lbt_hip
+
+    ctx = lbt_hip.Ctx(0)
+    cfg = lbt_hip.make_config()
+    model = lbt_hip.Model.synthetic(ctx, cfg, SEED)
+    prompt = np.random.default_rng(64).integers(0, cfg.vocab_size, PROMPT_LEN).astype(np.uint32)
+
+    # warmup: prefill + W decode steps
+    cache = model.new_cache()
+    toks, ms_pf, _ = model.generate_greedy(prompt, max(args.warmup, 1), cache)
+    cache.free()
+
+    # timed: prefill (untimed) then exactly K decode steps
+    cache = model.new_cache()
+    first = model.forward_argmax(prompt, cache)
+    ctx.sync()
+    t0 = time.perf_counter()
+    out, ms_dev = model.decode_greedy(cache, first, args.steps)
+    ctx.sync()
+    wall = time.perf_counter() - t0
+    cache.free()
+    ms_step = ms_dev / args.steps
+    tok_s = args.steps / (ms_dev / 1e3)
+
+    # roofline pass: HIP events around every kernel launch of a decode run
+    cache = model.new_cache()
+    first = model.forward_argmax(prompt, cache)
+    ctx.prof_read(reset=True)
+    ctx.prof_enable(True)
+    model.decode_greedy(cache, first, args.prof_steps)
+    prof = ctx.prof_read(reset=True)
+    ctx.prof_enable(False)
+    cache.free()
+    g = prof["gemv"]
+    achieved = g["bytes"] / (g["ms"] / 1e3) / 1e9 if g["ms"] > 0 else 0.0
+    head = prof["head"]
+    head_gbs = head["bytes"] / (head["ms"] / 1e3) / 1e9 if head["ms"] > 0 else 0.0
+
+    line = {
+        "metric": "decode tok/s @2B ternary batch 1; GEMV HBM GB/s as % of peak",
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8xternary/i32 (bf16 head, f32 norms)",
+        "data": "synthetic (random-init weights, uniform-random prompt ids)",
+        "config": {
+            "workload": "BitNet-b1.58-2B4T-shaped decoder (30 layers, hidden 2560, FFN 6912, 20/5 heads, "
+                        "vocab 128256), 64-token prompt then greedy decode, batch 1",
+            "global_batch": 1,
+            "seq_len": PROMPT_LEN + args.steps,
+            "parallelism": "single GPU",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel": "tgemv_kernel (ternary decode GEMV, all 4 per-layer groups)",
+            "bytes_per_launch": round(g["bytes"] / max(g["launches"], 1)),
+            "avg_launch_us": round(g["ms"] * 1e3 / max(g["launches"], 1), 3),
+            "launches": g["launches"],
+        },
+        "breakdown_ms_per_step": {k: round(v["ms"] / args.prof_steps, 4) for k, v in prof.items()},
+        "lm_head_GBs": round(head_gbs, 1),
+        "prefill_ms": round(ms_pf, 3),
+        "wall_tok_s": round(args.steps / wall, 2),
+        "tokens_head": [int(t) for t in out[:8]],
+    }
+    model.free()
+    ctx.close()
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,461 @@
+// lbt_api.cpp -- the C ABI (include/lbt.h): context, errors, profiling,
+// weights and the per-op entry points.  Host-pointer entry points stage
+// through a grow-only device workspace; `_dev` ones enqueue on the stream.
+#include <hip/hip_runtime.h>
+#include <string.h>
+
+#include <string>
+#include <vector>
+
+#include "lbt_internal.h"
+
+namespace lbt {
+
+int set_err(lbt_ctx* ctx, int code, const std::string& msg) {
+    if (ctx) ctx->err = msg;
+    return code;
+}
+
+int hip_err(lbt_ctx* ctx, hipError_t e, const char* what) {
+    std::string m = std::string(what) + ": " + hipGetErrorString(e);
+    return set_err(ctx, e == hipErrorOutOfMemory ? LBT_E_NOMEM : LBT_E_DEVICE, m);
+}
+
+int ws_reserve(lbt_ctx* ctx, size_t bytes, void** out) {
+    if (bytes > ctx->ws_bytes) {
+        if (ctx->ws) {
+            hipStreamSynchronize(ctx->stream);
+            hipFree(ctx->ws);
+            ctx->ws = nullptr;
+            ctx->ws_bytes = 0;
+        }
+        size_t nb = bytes < (1u << 20) ? (1u << 20) : bytes;
+        LBT_HIP(ctx, hipMalloc(&ctx->ws, nb));
+        ctx->ws_bytes = nb;
+    }
+    *out = ctx->ws;
+    return LBT_OK;
+}
+
+void prof_begin(lbt_ctx* ctx, hipEvent_t* ev) {
+    *ev = nullptr;
+    if (!ctx->prof) return;
+    hipEvent_t e;
+    if (!ctx->free_events.empty()) {
+        e = ctx->free_events.back();
+        ctx->free_events.pop_back();
+    } else if (hipEventCreate(&e) != hipSuccess) {
+        return;
+    }
+    hipEventRecord(e, ctx->stream);
+    *ev = e;
+}
+
+void prof_end(lbt_ctx* ctx, hipEvent_t ev, int cls, double bytes) {
+    if (!ctx->prof || !ev) return;
+    hipEvent_t e;
+    if (!ctx->free_events.empty()) {
+        e = ctx->free_events.back();
+        ctx->free_events.pop_back();
+    } else if (hipEventCreate(&e) != hipSuccess) {
+        return;
+    }
+    hipEventRecord(e, ctx->stream);
+    ctx->pending.push_back({cls, bytes, ev, e});
+}
+
+}  // namespace lbt
+
+using namespace lbt;
+
+namespace {
+
+size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+// Carves consecutive 256-byte aligned regions out of the workspace.
+struct Carve {
+    std::vector<size_t> sizes;
+    size_t add(size_t b) {
+        size_t off = 0;
+        for (size_t s : sizes) off += align256(s);
+        sizes.push_back(b);
+        return off;
+    }
+    size_t total() const {
+        size_t t = 0;
+        for (size_t s : sizes) t += align256(s);
+        return t;
+    }
+};
+
+int check_ws(lbt_ctx* ctx, const lbt_weight* const* ws, size_t n, size_t cols_expected, bool check_cols) {
+    if (!ws || n < 1 || n > 3) return set_err(ctx, LBT_E_INVALID, "expected 1 to 3 matrices");
+    for (size_t i = 0; i < n; i++) {
+        if (!ws[i]) return set_err(ctx, LBT_E_INVALID, "null weight");
+        if (ws[i]->cols != ws[0]->cols) return set_err(ctx, LBT_E_INVALID, "matrices differ in cols");
+    }
+    if (check_cols && ws[0]->cols != cols_expected) return set_err(ctx, LBT_E_INVALID, "inner dimension mismatch");
+    return LBT_OK;
+}
+
+TernaryOp make_op(const lbt_weight* const* ws, size_t n, size_t m) {
+    TernaryOp op;
+    op.nmat = (int)n;
+    for (size_t i = 0; i < n; i++) {
+        op.w[i] = ws[i]->d;
+        op.rows[i] = (int)ws[i]->rows;
+        op.sw[i] = ws[i]->scale;
+    }
+    op.cols = (int)ws[0]->cols;
+    op.m = (int)m;
+    return op;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* lbt_version(void) { return "lbt-hip 0.1 gfx950"; }
+
+int lbt_ctx_create(int device, lbt_ctx** out) {
+    if (!out) return LBT_E_INVALID;
+    *out = nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return LBT_E_DEVICE;
+    if (device < 0 || device >= n) return LBT_E_INVALID;
+    if (hipSetDevice(device) != hipSuccess) return LBT_E_DEVICE;
+    lbt_ctx* c = new lbt_ctx();
+    c->device = device;
+    if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
+        delete c;
+        return LBT_E_DEVICE;
+    }
+    *out = c;
+    return LBT_OK;
+}
+
+void lbt_ctx_destroy(lbt_ctx* ctx) {
+    if (!ctx) return;
+    hipSetDevice(ctx->device);
+    hipStreamSynchronize(ctx->stream);
+    for (auto& p : ctx->pending) {
+        hipEventDestroy(p.a);
+        hipEventDestroy(p.b);
+    }
+    for (auto e : ctx->free_events) hipEventDestroy(e);
+    if (ctx->ws) hipFree(ctx->ws);
+    hipStreamDestroy(ctx->stream);
+    delete ctx;
+}
+
+const char* lbt_last_error(const lbt_ctx* ctx) { return ctx ? ctx->err.c_str() : "null context"; }
+
+int lbt_ctx_synchronize(lbt_ctx* ctx) {
+    if (!ctx) return LBT_E_INVALID;
+    LBT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return LBT_OK;
+}
+
+void* lbt_ctx_stream(lbt_ctx* ctx) { return ctx ? (void*)ctx->stream : nullptr; }
+
+int lbt_dev_alloc(lbt_ctx* ctx, size_t bytes, void** out) {
+    if (!ctx || !out) return LBT_E_INVALID;
+    LBT_HIP(ctx, hipMalloc(out, bytes ? bytes : 1));
+    return LBT_OK;
+}
+
+int lbt_dev_free(lbt_ctx* ctx, void* p) {
+    if (!ctx) return LBT_E_INVALID;
+    if (p) {
+        LBT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        LBT_HIP(ctx, hipFree(p));
+    }
+    return LBT_OK;
+}
+
+int lbt_memcpy_h2d(lbt_ctx* ctx, void* dst, const void* src, size_t bytes) {
+    if (!ctx) return LBT_E_INVALID;
+    LBT_HIP(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream));
+    LBT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return LBT_OK;
+}
+
+int lbt_memcpy_d2h(lbt_ctx* ctx, void* dst, const void* src, size_t bytes) {
+    if (!ctx) return LBT_E_INVALID;
+    LBT_HIP(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream));
+    LBT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return LBT_OK;
+}
+
+// ---- weights ---------------------------------------------------------------
+static int weight_new(lbt_ctx* ctx, const uint8_t* src, bool src_dev, size_t rows, size_t cols, float scale,
+                      lbt_weight** out) {
+    if (!ctx || !out || !src || rows == 0 || cols == 0) return set_err(ctx, LBT_E_INVALID, "weight: bad arguments");
+    *out = nullptr;
+    lbt_weight* w = new lbt_weight();
+    w->ctx = ctx;
+    w->rows = rows;
+    w->cols = cols;
+    w->kp = padded_cols(cols);
+    w->scale = scale;
+    const size_t bytes = rows * w->kp / 4;
+    hipError_t e = hipMalloc(&w->d, bytes);
+    if (e != hipSuccess) {
+        delete w;
+        return hip_err(ctx, e, "hipMalloc(weight)");
+    }
+    e = hipMemcpyAsync(w->d, src, bytes, src_dev ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) {
+        hipFree(w->d);
+        delete w;
+        return hip_err(ctx, e, "upload weight");
+    }
+    *out = w;
+    return LBT_OK;
+}
+
+int lbt_weight_upload(lbt_ctx* ctx, const uint8_t* packed, size_t rows, size_t cols, float scale, lbt_weight** out) {
+    return weight_new(ctx, packed, false, rows, cols, scale, out);
+}
+
+int lbt_weight_upload_dev(lbt_ctx* ctx, const uint8_t* packed_dev, size_t rows, size_t cols, float scale,
+                          lbt_weight** out) {
+    return weight_new(ctx, packed_dev, true, rows, cols, scale, out);
+}
+
+void lbt_weight_free(lbt_weight* w) {
+    if (!w) return;
+    if (w->owns && w->d) {
+        hipStreamSynchronize(w->ctx->stream);
+        hipFree(w->d);
+    }
+    delete w;
+}
+
+size_t lbt_weight_rows(const lbt_weight* w) { return w ? w->rows : 0; }
+size_t lbt_weight_cols(const lbt_weight* w) { return w ? w->cols : 0; }
+const uint8_t* lbt_weight_device_ptr(const lbt_weight* w) { return w ? w->d : nullptr; }
+
+// ---- quantization ------------------------------------------------------------
+int lbt_quantize_acts_dev(lbt_ctx* ctx, const float* x, size_t m, size_t k, int8_t* q, float* scale, int32_t* sum) {
+    if (!ctx || k == 0) return set_err(ctx, LBT_E_INVALID, "quantize: bad arguments");
+    return launch_quantize(ctx, x, nullptr, 0.0f, (int)m, (int)k, q, scale, sum);
+}
+
+int lbt_rmsnorm_quantize_dev(lbt_ctx* ctx, const float* x, const float* norm_w, float eps, size_t m, size_t k,
+                             int8_t* q, float* scale, int32_t* sum) {
+    if (!ctx || k == 0 || !norm_w) return set_err(ctx, LBT_E_INVALID, "rmsnorm_quantize: bad arguments");
+    return launch_quantize(ctx, x, norm_w, eps, (int)m, (int)k, q, scale, sum);
+}
+
+int lbt_quantize_acts(lbt_ctx* ctx, const float* x, size_t m, size_t k, int8_t* q, float* scale, int32_t* sum) {
+    if (!ctx || k == 0) return set_err(ctx, LBT_E_INVALID, "quantize: bad arguments");
+    if (m == 0) return LBT_OK;
+    const size_t kp = padded_cols(k);
+    Carve cv;
+    size_t ox = cv.add(m * k * 4), oq = cv.add(m * kp), os = cv.add(m * 4), ou = cv.add(m * 4);
+    void* ws;
+    int rc = ws_reserve(ctx, cv.total(), &ws);
+    if (rc) return rc;
+    char* b = (char*)ws;
+    LBT_HIP(ctx, hipMemcpyAsync(b + ox, x, m * k * 4, hipMemcpyHostToDevice, ctx->stream));
+    rc = launch_quantize(ctx, (const float*)(b + ox), nullptr, 0.0f, (int)m, (int)k, (int8_t*)(b + oq),
+                         (float*)(b + os), (int32_t*)(b + ou));
+    if (rc) return rc;
+    LBT_HIP(ctx, hipMemcpyAsync(q, b + oq, m * kp, hipMemcpyDeviceToHost, ctx->stream));
+    LBT_HIP(ctx, hipMemcpyAsync(scale, b + os, m * 4, hipMemcpyDeviceToHost, ctx->stream));
+    LBT_HIP(ctx, hipMemcpyAsync(sum, b + ou, m * 4, hipMemcpyDeviceToHost, ctx->stream));
+    LBT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return LBT_OK;
+}
+
+// ---- ternary GEMM ------------------------------------------------------------
+int lbt_gemm_i32_dev(lbt_ctx* ctx, const lbt_weight* w, const int8_t* q, const int32_t* sum, size_t m, int32_t* out) {
+    if (!ctx || !w) return set_err(ctx, LBT_E_INVALID, "gemm_i32: bad arguments");
+    if (m == 0) return LBT_OK;
+    TernaryOp op = make_op(&w, 1, m);
+    op.in_mode = kInPreQ;
+    op.out_mode = kOutI32;
+    op.q = q;
+    op.qsum = sum;
+    op.out[0] = out;
+    return launch_ternary(ctx, op);
+}
+
+int lbt_gemm_i32(lbt_ctx* ctx, const lbt_weight* w, const int8_t* q, const int32_t* sum, size_t m, int32_t* out) {
+    if (!ctx || !w) return set_err(ctx, LBT_E_INVALID, "gemm_i32: bad arguments");
+    if (m == 0) return LBT_OK;
+    Carve cv;
+    size_t oq = cv.add(m * w->kp), os = cv.add(m * 4), oo = cv.add(m * w->rows * 4);
+    void* ws;
+    int rc = ws_reserve(ctx, cv.total(), &ws);
+    if (rc) return rc;
+    char* b = (char*)ws;
+    LBT_HIP(ctx, hipMemcpyAsync(b + oq, q, m * w->kp, hipMemcpyHostToDevice, ctx->stream));
+    LBT_HIP(ctx, hipMemcpyAsync(b + os, sum, m * 4, hipMemcpyHostToDevice, ctx->stream));
+    rc = lbt_gemm_i32_dev(ctx, w, (const int8_t*)(b + oq), (const int32_t*)(b + os), m, (int32_t*)(b + oo));
+    if (rc) return rc;
+    LBT_HIP(ctx, hipMemcpyAsync(out, b + oo, m * w->rows * 4, hipMemcpyDeviceToHost, ctx->stream));
+    LBT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return LBT_OK;
+}
+
+int lbt_gemm_multi_dev(lbt_ctx* ctx, const lbt_weight* const* ws, size_t n, const int8_t* q, const float* scale,
+                       const int32_t* sum, size_t m, float* const* outs) {
+    int rc = check_ws(ctx, ws, n, 0, false);
+    if (rc) return rc;
+    if (m == 0) return LBT_OK;
+    TernaryOp op = make_op(ws, n, m);
+    op.in_mode = kInPreQ;
+    op.out_mode = kOutF32;
+    op.q = q;
+    op.qscale = scale;
+    op.qsum = sum;
+    for (size_t i = 0; i < n; i++) op.out[i] = outs[i];
+    return launch_ternary(ctx, op);
+}
+
+int lbt_gemm_multi(lbt_ctx* ctx, const lbt_weight* const* ws, size_t n, const int8_t* q, const float* scale,
+                   const int32_t* sum, size_t m, float* const* outs) {
+    int rc = check_ws(ctx, ws, n, 0, false);
+    if (rc) return rc;
+    if (m == 0) return LBT_OK;
+    const size_t kp = ws[0]->kp;
+    Carve cv;
+    size_t oq = cv.add(m * kp), osc = cv.add(m * 4), osu = cv.add(m * 4);
+    size_t oo[3];
+    for (size_t i = 0; i < n; i++) oo[i] = cv.add(m * ws[i]->rows * 4);
+    void* wsp;
+    rc = ws_reserve(ctx, cv.total(), &wsp);
+    if (rc) return rc;
+    char* b = (char*)wsp;
+    LBT_HIP(ctx, hipMemcpyAsync(b + oq, q, m * kp, hipMemcpyHostToDevice, ctx->stream));
+    LBT_HIP(ctx, hipMemcpyAsync(b + osc, scale, m * 4, hipMemcpyHostToDevice, ctx->stream));
+    LBT_HIP(ctx, hipMemcpyAsync(b + osu, sum, m * 4, hipMemcpyHostToDevice, ctx->stream));
+    float* douts[3];
+    for (size_t i = 0; i < n; i++) douts[i] = (float*)(b + oo[i]);
+    rc = lbt_gemm_multi_dev(ctx, ws, n, (const int8_t*)(b + oq), (const float*)(b + osc), (const int32_t*)(b + osu),
+                            m, douts);
+    if (rc) return rc;
+    for (size_t i = 0; i < n; i++)
+        LBT_HIP(ctx, hipMemcpyAsync(outs[i], douts[i], m * ws[i]->rows * 4, hipMemcpyDeviceToHost, ctx->stream));
+    LBT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return LBT_OK;
+}
+
+int lbt_ternary_linear_dev(lbt_ctx* ctx, const lbt_weight* const* ws, size_t n, const float* x, size_t m, size_t cols,
+                           float* const* outs) {
+    int rc = check_ws(ctx, ws, n, cols, true);
+    if (rc) return rc;
+    if (m == 0) return LBT_OK;
+    TernaryOp op = make_op(ws, n, m);
+    op.in_mode = kInF32;
+    op.out_mode = kOutF32;
+    op.x = x;
+    for (size_t i = 0; i < n; i++) op.out[i] = outs[i];
+    return launch_ternary(ctx, op);
+}
+
+int lbt_ternary_linear(lbt_ctx* ctx, const lbt_weight* const* ws, size_t n, const float* x, size_t m, size_t cols,
+                       float* const* outs) {
+    int rc = check_ws(ctx, ws, n, cols, true);
+    if (rc) return rc;
+    if (m == 0) return LBT_OK;
+    Carve cv;
+    size_t ox = cv.add(m * cols * 4);
+    size_t oo[3];
+    for (size_t i = 0; i < n; i++) oo[i] = cv.add(m * ws[i]->rows * 4);
+    void* wsp;
+    rc = ws_reserve(ctx, cv.total(), &wsp);
+    if (rc) return rc;
+    char* b = (char*)wsp;
+    LBT_HIP(ctx, hipMemcpyAsync(b + ox, x, m * cols * 4, hipMemcpyHostToDevice, ctx->stream));
+    float* douts[3];
+    for (size_t i = 0; i < n; i++) douts[i] = (float*)(b + oo[i]);
+    rc = lbt_ternary_linear_dev(ctx, ws, n, (const float*)(b + ox), m, cols, douts);
+    if (rc) return rc;
+    for (size_t i = 0; i < n; i++)
+        LBT_HIP(ctx, hipMemcpyAsync(outs[i], douts[i], m * ws[i]->rows * 4, hipMemcpyDeviceToHost, ctx->stream));
+    LBT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return LBT_OK;
+}
+
+// ---- bf16 ----------------------------------------------------------------------
+int lbt_bf16_upload(lbt_ctx* ctx, const uint16_t* w, size_t rows, size_t cols, lbt_bf16** out) {
+    if (!ctx || !w || !out || rows == 0 || cols == 0 || cols % 8)
+        return set_err(ctx, LBT_E_INVALID, "bf16_upload: bad arguments (cols must be a multiple of 8)");
+    *out = nullptr;
+    lbt_bf16* b = new lbt_bf16();
+    b->ctx = ctx;
+    b->rows = rows;
+    b->cols = cols;
+    hipError_t e = hipMalloc(&b->d, rows * cols * 2);
+    if (e == hipSuccess) e = hipMemcpy(b->d, w, rows * cols * 2, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        if (b->d) hipFree(b->d);
+        delete b;
+        return hip_err(ctx, e, "bf16 upload");
+    }
+    *out = b;
+    return LBT_OK;
+}
+
+void lbt_bf16_free(lbt_bf16* w) {
+    if (!w) return;
+    if (w->owns && w->d) {
+        hipStreamSynchronize(w->ctx->stream);
+        hipFree(w->d);
+    }
+    delete w;
+}
+
+int lbt_bf16_linear_dev(lbt_ctx* ctx, const lbt_bf16* w, const float* x, size_t m, float* out) {
+    if (!ctx || !w) return set_err(ctx, LBT_E_INVALID, "bf16_linear: bad arguments");
+    return launch_bf16_linear(ctx, w->d, (int)w->rows, (int)w->cols, x, (int)m, nullptr, 0.0f, out, nullptr);
+}
+
+int lbt_bf16_linear(lbt_ctx* ctx, const lbt_bf16* w, const float* x, size_t m, float* out) {
+    if (!ctx || !w) return set_err(ctx, LBT_E_INVALID, "bf16_linear: bad arguments");
+    if (m == 0) return LBT_OK;
+    Carve cv;
+    size_t ox = cv.add(m * w->cols * 4), oo = cv.add(m * w->rows * 4);
+    void* wsp;
+    int rc = ws_reserve(ctx, cv.total(), &wsp);
+    if (rc) return rc;
+    char* b = (char*)wsp;
+    LBT_HIP(ctx, hipMemcpyAsync(b + ox, x, m * w->cols * 4, hipMemcpyHostToDevice, ctx->stream));
+    rc = lbt_bf16_linear_dev(ctx, w, (const float*)(b + ox), m, (float*)(b + oo));
+    if (rc) return rc;
+    LBT_HIP(ctx, hipMemcpyAsync(out, b + oo, m * w->rows * 4, hipMemcpyDeviceToHost, ctx->stream));
+    LBT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return LBT_OK;
+}
+
+// ---- profiling -------------------------------------------------------------------
+int lbt_prof_enable(lbt_ctx* ctx, int on) {
+    if (!ctx) return LBT_E_INVALID;
+    ctx->prof = on != 0;
+    return LBT_OK;
+}
+
+int lbt_prof_read(lbt_ctx* ctx, lbt_prof* out, int reset) {
+    if (!ctx || !out) return LBT_E_INVALID;
+    LBT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    for (auto& p : ctx->pending) {
+        float ms = 0.0f;
+        if (hipEventElapsedTime(&ms, p.a, p.b) == hipSuccess) {
+            ctx->acc.ms[p.cls] += ms;
+            ctx->acc.bytes[p.cls] += p.bytes;
+            ctx->acc.launches[p.cls] += 1;
+        }
+        ctx->free_events.push_back(p.a);
+        ctx->free_events.push_back(p.b);
+    }
+    ctx->pending.clear();
+    *out = ctx->acc;
+    if (reset) ctx->acc = lbt_prof{};
+    return LBT_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,121 @@
+// lbt_internal.h -- host-side internals shared by the C ABI, the model loop
+// and the kernel launchers.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+#include <vector>
+
+#include "../../include/lbt.h"
+
+struct lbt_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::string err;
+    // grow-only device workspace for the host-pointer entry points
+    void* ws = nullptr;
+    size_t ws_bytes = 0;
+    // profiling
+    bool prof = false;
+    struct Pending {
+        int cls;
+        double bytes;
+        hipEvent_t a, b;
+    };
+    std::vector<Pending> pending;
+    std::vector<hipEvent_t> free_events;
+    lbt_prof acc{};
+};
+
+struct lbt_weight {
+    lbt_ctx* ctx = nullptr;
+    uint8_t* d = nullptr;  // device bytes, rows * kp / 4
+    size_t rows = 0, cols = 0, kp = 0;
+    float scale = 1.0f;
+    bool owns = true;
+};
+
+struct lbt_bf16 {
+    lbt_ctx* ctx = nullptr;
+    uint16_t* d = nullptr;
+    size_t rows = 0, cols = 0;
+    bool owns = true;
+};
+
+namespace lbt {
+
+// Error helpers: every entry point converts failures into a status code.
+int set_err(lbt_ctx* ctx, int code, const std::string& msg);
+int hip_err(lbt_ctx* ctx, hipError_t e, const char* what);
+#define LBT_HIP(ctx, call)                                        \
+    do {                                                          \
+        hipError_t e_ = (call);                                   \
+        if (e_ != hipSuccess) return ::lbt::hip_err(ctx, e_, #call); \
+    } while (0)
+
+// Grow-only device workspace.
+int ws_reserve(lbt_ctx* ctx, size_t bytes, void** out);
+
+// Profiling brackets around one launch (no-ops unless ctx->prof).
+enum ProfClass { kProfGemv = 0, kProfGemm = 1, kProfHead = 2, kProfAttn = 3, kProfOther = 4 };
+void prof_begin(lbt_ctx* ctx, hipEvent_t* ev);
+void prof_end(lbt_ctx* ctx, hipEvent_t ev, int cls, double bytes);
+
+// ---- ternary GEMV / GEMM ------------------------------------------------
+enum InMode { kInPreQ = 0, kInF32 = 1 };
+enum OutMode { kOutI32 = 0, kOutF32 = 1, kOutF32Add = 2, kOutRelu2 = 3 };
+
+struct TernaryOp {
+    int nmat = 1;
+    const uint8_t* w[3] = {nullptr, nullptr, nullptr};
+    int rows[3] = {0, 0, 0};
+    float sw[3] = {1.f, 1.f, 1.f};
+    int cols = 0;
+    int m = 0;
+    // kInPreQ
+    const int8_t* q = nullptr;
+    const float* qscale = nullptr;
+    const int32_t* qsum = nullptr;
+    // kInF32
+    const float* x = nullptr;
+    const float* norm_w = nullptr;  // nullable: plain ActQuant
+    float eps = 0.f;
+    int in_mode = kInPreQ;
+    int out_mode = kOutF32;
+    void* out[3] = {nullptr, nullptr, nullptr};
+};
+// Dispatches decode GEMV (small m) or the int8-MFMA prefill GEMM (large m).
+int launch_ternary(lbt_ctx* ctx, const TernaryOp& op);
+int launch_ternary_gemv(lbt_ctx* ctx, const TernaryOp& op);
+int launch_ternary_mfma(lbt_ctx* ctx, const TernaryOp& op);
+
+// Standalone (rms)norm + quantize of m rows into global q [m, kp], scale, sum.
+int launch_quantize(lbt_ctx* ctx, const float* x, const float* norm_w, float eps, int m, int k, int8_t* q,
+                    float* scale, int32_t* sum);
+
+// ---- bf16 linear / LM head ------------------------------------------------
+// logits[t*rows + r] = sum_k xn[t,k] * W[r,k] with xn = rmsnorm(x) if norm_w.
+// If key != nullptr, the first-max key of row t is atomically maxed into key[t].
+int launch_bf16_linear(lbt_ctx* ctx, const uint16_t* w, int rows, int cols, const float* x, int m,
+                       const float* norm_w, float eps, float* logits, unsigned long long* key);
+
+// ---- model pieces --------------------------------------------------------
+int launch_embed(lbt_ctx* ctx, const uint16_t* embed, int hidden, const uint32_t* tokens,
+                 const unsigned long long* key, uint32_t* tok_out, int m, float* x);
+int launch_rope_append(lbt_ctx* ctx, const float* k, const float* v, int m, int kvh, int hd, int pos0,
+                       const float* cos_t, const float* sin_t, uint16_t* kc, uint16_t* vc, int cap);
+int launch_attention(lbt_ctx* ctx, const float* q, int m, int nh, int kvh, int hd, int pos0,
+                     const float* cos_t, const float* sin_t, const uint16_t* kc, const uint16_t* vc,
+                     int cap, float scaling, float* out);
+int launch_fill_u64(lbt_ctx* ctx, unsigned long long* p, int n, unsigned long long v);
+
+// Synthetic weights (same generator as oracle/lbt_oracle.c or_synth_*).
+int launch_synth_packed(lbt_ctx* ctx, uint64_t seed, uint64_t tensor, int rows, int cols, uint8_t* out);
+int launch_synth_f32(lbt_ctx* ctx, uint64_t seed, uint64_t tensor, size_t n, float lo, float span,
+                     float* out);
+int launch_synth_bf16(lbt_ctx* ctx, uint64_t seed, uint64_t tensor, size_t n, uint16_t* out);
+
+inline size_t padded_cols(size_t cols) { return (cols + 127) / 128 * 128; }
+
+}  // namespace lbt

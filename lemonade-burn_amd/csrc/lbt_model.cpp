@@ -1,0 +1,862 @@
+// lbt_model.cpp -- BitNet b1.58 2B4T token loop on the device.
+//
+// Host-side mirror of crates/lb-model/src/model.rs: BitNet::load (:149-232),
+// new_cache (:234), ensure_cap (:238-265), forward (:305-374).  Every op of a
+// step runs on the device; the host only enqueues kernels.  Per layer:
+//   qkv   : ternary GEMV, prologue RMSNorm(input_norm)+ActQuant (3 matrices)
+//   rope  : RoPE on k + bf16 append of K and V
+//   attn  : GQA attention over the bf16 cache (q rotated in-kernel)
+//   o     : ternary GEMV, prologue RMSNorm(attn_sub_norm)+ActQuant, x += y
+//   gu    : ternary GEMV over interleaved gate/up rows, prologue
+//           RMSNorm(post_attention_norm)+ActQuant, epilogue relu(g)^2 * u
+//   down  : ternary GEMV, prologue RMSNorm(ffn_sub_norm)+ActQuant, x += y
+// then the bf16 LM head with fused final RMSNorm and device argmax.
+#include <fcntl.h>
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdio.h>
+#include <string.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "lbt_internal.h"
+
+using namespace lbt;
+
+// ---------------------------------------------------------------------------
+// minimal JSON reader (config.json and the safetensors header)
+namespace {
+
+struct JVal {
+    enum Kind { Null, Bool, Num, Str, Arr, Obj } kind = Null;
+    bool b = false;
+    double num = 0.0;
+    std::string str;
+    std::vector<JVal> arr;
+    std::vector<std::pair<std::string, JVal>> obj;
+    const JVal* get(const std::string& k) const {
+        for (auto& kv : obj)
+            if (kv.first == k) return &kv.second;
+        return nullptr;
+    }
+};
+
+struct JParser {
+    const char* p;
+    const char* e;
+    bool ok = true;
+    void ws() {
+        while (p < e && (*p == ' ' || *p == '\n' || *p == '\r' || *p == '\t')) p++;
+    }
+    bool lit(const char* s) {
+        size_t n = strlen(s);
+        if ((size_t)(e - p) >= n && !memcmp(p, s, n)) {
+            p += n;
+            return true;
+        }
+        return false;
+    }
+    std::string str() {
+        std::string out;
+        if (p >= e || *p != '"') {
+            ok = false;
+            return out;
+        }
+        p++;
+        while (p < e && *p != '"') {
+            if (*p == '\\' && p + 1 < e) {
+                p++;
+                char c = *p;
+                if (c == 'n') out += '\n';
+                else if (c == 't') out += '\t';
+                else if (c == 'u') {
+                    // keep escapes verbatim (not needed for the keys we read)
+                    out += "\\u";
+                } else out += c;
+                p++;
+            } else {
+                out += *p++;
+            }
+        }
+        if (p >= e) ok = false;
+        else p++;
+        return out;
+    }
+    JVal val(int depth = 0) {
+        JVal v;
+        if (depth > 64) {
+            ok = false;
+            return v;
+        }
+        ws();
+        if (p >= e) {
+            ok = false;
+            return v;
+        }
+        if (*p == '{') {
+            p++;
+            v.kind = JVal::Obj;
+            ws();
+            if (p < e && *p == '}') {
+                p++;
+                return v;
+            }
+            while (ok) {
+                ws();
+                std::string k = str();
+                ws();
+                if (p >= e || *p != ':') {
+                    ok = false;
+                    break;
+                }
+                p++;
+                JVal c = val(depth + 1);
+                v.obj.emplace_back(k, std::move(c));
+                ws();
+                if (p < e && *p == ',') {
+                    p++;
+                    continue;
+                }
+                if (p < e && *p == '}') {
+                    p++;
+                    break;
+                }
+                ok = false;
+            }
+        } else if (*p == '[') {
+            p++;
+            v.kind = JVal::Arr;
+            ws();
+            if (p < e && *p == ']') {
+                p++;
+                return v;
+            }
+            while (ok) {
+                v.arr.push_back(val(depth + 1));
+                ws();
+                if (p < e && *p == ',') {
+                    p++;
+                    continue;
+                }
+                if (p < e && *p == ']') {
+                    p++;
+                    break;
+                }
+                ok = false;
+            }
+        } else if (*p == '"') {
+            v.kind = JVal::Str;
+            v.str = str();
+        } else if (lit("true")) {
+            v.kind = JVal::Bool;
+            v.b = true;
+        } else if (lit("false")) {
+            v.kind = JVal::Bool;
+        } else if (lit("null")) {
+            v.kind = JVal::Null;
+        } else {
+            char* end = nullptr;
+            std::string tmp(p, (size_t)std::min<ptrdiff_t>(e - p, 64));
+            v.num = strtod(tmp.c_str(), &end);
+            if (end == tmp.c_str()) {
+                ok = false;
+                return v;
+            }
+            v.kind = JVal::Num;
+            p += end - tmp.c_str();
+        }
+        return v;
+    }
+};
+
+bool parse_json(const char* s, size_t n, JVal& out) {
+    JParser jp{s, s + n};
+    out = jp.val();
+    return jp.ok;
+}
+
+struct MappedFile {
+    void* base = MAP_FAILED;
+    size_t size = 0;
+    ~MappedFile() {
+        if (base != MAP_FAILED) munmap(base, size);
+    }
+    bool open(const std::string& path) {
+        int fd = ::open(path.c_str(), O_RDONLY);
+        if (fd < 0) return false;
+        struct stat st;
+        if (fstat(fd, &st) != 0 || st.st_size <= 0) {
+            ::close(fd);
+            return false;
+        }
+        size = (size_t)st.st_size;
+        base = mmap(nullptr, size, PROT_READ, MAP_PRIVATE, fd, 0);
+        ::close(fd);
+        return base != MAP_FAILED;
+    }
+};
+
+struct StTensor {
+    std::string dtype;
+    std::vector<size_t> shape;
+    const uint8_t* data = nullptr;
+    size_t bytes = 0;
+};
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+struct lbt_model {
+    lbt_ctx* ctx = nullptr;
+    lbt_config cfg{};
+    int hd = 0;
+    uint8_t* wbuf = nullptr;  // all packed linears
+    std::vector<lbt_weight> lin;  // layers * 7, views into wbuf
+    float* fbuf = nullptr;        // norms (layers * 4) + final norm
+    std::vector<const float*> norm;
+    const float* final_norm = nullptr;
+    uint16_t* embed = nullptr;
+    float* cos_t = nullptr;
+    float* sin_t = nullptr;
+    float scaling = 0.0f;
+    // workspace sized for `mcap` tokens
+    int mcap = 0;
+    float *x = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr, *h = nullptr, *logits = nullptr;
+    uint32_t* toks = nullptr;
+    uint32_t* tok_out = nullptr;
+    int tok_out_cap = 0;
+    unsigned long long* key = nullptr;
+    int last_n = 0;
+};
+
+struct lbt_cache {
+    lbt_model* m = nullptr;
+    uint16_t* k = nullptr;  // [layers][kvh][cap][hd]
+    uint16_t* v = nullptr;
+    int len = 0;
+    int cap = 0;
+};
+
+namespace {
+
+void lin_shape(const lbt_config& c, int which, int& rows, int& cols) {
+    const int hd = c.hidden_size / c.num_attention_heads;
+    const int kv = c.num_key_value_heads * hd;
+    rows = (which == 1 || which == 2) ? kv : ((which == 4 || which == 5) ? c.intermediate_size : c.hidden_size);
+    cols = which == 6 ? c.intermediate_size : c.hidden_size;
+}
+
+int validate_config(lbt_ctx* ctx, const lbt_config& c) {
+    if (c.hidden_size <= 0 || c.intermediate_size <= 0 || c.num_attention_heads <= 0 || c.num_key_value_heads <= 0 ||
+        c.num_hidden_layers <= 0 || c.vocab_size <= 0 || c.max_position_embeddings <= 0)
+        return set_err(ctx, LBT_E_INVALID, "config: non-positive dimension");
+    if (c.hidden_size % c.num_attention_heads || c.num_attention_heads % c.num_key_value_heads)
+        return set_err(ctx, LBT_E_INVALID, "config: heads do not divide");
+    const int hd = c.hidden_size / c.num_attention_heads;
+    if (hd % 8 || hd > 256) return set_err(ctx, LBT_E_INVALID, "config: head_dim must be a multiple of 8, <= 256");
+    if (c.hidden_size % 8) return set_err(ctx, LBT_E_INVALID, "config: hidden_size must be a multiple of 8");
+    return LBT_OK;
+}
+
+// Device buffers and RoPE tables shared by load and synthetic creation.
+int model_alloc(lbt_model* m) {
+    lbt_ctx* ctx = m->ctx;
+    const lbt_config& c = m->cfg;
+    m->hd = c.hidden_size / c.num_attention_heads;
+    size_t wbytes = 0;
+    std::vector<size_t> off;
+    for (int l = 0; l < c.num_hidden_layers; l++)
+        for (int w = 0; w < 7; w++) {
+            int rows, cols;
+            lin_shape(c, w, rows, cols);
+            off.push_back(wbytes);
+            wbytes += ((size_t)rows * padded_cols((size_t)cols) / 4 + 255) & ~(size_t)255;
+        }
+    LBT_HIP(ctx, hipMalloc(&m->wbuf, wbytes));
+    m->lin.resize(off.size());
+    for (int l = 0; l < c.num_hidden_layers; l++)
+        for (int w = 0; w < 7; w++) {
+            int rows, cols;
+            lin_shape(c, w, rows, cols);
+            lbt_weight& lw = m->lin[l * 7 + w];
+            lw.ctx = ctx;
+            lw.d = m->wbuf + off[l * 7 + w];
+            lw.rows = (size_t)rows;
+            lw.cols = (size_t)cols;
+            lw.kp = padded_cols((size_t)cols);
+            lw.owns = false;
+        }
+    size_t nf = 0;
+    std::vector<size_t> foff;
+    for (int l = 0; l < c.num_hidden_layers; l++)
+        for (int k = 0; k < 4; k++) {
+            foff.push_back(nf);
+            nf += (size_t)(k == 3 ? c.intermediate_size : c.hidden_size);
+        }
+    foff.push_back(nf);
+    nf += (size_t)c.hidden_size;
+    LBT_HIP(ctx, hipMalloc(&m->fbuf, nf * sizeof(float)));
+    for (size_t i = 0; i + 1 < foff.size(); i++) m->norm.push_back(m->fbuf + foff[i]);
+    m->final_norm = m->fbuf + foff.back();
+    LBT_HIP(ctx, hipMalloc(&m->embed, (size_t)c.vocab_size * c.hidden_size * 2));
+
+    // RoPE tables as model.rs:213-230 builds them: inv in f64 rounded to f32,
+    // angle = pos (f32) * inv (f32), sin/cos in f64 rounded to f32.  Only the
+    // first half is stored: dims i and i + hd/2 share an entry.
+    const int h2 = m->hd / 2;
+    const size_t tn = (size_t)c.max_position_embeddings * h2;
+    std::vector<float> ct(tn), st(tn), inv(h2);
+    for (int i = 0; i < h2; i++) inv[i] = (float)(1.0 / pow(c.rope_theta, (double)(2 * i) / (double)m->hd));
+    for (int p = 0; p < c.max_position_embeddings; p++)
+        for (int i = 0; i < h2; i++) {
+            const float f = (float)p * inv[i];
+            ct[(size_t)p * h2 + i] = (float)cos((double)f);
+            st[(size_t)p * h2 + i] = (float)sin((double)f);
+        }
+    LBT_HIP(ctx, hipMalloc(&m->cos_t, tn * sizeof(float)));
+    LBT_HIP(ctx, hipMalloc(&m->sin_t, tn * sizeof(float)));
+    LBT_HIP(ctx, hipMemcpy(m->cos_t, ct.data(), tn * sizeof(float), hipMemcpyHostToDevice));
+    LBT_HIP(ctx, hipMemcpy(m->sin_t, st.data(), tn * sizeof(float), hipMemcpyHostToDevice));
+    m->scaling = powf((float)m->hd, -0.5f);  // (hd as f32).powf(-0.5), model.rs:314
+    return LBT_OK;
+}
+
+int ensure_ws(lbt_model* m, int n) {
+    if (n <= m->mcap) return LBT_OK;
+    lbt_ctx* ctx = m->ctx;
+    hipStreamSynchronize(ctx->stream);
+    float** bufs[] = {&m->x, &m->q, &m->k, &m->v, &m->att, &m->h, &m->logits};
+    for (auto b : bufs)
+        if (*b) {
+            hipFree(*b);
+            *b = nullptr;
+        }
+    if (m->toks) hipFree(m->toks);
+    if (m->key) hipFree(m->key);
+    const lbt_config& c = m->cfg;
+    const size_t H = (size_t)c.hidden_size, I = (size_t)c.intermediate_size;
+    const size_t KV = (size_t)c.num_key_value_heads * m->hd;
+    LBT_HIP(ctx, hipMalloc(&m->x, n * H * 4));
+    LBT_HIP(ctx, hipMalloc(&m->q, n * H * 4));
+    LBT_HIP(ctx, hipMalloc(&m->k, n * KV * 4));
+    LBT_HIP(ctx, hipMalloc(&m->v, n * KV * 4));
+    LBT_HIP(ctx, hipMalloc(&m->att, n * H * 4));
+    LBT_HIP(ctx, hipMalloc(&m->h, n * I * 4));
+    LBT_HIP(ctx, hipMalloc(&m->logits, (size_t)n * c.vocab_size * 4));
+    LBT_HIP(ctx, hipMalloc(&m->toks, n * 4));
+    LBT_HIP(ctx, hipMalloc(&m->key, n * 8));
+    m->mcap = n;
+    return LBT_OK;
+}
+
+// ensure_cap (model.rs:238-265): next power of two, at least 256, at most
+// max_position_embeddings (or the need); old contents are kept.
+int ensure_cap(lbt_cache* cc, int need) {
+    if (need <= cc->cap) return LBT_OK;
+    lbt_model* m = cc->m;
+    lbt_ctx* ctx = m->ctx;
+    const lbt_config& c = m->cfg;
+    if (need > c.max_position_embeddings)
+        return set_err(ctx, LBT_E_RANGE, "context length " + std::to_string(c.max_position_embeddings) + " exceeded");
+    int cap = 1;
+    while (cap < need) cap <<= 1;
+    if (cap < 256) cap = 256;
+    if (cap > c.max_position_embeddings) cap = c.max_position_embeddings;
+    const size_t kvh = (size_t)c.num_key_value_heads, hd = (size_t)m->hd, L = (size_t)c.num_hidden_layers;
+    uint16_t *nk = nullptr, *nv = nullptr;
+    LBT_HIP(ctx, hipMalloc(&nk, L * kvh * cap * hd * 2));
+    LBT_HIP(ctx, hipMalloc(&nv, L * kvh * cap * hd * 2));
+    if (cc->k && cc->len > 0) {
+        // per (layer, head): copy the first len rows
+        LBT_HIP(ctx, hipMemcpy2DAsync(nk, (size_t)cap * hd * 2, cc->k, (size_t)cc->cap * hd * 2, (size_t)cc->len * hd * 2,
+                                      L * kvh, hipMemcpyDeviceToDevice, ctx->stream));
+        LBT_HIP(ctx, hipMemcpy2DAsync(nv, (size_t)cap * hd * 2, cc->v, (size_t)cc->cap * hd * 2, (size_t)cc->len * hd * 2,
+                                      L * kvh, hipMemcpyDeviceToDevice, ctx->stream));
+    }
+    LBT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    if (cc->k) hipFree(cc->k);
+    if (cc->v) hipFree(cc->v);
+    cc->k = nk;
+    cc->v = nv;
+    cc->cap = cap;
+    return LBT_OK;
+}
+
+// One forward over n tokens at positions cache.len.. (tokens from `toks_dev`,
+// or from the previous step's argmax key when null).  Leaves the argmax key of
+// the last row in m->key[0] and logits (if `logits_all` or `want_logits`).
+int forward_dev(lbt_model* m, lbt_cache* cc, const uint32_t* toks_dev, int n, bool all_logits, bool want_logits,
+                uint32_t* tok_out_dev) {
+    lbt_ctx* ctx = m->ctx;
+    const lbt_config& c = m->cfg;
+    const int H = c.hidden_size, I = c.intermediate_size, nh = c.num_attention_heads, kvh = c.num_key_value_heads;
+    const int hd = m->hd, pos0 = cc->len;
+    const float eps = (float)c.rms_norm_eps;
+    int rc = launch_embed(ctx, m->embed, H, toks_dev, m->key, tok_out_dev, n, m->x);
+    if (rc) return rc;
+    const size_t layer_kv = (size_t)kvh * cc->cap * hd;
+    for (int l = 0; l < c.num_hidden_layers; l++) {
+        const lbt_weight* W = &m->lin[l * 7];
+        TernaryOp op;
+        op.cols = H;
+        op.m = n;
+        op.in_mode = kInF32;
+        op.eps = eps;
+        // q/k/v (forward3, model.rs:68-74 / :333)
+        op.nmat = 3;
+        for (int i = 0; i < 3; i++) {
+            op.w[i] = W[i].d;
+            op.rows[i] = (int)W[i].rows;
+            op.sw[i] = W[i].scale;
+        }
+        op.x = m->x;
+        op.norm_w = m->norm[l * 4 + 0];
+        op.out_mode = kOutF32;
+        op.out[0] = m->q;
+        op.out[1] = m->k;
+        op.out[2] = m->v;
+        if ((rc = launch_ternary(ctx, op))) return rc;
+        uint16_t* Kl = cc->k + (size_t)l * layer_kv;
+        uint16_t* Vl = cc->v + (size_t)l * layer_kv;
+        if ((rc = launch_rope_append(ctx, m->k, m->v, n, kvh, hd, pos0, m->cos_t, m->sin_t, Kl, Vl, cc->cap))) return rc;
+        if ((rc = launch_attention(ctx, m->q, n, nh, kvh, hd, pos0, m->cos_t, m->sin_t, Kl, Vl, cc->cap, m->scaling,
+                                   m->att)))
+            return rc;
+        // o_proj on attn_sub_norm(attn), residual (model.rs:358-359)
+        TernaryOp o;
+        o.nmat = 1;
+        o.w[0] = W[3].d;
+        o.rows[0] = (int)W[3].rows;
+        o.sw[0] = W[3].scale;
+        o.cols = H;
+        o.m = n;
+        o.in_mode = kInF32;
+        o.x = m->att;
+        o.norm_w = m->norm[l * 4 + 2];
+        o.eps = eps;
+        o.out_mode = kOutF32Add;
+        o.out[0] = m->x;
+        if ((rc = launch_ternary(ctx, o))) return rc;
+        // gate/up on post_attention_norm(x), relu(g)^2 * u (model.rs:361-363)
+        TernaryOp gu;
+        gu.nmat = 2;
+        for (int i = 0; i < 2; i++) {
+            gu.w[i] = W[4 + i].d;
+            gu.rows[i] = (int)W[4 + i].rows;
+            gu.sw[i] = W[4 + i].scale;
+        }
+        gu.cols = H;
+        gu.m = n;
+        gu.in_mode = kInF32;
+        gu.x = m->x;
+        gu.norm_w = m->norm[l * 4 + 1];
+        gu.eps = eps;
+        gu.out_mode = kOutRelu2;
+        gu.out[0] = m->h;
+        if ((rc = launch_ternary(ctx, gu))) return rc;
+        // down on ffn_sub_norm(h), residual (model.rs:364-365)
+        TernaryOp dn;
+        dn.nmat = 1;
+        dn.w[0] = W[6].d;
+        dn.rows[0] = (int)W[6].rows;
+        dn.sw[0] = W[6].scale;
+        dn.cols = I;
+        dn.m = n;
+        dn.in_mode = kInF32;
+        dn.x = m->h;
+        dn.norm_w = m->norm[l * 4 + 3];
+        dn.eps = eps;
+        dn.out_mode = kOutF32Add;
+        dn.out[0] = m->x;
+        if ((rc = launch_ternary(ctx, dn))) return rc;
+    }
+    cc->len = pos0 + n;
+    m->last_n = n;
+    // final norm + tied LM head (model.rs:368-373) + argmax
+    const int first = all_logits ? 0 : n - 1;
+    const int rows_out = n - first;
+    return launch_bf16_linear(ctx, m->embed, c.vocab_size, H, m->x + (size_t)first * H, rows_out, m->final_norm, eps,
+                              (all_logits || want_logits) ? m->logits : nullptr, all_logits ? nullptr : m->key);
+}
+
+int read_config(lbt_ctx* ctx, const std::string& dir, lbt_config& c) {
+    std::string path = dir + "/config.json";
+    FILE* f = fopen(path.c_str(), "rb");
+    if (!f) return set_err(ctx, LBT_E_IO, "cannot open " + path);
+    std::string s;
+    char buf[4096];
+    size_t n;
+    while ((n = fread(buf, 1, sizeof(buf), f)) > 0) s.append(buf, n);
+    fclose(f);
+    JVal j;
+    if (!parse_json(s.data(), s.size(), j) || j.kind != JVal::Obj) return set_err(ctx, LBT_E_IO, "bad json: " + path);
+    auto num = [&](const char* k, double& out) -> bool {
+        const JVal* v = j.get(k);
+        if (!v || v->kind != JVal::Num) return false;
+        out = v->num;
+        return true;
+    };
+    double d;
+    const char* keys[] = {"hidden_size", "intermediate_size", "num_attention_heads", "num_key_value_heads",
+                          "num_hidden_layers", "vocab_size", "max_position_embeddings"};
+    int32_t* dst[] = {&c.hidden_size, &c.intermediate_size, &c.num_attention_heads, &c.num_key_value_heads,
+                      &c.num_hidden_layers, &c.vocab_size, &c.max_position_embeddings};
+    for (int i = 0; i < 7; i++) {
+        if (!num(keys[i], d)) return set_err(ctx, LBT_E_IO, std::string("config.json: missing ") + keys[i]);
+        *dst[i] = (int32_t)d;
+    }
+    if (!num("rms_norm_eps", c.rms_norm_eps)) return set_err(ctx, LBT_E_IO, "config.json: missing rms_norm_eps");
+    if (!num("rope_theta", c.rope_theta)) return set_err(ctx, LBT_E_IO, "config.json: missing rope_theta");
+    c.bos_token_id = num("bos_token_id", d) ? (uint32_t)d : 0u;
+    const JVal* act = j.get("hidden_act");
+    const JVal* tied = j.get("tie_word_embeddings");
+    // model.rs:151-153
+    if (!act || act->kind != JVal::Str || act->str != "relu2" || !tied || tied->kind != JVal::Bool || !tied->b)
+        return set_err(ctx, LBT_E_INVALID, "unsupported config: needs hidden_act=relu2 and tie_word_embeddings=true");
+    return LBT_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int lbt_model_create_synthetic(lbt_ctx* ctx, const lbt_config* cfg, uint64_t seed, lbt_model** out) {
+    if (!ctx || !cfg || !out) return set_err(ctx, LBT_E_INVALID, "create_synthetic: bad arguments");
+    *out = nullptr;
+    int rc = validate_config(ctx, *cfg);
+    if (rc) return rc;
+    std::unique_ptr<lbt_model> m(new lbt_model());
+    m->ctx = ctx;
+    m->cfg = *cfg;
+    if ((rc = model_alloc(m.get()))) {
+        lbt_model_free(m.release());
+        return rc;
+    }
+    const lbt_config& c = m->cfg;
+    const uint64_t T_EMBED = 1, T_FINAL = 2;
+    for (int l = 0; l < c.num_hidden_layers; l++) {
+        for (int w = 0; w < 7; w++) {
+            lbt_weight& lw = m->lin[l * 7 + w];
+            lw.scale = (float)sqrt(0.6 * (double)lw.cols);
+            if ((rc = launch_synth_packed(ctx, seed, 16u + (uint64_t)l * 16u + w, (int)lw.rows, (int)lw.cols,
+                                          lw.d))) {
+                lbt_model_free(m.release());
+                return rc;
+            }
+        }
+        for (int k = 0; k < 4; k++) {
+            const size_t n = (size_t)(k == 3 ? c.intermediate_size : c.hidden_size);
+            if ((rc = launch_synth_f32(ctx, seed, 16u + (uint64_t)l * 16u + 7 + k, n, 0.5f, 1.0f,
+                                       (float*)m->norm[l * 4 + k]))) {
+                lbt_model_free(m.release());
+                return rc;
+            }
+        }
+    }
+    if ((rc = launch_synth_f32(ctx, seed, T_FINAL, (size_t)c.hidden_size, 0.5f, 1.0f, (float*)m->final_norm)) ||
+        (rc = launch_synth_bf16(ctx, seed, T_EMBED, (size_t)c.vocab_size * c.hidden_size, m->embed))) {
+        lbt_model_free(m.release());
+        return rc;
+    }
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) {
+        lbt_model_free(m.release());
+        return hip_err(ctx, e, "synthetic model");
+    }
+    *out = m.release();
+    return LBT_OK;
+}
+
+int lbt_model_load(lbt_ctx* ctx, const char* dir, lbt_model** out) {
+    if (!ctx || !dir || !out) return set_err(ctx, LBT_E_INVALID, "model_load: bad arguments");
+    *out = nullptr;
+    lbt_config c{};
+    int rc = read_config(ctx, dir, c);
+    if (rc) return rc;
+    if ((rc = validate_config(ctx, c))) return rc;
+    MappedFile mf;
+    std::string path = std::string(dir) + "/model.lbt.safetensors";
+    if (!mf.open(path)) return set_err(ctx, LBT_E_IO, "cannot open " + path);
+    const uint8_t* base = (const uint8_t*)mf.base;
+    if (mf.size < 8) return set_err(ctx, LBT_E_IO, "truncated safetensors file");
+    uint64_t hlen = 0;
+    memcpy(&hlen, base, 8);
+    if (hlen > mf.size - 8) return set_err(ctx, LBT_E_IO, "bad safetensors header length");
+    JVal hdr;
+    if (!parse_json((const char*)base + 8, (size_t)hlen, hdr) || hdr.kind != JVal::Obj)
+        return set_err(ctx, LBT_E_IO, "bad safetensors header");
+    const uint8_t* data0 = base + 8 + hlen;
+    const size_t data_size = mf.size - 8 - hlen;
+    // format check (model.rs:158-161, lb-convert/src/lib.rs:14)
+    const JVal* meta = hdr.get("__metadata__");
+    const JVal* fmt = meta ? meta->get("format") : nullptr;
+    if (!fmt || fmt->kind != JVal::Str || fmt->str != "lemonade-burn-ternary")
+        return set_err(ctx, LBT_E_IO, path + " is not a lemonade-burn ternary file");
+    std::map<std::string, StTensor> tensors;
+    for (auto& kv : hdr.obj) {
+        if (kv.first == "__metadata__") continue;
+        const JVal& t = kv.second;
+        const JVal* dt = t.get("dtype");
+        const JVal* sh = t.get("shape");
+        const JVal* of = t.get("data_offsets");
+        if (!dt || !sh || !of || of->arr.size() != 2) return set_err(ctx, LBT_E_IO, "bad tensor entry " + kv.first);
+        StTensor st;
+        st.dtype = dt->str;
+        for (auto& d : sh->arr) st.shape.push_back((size_t)d.num);
+        size_t b = (size_t)of->arr[0].num, e = (size_t)of->arr[1].num;
+        if (b > e || e > data_size) return set_err(ctx, LBT_E_IO, "bad offsets for " + kv.first);
+        st.data = data0 + b;
+        st.bytes = e - b;
+        tensors[kv.first] = st;
+    }
+    std::unique_ptr<lbt_model> m(new lbt_model());
+    m->ctx = ctx;
+    m->cfg = c;
+    if ((rc = model_alloc(m.get()))) {
+        lbt_model_free(m.release());
+        return rc;
+    }
+    auto fail = [&](int code, const std::string& msg) {
+        lbt_model_free(m.release());
+        return set_err(ctx, code, msg);
+    };
+    static const char* lin_names[7] = {"self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj",
+                                       "mlp.gate_proj",    "mlp.up_proj",      "mlp.down_proj"};
+    static const char* norm_names[4] = {"input_layernorm.weight", "post_attention_layernorm.weight",
+                                        "self_attn.attn_sub_norm.weight", "mlp.ffn_sub_norm.weight"};
+    for (int l = 0; l < c.num_hidden_layers; l++) {
+        const std::string p = "model.layers." + std::to_string(l) + ".";
+        for (int w = 0; w < 7; w++) {
+            lbt_weight& lw = m->lin[l * 7 + w];
+            auto qi = tensors.find(p + lin_names[w] + ".qweight");
+            auto si = tensors.find(p + lin_names[w] + ".wscale");
+            if (qi == tensors.end() || si == tensors.end())
+                return fail(LBT_E_IO, "missing " + p + lin_names[w]);
+            const StTensor& qt = qi->second;
+            const size_t rb = lw.kp / 4;
+            if (qt.dtype != "U8" || qt.shape.size() != 2 || qt.shape[0] != lw.rows || qt.shape[1] != rb ||
+                qt.bytes != lw.rows * rb)
+                return fail(LBT_E_IO, "unexpected qweight shape for " + p + lin_names[w]);
+            if (si->second.dtype != "F32" || si->second.bytes < 4) return fail(LBT_E_IO, "bad wscale " + p + lin_names[w]);
+            memcpy(&lw.scale, si->second.data, 4);
+            hipError_t e = hipMemcpy(lw.d, qt.data, qt.bytes, hipMemcpyHostToDevice);
+            if (e != hipSuccess) {
+                int r = hip_err(ctx, e, "upload qweight");
+                lbt_model_free(m.release());
+                return r;
+            }
+        }
+        for (int k = 0; k < 4; k++) {
+            auto ni = tensors.find(p + norm_names[k]);
+            const size_t n = (size_t)(k == 3 ? c.intermediate_size : c.hidden_size);
+            if (ni == tensors.end() || ni->second.dtype != "F32" || ni->second.bytes != n * 4)
+                return fail(LBT_E_IO, "missing or bad " + p + norm_names[k]);
+            if (hipMemcpy((void*)m->norm[l * 4 + k], ni->second.data, n * 4, hipMemcpyHostToDevice) != hipSuccess)
+                return fail(LBT_E_DEVICE, "upload norm");
+        }
+    }
+    auto fi = tensors.find("model.norm.weight");
+    if (fi == tensors.end() || fi->second.dtype != "F32" || fi->second.bytes != (size_t)c.hidden_size * 4)
+        return fail(LBT_E_IO, "missing or bad model.norm.weight");
+    if (hipMemcpy((void*)m->final_norm, fi->second.data, fi->second.bytes, hipMemcpyHostToDevice) != hipSuccess)
+        return fail(LBT_E_DEVICE, "upload final norm");
+    auto ei = tensors.find("model.embed_tokens.weight");
+    // model.rs:203-206
+    if (ei == tensors.end() || ei->second.dtype != "BF16" || ei->second.shape.size() != 2 ||
+        ei->second.shape[0] != (size_t)c.vocab_size || ei->second.shape[1] != (size_t)c.hidden_size)
+        return fail(LBT_E_IO, "embed_tokens: unexpected dtype/shape");
+    if (hipMemcpy(m->embed, ei->second.data, ei->second.bytes, hipMemcpyHostToDevice) != hipSuccess)
+        return fail(LBT_E_DEVICE, "upload embedding");
+    *out = m.release();
+    return LBT_OK;
+}
+
+void lbt_model_free(lbt_model* m) {
+    if (!m) return;
+    hipStreamSynchronize(m->ctx->stream);
+    void* bufs[] = {m->wbuf, m->fbuf, m->embed, m->cos_t, m->sin_t, m->x,   m->q,       m->k,
+                    m->v,    m->att,  m->h,     m->logits, m->toks, m->key, m->tok_out};
+    for (void* b : bufs)
+        if (b) hipFree(b);
+    delete m;
+}
+
+int lbt_model_get_config(const lbt_model* m, lbt_config* out) {
+    if (!m || !out) return LBT_E_INVALID;
+    *out = m->cfg;
+    return LBT_OK;
+}
+
+const lbt_weight* lbt_model_linear(const lbt_model* m, int layer, int which) {
+    if (!m || layer < 0 || layer >= m->cfg.num_hidden_layers || which < 0 || which > 6) return nullptr;
+    return &m->lin[layer * 7 + which];
+}
+
+int lbt_cache_new(lbt_model* m, lbt_cache** out) {
+    if (!m || !out) return LBT_E_INVALID;
+    lbt_cache* c = new lbt_cache();
+    c->m = m;
+    *out = c;
+    return LBT_OK;
+}
+
+void lbt_cache_free(lbt_cache* c) {
+    if (!c) return;
+    hipStreamSynchronize(c->m->ctx->stream);
+    if (c->k) hipFree(c->k);
+    if (c->v) hipFree(c->v);
+    delete c;
+}
+
+int lbt_cache_len(const lbt_cache* c) { return c ? c->len : -1; }
+
+int lbt_cache_read(lbt_cache* c, int layer, int is_v, uint16_t* out) {
+    if (!c || !out) return LBT_E_INVALID;
+    lbt_model* m = c->m;
+    lbt_ctx* ctx = m->ctx;
+    if (layer < 0 || layer >= m->cfg.num_hidden_layers) return set_err(ctx, LBT_E_INVALID, "cache_read: bad layer");
+    if (c->len == 0) return LBT_OK;
+    const size_t kvh = (size_t)m->cfg.num_key_value_heads, hd = (size_t)m->hd;
+    const uint16_t* src = (is_v ? c->v : c->k) + (size_t)layer * kvh * c->cap * hd;
+    LBT_HIP(ctx, hipMemcpy2DAsync(out, (size_t)c->len * hd * 2, src, (size_t)c->cap * hd * 2, (size_t)c->len * hd * 2,
+                                  kvh, hipMemcpyDeviceToHost, ctx->stream));
+    LBT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return LBT_OK;
+}
+
+static int upload_tokens(lbt_model* m, const uint32_t* tokens, size_t n) {
+    lbt_ctx* ctx = m->ctx;
+    for (size_t i = 0; i < n; i++)
+        if (tokens[i] >= (uint32_t)m->cfg.vocab_size) return set_err(ctx, LBT_E_INVALID, "token id out of range");
+    LBT_HIP(ctx, hipMemcpyAsync(m->toks, tokens, n * 4, hipMemcpyHostToDevice, ctx->stream));
+    return LBT_OK;
+}
+
+int lbt_model_forward(lbt_model* m, const uint32_t* tokens, size_t n, lbt_cache* c, int all_logits, float* logits) {
+    if (!m || !c || !tokens || n == 0) return set_err(m ? m->ctx : nullptr, LBT_E_INVALID, "forward: bad arguments");
+    lbt_ctx* ctx = m->ctx;
+    int rc;
+    if ((rc = ensure_cap(c, c->len + (int)n))) return rc;
+    if ((rc = ensure_ws(m, (int)n))) return rc;
+    if ((rc = upload_tokens(m, tokens, n))) return rc;
+    if ((rc = forward_dev(m, c, m->toks, (int)n, all_logits != 0, true, nullptr))) return rc;
+    const size_t rows = all_logits ? n : 1;
+    if (logits)
+        LBT_HIP(ctx, hipMemcpyAsync(logits, m->logits, rows * (size_t)m->cfg.vocab_size * 4, hipMemcpyDeviceToHost,
+                                    ctx->stream));
+    LBT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return LBT_OK;
+}
+
+int lbt_model_forward_argmax(lbt_model* m, const uint32_t* tokens, size_t n, lbt_cache* c, uint32_t* next) {
+    if (!m || !c || !tokens || n == 0 || !next) return set_err(m ? m->ctx : nullptr, LBT_E_INVALID, "bad arguments");
+    lbt_ctx* ctx = m->ctx;
+    int rc;
+    if ((rc = ensure_cap(c, c->len + (int)n))) return rc;
+    if ((rc = ensure_ws(m, (int)n))) return rc;
+    if ((rc = upload_tokens(m, tokens, n))) return rc;
+    if ((rc = forward_dev(m, c, m->toks, (int)n, false, false, nullptr))) return rc;
+    unsigned long long key = 0;
+    LBT_HIP(ctx, hipMemcpyAsync(&key, m->key, 8, hipMemcpyDeviceToHost, ctx->stream));
+    LBT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    *next = 0xffffffffu - (uint32_t)(key & 0xffffffffull);
+    return LBT_OK;
+}
+
+int lbt_model_generate_greedy(lbt_model* m, const uint32_t* prompt, size_t n, size_t steps, lbt_cache* c,
+                              uint32_t* out_tokens, float* ms_prefill, float* ms_decode) {
+    if (!m || !c || !prompt || n == 0 || !out_tokens) return set_err(m ? m->ctx : nullptr, LBT_E_INVALID, "bad arguments");
+    lbt_ctx* ctx = m->ctx;
+    int rc;
+    if ((rc = ensure_cap(c, c->len + (int)n + (int)steps))) return rc;
+    if ((rc = ensure_ws(m, (int)n))) return rc;
+    if ((int)steps + 1 > m->tok_out_cap) {
+        if (m->tok_out) hipFree(m->tok_out);
+        m->tok_out = nullptr;
+        LBT_HIP(ctx, hipMalloc(&m->tok_out, (steps + 1) * 4));
+        m->tok_out_cap = (int)steps + 1;
+    }
+    if ((rc = upload_tokens(m, prompt, n))) return rc;
+    hipEvent_t e0, e1, e2;
+    LBT_HIP(ctx, hipEventCreate(&e0));
+    LBT_HIP(ctx, hipEventCreate(&e1));
+    LBT_HIP(ctx, hipEventCreate(&e2));
+    LBT_HIP(ctx, hipEventRecord(e0, ctx->stream));
+    rc = forward_dev(m, c, m->toks, (int)n, false, false, nullptr);
+    if (!rc) {
+        hipEventRecord(e1, ctx->stream);
+        for (size_t s = 0; s < steps && !rc; s++) rc = forward_dev(m, c, nullptr, 1, false, false, m->tok_out + s);
+        // the last argmax
+        if (!rc) rc = launch_embed(ctx, m->embed, 0, nullptr, m->key, m->tok_out + steps, 1, m->x);
+        hipEventRecord(e2, ctx->stream);
+    }
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (!rc && e != hipSuccess) rc = hip_err(ctx, e, "generate");
+    if (!rc) {
+        float a = 0, b = 0;
+        hipEventElapsedTime(&a, e0, e1);
+        hipEventElapsedTime(&b, e1, e2);
+        if (ms_prefill) *ms_prefill = a;
+        if (ms_decode) *ms_decode = b;
+        e = hipMemcpy(out_tokens, m->tok_out, (steps + 1) * 4, hipMemcpyDeviceToHost);
+        if (e != hipSuccess) rc = hip_err(ctx, e, "read tokens");
+    }
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    hipEventDestroy(e2);
+    return rc;
+}
+
+int lbt_model_decode_greedy(lbt_model* m, lbt_cache* c, uint32_t first, size_t steps, uint32_t* out_tokens,
+                            float* ms_decode) {
+    if (!m || !c || !out_tokens || steps == 0) return set_err(m ? m->ctx : nullptr, LBT_E_INVALID, "bad arguments");
+    lbt_ctx* ctx = m->ctx;
+    if (first >= (uint32_t)m->cfg.vocab_size) return set_err(ctx, LBT_E_INVALID, "token id out of range");
+    int rc;
+    if ((rc = ensure_cap(c, c->len + (int)steps))) return rc;
+    if ((rc = ensure_ws(m, 1))) return rc;
+    if ((int)steps + 1 > m->tok_out_cap) {
+        if (m->tok_out) hipFree(m->tok_out);
+        m->tok_out = nullptr;
+        LBT_HIP(ctx, hipMalloc(&m->tok_out, (steps + 1) * 4));
+        m->tok_out_cap = (int)steps + 1;
+    }
+    LBT_HIP(ctx, hipMemcpyAsync(m->toks, &first, 4, hipMemcpyHostToDevice, ctx->stream));
+    hipEvent_t e0, e1;
+    LBT_HIP(ctx, hipEventCreate(&e0));
+    LBT_HIP(ctx, hipEventCreate(&e1));
+    hipEventRecord(e0, ctx->stream);
+    rc = forward_dev(m, c, m->toks, 1, false, false, nullptr);
+    for (size_t s = 1; s < steps && !rc; s++) rc = forward_dev(m, c, nullptr, 1, false, false, m->tok_out + s - 1);
+    if (!rc) rc = launch_embed(ctx, m->embed, 0, nullptr, m->key, m->tok_out + steps - 1, 1, m->x);
+    hipEventRecord(e1, ctx->stream);
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (!rc && e != hipSuccess) rc = hip_err(ctx, e, "decode");
+    if (!rc) {
+        float a = 0;
+        hipEventElapsedTime(&a, e0, e1);
+        if (ms_decode) *ms_decode = a;
+        e = hipMemcpy(out_tokens, m->tok_out, steps * 4, hipMemcpyDeviceToHost);
+        if (e != hipSuccess) rc = hip_err(ctx, e, "read tokens");
+    }
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    return rc;
+}
+
+int lbt_model_read_hidden(lbt_model* m, float* out, size_t n) {
+    if (!m || !out) return LBT_E_INVALID;
+    lbt_ctx* ctx = m->ctx;
+    if (n > (size_t)m->last_n) return set_err(ctx, LBT_E_INVALID, "read_hidden: more rows than the last forward");
+    LBT_HIP(ctx, hipMemcpyAsync(out, m->x, n * (size_t)m->cfg.hidden_size * 4, hipMemcpyDeviceToHost, ctx->stream));
+    LBT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return LBT_OK;
+}
+
+}  // extern "C"

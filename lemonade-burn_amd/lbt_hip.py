@@ -1,0 +1,360 @@
+"""ctypes binding of liblbt_hip.so (include/lbt.h) for Python callers.
+
+This is the Python mirror of the reference's `lb-ternary` / `lb-model`
+entry points (quantize_acts, ternary_gemm_i32, ternary_gemm_multi,
+ternary_linear{,2,3}, bf16_linear, BitNet::load/new_cache/forward) over the
+C ABI.  It loads the in-tree HIP library and raises if it is missing: there is
+no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+import numpy as np
+
+PKG = Path(__file__).resolve().parent
+LIB_PATH = PKG / "liblbt_hip.so"
+
+LBT_OK = 0
+ERRORS = {-1: "LBT_E_INVALID", -2: "LBT_E_DEVICE", -3: "LBT_E_NOMEM", -4: "LBT_E_IO", -5: "LBT_E_RANGE"}
+
+# Every exported entry point and its (restype, argtypes); test_abi checks that
+# this list equals the declarations of include/lbt.h.
+vp = C.c_void_p
+sz = C.c_size_t
+i32 = C.c_int
+f32 = C.c_float
+u64 = C.c_uint64
+
+
+class LbtConfig(C.Structure):
+    _fields_ = [
+        ("hidden_size", C.c_int32),
+        ("intermediate_size", C.c_int32),
+        ("num_attention_heads", C.c_int32),
+        ("num_key_value_heads", C.c_int32),
+        ("num_hidden_layers", C.c_int32),
+        ("vocab_size", C.c_int32),
+        ("max_position_embeddings", C.c_int32),
+        ("bos_token_id", C.c_uint32),
+        ("rms_norm_eps", C.c_double),
+        ("rope_theta", C.c_double),
+    ]
+
+
+class LbtProf(C.Structure):
+    _fields_ = [("ms", C.c_double * 5), ("bytes", C.c_double * 5), ("launches", C.c_uint64 * 5)]
+
+
+SIGNATURES = {
+    "lbt_ctx_create": (i32, [i32, C.POINTER(vp)]),
+    "lbt_ctx_destroy": (None, [vp]),
+    "lbt_last_error": (C.c_char_p, [vp]),
+    "lbt_ctx_synchronize": (i32, [vp]),
+    "lbt_ctx_stream": (vp, [vp]),
+    "lbt_dev_alloc": (i32, [vp, sz, C.POINTER(vp)]),
+    "lbt_dev_free": (i32, [vp, vp]),
+    "lbt_memcpy_h2d": (i32, [vp, vp, vp, sz]),
+    "lbt_memcpy_d2h": (i32, [vp, vp, vp, sz]),
+    "lbt_version": (C.c_char_p, []),
+    "lbt_weight_upload": (i32, [vp, vp, sz, sz, f32, C.POINTER(vp)]),
+    "lbt_weight_upload_dev": (i32, [vp, vp, sz, sz, f32, C.POINTER(vp)]),
+    "lbt_weight_free": (None, [vp]),
+    "lbt_weight_rows": (sz, [vp]),
+    "lbt_weight_cols": (sz, [vp]),
+    "lbt_weight_device_ptr": (vp, [vp]),
+    "lbt_quantize_acts": (i32, [vp, vp, sz, sz, vp, vp, vp]),
+    "lbt_quantize_acts_dev": (i32, [vp, vp, sz, sz, vp, vp, vp]),
+    "lbt_rmsnorm_quantize_dev": (i32, [vp, vp, vp, f32, sz, sz, vp, vp, vp]),
+    "lbt_gemm_i32": (i32, [vp, vp, vp, vp, sz, vp]),
+    "lbt_gemm_i32_dev": (i32, [vp, vp, vp, vp, sz, vp]),
+    "lbt_gemm_multi": (i32, [vp, vp, sz, vp, vp, vp, sz, vp]),
+    "lbt_gemm_multi_dev": (i32, [vp, vp, sz, vp, vp, vp, sz, vp]),
+    "lbt_ternary_linear": (i32, [vp, vp, sz, vp, sz, sz, vp]),
+    "lbt_ternary_linear_dev": (i32, [vp, vp, sz, vp, sz, sz, vp]),
+    "lbt_bf16_upload": (i32, [vp, vp, sz, sz, C.POINTER(vp)]),
+    "lbt_bf16_free": (None, [vp]),
+    "lbt_bf16_linear": (i32, [vp, vp, vp, sz, vp]),
+    "lbt_bf16_linear_dev": (i32, [vp, vp, vp, sz, vp]),
+    "lbt_model_load": (i32, [vp, C.c_char_p, C.POINTER(vp)]),
+    "lbt_model_create_synthetic": (i32, [vp, C.POINTER(LbtConfig), u64, C.POINTER(vp)]),
+    "lbt_model_free": (None, [vp]),
+    "lbt_model_get_config": (i32, [vp, C.POINTER(LbtConfig)]),
+    "lbt_model_linear": (vp, [vp, i32, i32]),
+    "lbt_cache_new": (i32, [vp, C.POINTER(vp)]),
+    "lbt_cache_free": (None, [vp]),
+    "lbt_cache_len": (i32, [vp]),
+    "lbt_cache_read": (i32, [vp, i32, i32, vp]),
+    "lbt_model_forward": (i32, [vp, vp, sz, vp, i32, vp]),
+    "lbt_model_forward_argmax": (i32, [vp, vp, sz, vp, vp]),
+    "lbt_model_generate_greedy": (i32, [vp, vp, sz, sz, vp, vp, vp, vp]),
+    "lbt_model_decode_greedy": (i32, [vp, vp, C.c_uint32, sz, vp, vp]),
+    "lbt_model_read_hidden": (i32, [vp, vp, sz]),
+    "lbt_prof_enable": (i32, [vp, i32]),
+    "lbt_prof_read": (i32, [vp, C.POINTER(LbtProf), i32]),
+}
+
+_lib = None
+
+
+def load_library(path: str | os.PathLike | None = None) -> C.CDLL:
+    """Loads the HIP library; raises FileNotFoundError if it was not built."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = Path(path) if path else LIB_PATH
+    if not p.exists():
+        raise FileNotFoundError(f"{p} is missing: build it with __graft_entry__.build() (no CPU fallback exists)")
+    lib = C.CDLL(str(p))
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    if path is None:
+        _lib = lib
+    return lib
+
+
+class LbtError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"{ERRORS.get(code, code)}: {msg}")
+        self.code = code
+
+
+def _ptr(a: np.ndarray) -> C.c_void_p:
+    assert a.flags["C_CONTIGUOUS"], "arrays passed to the C ABI must be contiguous"
+    return C.c_void_p(a.ctypes.data)
+
+
+def padded_cols(cols: int) -> int:
+    return (cols + 127) // 128 * 128
+
+
+class Ctx:
+    """One device context (stream + workspace); lbt_ctx_create/destroy."""
+
+    def __init__(self, device: int = 0):
+        self.lib = load_library()
+        h = C.c_void_p()
+        rc = self.lib.lbt_ctx_create(device, C.byref(h))
+        if rc != LBT_OK:
+            raise LbtError(rc, f"lbt_ctx_create({device}) failed")
+        self.h = h
+
+    def check(self, rc: int):
+        if rc != LBT_OK:
+            raise LbtError(rc, self.lib.lbt_last_error(self.h).decode())
+
+    def close(self):
+        if self.h:
+            self.lib.lbt_ctx_destroy(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def sync(self):
+        self.check(self.lib.lbt_ctx_synchronize(self.h))
+
+    # ---- weights -----------------------------------------------------------
+    def upload(self, packed: np.ndarray, rows: int, cols: int, scale: float) -> "Weight":
+        packed = np.ascontiguousarray(packed, dtype=np.uint8)
+        h = C.c_void_p()
+        self.check(self.lib.lbt_weight_upload(self.h, _ptr(packed), rows, cols, C.c_float(scale), C.byref(h)))
+        return Weight(self, h, rows, cols, scale)
+
+    # ---- ops ------------------------------------------------------------------
+    def quantize_acts(self, x: np.ndarray):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        m, k = x.shape
+        kp = padded_cols(k)
+        q = np.zeros((m, kp), np.int8)
+        s = np.zeros(m, np.float32)
+        su = np.zeros(m, np.int32)
+        self.check(self.lib.lbt_quantize_acts(self.h, _ptr(x), m, k, _ptr(q), _ptr(s), _ptr(su)))
+        return q, s, su
+
+    def gemm_i32(self, w: "Weight", q: np.ndarray, qsum: np.ndarray) -> np.ndarray:
+        q = np.ascontiguousarray(q, dtype=np.int8)
+        qsum = np.ascontiguousarray(qsum, dtype=np.int32)
+        m = q.shape[0]
+        out = np.zeros((m, w.rows), np.int32)
+        self.check(self.lib.lbt_gemm_i32(self.h, w.h, _ptr(q), _ptr(qsum), m, _ptr(out)))
+        return out
+
+    def gemm_multi(self, ws: list["Weight"], q, scale, qsum) -> list[np.ndarray]:
+        q = np.ascontiguousarray(q, dtype=np.int8)
+        scale = np.ascontiguousarray(scale, dtype=np.float32)
+        qsum = np.ascontiguousarray(qsum, dtype=np.int32)
+        m = q.shape[0]
+        outs = [np.zeros((m, w.rows), np.float32) for w in ws]
+        wa = (C.c_void_p * len(ws))(*[w.h for w in ws])
+        oa = (C.c_void_p * len(ws))(*[o.ctypes.data for o in outs])
+        self.check(self.lib.lbt_gemm_multi(self.h, wa, len(ws), _ptr(q), _ptr(scale), _ptr(qsum), m, oa))
+        return outs
+
+    def ternary_linear(self, ws: list["Weight"], x: np.ndarray) -> list[np.ndarray]:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        m, cols = x.shape
+        outs = [np.zeros((m, w.rows), np.float32) for w in ws]
+        wa = (C.c_void_p * len(ws))(*[w.h for w in ws])
+        oa = (C.c_void_p * len(ws))(*[o.ctypes.data for o in outs])
+        self.check(self.lib.lbt_ternary_linear(self.h, wa, len(ws), _ptr(x), m, cols, oa))
+        return outs
+
+    def bf16_upload(self, w: np.ndarray) -> "Bf16Weight":
+        w = np.ascontiguousarray(w, dtype=np.uint16)
+        rows, cols = w.shape
+        h = C.c_void_p()
+        self.check(self.lib.lbt_bf16_upload(self.h, _ptr(w), rows, cols, C.byref(h)))
+        return Bf16Weight(self, h, rows, cols)
+
+    def bf16_linear(self, w: "Bf16Weight", x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        m = x.shape[0]
+        out = np.zeros((m, w.rows), np.float32)
+        self.check(self.lib.lbt_bf16_linear(self.h, w.h, _ptr(x), m, _ptr(out)))
+        return out
+
+    # ---- profiling ---------------------------------------------------------------
+    def prof_enable(self, on: bool):
+        self.check(self.lib.lbt_prof_enable(self.h, 1 if on else 0))
+
+    def prof_read(self, reset: bool = True) -> dict:
+        p = LbtProf()
+        self.check(self.lib.lbt_prof_read(self.h, C.byref(p), 1 if reset else 0))
+        names = ["gemv", "gemm", "head", "attn", "other"]
+        return {n: {"ms": p.ms[i], "bytes": p.bytes[i], "launches": int(p.launches[i])} for i, n in enumerate(names)}
+
+
+class Weight:
+    def __init__(self, ctx: Ctx, h, rows, cols, scale):
+        self.ctx, self.h, self.rows, self.cols, self.scale = ctx, h, rows, cols, scale
+
+    def free(self):
+        if self.h:
+            self.ctx.lib.lbt_weight_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            if self.ctx.h:
+                self.free()
+        except Exception:
+            pass
+
+
+class Bf16Weight:
+    def __init__(self, ctx: Ctx, h, rows, cols):
+        self.ctx, self.h, self.rows, self.cols = ctx, h, rows, cols
+
+    def free(self):
+        if self.h:
+            self.ctx.lib.lbt_bf16_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            if self.ctx.h:
+                self.free()
+        except Exception:
+            pass
+
+
+def make_config(hidden=2560, intermediate=6912, heads=20, kv_heads=5, layers=30, vocab=128256, max_pos=4096,
+                eps=1e-5, theta=500000.0, bos=128000) -> LbtConfig:
+    """BitNet b1.58 2B4T shape by default."""
+    return LbtConfig(hidden, intermediate, heads, kv_heads, layers, vocab, max_pos, bos, eps, theta)
+
+
+class Model:
+    """BitNet::load / synthetic creation + new_cache + forward over the C ABI."""
+
+    def __init__(self, ctx: Ctx, handle):
+        self.ctx, self.h = ctx, handle
+        self.cfg = LbtConfig()
+        ctx.check(ctx.lib.lbt_model_get_config(handle, C.byref(self.cfg)))
+
+    @classmethod
+    def synthetic(cls, ctx: Ctx, cfg: LbtConfig, seed: int) -> "Model":
+        h = C.c_void_p()
+        ctx.check(ctx.lib.lbt_model_create_synthetic(ctx.h, C.byref(cfg), C.c_uint64(seed), C.byref(h)))
+        return cls(ctx, h)
+
+    @classmethod
+    def load(cls, ctx: Ctx, path: str) -> "Model":
+        h = C.c_void_p()
+        ctx.check(ctx.lib.lbt_model_load(ctx.h, str(path).encode(), C.byref(h)))
+        return cls(ctx, h)
+
+    def free(self):
+        if self.h:
+            self.ctx.lib.lbt_model_free(self.h)
+            self.h = None
+
+    def new_cache(self) -> "Cache":
+        h = C.c_void_p()
+        self.ctx.check(self.ctx.lib.lbt_cache_new(self.h, C.byref(h)))
+        return Cache(self, h)
+
+    def forward(self, tokens, cache: "Cache", all_logits: bool = False) -> np.ndarray:
+        t = np.ascontiguousarray(tokens, dtype=np.uint32)
+        rows = len(t) if all_logits else 1
+        out = np.zeros((rows, self.cfg.vocab_size), np.float32)
+        self.ctx.check(self.ctx.lib.lbt_model_forward(self.h, _ptr(t), len(t), cache.h, 1 if all_logits else 0,
+                                                      _ptr(out)))
+        return out
+
+    def forward_argmax(self, tokens, cache: "Cache") -> int:
+        t = np.ascontiguousarray(tokens, dtype=np.uint32)
+        nxt = C.c_uint32()
+        self.ctx.check(self.ctx.lib.lbt_model_forward_argmax(self.h, _ptr(t), len(t), cache.h, C.byref(nxt)))
+        return int(nxt.value)
+
+    def generate_greedy(self, prompt, steps: int, cache: "Cache"):
+        t = np.ascontiguousarray(prompt, dtype=np.uint32)
+        out = np.zeros(steps + 1, np.uint32)
+        mp, md = C.c_float(), C.c_float()
+        self.ctx.check(self.ctx.lib.lbt_model_generate_greedy(self.h, _ptr(t), len(t), steps, cache.h, _ptr(out),
+                                                              C.byref(mp), C.byref(md)))
+        return out, float(mp.value), float(md.value)
+
+    def decode_greedy(self, cache: "Cache", first: int, steps: int):
+        out = np.zeros(steps, np.uint32)
+        md = C.c_float()
+        self.ctx.check(self.ctx.lib.lbt_model_decode_greedy(self.h, cache.h, C.c_uint32(first), steps, _ptr(out),
+                                                            C.byref(md)))
+        return out, float(md.value)
+
+    def read_hidden(self, n: int) -> np.ndarray:
+        out = np.zeros((n, self.cfg.hidden_size), np.float32)
+        self.ctx.check(self.ctx.lib.lbt_model_read_hidden(self.h, _ptr(out), n))
+        return out
+
+    def linear(self, layer: int, which: int) -> int:
+        return self.ctx.lib.lbt_model_linear(self.h, layer, which)
+
+
+class Cache:
+    def __init__(self, model: Model, h):
+        self.model, self.h = model, h
+
+    def __len__(self):
+        return self.model.ctx.lib.lbt_cache_len(self.h)
+
+    def read(self, layer: int, is_v: bool) -> np.ndarray:
+        c = self.model.cfg
+        hd = c.hidden_size // c.num_attention_heads
+        out = np.zeros((c.num_key_value_heads, len(self), hd), np.uint16)
+        self.model.ctx.check(self.model.ctx.lib.lbt_cache_read(self.h, layer, 1 if is_v else 0, _ptr(out)))
+        return out
+
+    def free(self):
+        if self.h:
+            self.model.ctx.lib.lbt_cache_free(self.h)
+            self.h = None

@@ -1,0 +1,648 @@
+/*
+ * lbt_oracle.c -- CPU restatement of lemonade-burn's ternary hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY: loaded by tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py, as the checker.  Never linked into the product.
+ *
+ * Build: see oracle/Makefile (gcc -O2 -ffp-contract=off: no contraction, so
+ * every float operation below is one IEEE-754 binary32 operation; fmaf() is
+ * used explicitly wherever the device kernels use a fused multiply-add).
+ *
+ * Reference files restated (paths relative to festeraeb/lemonade-burn):
+ *   crates/lb-ternary/src/pack.rs, quant.rs, gemm.rs, bf16.rs
+ *   crates/ternary-kernels/src/reference.rs
+ *   crates/lb-model/src/model.rs, sample.rs
+ *
+ * Float reduction order.  The reference's non-GEMM float ops run inside Burn
+ * Flex (burn-flex 0.22.1, not vendored); their summation order cannot be
+ * restated.  The device kernels therefore use one fixed, documented order and
+ * this oracle follows the same order, so the device path can be compared bit
+ * for bit.  The order itself is pinned against an f64 evaluation of the same
+ * formulas (tests/test_oracle.py) to the north-star tolerance.
+ */
+#include "lbt_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#include "lbt_port.h"
+
+#define BLOCK 128
+#define BLOCK_BYTES 32
+
+/* ------------------------------------------------------------------------ */
+/* pack.rs                                                                   */
+/* ------------------------------------------------------------------------ */
+
+/* pack.rs:22-24 */
+size_t or_padded_cols(size_t cols) { return (cols + BLOCK - 1) / BLOCK * BLOCK; }
+
+/* pack.rs:83-85 */
+size_t or_row_bytes(size_t cols) { return or_padded_cols(cols) / 4; }
+
+/* pack.rs:88-103: byte j of block b holds, in bits 2k..2k+1, code (w+1) of
+ * weight b*128 + k*32 + j; columns past `cols` are weight 0 (code 1). */
+void or_pack_row(const int8_t* vals, size_t cols, uint8_t* out) {
+    size_t nb = or_padded_cols(cols) / BLOCK;
+    for (size_t b = 0; b < nb; b++) {
+        for (size_t j = 0; j < BLOCK_BYTES; j++) {
+            uint8_t v = 0;
+            for (size_t k = 0; k < 4; k++) {
+                size_t idx = b * BLOCK + k * 32 + j;
+                int w = idx < cols ? vals[idx] : 0;
+                v |= (uint8_t)(((w + 1) & 3) << (2 * k));
+            }
+            out[b * BLOCK_BYTES + j] = v;
+        }
+    }
+}
+
+/* pack.rs:106-116 */
+void or_unpack_row(const uint8_t* row, size_t padded, int8_t* out) {
+    size_t nb = padded / BLOCK;
+    for (size_t b = 0; b < nb; b++)
+        for (size_t j = 0; j < BLOCK_BYTES; j++)
+            for (size_t k = 0; k < 4; k++)
+                out[b * BLOCK + k * 32 + j] = (int8_t)(((row[b * BLOCK_BYTES + j] >> (2 * k)) & 3) - 1);
+}
+
+/* PackedTernary::from_ternary (pack.rs:69-77) */
+void or_pack(const int8_t* vals, size_t rows, size_t cols, uint8_t* out) {
+    size_t rb = or_row_bytes(cols);
+    for (size_t r = 0; r < rows; r++) or_pack_row(vals + r * cols, cols, out + r * rb);
+}
+
+/* absmean_f32 (pack.rs:135-138): f64 sum of |w|, one rounding to f32. */
+float or_absmean(const float* w, size_t n) {
+    double s = 0.0;
+    for (size_t i = 0; i < n; i++) s += fabs((double)w[i]);
+    return (float)(s / (double)n);
+}
+
+/* ternarize_absmean + ternarize_with_scale (pack.rs:129-142) */
+float or_ternarize_absmean(const float* w, size_t n, int8_t* t) {
+    float mean = or_absmean(w, n);
+    float scale = 1.0f / fmaxf(mean, 1e-5f);
+    for (size_t i = 0; i < n; i++) {
+        float r = rintf(w[i] * scale); /* round_ties_even (default rounding mode) */
+        if (r > 1.0f) r = 1.0f;
+        if (r < -1.0f) r = -1.0f;
+        t[i] = (int8_t)r;
+    }
+    return scale;
+}
+
+/* ------------------------------------------------------------------------ */
+/* quant.rs                                                                  */
+/* ------------------------------------------------------------------------ */
+
+/* quant_one (quant.rs:116-118): (v*scale).round_ties_even().clamp(-128,127) as i8.
+ * Rust's float->int `as` maps NaN to 0; clamp keeps +-inf at the bounds. */
+static int8_t quant_one(float v, float scale) {
+    float y = rintf(v * scale);
+    if (y != y) return 0;
+    if (y < -128.0f) y = -128.0f;
+    if (y > 127.0f) y = 127.0f;
+    return (int8_t)y;
+}
+
+/* quantize_row_scalar (quant.rs:100-113).  f32::max ignores a NaN operand,
+ * as fmaxf does. */
+float or_quantize_row(const float* x, size_t k, int8_t* q, int32_t* sum) {
+    float amax = 0.0f;
+    for (size_t i = 0; i < k; i++) amax = fmaxf(amax, fabsf(x[i]));
+    float scale = 127.0f / fmaxf(amax, 1e-5f);
+    int32_t s = 0;
+    for (size_t i = 0; i < k; i++) {
+        int8_t r = quant_one(x[i], scale);
+        q[i] = r;
+        s += r;
+    }
+    *sum = s;
+    return scale;
+}
+
+/* quantize_acts_into (quant.rs:45-75): rows padded with zeros to kp. */
+void or_quantize_acts(const float* x, size_t m, size_t k, int8_t* q, float* scale, int32_t* sum) {
+    size_t kp = or_padded_cols(k);
+    memset(q, 0, m * kp);
+    for (size_t i = 0; i < m; i++) scale[i] = or_quantize_row(x + i * k, k, q + i * kp, sum + i);
+}
+
+/* ------------------------------------------------------------------------ */
+/* gemm.rs                                                                   */
+/* ------------------------------------------------------------------------ */
+
+/* codes_dot_scalar (gemm.rs:329-343): sum of code * x over the padded row. */
+int32_t or_codes_dot(const uint8_t* row, size_t kp, const int8_t* x) {
+    int32_t acc = 0;
+    size_t nb = kp / BLOCK;
+    for (size_t b = 0; b < nb; b++) {
+        const uint8_t* blk = row + b * BLOCK_BYTES;
+        for (size_t k = 0; k < 4; k++)
+            for (size_t j = 0; j < BLOCK_BYTES; j++) {
+                int32_t c = (blk[j] >> (2 * k)) & 3;
+                acc += c * (int32_t)x[b * BLOCK + k * 32 + j];
+            }
+    }
+    return acc;
+}
+
+/* ternary_gemm_i32 (gemm.rs:95-114) with dot_row's -sum(q) (gemm.rs:306-308). */
+void or_gemm_i32(const uint8_t* packed, size_t rows, size_t cols, const int8_t* q,
+                 const int32_t* qsum, size_t m, int32_t* out) {
+    size_t kp = or_padded_cols(cols), rb = kp / 4;
+#pragma omp parallel for schedule(static) if (rows * m * kp > (1u << 22))
+    for (long r = 0; r < (long)rows; r++)
+        for (size_t t = 0; t < m; t++)
+            out[t * rows + r] = or_codes_dot(packed + r * rb, kp, q + t * kp) - qsum[t];
+}
+
+/* ternary_gemm / multi (gemm.rs:128-195): y = (dot as f32) * (1 / (s_a * s_w)). */
+void or_gemm_f32(const uint8_t* packed, size_t rows, size_t cols, float s_w,
+                 const int8_t* q, const float* s_a, const int32_t* qsum, size_t m, float* out) {
+    int32_t* d = (int32_t*)malloc(rows * m * sizeof(int32_t));
+    or_gemm_i32(packed, rows, cols, q, qsum, m, d);
+    for (size_t t = 0; t < m; t++) {
+        float inv = 1.0f / (s_a[t] * s_w);
+        for (size_t r = 0; r < rows; r++) out[t * rows + r] = (float)d[t * rows + r] * inv;
+    }
+    free(d);
+}
+
+/* gemv_i32_reference (ternary-kernels/src/reference.rs:7-16) */
+void or_gemm_i32_bruteforce(const uint8_t* packed, size_t rows, size_t cols,
+                            const int8_t* q, size_t m, int32_t* out) {
+    size_t kp = or_padded_cols(cols), rb = kp / 4;
+    int8_t* w = (int8_t*)malloc(kp);
+    for (size_t r = 0; r < rows; r++) {
+        or_unpack_row(packed + r * rb, kp, w);
+        for (size_t t = 0; t < m; t++) {
+            int64_t acc = 0;
+            for (size_t k = 0; k < kp; k++) acc += (int64_t)w[k] * q[t * kp + k];
+            out[t * rows + r] = (int32_t)acc;
+        }
+    }
+    free(w);
+}
+
+/* ------------------------------------------------------------------------ */
+/* bf16.rs                                                                   */
+/* ------------------------------------------------------------------------ */
+
+static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+/* bf16_to_f32 (bf16.rs:9-11) */
+float or_bf16_to_f32(uint16_t b) { return u2f((uint32_t)b << 16); }
+
+/* f32 -> bf16, round to nearest even; NaN -> canonical quiet NaN. */
+uint16_t or_f32_to_bf16(float f) {
+    uint32_t u = f2u(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+/* dot_scalar (bf16.rs:38-51) */
+float or_bf16_dot_ref(const uint16_t* w, const float* x, size_t n) {
+    float acc[8] = {0};
+    size_t n8 = n / 8 * 8;
+    for (size_t i = 0; i < n8; i += 8)
+        for (int l = 0; l < 8; l++) acc[l] += or_bf16_to_f32(w[i + l]) * x[i + l];
+    float s = 0.0f;
+    for (int l = 0; l < 8; l++) s += acc[l];
+    for (size_t i = n8; i < n; i++) s += or_bf16_to_f32(w[i]) * x[i];
+    return s;
+}
+
+/* xor butterfly over 64 lane values, as the device reduces a wavefront:
+ * step m: lane l takes v[l] + v[l ^ m] for m = 32, 16, ..., 1. */
+static float butterfly64(float* v) {
+    float t[64];
+    for (int m = 32; m >= 1; m >>= 1) {
+        for (int l = 0; l < 64; l++) t[l] = v[l] + v[l ^ m];
+        memcpy(v, t, sizeof(t));
+    }
+    return v[0];
+}
+
+/* The device LM-head dot: n % 8 == 0; lane l accumulates chunks c = l + 64 i. */
+float or_bf16_dot_lanes(const uint16_t* w, const float* x, size_t n) {
+    float lane[64];
+    size_t chunks = n / 8;
+    for (int l = 0; l < 64; l++) {
+        float acc = 0.0f;
+        for (size_t c = (size_t)l; c < chunks; c += 64)
+            for (int e = 0; e < 8; e++) acc = fmaf(or_bf16_to_f32(w[c * 8 + e]), x[c * 8 + e], acc);
+        lane[l] = acc;
+    }
+    return butterfly64(lane);
+}
+
+void or_bf16_gemv_lanes(const uint16_t* w, size_t rows, size_t cols, const float* x, float* out) {
+#pragma omp parallel for schedule(static) if (rows * cols > (1u << 22))
+    for (long r = 0; r < (long)rows; r++) out[r] = or_bf16_dot_lanes(w + (size_t)r * cols, x, cols);
+}
+
+/* ------------------------------------------------------------------------ */
+/* device-order float building blocks                                        */
+/* ------------------------------------------------------------------------ */
+
+/* 256 partials reduced in LDS: p[t] += p[t + s] for s = 128, 64, ..., 1. */
+float or_tree256(const float* partials) {
+    float p[256];
+    memcpy(p, partials, sizeof(p));
+    for (int s = 128; s >= 1; s >>= 1)
+        for (int t = 0; t < s; t++) p[t] = p[t] + p[t + s];
+    return p[0];
+}
+
+/* Thread t of 256 accumulates x[i]^2 (fma) over i = t, t+256, ... ascending. */
+float or_sumsq256(const float* x, size_t n) {
+    float p[256];
+    for (int t = 0; t < 256; t++) {
+        float a = 0.0f;
+        for (size_t i = (size_t)t; i < n; i += 256) a = fmaf(x[i], x[i], a);
+        p[t] = a;
+    }
+    return or_tree256(p);
+}
+
+/* rms_norm (model.rs:267-272): x * (mean(x^2) + eps).sqrt().recip() * w */
+void or_rmsnorm(const float* x, const float* w, size_t n, float eps, float* out) {
+    float mean = or_sumsq256(x, n) / (float)n;
+    float r = 1.0f / sqrtf(mean + eps);
+    for (size_t i = 0; i < n; i++) out[i] = (x[i] * r) * w[i];
+}
+
+/* exp(x) for the softmax: Cody & Waite (1980) two-constant reduction
+ * x = n ln2 + r, |r| <= ln2/2, then the degree-7 Taylor polynomial of e^r in
+ * Horner form (truncation error < 2e-9 relative), scaled by 2^n through the
+ * exponent bits.  Results below 2^-126 flush to zero. */
+#define EXP_LOG2E 1.44269504088896341f
+#define EXP_LN2_HI 0.693145751953125f
+#define EXP_LN2_LO 1.42860682030941723212e-6f
+float or_expf(float x) {
+    if (x != x) return x;
+    if (x > 88.5f) return INFINITY;
+    if (x < -87.0f) return 0.0f;
+    float n = rintf(x * EXP_LOG2E);
+    float r = fmaf(-n, EXP_LN2_HI, x);
+    r = fmaf(-n, EXP_LN2_LO, r);
+    float p = 1.98412698412698e-4f;          /* 1/5040 */
+    p = fmaf(p, r, 1.38888888888889e-3f);    /* 1/720 */
+    p = fmaf(p, r, 8.33333333333333e-3f);    /* 1/120 */
+    p = fmaf(p, r, 4.16666666666667e-2f);    /* 1/24 */
+    p = fmaf(p, r, 1.66666666666667e-1f);    /* 1/6 */
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    int ni = (int)n;
+    if (ni > 127) return (p * 2.0f) * u2f(0x7f000000u); /* n = 128 */
+    if (ni < -126) return 0.0f;
+    return p * u2f((uint32_t)(ni + 127) << 23);
+}
+
+/* argmax (sample.rs:17-25): first index of the maximum (strict >). */
+uint32_t or_argmax(const float* v, size_t n) {
+    size_t best = 0;
+    for (size_t i = 0; i < n; i++)
+        if (v[i] > v[best]) best = i;
+    return (uint32_t)best;
+}
+
+/* ------------------------------------------------------------------------ */
+/* RoPE tables (model.rs:213-230)                                            */
+/* ------------------------------------------------------------------------ */
+void or_rope_tables(size_t hd, size_t max_pos, double theta, float* cos_t, float* sin_t) {
+    size_t h2 = hd / 2;
+    float* inv = (float*)malloc(h2 * sizeof(float));
+    for (size_t i = 0; i < h2; i++) inv[i] = (float)(1.0 / pow(theta, (double)(2 * i) / (double)hd));
+    for (size_t p = 0; p < max_pos; p++)
+        for (size_t i = 0; i < h2; i++) {
+            float f = (float)p * inv[i];
+            cos_t[p * h2 + i] = (float)cos((double)f);
+            sin_t[p * h2 + i] = (float)sin((double)f);
+        }
+    free(inv);
+}
+
+/* ------------------------------------------------------------------------ */
+/* synthetic weights                                                         */
+/* ------------------------------------------------------------------------ */
+uint64_t or_splitmix64(uint64_t z) {
+    z += 0x9e3779b97f4a7c15ull;
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+}
+
+uint64_t or_synth_hash(uint64_t seed, uint64_t tensor, uint64_t i) {
+    return or_splitmix64(or_splitmix64(seed ^ (tensor << 40)) + i);
+}
+
+/* i.i.d. ternary with P(-1, 0, +1) = (0.3, 0.4, 0.3): bucket = hi32 * 10 >> 32. */
+int8_t or_synth_ternary(uint64_t seed, uint64_t tensor, uint64_t i) {
+    uint64_t b = ((or_synth_hash(seed, tensor, i) >> 32) * 10u) >> 32;
+    return b < 3 ? -1 : (b < 7 ? 0 : 1);
+}
+
+void or_synth_packed(uint64_t seed, uint64_t tensor, size_t rows, size_t cols, uint8_t* out) {
+    size_t rb = or_row_bytes(cols);
+#pragma omp parallel for schedule(static) if (rows * cols > (1u << 20))
+    for (long r = 0; r < (long)rows; r++)
+        for (size_t byte = 0; byte < rb; byte++) {
+            size_t b = byte / BLOCK_BYTES, j = byte % BLOCK_BYTES;
+            uint8_t v = 0;
+            for (size_t k = 0; k < 4; k++) {
+                size_t c = b * BLOCK + k * 32 + j;
+                int w = c < cols ? or_synth_ternary(seed, tensor, (uint64_t)r * cols + c) : 0;
+                v |= (uint8_t)((w + 1) << (2 * k));
+            }
+            out[(size_t)r * rb + byte] = v;
+        }
+}
+
+/* u = (hash >> 40) * 2^-24 in [0, 1) (exact), value = lo + span * u. */
+void or_synth_f32(uint64_t seed, uint64_t tensor, size_t n, float lo, float span, float* out) {
+    for (size_t i = 0; i < n; i++) {
+        float u = (float)(or_synth_hash(seed, tensor, i) >> 40) * 5.9604644775390625e-8f;
+        out[i] = lo + span * u;
+    }
+}
+
+/* bf16 of uniform [-1, 1). */
+void or_synth_bf16(uint64_t seed, uint64_t tensor, size_t n, uint16_t* out) {
+#pragma omp parallel for schedule(static) if (n > (1u << 20))
+    for (long i = 0; i < (long)n; i++) {
+        float u = (float)(or_synth_hash(seed, tensor, (uint64_t)i) >> 40) * 5.9604644775390625e-8f;
+        out[i] = or_f32_to_bf16(u * 2.0f - 1.0f);
+    }
+}
+
+/* Per-tensor weight scale of a synthetic matrix: sqrt(0.6 cols) keeps the
+ * scaled outputs O(1) for O(1) activations. */
+float or_synth_wscale(size_t cols) { return (float)sqrt(0.6 * (double)cols); }
+
+/* ------------------------------------------------------------------------ */
+/* BitNet forward (model.rs)                                                 */
+/* ------------------------------------------------------------------------ */
+struct or_model {
+    or_config c;
+    int owns;
+    const uint8_t* packed[7 * 64];
+    float wscale[7 * 64];
+    const float* norm[4 * 64];
+    const float* final_norm;
+    const uint16_t* embed;
+    float *cos_t, *sin_t;
+    uint16_t* kc; /* [layers][kvh][cap][hd] */
+    uint16_t* vc;
+    int cap, len;
+    float* hidden; /* residual stream of the last forward, [n, hidden] */
+    size_t hidden_rows;
+};
+
+static int g_fast = 0;
+int or_set_fast(int fast) { int o = g_fast; g_fast = fast; return o; }
+
+static const int kLinRows[7] = {0, 1, 1, 0, 2, 2, 0}; /* rows: 0=hidden 1=kv 2=inter */
+
+static void lin_shape(const or_config* c, int which, size_t* rows, size_t* cols) {
+    size_t kv = (size_t)c->kv_heads * (c->hidden / c->heads);
+    size_t r = which == 1 || which == 2 ? kv : (which == 4 || which == 5 ? (size_t)c->intermediate : (size_t)c->hidden);
+    (void)kLinRows;
+    *rows = r;
+    *cols = which == 6 ? (size_t)c->intermediate : (size_t)c->hidden;
+}
+
+static void model_alloc_runtime(or_model* m) {
+    const or_config* c = &m->c;
+    size_t hd = (size_t)(c->hidden / c->heads);
+    m->cos_t = (float*)malloc((size_t)c->max_pos * hd / 2 * sizeof(float));
+    m->sin_t = (float*)malloc((size_t)c->max_pos * hd / 2 * sizeof(float));
+    or_rope_tables(hd, (size_t)c->max_pos, c->rope_theta, m->cos_t, m->sin_t);
+    m->cap = c->max_pos;
+    size_t kvn = (size_t)c->layers * c->kv_heads * (size_t)m->cap * hd;
+    m->kc = (uint16_t*)calloc(kvn, 2);
+    m->vc = (uint16_t*)calloc(kvn, 2);
+    m->len = 0;
+}
+
+or_model* or_model_synthetic(const or_config* cfg, uint64_t seed) {
+    or_model* m = (or_model*)calloc(1, sizeof(or_model));
+    m->c = *cfg;
+    m->owns = 1;
+    for (int l = 0; l < cfg->layers; l++) {
+        for (int w = 0; w < 7; w++) {
+            size_t rows, cols;
+            lin_shape(cfg, w, &rows, &cols);
+            uint8_t* p = (uint8_t*)malloc(rows * or_row_bytes(cols));
+            or_synth_packed(seed, OR_T_LAYER(l, w), rows, cols, p);
+            m->packed[l * 7 + w] = p;
+            m->wscale[l * 7 + w] = or_synth_wscale(cols);
+        }
+        for (int k = 0; k < 4; k++) {
+            size_t n = k == 3 ? (size_t)cfg->intermediate : (size_t)cfg->hidden;
+            float* v = (float*)malloc(n * sizeof(float));
+            or_synth_f32(seed, OR_T_LAYER(l, 7 + k), n, 0.5f, 1.0f, v);
+            m->norm[l * 4 + k] = v;
+        }
+    }
+    float* fnorm = (float*)malloc((size_t)cfg->hidden * sizeof(float));
+    or_synth_f32(seed, OR_T_FINAL_NORM, (size_t)cfg->hidden, 0.5f, 1.0f, fnorm);
+    m->final_norm = fnorm;
+    uint16_t* e = (uint16_t*)malloc((size_t)cfg->vocab * cfg->hidden * 2);
+    or_synth_bf16(seed, OR_T_EMBED, (size_t)cfg->vocab * cfg->hidden, e);
+    m->embed = e;
+    model_alloc_runtime(m);
+    return m;
+}
+
+or_model* or_model_wrap(const or_config* cfg, const uint8_t* const* packed, const float* wscales,
+                        const float* const* norms, const float* final_norm, const uint16_t* embed) {
+    or_model* m = (or_model*)calloc(1, sizeof(or_model));
+    m->c = *cfg;
+    m->owns = 0;
+    for (int i = 0; i < cfg->layers * 7; i++) { m->packed[i] = packed[i]; m->wscale[i] = wscales[i]; }
+    for (int i = 0; i < cfg->layers * 4; i++) m->norm[i] = norms[i];
+    m->final_norm = final_norm;
+    m->embed = embed;
+    model_alloc_runtime(m);
+    return m;
+}
+
+void or_model_free(or_model* m) {
+    if (!m) return;
+    if (m->owns) {
+        for (int i = 0; i < m->c.layers * 7; i++) free((void*)m->packed[i]);
+        for (int i = 0; i < m->c.layers * 4; i++) free((void*)m->norm[i]);
+        free((void*)m->final_norm);
+        free((void*)m->embed);
+    }
+    free(m->cos_t); free(m->sin_t); free(m->kc); free(m->vc); free(m->hidden);
+    free(m);
+}
+
+const uint8_t* or_model_packed(const or_model* m, int layer, int which) { return m->packed[layer * 7 + which]; }
+float or_model_wscale(const or_model* m, int layer, int which) { return m->wscale[layer * 7 + which]; }
+const uint16_t* or_model_embed(const or_model* m) { return m->embed; }
+void or_model_reset(or_model* m) { m->len = 0; }
+int or_model_len(const or_model* m) { return m->len; }
+const float* or_model_hidden(const or_model* m) { return m->hidden; }
+int or_model_cap(const or_model* m) { return m->cap; }
+const uint16_t* or_model_kcache(const or_model* m, int layer) {
+    size_t hd = (size_t)(m->c.hidden / m->c.heads);
+    return m->kc + (size_t)layer * m->c.kv_heads * m->cap * hd;
+}
+const uint16_t* or_model_vcache(const or_model* m, int layer) {
+    size_t hd = (size_t)(m->c.hidden / m->c.heads);
+    return m->vc + (size_t)layer * m->c.kv_heads * m->cap * hd;
+}
+
+/* Quantize each of n rows (width k), then y[t, r] = dot * (1/(s_a s_w)) for
+ * each matrix sharing the input (ops.rs:301-329: quantize once, fused GEMM). */
+static void linear(const or_model* m, const float* x, size_t n, size_t k, int layer, int which, float* y) {
+    size_t rows, cols;
+    lin_shape(&m->c, which, &rows, &cols);
+    size_t kp = or_padded_cols(k);
+    int8_t* q = (int8_t*)calloc(n * kp, 1);
+    float* sa = (float*)malloc(n * sizeof(float));
+    int32_t* qs = (int32_t*)malloc(n * sizeof(int32_t));
+    or_quantize_acts(x, n, k, q, sa, qs);
+    int32_t* d = (int32_t*)malloc(n * rows * sizeof(int32_t));
+    if (g_fast) port_gemm_i32(m->packed[layer * 7 + which], rows, cols, q, qs, n, d, 0);
+    else or_gemm_i32(m->packed[layer * 7 + which], rows, cols, q, qs, n, d);
+    float sw = m->wscale[layer * 7 + which];
+    for (size_t t = 0; t < n; t++) {
+        float inv = 1.0f / (sa[t] * sw);
+        for (size_t r = 0; r < rows; r++) y[t * rows + r] = (float)d[t * rows + r] * inv;
+    }
+    free(q); free(sa); free(qs); free(d);
+}
+
+/* apply_rope (model.rs:295-301): x*cos + rot*sin, rot = cat(-x2, x1). */
+static void rope(float* v, size_t hd, const float* c, const float* s) {
+    size_t h2 = hd / 2;
+    float tmp[512];
+    for (size_t d = 0; d < hd; d++) {
+        size_t i = d % h2;
+        float rot = d < h2 ? -v[d + h2] : v[d - h2];
+        tmp[d] = v[d] * c[i] + rot * s[i];
+    }
+    memcpy(v, tmp, hd * sizeof(float));
+}
+
+int or_model_forward(or_model* m, const uint32_t* tokens, size_t n, int all_logits, float* logits) {
+    const or_config* c = &m->c;
+    size_t H = (size_t)c->hidden, I = (size_t)c->intermediate;
+    size_t nh = (size_t)c->heads, kvh = (size_t)c->kv_heads, hd = H / nh, group = nh / kvh;
+    size_t h2 = hd / 2, cap = (size_t)m->cap;
+    size_t pos0 = (size_t)m->len, total = pos0 + n;
+    float eps = (float)c->rms_norm_eps;
+    if (total > (size_t)c->max_pos) return -1;
+    float scaling = powf((float)hd, -0.5f);
+
+    float* x = (float*)malloc(n * H * sizeof(float));
+    float* nrm = (float*)malloc(n * I * sizeof(float));
+    float* q = (float*)malloc(n * H * sizeof(float));
+    float* kk = (float*)malloc(n * kvh * hd * sizeof(float));
+    float* vv = (float*)malloc(n * kvh * hd * sizeof(float));
+    float* att = (float*)malloc(n * H * sizeof(float));
+    float* y = (float*)malloc(n * H * sizeof(float));
+    float* g = (float*)malloc(n * I * sizeof(float));
+    float* u = (float*)malloc(n * I * sizeof(float));
+    float* e = (float*)malloc(total * sizeof(float));
+
+    /* embed (model.rs:274-282) */
+    for (size_t t = 0; t < n; t++)
+        for (size_t i = 0; i < H; i++) x[t * H + i] = or_bf16_to_f32(m->embed[(size_t)tokens[t] * H + i]);
+
+    for (int l = 0; l < c->layers; l++) {
+        const float* const* nw = &m->norm[l * 4]; /* input, post_attn, attn_sub, ffn_sub */
+        uint16_t* K = m->kc + (size_t)l * kvh * cap * hd;
+        uint16_t* V = m->vc + (size_t)l * kvh * cap * hd;
+        for (size_t t = 0; t < n; t++) or_rmsnorm(x + t * H, nw[0], H, eps, nrm + t * H);
+        linear(m, nrm, n, H, l, 0, q);
+        linear(m, nrm, n, H, l, 1, kk);
+        linear(m, nrm, n, H, l, 2, vv);
+        for (size_t t = 0; t < n; t++) {
+            size_t p = pos0 + t;
+            const float* cs = m->cos_t + p * h2;
+            const float* sn = m->sin_t + p * h2;
+            for (size_t h = 0; h < nh; h++) rope(q + t * H + h * hd, hd, cs, sn);
+            for (size_t h = 0; h < kvh; h++) {
+                rope(kk + (t * kvh + h) * hd, hd, cs, sn);
+                for (size_t d = 0; d < hd; d++) {
+                    K[(h * cap + p) * hd + d] = or_f32_to_bf16(kk[(t * kvh + h) * hd + d]);
+                    V[(h * cap + p) * hd + d] = or_f32_to_bf16(vv[(t * kvh + h) * hd + d]);
+                }
+            }
+        }
+        /* GQA attention (model.rs:349-357): q head h reads kv head h / group. */
+        for (size_t t = 0; t < n; t++) {
+            size_t vis = pos0 + t + 1;
+            for (size_t h = 0; h < nh; h++) {
+                const float* qh = q + t * H + h * hd;
+                const uint16_t* Kh = K + (h / group) * cap * hd;
+                const uint16_t* Vh = V + (h / group) * cap * hd;
+                float mx = -INFINITY;
+                for (size_t j = 0; j < vis; j++) {
+                    float a = 0.0f;
+                    for (size_t d = 0; d < hd; d++) a = fmaf(qh[d], or_bf16_to_f32(Kh[j * hd + d]), a);
+                    e[j] = a * scaling;
+                    mx = fmaxf(mx, e[j]);
+                }
+                float part[256];
+                for (int th = 0; th < 256; th++) {
+                    float s = 0.0f;
+                    for (size_t j = (size_t)th; j < vis; j += 256) s = s + or_expf(e[j] - mx);
+                    part[th] = s;
+                }
+                float sum = or_tree256(part);
+                for (size_t j = 0; j < vis; j++) e[j] = or_expf(e[j] - mx) / sum;
+                for (size_t d = 0; d < hd; d++) {
+                    float a = 0.0f;
+                    for (size_t j = 0; j < vis; j++) a = fmaf(e[j], or_bf16_to_f32(Vh[j * hd + d]), a);
+                    att[t * H + h * hd + d] = a;
+                }
+            }
+        }
+        for (size_t t = 0; t < n; t++) or_rmsnorm(att + t * H, nw[2], H, eps, nrm + t * H);
+        linear(m, nrm, n, H, l, 3, y);
+        for (size_t i = 0; i < n * H; i++) x[i] = x[i] + y[i];
+        for (size_t t = 0; t < n; t++) or_rmsnorm(x + t * H, nw[1], H, eps, nrm + t * H);
+        linear(m, nrm, n, H, l, 4, g);
+        linear(m, nrm, n, H, l, 5, u);
+        /* relu(g)^2 * u (model.rs:363) */
+        for (size_t i = 0; i < n * I; i++) {
+            float r = g[i] > 0.0f ? g[i] : 0.0f;
+            g[i] = (r * r) * u[i];
+        }
+        for (size_t t = 0; t < n; t++) or_rmsnorm(g + t * I, nw[3], I, eps, nrm + t * I);
+        linear(m, nrm, n, I, l, 6, y);
+        for (size_t i = 0; i < n * H; i++) x[i] = x[i] + y[i];
+    }
+    m->len = (int)total;
+    free(m->hidden);
+    m->hidden = (float*)malloc(n * H * sizeof(float));
+    memcpy(m->hidden, x, n * H * sizeof(float));
+    m->hidden_rows = n;
+
+    /* final norm + tied bf16 LM head (model.rs:368-373) */
+    size_t first = all_logits ? 0 : n - 1;
+    for (size_t t = first; t < n; t++) {
+        or_rmsnorm(x + t * H, m->final_norm, H, eps, nrm);
+        float* lt = logits + (t - first) * (size_t)c->vocab;
+        if (g_fast >= 2) port_bf16_gemv(m->embed, (size_t)c->vocab, H, nrm, lt, 0); /* reference order */
+        else or_bf16_gemv_lanes(m->embed, (size_t)c->vocab, H, nrm, lt);
+    }
+    free(x); free(nrm); free(q); free(kk); free(vv); free(att); free(y); free(g); free(u); free(e);
+    return 0;
+}

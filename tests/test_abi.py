@@ -1,0 +1,49 @@
+"""CPU-side checks of the drop-in boundary: the HIP library loads (no GPU
+needed), exports exactly what include/lbt.h declares, the ctypes binding
+covers every declaration, and with no GPU present entry points fail with a
+status code instead of aborting."""
+import ctypes as C
+import re
+from pathlib import Path
+
+import pytest
+
+import lbt_hip
+
+REPO = Path(__file__).resolve().parent.parent
+HEADER = REPO / "include" / "lbt.h"
+
+
+def declared() -> set:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return set(re.findall(r"\b(lbt_\w+)\s*\(", text))
+
+
+def test_library_exports_every_declaration():
+    lib = lbt_hip.load_library()
+    for name in declared():
+        assert hasattr(lib, name), name
+
+
+def test_binding_matches_header():
+    assert set(lbt_hip.SIGNATURES) == declared()
+
+
+def test_no_gpu_returns_status():
+    import os
+
+    if os.path.exists("/dev/kfd"):
+        pytest.skip("a GPU is present")
+    lib = lbt_hip.load_library()
+    h = C.c_void_p()
+    assert lib.lbt_ctx_create(0, C.byref(h)) != 0
+    assert lib.lbt_version().decode().startswith("lbt-hip")
+
+
+def test_header_compiles_as_c():
+    import subprocess
+
+    src = '#include "lbt.h"\nint main(void){lbt_config c; (void)c; return 0;}\n'
+    r = subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", f"-I{REPO / 'include'}", "-x", "c", "-", "-o",
+                        "/dev/null"], input=src, text=True, capture_output=True)
+    assert r.returncode == 0, r.stderr

@@ -1,0 +1,196 @@
+"""GPU token loop vs the oracle model (device float order): logits, hidden
+state and bf16 KV cache bit-exact; greedy tokens identical; the lb-convert v1
+file loader reads what the synthetic generator makes; and the full 2B-shaped
+model's 64-token prompt + greedy decode matches the oracle token for token
+and within 1e-3 rel / 1e-2 abs on logits."""
+import json
+
+import numpy as np
+import pytest
+
+import lbt_hip
+import lbt_oracle as orc
+from conftest import announce
+
+pytestmark = pytest.mark.gpu
+
+SMALL = dict(hidden=256, intermediate=512, heads=4, kv_heads=2, layers=2, vocab=1000, max_pos=1024)
+
+
+def cfgs(**kw):
+    d = dict(SMALL, **kw)
+    hip = lbt_hip.make_config(d["hidden"], d["intermediate"], d["heads"], d["kv_heads"], d["layers"], d["vocab"],
+                              d["max_pos"])
+    orcfg = orc.config(d["hidden"], d["intermediate"], d["heads"], d["kv_heads"], d["layers"], d["vocab"], d["max_pos"])
+    return hip, orcfg
+
+
+@pytest.mark.parametrize("shape", [dict(), dict(hidden=512, intermediate=1536, heads=4, kv_heads=1, layers=3),
+                                   dict(hidden=384, intermediate=1000, heads=3, kv_heads=3, layers=1)])
+def test_small_model_bitexact(ctx, shape):
+    hip_cfg, or_cfg = cfgs(**shape)
+    announce(f"small model {shape}")
+    seed = 21
+    m = lbt_hip.Model.synthetic(ctx, hip_cfg, seed)
+    om = orc.OracleModel(or_cfg, seed)
+    cache = m.new_cache()
+    rng = np.random.default_rng(1)
+    prompt = rng.integers(0, or_cfg.vocab, 9).astype(np.uint32)
+    got = m.forward(prompt, cache, all_logits=True)
+    exp = om.forward(prompt, all_logits=True)
+    assert np.array_equal(m.read_hidden(9), om.hidden(9))
+    assert np.array_equal(got, exp)
+    for layer in range(or_cfg.layers):
+        assert np.array_equal(cache.read(layer, False), om.kcache(layer, 9))
+        assert np.array_equal(cache.read(layer, True), om.kcache(layer, 9, is_v=True))
+    tok = int(exp[-1].argmax())
+    for step in range(5):
+        g = m.forward([tok], cache)
+        e = om.forward([tok])
+        assert np.array_equal(g, e), f"step {step}"
+        tok = int(e[0].argmax())
+    cache.free()
+    m.free()
+    om.free()
+
+
+def test_generate_greedy_matches_oracle(ctx):
+    hip_cfg, or_cfg = cfgs()
+    announce("generate_greedy small")
+    m = lbt_hip.Model.synthetic(ctx, hip_cfg, 5)
+    om = orc.OracleModel(or_cfg, 5)
+    prompt = np.arange(1, 17, dtype=np.uint32) * 37 % or_cfg.vocab
+    cache = m.new_cache()
+    toks, _, _ = m.generate_greedy(prompt, 24, cache)
+    exp = [int(om.forward(prompt)[0].argmax())]
+    for _ in range(24):
+        exp.append(int(om.forward([exp[-1]])[0].argmax()))
+    assert list(toks) == exp
+    assert len(cache) == 16 + 24
+    # forward_argmax on a fresh cache equals the prefill's first token
+    c2 = m.new_cache()
+    assert m.forward_argmax(prompt, c2) == exp[0]
+    c2.free()
+    cache.free()
+    m.free()
+    om.free()
+
+
+def test_cache_growth_keeps_contents(ctx):
+    # ensure_cap doubling (model.rs:238-265): 300 positions cross the 256 boundary
+    hip_cfg, or_cfg = cfgs(layers=1)
+    announce("cache growth")
+    m = lbt_hip.Model.synthetic(ctx, hip_cfg, 8)
+    om = orc.OracleModel(or_cfg, 8)
+    cache = m.new_cache()
+    toks = (np.arange(250) * 13 % or_cfg.vocab).astype(np.uint32)
+    m.forward(toks, cache)
+    om.forward(toks)
+    for t in (5, 6, 7, 8, 9, 10, 11):
+        for _ in range(1):
+            g = m.forward([t], cache)
+            e = om.forward([t])
+            assert np.array_equal(g, e)
+    big = (np.arange(40) * 7 % or_cfg.vocab).astype(np.uint32)
+    assert np.array_equal(m.forward(big, cache), om.forward(big))
+    assert np.array_equal(cache.read(0, False), om.kcache(0, len(cache)))
+    cache.free()
+    m.free()
+    om.free()
+
+
+def test_context_limit_is_an_error(ctx):
+    hip_cfg, _ = cfgs(max_pos=64, layers=1)
+    m = lbt_hip.Model.synthetic(ctx, hip_cfg, 1)
+    cache = m.new_cache()
+    with pytest.raises(lbt_hip.LbtError):
+        m.forward(np.zeros(65, np.uint32), cache)
+    cache.free()
+    m.free()
+
+
+def write_lbt_file(tmp_path, or_cfg, seed):
+    """An lb-convert v1 directory (crates/lb-convert/src/lib.rs:1-16) holding the
+    oracle's synthetic weights."""
+    H, I = or_cfg.hidden, or_cfg.intermediate
+    hd = H // or_cfg.heads
+    kv = or_cfg.kv_heads * hd
+    shapes = [(H, H), (kv, H), (kv, H), (H, H), (I, H), (I, H), (H, I)]
+    names = ["self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj", "mlp.gate_proj",
+             "mlp.up_proj", "mlp.down_proj"]
+    norms = ["input_layernorm.weight", "post_attention_layernorm.weight", "self_attn.attn_sub_norm.weight",
+             "mlp.ffn_sub_norm.weight"]
+    t = {}
+    for l in range(or_cfg.layers):
+        for w, ((r, c), n) in enumerate(zip(shapes, names)):
+            t[f"model.layers.{l}.{n}.qweight"] = orc.synth_packed(seed, orc.t_layer(l, w), r, c)
+            t[f"model.layers.{l}.{n}.wscale"] = np.array([orc.lib().or_synth_wscale(c)], np.float32)
+        for k, n in enumerate(norms):
+            t[f"model.layers.{l}.{n}"] = orc.synth_f32(seed, orc.t_layer(l, 7 + k), I if k == 3 else H)
+    t["model.norm.weight"] = orc.synth_f32(seed, orc.T_FINAL_NORM, H)
+    emb = orc.synth_bf16(seed, orc.T_EMBED, or_cfg.vocab * H).reshape(or_cfg.vocab, H)
+    import torch
+    from safetensors.torch import save_file as save_torch
+
+    tt = {k: torch.from_numpy(np.ascontiguousarray(v)) for k, v in t.items()}
+    tt["model.embed_tokens.weight"] = torch.from_numpy(emb.view(np.int16)).view(torch.bfloat16)
+    save_torch(tt, str(tmp_path / "model.lbt.safetensors"), metadata={"format": "lemonade-burn-ternary", "version": "1"})
+    (tmp_path / "config.json").write_text(json.dumps({
+        "hidden_size": H, "intermediate_size": I, "num_attention_heads": or_cfg.heads,
+        "num_key_value_heads": or_cfg.kv_heads, "num_hidden_layers": or_cfg.layers, "vocab_size": or_cfg.vocab,
+        "rms_norm_eps": 1e-5, "rope_theta": 500000.0, "max_position_embeddings": or_cfg.max_pos,
+        "hidden_act": "relu2", "tie_word_embeddings": True, "bos_token_id": 1}))
+
+
+def test_load_lb_convert_file(ctx, tmp_path):
+    hip_cfg, or_cfg = cfgs()
+    announce("model_load")
+    write_lbt_file(tmp_path, or_cfg, 33)
+    m = lbt_hip.Model.load(ctx, tmp_path)
+    s = lbt_hip.Model.synthetic(ctx, hip_cfg, 33)
+    toks = np.array([5, 6, 7, 800], np.uint32)
+    c1, c2 = m.new_cache(), s.new_cache()
+    assert np.array_equal(m.forward(toks, c1, True), s.forward(toks, c2, True))
+    c1.free()
+    c2.free()
+    m.free()
+    s.free()
+    bad = tmp_path / "config.json"
+    bad.write_text(bad.read_text().replace("relu2", "silu"))
+    with pytest.raises(lbt_hip.LbtError):
+        lbt_hip.Model.load(ctx, tmp_path)
+
+
+def test_full_2b_prompt64_decode_matches_oracle(ctx):
+    """2B4T-shaped model, 64-token uniform-random prompt,
+    greedy decode; tokens identical to the oracle, logits within 1e-3/1e-2."""
+    steps = 32
+    hip_cfg = lbt_hip.make_config()
+    or_cfg = orc.config()
+    seed = 2026
+    announce("full 2B synthetic model")
+    m = lbt_hip.Model.synthetic(ctx, hip_cfg, seed)
+    prompt = np.random.default_rng(64).integers(0, 128256, 64).astype(np.uint32)
+    cache = m.new_cache()
+    toks, _, _ = m.generate_greedy(prompt, steps, cache)
+    cache.free()
+    old = orc.set_fast(1)  # same integers and logits, multi-threaded SIMD integer kernels
+    try:
+        om = orc.OracleModel(or_cfg, seed)
+        cache = m.new_cache()
+        lg = m.forward(prompt, cache)
+        le = om.forward(prompt)
+        assert np.allclose(lg, le, rtol=1e-3, atol=1e-2)
+        assert int(le[0].argmax()) == toks[0]
+        exp = [int(le[0].argmax())]
+        for s in range(steps):
+            le = om.forward([exp[-1]])
+            lg = m.forward([exp[-1]], cache)
+            assert np.allclose(lg, le, rtol=1e-3, atol=1e-2), s
+            exp.append(int(le[0].argmax()))
+        assert list(toks) == exp
+        om.free()
+        cache.free()
+    finally:
+        orc.set_fast(old)
+    m.free()
