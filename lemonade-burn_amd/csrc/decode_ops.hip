@@ -16,12 +16,15 @@ namespace lbt {
 // embedding (model.rs:274-282).  Token ids come from `tokens`, or, when it is
 // null, from the argmax key of the previous step (device-side feedback).  The
 // key is cleared for the next LM head.
-__global__ __launch_bounds__(kThreads) void embed_kernel(const uint16_t* embed, int hidden, const uint32_t* tokens,
-                                                         unsigned long long* key, uint32_t* tok_out, float* x) {
+__global__ __launch_bounds__(kThreads) void embed_kernel(const uint16_t* embed, int hidden, int vocab,
+                                                         const uint32_t* tokens, unsigned long long* key,
+                                                         uint32_t* tok_out, float* x) {
     __shared__ uint32_t tok_s;
     const int t = blockIdx.x;
     if (threadIdx.x == 0) {
         uint32_t tok = tokens ? tokens[t] : 0xffffffffu - (uint32_t)(key[t] & 0xffffffffull);
+        // a key that was never written (no finite logit) must not index past the table
+        if (tok >= (uint32_t)vocab) tok = 0;
         tok_s = tok;
         if (tok_out) tok_out[t] = tok;
     }
@@ -216,9 +219,9 @@ __global__ void synth_bf16_kernel(uint64_t seed, uint64_t tensor, size_t n, uint
 
 // ---------------------------------------------------------------------------
 // launchers
-int launch_embed(lbt_ctx* ctx, const uint16_t* embed, int hidden, const uint32_t* tokens,
+int launch_embed(lbt_ctx* ctx, const uint16_t* embed, int hidden, int vocab, const uint32_t* tokens,
                  const unsigned long long* key, uint32_t* tok_out, int m, float* x) {
-    hipLaunchKernelGGL(embed_kernel, dim3(m), dim3(kThreads), 0, ctx->stream, embed, hidden, tokens,
+    hipLaunchKernelGGL(embed_kernel, dim3(m), dim3(kThreads), 0, ctx->stream, embed, hidden, vocab, tokens,
                        (unsigned long long*)key, tok_out, x);
     LBT_HIP(ctx, hipGetLastError());
     return LBT_OK;

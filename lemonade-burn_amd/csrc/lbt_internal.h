@@ -101,7 +101,7 @@ int launch_bf16_linear(lbt_ctx* ctx, const uint16_t* w, int rows, int cols, cons
                        const float* norm_w, float eps, float* logits, unsigned long long* key);
 
 // ---- model pieces --------------------------------------------------------
-int launch_embed(lbt_ctx* ctx, const uint16_t* embed, int hidden, const uint32_t* tokens,
+int launch_embed(lbt_ctx* ctx, const uint16_t* embed, int hidden, int vocab, const uint32_t* tokens,
                  const unsigned long long* key, uint32_t* tok_out, int m, float* x);
 int launch_rope_append(lbt_ctx* ctx, const float* k, const float* v, int m, int kvh, int hd, int pos0,
                        const float* cos_t, const float* sin_t, uint16_t* kc, uint16_t* vc, int cap);

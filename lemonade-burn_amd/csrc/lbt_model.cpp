@@ -398,7 +398,7 @@ int forward_dev(lbt_model* m, lbt_cache* cc, const uint32_t* toks_dev, int n, bo
     const int H = c.hidden_size, I = c.intermediate_size, nh = c.num_attention_heads, kvh = c.num_key_value_heads;
     const int hd = m->hd, pos0 = cc->len;
     const float eps = (float)c.rms_norm_eps;
-    int rc = launch_embed(ctx, m->embed, H, toks_dev, m->key, tok_out_dev, n, m->x);
+    int rc = launch_embed(ctx, m->embed, H, c.vocab_size, toks_dev, m->key, tok_out_dev, n, m->x);
     if (rc) return rc;
     const size_t layer_kv = (size_t)kvh * cc->cap * hd;
     for (int l = 0; l < c.num_hidden_layers; l++) {
@@ -793,7 +793,7 @@ int lbt_model_generate_greedy(lbt_model* m, const uint32_t* prompt, size_t n, si
         hipEventRecord(e1, ctx->stream);
         for (size_t s = 0; s < steps && !rc; s++) rc = forward_dev(m, c, nullptr, 1, false, false, m->tok_out + s);
         // the last argmax
-        if (!rc) rc = launch_embed(ctx, m->embed, 0, nullptr, m->key, m->tok_out + steps, 1, m->x);
+        if (!rc) rc = launch_embed(ctx, m->embed, 0, m->cfg.vocab_size, nullptr, m->key, m->tok_out + steps, 1, m->x);
         hipEventRecord(e2, ctx->stream);
     }
     hipError_t e = hipStreamSynchronize(ctx->stream);
@@ -834,7 +834,7 @@ int lbt_model_decode_greedy(lbt_model* m, lbt_cache* c, uint32_t first, size_t s
     hipEventRecord(e0, ctx->stream);
     rc = forward_dev(m, c, m->toks, 1, false, false, nullptr);
     for (size_t s = 1; s < steps && !rc; s++) rc = forward_dev(m, c, nullptr, 1, false, false, m->tok_out + s - 1);
-    if (!rc) rc = launch_embed(ctx, m->embed, 0, nullptr, m->key, m->tok_out + steps - 1, 1, m->x);
+    if (!rc) rc = launch_embed(ctx, m->embed, 0, m->cfg.vocab_size, nullptr, m->key, m->tok_out + steps - 1, 1, m->x);
     hipEventRecord(e1, ctx->stream);
     hipError_t e = hipStreamSynchronize(ctx->stream);
     if (!rc && e != hipSuccess) rc = hip_err(ctx, e, "decode");
