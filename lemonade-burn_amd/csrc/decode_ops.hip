@@ -18,7 +18,7 @@ namespace lbt {
 // key is cleared for the next LM head.
 __global__ __launch_bounds__(kThreads) void embed_kernel(const uint16_t* embed, int hidden, int vocab,
                                                          const uint32_t* tokens, unsigned long long* key,
-                                                         uint32_t* tok_out, float* x) {
+                                                         uint32_t* tok_out, float* x, int* state) {
     __shared__ uint32_t tok_s;
     const int t = blockIdx.x;
     if (threadIdx.x == 0) {
@@ -26,7 +26,12 @@ __global__ __launch_bounds__(kThreads) void embed_kernel(const uint16_t* embed, 
         // a key that was never written (no finite logit) must not index past the table
         if (tok >= (uint32_t)vocab) tok = 0;
         tok_s = tok;
-        if (tok_out) tok_out[t] = tok;
+        if (state) {  // graph-replayed decode step (one token): next position, next output slot
+            state[0] += 1;
+            tok_out[state[1]++] = tok;
+        } else if (tok_out) {
+            tok_out[t] = tok;
+        }
     }
     __syncthreads();
     if (threadIdx.x == 0 && key) key[t] = 0ull;
@@ -36,75 +41,98 @@ __global__ __launch_bounds__(kThreads) void embed_kernel(const uint16_t* embed, 
 }
 
 // ---------------------------------------------------------------------------
-// RoPE on the new keys and bf16 append of K and V at positions pos0.. .
-// apply_rope (model.rs:295-301): out = x*cos + rot*sin, rot = cat(-x2, x1).
-__global__ void rope_append_kernel(const float* k, const float* v, int kvh, int hd, int pos0, const float* cos_t,
-                                   const float* sin_t, uint16_t* kc, uint16_t* vc, int cap) {
-    const int t = blockIdx.x, h = blockIdx.y, d = threadIdx.x;
-    const int h2 = hd >> 1, p = pos0 + t, i = d % h2;
-    const float* kr = k + ((size_t)t * kvh + h) * hd;
-    const float rot = d < h2 ? -kr[d + h2] : kr[d - h2];
-    const float y = kr[d] * cos_t[(size_t)p * h2 + i] + rot * sin_t[(size_t)p * h2 + i];
-    const size_t o = ((size_t)h * cap + p) * hd + d;
-    kc[o] = f32_to_bf16(y);
-    vc[o] = f32_to_bf16(v[((size_t)t * kvh + h) * hd + d]);
-}
-
-// ---------------------------------------------------------------------------
-// GQA attention for query row t (absolute position pos0 + t) and head h:
-// q is rotated here, scores = q.K^T * scaling over the visible keys 0..p,
-// softmax (exp(s - max) / sum), then probs @ V (model.rs:349-357; the causal
-// mask of :316-328 is the visibility bound).  One workgroup per (head, row).
-__global__ __launch_bounds__(kThreads) void attention_kernel(const float* q, int nh, int kvh, int hd, int pos0,
-                                                             const float* cos_t, const float* sin_t,
+// GQA attention for query row t (absolute position p = pos0 + t) and head h,
+// over keys 0..p of the bf16 cache (the q/k/v GEMV has already rotated q and
+// appended the rotated k and v).  model.rs:349-357: scores = q.K^T * scaling,
+// softmax = exp(s - max) / sum, out = probs @ V; the causal mask of :316-328
+// is the visibility bound.  One workgroup per (head, row).  Float order (the
+// oracle mirrors it), with LK = hd/8 lanes per key and 8 dims per lane:
+//   score: lane c sums q[8c+e]*k[8c+e] over e = 0..7 by fused multiply-adds,
+//          the LK lanes combine with an xor butterfly (m = LK/2 .. 1), then
+//          * scaling;
+//   sum:   thread t adds exp(s_j - max) over j = t, t+256, ...; block_sum;
+//   p_j:   exp(s_j - max) / sum;
+//   out:   thread (group g = t/LK, chunk c = t%LK) accumulates
+//          p_j * v[j][8c+e] by fused multiply-adds over j = g, g+256/LK, ...;
+//          the 64/LK groups of a wave combine by xor over the group index
+//          (m = 1, 2, ...), the four waves as (w0 + w1) + (w2 + w3).
+template <int LK>
+__global__ __launch_bounds__(kThreads) void attention_kernel(const float* q, int nh, int kvh, int pos0,
                                                              const uint16_t* kc, const uint16_t* vc, int cap,
-                                                             float scaling, float* out) {
+                                                             float scaling, float* out, const int* pos_dev) {
+    constexpr int HD = LK * 8, GW = 64 / LK, NG = kThreads / LK;
     extern __shared__ float sc[];  // [p + 1]
-    __shared__ float qr[256];
-    __shared__ float red[kThreads];
-    const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
-    const int H = nh * hd, h2 = hd >> 1, p = pos0 + t, vis = p + 1, g = h / (nh / kvh);
-    const float* qh = q + (size_t)t * H + (size_t)h * hd;
-    if (tid < hd) {
-        const int i = tid % h2;
-        const float rot = tid < h2 ? -qh[tid + h2] : qh[tid - h2];
-        qr[tid] = qh[tid] * cos_t[(size_t)p * h2 + i] + rot * sin_t[(size_t)p * h2 + i];
-    }
+    __shared__ __align__(16) float qs[HD];
+    __shared__ float red[8];
+    __shared__ __align__(16) float pv[4][HD];
+    const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    if (pos_dev) pos0 = *pos_dev;
+    const int H = nh * HD, p = pos0 + t, vis = p + 1, g = h / (nh / kvh);
+    if (tid < HD) qs[tid] = q[(size_t)t * H + (size_t)h * HD + tid];
     __syncthreads();
-    const uint16_t* K = kc + (size_t)g * cap * hd;
-    const uint16_t* V = vc + (size_t)g * cap * hd;
+    const uint16_t* K = kc + (size_t)g * cap * HD;
+    const uint16_t* V = vc + (size_t)g * cap * HD;
+    const int ks = lane / LK, cc = lane % LK;
+    float q8[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) q8[e] = qs[8 * cc + e];
     float mx = -__builtin_inff();
-    for (int j = tid; j < vis; j += kThreads) {
-        const uint16_t* kr = K + (size_t)j * hd;
+    for (int j0 = w * GW; j0 < vis; j0 += 4 * GW) {
+        const int j = j0 + ks;
         float a = 0.0f;
-        for (int d = 0; d < hd; d += 8) {
-            const uint4 kv = *(const uint4*)(kr + d);
+        if (j < vis) {
+            const uint4 kv = *(const uint4*)(K + (size_t)j * HD + 8 * cc);
             const uint32_t wv[4] = {kv.x, kv.y, kv.z, kv.w};
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                a = __builtin_fmaf(qr[d + 2 * e], bf16_to_f32((uint16_t)(wv[e] & 0xffffu)), a);
-                a = __builtin_fmaf(qr[d + 2 * e + 1], bf16_to_f32((uint16_t)(wv[e] >> 16)), a);
+                a = __builtin_fmaf(q8[2 * e], bf16_to_f32((uint16_t)(wv[e] & 0xffffu)), a);
+                a = __builtin_fmaf(q8[2 * e + 1], bf16_to_f32((uint16_t)(wv[e] >> 16)), a);
             }
         }
-        const float s = a * scaling;
-        sc[j] = s;
-        mx = fmaxf(mx, s);
+#pragma unroll
+        for (int m = LK / 2; m >= 1; m >>= 1) a = a + __shfl_xor(a, m);
+        if (j < vis) {
+            const float s = a * scaling;
+            if (cc == 0) sc[j] = s;
+            mx = fmaxf(mx, s);
+        }
     }
-    mx = block_max(mx, red);
+    mx = block_max(mx, red);  // includes the barrier that publishes sc
     float ps = 0.0f;
     for (int j = tid; j < vis; j += kThreads) {
         const float e = lbt_expf(sc[j] - mx);
         sc[j] = e;
         ps = ps + e;
     }
-    const float sum = block_tree256(ps, red);
+    const float sum = block_sum(ps, red);
     for (int j = tid; j < vis; j += kThreads) sc[j] = sc[j] / sum;
     __syncthreads();
-    if (tid < hd) {
-        float a = 0.0f;
-        for (int j = 0; j < vis; j++) a = __builtin_fmaf(sc[j], bf16_to_f32(V[(size_t)j * hd + tid]), a);
-        out[(size_t)t * H + (size_t)h * hd + tid] = a;
+    const int grp = tid / LK, c = tid % LK;
+    float acc[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) acc[e] = 0.0f;
+    for (int j = grp; j < vis; j += NG) {
+        const float pj = sc[j];
+        const uint4 vv = *(const uint4*)(V + (size_t)j * HD + 8 * c);
+        const uint32_t wv[4] = {vv.x, vv.y, vv.z, vv.w};
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            acc[2 * e] = __builtin_fmaf(pj, bf16_to_f32((uint16_t)(wv[e] & 0xffffu)), acc[2 * e]);
+            acc[2 * e + 1] = __builtin_fmaf(pj, bf16_to_f32((uint16_t)(wv[e] >> 16)), acc[2 * e + 1]);
+        }
     }
+#pragma unroll
+    for (int m = 1; m < GW; m <<= 1) {
+#pragma unroll
+        for (int e = 0; e < 8; e++) acc[e] = acc[e] + __shfl_xor(acc[e], m * LK);
+    }
+    if (lane < LK) {
+#pragma unroll
+        for (int e = 0; e < 8; e++) pv[w][8 * c + e] = acc[e];
+    }
+    __syncthreads();
+    if (tid < HD)
+        out[(size_t)t * H + (size_t)h * HD + tid] = (pv[0][tid] + pv[1][tid]) + (pv[2][tid] + pv[3][tid]);
 }
 
 // ---------------------------------------------------------------------------
@@ -113,18 +141,25 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(const float* q, int
 // the 16-byte chunks l, l+64, ... (8 bf16 each), fused multiply-adds in
 // element order, then an xor butterfly.  The first-max key of each row t is
 // atomically maxed into key[t] (argmax, sample.rs:17-25).
-__device__ __forceinline__ float norm_factor_lm(const float* xr, int cols, const float* norm_w, float eps,
-                                                float* red) {
-    if (!norm_w) return 1.0f;
-    float p = 0.0f;
-    for (int i = threadIdx.x; i < cols; i += kThreads) p = __builtin_fmaf(xr[i], xr[i], p);
-    float ss = block_tree256(p, red);
-    float mean = ss / (float)cols;
-    return 1.0f / __builtin_sqrtf(mean + eps);
-}
-
 __device__ __forceinline__ float bf_lo(uint32_t v) { return __uint_as_float(v << 16); }
 __device__ __forceinline__ float bf_hi(uint32_t v) { return __uint_as_float(v & 0xffff0000u); }
+
+// acc += sum over e of bf16(w[e]) * x[e] for the 8 bf16 of one 16-byte chunk, in order.
+__device__ __forceinline__ float dot8(uint4 wv, const float* x, float acc) {
+    const float4 x0 = *(const float4*)x;
+    const float4 x1 = *(const float4*)(x + 4);
+    acc = __builtin_fmaf(bf_lo(wv.x), x0.x, acc);
+    acc = __builtin_fmaf(bf_hi(wv.x), x0.y, acc);
+    acc = __builtin_fmaf(bf_lo(wv.y), x0.z, acc);
+    acc = __builtin_fmaf(bf_hi(wv.y), x0.w, acc);
+    acc = __builtin_fmaf(bf_lo(wv.z), x1.x, acc);
+    acc = __builtin_fmaf(bf_hi(wv.z), x1.y, acc);
+    acc = __builtin_fmaf(bf_lo(wv.w), x1.z, acc);
+    acc = __builtin_fmaf(bf_hi(wv.w), x1.w, acc);
+    return acc;
+}
+
+constexpr int kLmChunks = 5;  // 16-byte chunks per lane per row (hidden <= 2560 on the fast path)
 
 __global__ __launch_bounds__(kThreads) void lmhead_kernel(const uint16_t* W, int rows, int cols, const float* x,
                                                           const float* norm_w, float eps, float* logits,
@@ -133,37 +168,81 @@ __global__ __launch_bounds__(kThreads) void lmhead_kernel(const uint16_t* W, int
     __shared__ float red[kThreads];
     const int t = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
     const float* xr = x + (size_t)t * cols;
-    const float rr = norm_factor_lm(xr, cols, norm_w, eps, red);
-    for (int i = tid; i < cols; i += kThreads) xs[i] = norm_w ? (xr[i] * rr) * norm_w[i] : xr[i];
+    if (cols <= 16 * kThreads) {
+        float v[16];
+        load_norm_row<16>(xr, cols, norm_w, eps, v, red);
+#pragma unroll
+        for (int e = 0; e < 16; e++)
+            if (tid + e * kThreads < cols) xs[tid + e * kThreads] = v[e];
+    } else {
+        const float rr = norm_factor_global(xr, cols, norm_w, eps, red);
+        for (int i = tid; i < cols; i += kThreads) xs[i] = norm_w ? (xr[i] * rr) * norm_w[i] : xr[i];
+    }
     __syncthreads();
     const int nchunks = cols >> 3;
     const int gw = blockIdx.x * 4 + (tid >> 6), nw = gridDim.x * 4;
     unsigned long long best = 0ull;
-    for (int r = gw; r < rows; r += nw) {
-        const uint4* wr = (const uint4*)(W + (size_t)r * cols);
-        float acc = 0.0f;
-        for (int c = lane; c < nchunks; c += 64) {
-            const uint4 wv = wr[c];
-            const float4 x0 = *(const float4*)(xs + 8 * c);
-            const float4 x1 = *(const float4*)(xs + 8 * c + 4);
-            acc = __builtin_fmaf(bf_lo(wv.x), x0.x, acc);
-            acc = __builtin_fmaf(bf_hi(wv.x), x0.y, acc);
-            acc = __builtin_fmaf(bf_lo(wv.y), x0.z, acc);
-            acc = __builtin_fmaf(bf_hi(wv.y), x0.w, acc);
-            acc = __builtin_fmaf(bf_lo(wv.z), x1.x, acc);
-            acc = __builtin_fmaf(bf_hi(wv.z), x1.y, acc);
-            acc = __builtin_fmaf(bf_lo(wv.w), x1.z, acc);
-            acc = __builtin_fmaf(bf_hi(wv.w), x1.w, acc);
-        }
+    if (nchunks <= 64 * kLmChunks) {
+        // two rows per iteration, all their chunk loads in flight at once
+        for (int r = gw; r < rows; r += 2 * nw) {
+            const int r1 = r + nw;
+            const bool has1 = r1 < rows;
+            const uint4* w0 = (const uint4*)(W + (size_t)r * cols);
+            const uint4* w1 = (const uint4*)(W + (size_t)(has1 ? r1 : r) * cols);
+            uint4 a0[kLmChunks], a1[kLmChunks];
 #pragma unroll
-        for (int m = 32; m >= 1; m >>= 1) acc = acc + __shfl_xor(acc, m);
-        if (lane == 0) {
-            if (logits) logits[(size_t)t * rows + r] = acc;
-            const unsigned long long k = argmax_key(acc, (uint32_t)r);
-            best = k > best ? k : best;
+            for (int i = 0; i < kLmChunks; i++) {
+                const int c = lane + 64 * i;
+                a0[i] = c < nchunks ? ld_stream(w0 + c) : make_uint4(0, 0, 0, 0);
+                a1[i] = (has1 && c < nchunks) ? ld_stream(w1 + c) : make_uint4(0, 0, 0, 0);
+            }
+            float acc0 = 0.0f, acc1 = 0.0f;
+#pragma unroll
+            for (int i = 0; i < kLmChunks; i++) {
+                const int c = lane + 64 * i;
+                if (c < nchunks) {
+                    acc0 = dot8(a0[i], xs + 8 * c, acc0);
+                    acc1 = dot8(a1[i], xs + 8 * c, acc1);
+                }
+            }
+#pragma unroll
+            for (int m = 32; m >= 1; m >>= 1) {
+                acc0 = acc0 + __shfl_xor(acc0, m);
+                acc1 = acc1 + __shfl_xor(acc1, m);
+            }
+            if (lane == 0) {
+                if (logits) logits[(size_t)t * rows + r] = acc0;
+                unsigned long long k = argmax_key(acc0, (uint32_t)r);
+                best = k > best ? k : best;
+                if (has1) {
+                    if (logits) logits[(size_t)t * rows + r1] = acc1;
+                    k = argmax_key(acc1, (uint32_t)r1);
+                    best = k > best ? k : best;
+                }
+            }
+        }
+    } else {
+        for (int r = gw; r < rows; r += nw) {
+            const uint4* wr = (const uint4*)(W + (size_t)r * cols);
+            float acc = 0.0f;
+            for (int c = lane; c < nchunks; c += 64) acc = dot8(ld_stream(wr + c), xs + 8 * c, acc);
+#pragma unroll
+            for (int m = 32; m >= 1; m >>= 1) acc = acc + __shfl_xor(acc, m);
+            if (lane == 0) {
+                if (logits) logits[(size_t)t * rows + r] = acc;
+                const unsigned long long k = argmax_key(acc, (uint32_t)r);
+                best = k > best ? k : best;
+            }
         }
     }
     if (key && lane == 0 && best) atomicMax(&key[t], best);
+}
+
+__global__ void set_state_kernel(int* state, int pos, int slot) {
+    if (threadIdx.x == 0) {
+        state[0] = pos;
+        state[1] = slot;
+    }
 }
 
 __global__ void fill_u64_kernel(unsigned long long* p, int n, unsigned long long v) {
@@ -220,31 +299,37 @@ __global__ void synth_bf16_kernel(uint64_t seed, uint64_t tensor, size_t n, uint
 // ---------------------------------------------------------------------------
 // launchers
 int launch_embed(lbt_ctx* ctx, const uint16_t* embed, int hidden, int vocab, const uint32_t* tokens,
-                 const unsigned long long* key, uint32_t* tok_out, int m, float* x) {
+                 const unsigned long long* key, uint32_t* tok_out, int m, float* x, int* state) {
     hipLaunchKernelGGL(embed_kernel, dim3(m), dim3(kThreads), 0, ctx->stream, embed, hidden, vocab, tokens,
-                       (unsigned long long*)key, tok_out, x);
+                       (unsigned long long*)key, tok_out, x, state);
     LBT_HIP(ctx, hipGetLastError());
     return LBT_OK;
 }
 
-int launch_rope_append(lbt_ctx* ctx, const float* k, const float* v, int m, int kvh, int hd, int pos0,
-                       const float* cos_t, const float* sin_t, uint16_t* kc, uint16_t* vc, int cap) {
-    hipLaunchKernelGGL(rope_append_kernel, dim3(m, kvh), dim3(hd), 0, ctx->stream, k, v, kvh, hd, pos0, cos_t,
-                       sin_t, kc, vc, cap);
-    LBT_HIP(ctx, hipGetLastError());
-    return LBT_OK;
-}
-
-int launch_attention(lbt_ctx* ctx, const float* q, int m, int nh, int kvh, int hd, int pos0, const float* cos_t,
-                     const float* sin_t, const uint16_t* kc, const uint16_t* vc, int cap, float scaling,
-                     float* out) {
-    if (hd > 256 || hd % 8) return set_err(ctx, LBT_E_INVALID, "attention: head_dim must be <= 256, multiple of 8");
-    const size_t lds = (size_t)(pos0 + m) * sizeof(float);
+int launch_attention(lbt_ctx* ctx, const float* q, int m, int nh, int kvh, int hd, int pos0, const uint16_t* kc,
+                     const uint16_t* vc, int cap, float scaling, float* out, const int* pos_dev) {
+    // a graph-replayed step reads its position on the device: size for the cache
+    const size_t lds = (size_t)(pos_dev ? cap : pos0 + m) * sizeof(float);
     if (lds > 64 * 1024) return set_err(ctx, LBT_E_RANGE, "attention: context too long for the LDS score buffer");
     hipEvent_t ev = nullptr;
     prof_begin(ctx, &ev);
-    hipLaunchKernelGGL(attention_kernel, dim3(nh, m), dim3(kThreads), lds, ctx->stream, q, nh, kvh, hd, pos0, cos_t,
-                       sin_t, kc, vc, cap, scaling, out);
+    dim3 grid(nh, m);
+    switch (hd) {
+        case 64:
+            hipLaunchKernelGGL(attention_kernel<8>, grid, dim3(kThreads), lds, ctx->stream, q, nh, kvh, pos0, kc, vc,
+                               cap, scaling, out, pos_dev);
+            break;
+        case 128:
+            hipLaunchKernelGGL(attention_kernel<16>, grid, dim3(kThreads), lds, ctx->stream, q, nh, kvh, pos0, kc, vc,
+                               cap, scaling, out, pos_dev);
+            break;
+        case 256:
+            hipLaunchKernelGGL(attention_kernel<32>, grid, dim3(kThreads), lds, ctx->stream, q, nh, kvh, pos0, kc, vc,
+                               cap, scaling, out, pos_dev);
+            break;
+        default:
+            return set_err(ctx, LBT_E_INVALID, "attention: head_dim must be 64, 128 or 256");
+    }
     LBT_HIP(ctx, hipGetLastError());
     const double kv_bytes = 2.0 * kvh * (double)(pos0 + m) * hd * 2.0;
     prof_end(ctx, ev, kProfAttn, kv_bytes);
@@ -271,6 +356,12 @@ int launch_bf16_linear(lbt_ctx* ctx, const uint16_t* w, int rows, int cols, cons
 
 int launch_fill_u64(lbt_ctx* ctx, unsigned long long* p, int n, unsigned long long v) {
     hipLaunchKernelGGL(fill_u64_kernel, dim3((n + 255) / 256), dim3(256), 0, ctx->stream, p, n, v);
+    LBT_HIP(ctx, hipGetLastError());
+    return LBT_OK;
+}
+
+int launch_set_state(lbt_ctx* ctx, int* state, int pos, int slot) {
+    hipLaunchKernelGGL(set_state_kernel, dim3(1), dim3(64), 0, ctx->stream, state, pos, slot);
     LBT_HIP(ctx, hipGetLastError());
     return LBT_OK;
 }

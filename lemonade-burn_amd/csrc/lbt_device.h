@@ -2,10 +2,9 @@
 //
 // Float reduction order is fixed and documented here; the CPU oracle
 // (oracle/lbt_oracle.c) follows the same order so results compare bit for bit.
-//   * block sums: 256 per-thread partials reduced in LDS, p[t] += p[t+s] for
-//     s = 128, 64, ..., 1 (tree256);
-//   * wavefront dots (LM head): xor butterfly, lane l takes v[l] + v[l ^ m]
-//     for m = 32, ..., 1;
+//   * wavefront sums: xor butterfly, lane l takes v[l] + v[l ^ m] for
+//     m = 32, ..., 1;
+//   * block sums (256 threads): wavefront sums, then (w0 + w1) + (w2 + w3);
 //   * max and integer sums are order independent.
 // All code is compiled with -ffp-contract=off; fused multiply-adds are written
 // explicitly with __builtin_fmaf.
@@ -18,6 +17,14 @@ namespace lbt {
 constexpr int kBlock = 128;      // weights per LB2 block (pack.rs:18)
 constexpr int kBlockBytes = 32;  // bytes per LB2 block (pack.rs:19)
 constexpr int kThreads = 256;    // threads per workgroup everywhere
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// 16-byte streaming load (nontemporal: the weights are read once per token).
+__device__ __forceinline__ uint4 ld_stream(const uint4* p) {
+    const u32x4 v = __builtin_nontemporal_load((const u32x4*)p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
 
@@ -63,17 +70,22 @@ __device__ __forceinline__ float lbt_expf(float x) {
     return p * __uint_as_float((uint32_t)(ni + 127) << 23);
 }
 
-// tree256 over one value per thread (blockDim.x == 256); `red` is 256 floats of LDS.
-__device__ __forceinline__ float block_tree256(float v, float* red) {
-    const int t = threadIdx.x;
-    red[t] = v;
-    __syncthreads();
+// xor butterfly over the 64 lanes of a wavefront: every lane ends with the
+// same value, lane l having added v[l] + v[l ^ m] for m = 32, 16, ..., 1.
+__device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
-    for (int s = 128; s >= 1; s >>= 1) {
-        if (t < s) red[t] = red[t] + red[t + s];
-        __syncthreads();
-    }
-    float r = red[0];
+    for (int m = 32; m >= 1; m >>= 1) v = v + __shfl_xor(v, m);
+    return v;
+}
+
+// Block sum of one value per thread (blockDim.x == 256): wave butterflies,
+// then (w0 + w1) + (w2 + w3).  `red` >= 4 floats of LDS.
+__device__ __forceinline__ float block_sum(float v, float* red) {
+    v = wave_sum(v);
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) red[w] = v;
+    __syncthreads();
+    float r = (red[0] + red[1]) + (red[2] + red[3]);
     __syncthreads();
     return r;
 }
@@ -109,6 +121,42 @@ __device__ __forceinline__ int block_sum_i(int v, int* red) {
     int r = red[0] + red[1] + red[2] + red[3];
     __syncthreads();
     return r;
+}
+
+// Loads row xr[0..cols) into registers, v[e] = x[threadIdx.x + 256 e] (0 past
+// cols), and if norm_w is set applies rms_norm (crates/lb-model/src/model.rs:
+// 267-272) in place: r = 1 / sqrt(sum(x^2)/cols + eps) with the sum of squares
+// accumulated per thread by fused multiply-adds in ascending i and combined by
+// block_sum; v = (x * r) * w.  Requires cols <= 256 * EPT.  One global pass.
+template <int EPT>
+__device__ __forceinline__ void load_norm_row(const float* xr, int cols, const float* norm_w, float eps,
+                                              float (&v)[EPT], float* red) {
+    float nw[EPT];
+#pragma unroll
+    for (int e = 0; e < EPT; e++) {
+        const int i = threadIdx.x + e * kThreads;
+        v[e] = i < cols ? xr[i] : 0.0f;
+        nw[e] = (norm_w && i < cols) ? norm_w[i] : 0.0f;
+    }
+    if (!norm_w) return;
+    float p = 0.0f;
+#pragma unroll
+    for (int e = 0; e < EPT; e++)
+        if (threadIdx.x + e * kThreads < cols) p = __builtin_fmaf(v[e], v[e], p);
+    const float ss = block_sum(p, red);
+    const float r = 1.0f / __builtin_sqrtf(ss / (float)cols + eps);
+#pragma unroll
+    for (int e = 0; e < EPT; e++) v[e] = (v[e] * r) * nw[e];
+}
+
+// Same result for rows longer than 256 * EPT, re-reading x from memory.
+__device__ __forceinline__ float norm_factor_global(const float* xr, int cols, const float* norm_w, float eps,
+                                                    float* red) {
+    if (!norm_w) return 1.0f;
+    float p = 0.0f;
+    for (int i = threadIdx.x; i < cols; i += kThreads) p = __builtin_fmaf(xr[i], xr[i], p);
+    const float ss = block_sum(p, red);
+    return 1.0f / __builtin_sqrtf(ss / (float)cols + eps);
 }
 
 // Ordered key for an f32 so that unsigned comparison follows float order; NaN

@@ -64,7 +64,7 @@ void prof_end(lbt_ctx* ctx, hipEvent_t ev, int cls, double bytes);
 
 // ---- ternary GEMV / GEMM ------------------------------------------------
 enum InMode { kInPreQ = 0, kInF32 = 1 };
-enum OutMode { kOutI32 = 0, kOutF32 = 1, kOutF32Add = 2, kOutRelu2 = 3 };
+enum OutMode { kOutI32 = 0, kOutF32 = 1, kOutF32Add = 2, kOutRelu2 = 3, kOutQKV = 4 };
 
 struct TernaryOp {
     int nmat = 1;
@@ -84,6 +84,14 @@ struct TernaryOp {
     int in_mode = kInPreQ;
     int out_mode = kOutF32;
     void* out[3] = {nullptr, nullptr, nullptr};
+    // kOutQKV: out[0] gets rotated q (f32); rotated k and v go to the bf16
+    // cache at positions pos0 + token ([kv_heads][cap][hd] of this layer)
+    int hd = 0, pos0 = 0, cap = 0;
+    const int* pos_dev = nullptr;  // device position (graph replay) instead of pos0
+    const float* cos_t = nullptr;
+    const float* sin_t = nullptr;
+    uint16_t* kc = nullptr;
+    uint16_t* vc = nullptr;
 };
 // Dispatches decode GEMV (small m) or the int8-MFMA prefill GEMM (large m).
 int launch_ternary(lbt_ctx* ctx, const TernaryOp& op);
@@ -101,14 +109,14 @@ int launch_bf16_linear(lbt_ctx* ctx, const uint16_t* w, int rows, int cols, cons
                        const float* norm_w, float eps, float* logits, unsigned long long* key);
 
 // ---- model pieces --------------------------------------------------------
+// state (nullable, device): {position, output slot}; when set, the kernel
+// advances the position by one and writes the token to tok_out[slot++].
 int launch_embed(lbt_ctx* ctx, const uint16_t* embed, int hidden, int vocab, const uint32_t* tokens,
-                 const unsigned long long* key, uint32_t* tok_out, int m, float* x);
-int launch_rope_append(lbt_ctx* ctx, const float* k, const float* v, int m, int kvh, int hd, int pos0,
-                       const float* cos_t, const float* sin_t, uint16_t* kc, uint16_t* vc, int cap);
-int launch_attention(lbt_ctx* ctx, const float* q, int m, int nh, int kvh, int hd, int pos0,
-                     const float* cos_t, const float* sin_t, const uint16_t* kc, const uint16_t* vc,
-                     int cap, float scaling, float* out);
+                 const unsigned long long* key, uint32_t* tok_out, int m, float* x, int* state = nullptr);
+int launch_attention(lbt_ctx* ctx, const float* q, int m, int nh, int kvh, int hd, int pos0, const uint16_t* kc,
+                     const uint16_t* vc, int cap, float scaling, float* out, const int* pos_dev = nullptr);
 int launch_fill_u64(lbt_ctx* ctx, unsigned long long* p, int n, unsigned long long v);
+int launch_set_state(lbt_ctx* ctx, int* state, int pos, int slot);
 
 // Synthetic weights (same generator as oracle/lbt_oracle.c or_synth_*).
 int launch_synth_packed(lbt_ctx* ctx, uint64_t seed, uint64_t tensor, int rows, int cols, uint8_t* out);

@@ -15,6 +15,7 @@
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 #include <sys/mman.h>
 #include <sys/stat.h>
@@ -233,6 +234,11 @@ struct lbt_model {
     int tok_out_cap = 0;
     unsigned long long* key = nullptr;
     int last_n = 0;
+    // graph of one decode step (embed from the argmax key .. LM head), valid
+    // for the cache buffers and workspace it was captured with
+    int* state = nullptr;  // device {position, output slot}
+    hipGraphExec_t step_exec = nullptr;
+    const void* step_key[6] = {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
 };
 
 struct lbt_cache {
@@ -392,13 +398,15 @@ int ensure_cap(lbt_cache* cc, int need) {
 // or from the previous step's argmax key when null).  Leaves the argmax key of
 // the last row in m->key[0] and logits (if `logits_all` or `want_logits`).
 int forward_dev(lbt_model* m, lbt_cache* cc, const uint32_t* toks_dev, int n, bool all_logits, bool want_logits,
-                uint32_t* tok_out_dev) {
+                uint32_t* tok_out_dev, int* state = nullptr) {
     lbt_ctx* ctx = m->ctx;
     const lbt_config& c = m->cfg;
     const int H = c.hidden_size, I = c.intermediate_size, nh = c.num_attention_heads, kvh = c.num_key_value_heads;
     const int hd = m->hd, pos0 = cc->len;
     const float eps = (float)c.rms_norm_eps;
-    int rc = launch_embed(ctx, m->embed, H, c.vocab_size, toks_dev, m->key, tok_out_dev, n, m->x);
+    // with `state`, positions come from the device (state[0]) so that the step
+    // can be captured once and replayed
+    int rc = launch_embed(ctx, m->embed, H, c.vocab_size, toks_dev, m->key, tok_out_dev, n, m->x, state);
     if (rc) return rc;
     const size_t layer_kv = (size_t)kvh * cc->cap * hd;
     for (int l = 0; l < c.num_hidden_layers; l++) {
@@ -417,16 +425,20 @@ int forward_dev(lbt_model* m, lbt_cache* cc, const uint32_t* toks_dev, int n, bo
         }
         op.x = m->x;
         op.norm_w = m->norm[l * 4 + 0];
-        op.out_mode = kOutF32;
+        op.out_mode = kOutQKV;
         op.out[0] = m->q;
-        op.out[1] = m->k;
-        op.out[2] = m->v;
-        if ((rc = launch_ternary(ctx, op))) return rc;
         uint16_t* Kl = cc->k + (size_t)l * layer_kv;
         uint16_t* Vl = cc->v + (size_t)l * layer_kv;
-        if ((rc = launch_rope_append(ctx, m->k, m->v, n, kvh, hd, pos0, m->cos_t, m->sin_t, Kl, Vl, cc->cap))) return rc;
-        if ((rc = launch_attention(ctx, m->q, n, nh, kvh, hd, pos0, m->cos_t, m->sin_t, Kl, Vl, cc->cap, m->scaling,
-                                   m->att)))
+        op.hd = hd;
+        op.pos0 = pos0;
+        op.pos_dev = state;
+        op.cap = cc->cap;
+        op.cos_t = m->cos_t;
+        op.sin_t = m->sin_t;
+        op.kc = Kl;
+        op.vc = Vl;
+        if ((rc = launch_ternary(ctx, op))) return rc;
+        if ((rc = launch_attention(ctx, m->q, n, nh, kvh, hd, pos0, Kl, Vl, cc->cap, m->scaling, m->att, state)))
             return rc;
         // o_proj on attn_sub_norm(attn), residual (model.rs:358-359)
         TernaryOp o;
@@ -483,6 +495,53 @@ int forward_dev(lbt_model* m, lbt_cache* cc, const uint32_t* toks_dev, int n, bo
     const int rows_out = n - first;
     return launch_bf16_linear(ctx, m->embed, c.vocab_size, H, m->x + (size_t)first * H, rows_out, m->final_norm, eps,
                               (all_logits || want_logits) ? m->logits : nullptr, all_logits ? nullptr : m->key);
+}
+
+// Runs n decode steps, each fed with the previous step's argmax (the key);
+// the token consumed by step s goes to m->tok_out[slot0 + s].  Outside
+// profiling one captured step is replayed as a HIP graph (positions and
+// output slots advance on the device); the graph is re-captured when the
+// cache or workspace buffers change.
+int decode_steps(lbt_model* m, lbt_cache* c, int n, int slot0) {
+    lbt_ctx* ctx = m->ctx;
+    if (n <= 0) return LBT_OK;
+    int rc;
+    if (ctx->prof || getenv("LBT_NO_GRAPH")) {
+        for (int s = 0; s < n; s++)
+            if ((rc = forward_dev(m, c, nullptr, 1, false, false, m->tok_out + slot0 + s))) return rc;
+        return LBT_OK;
+    }
+    if (!m->state) LBT_HIP(ctx, hipMalloc(&m->state, 2 * sizeof(int)));
+    const void* key[6] = {c->k, c->v, (const void*)(intptr_t)c->cap, m->tok_out, m->x, m->key};
+    if (!m->step_exec || memcmp(key, m->step_key, sizeof(key)) != 0) {
+        if (m->step_exec) {
+            hipGraphExecDestroy(m->step_exec);
+            m->step_exec = nullptr;
+        }
+        hipGraph_t g = nullptr;
+        LBT_HIP(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+        const int len = c->len;
+        rc = forward_dev(m, c, nullptr, 1, false, false, m->tok_out, m->state);
+        c->len = len;
+        hipError_t e = hipStreamEndCapture(ctx->stream, &g);
+        if (rc) {
+            if (g) hipGraphDestroy(g);
+            return rc;
+        }
+        if (e != hipSuccess) return hip_err(ctx, e, "capture decode step");
+        e = hipGraphInstantiate(&m->step_exec, g, nullptr, nullptr, 0);
+        hipGraphDestroy(g);
+        if (e != hipSuccess) {
+            m->step_exec = nullptr;
+            return hip_err(ctx, e, "instantiate decode step");
+        }
+        memcpy(m->step_key, key, sizeof(key));
+    }
+    if ((rc = launch_set_state(ctx, m->state, c->len - 1, slot0))) return rc;
+    for (int s = 0; s < n; s++) LBT_HIP(ctx, hipGraphLaunch(m->step_exec, ctx->stream));
+    c->len += n;
+    m->last_n = 1;
+    return LBT_OK;
 }
 
 int read_config(lbt_ctx* ctx, const std::string& dir, lbt_config& c) {
@@ -680,8 +739,9 @@ int lbt_model_load(lbt_ctx* ctx, const char* dir, lbt_model** out) {
 void lbt_model_free(lbt_model* m) {
     if (!m) return;
     hipStreamSynchronize(m->ctx->stream);
+    if (m->step_exec) hipGraphExecDestroy(m->step_exec);
     void* bufs[] = {m->wbuf, m->fbuf, m->embed, m->cos_t, m->sin_t, m->x,   m->q,       m->k,
-                    m->v,    m->att,  m->h,     m->logits, m->toks, m->key, m->tok_out};
+                    m->v,    m->att,  m->h,     m->logits, m->toks, m->key, m->tok_out, m->state};
     for (void* b : bufs)
         if (b) hipFree(b);
     delete m;
@@ -791,7 +851,7 @@ int lbt_model_generate_greedy(lbt_model* m, const uint32_t* prompt, size_t n, si
     rc = forward_dev(m, c, m->toks, (int)n, false, false, nullptr);
     if (!rc) {
         hipEventRecord(e1, ctx->stream);
-        for (size_t s = 0; s < steps && !rc; s++) rc = forward_dev(m, c, nullptr, 1, false, false, m->tok_out + s);
+        rc = decode_steps(m, c, (int)steps, 0);
         // the last argmax
         if (!rc) rc = launch_embed(ctx, m->embed, 0, m->cfg.vocab_size, nullptr, m->key, m->tok_out + steps, 1, m->x);
         hipEventRecord(e2, ctx->stream);
@@ -833,7 +893,7 @@ int lbt_model_decode_greedy(lbt_model* m, lbt_cache* c, uint32_t first, size_t s
     LBT_HIP(ctx, hipEventCreate(&e1));
     hipEventRecord(e0, ctx->stream);
     rc = forward_dev(m, c, m->toks, 1, false, false, nullptr);
-    for (size_t s = 1; s < steps && !rc; s++) rc = forward_dev(m, c, nullptr, 1, false, false, m->tok_out + s - 1);
+    if (!rc) rc = decode_steps(m, c, (int)steps - 1, 0);
     if (!rc) rc = launch_embed(ctx, m->embed, 0, m->cfg.vocab_size, nullptr, m->key, m->tok_out + steps - 1, 1, m->x);
     hipEventRecord(e1, ctx->stream);
     hipError_t e = hipStreamSynchronize(ctx->stream);

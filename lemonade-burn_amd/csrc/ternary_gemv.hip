@@ -41,20 +41,14 @@ struct GemvArgs {
     const float* norm_w;
     float eps;
     void* out[3];
+    // kOutQKV: RoPE at positions pos0 + token and bf16 K/V cache append
+    int hd, pos0, cap;
+    const int* pos_dev;  // if set, *pos_dev replaces pos0 (graph-replayed steps)
+    const float* cos_t;
+    const float* sin_t;
+    uint16_t* kc;
+    uint16_t* vc;
 };
-
-// Per-row prep shared by the GEMV prologue and the standalone quantizer:
-// returns the RMSNorm factor r (1 when no norm) and the ActQuant scale.
-// rms_norm (model.rs:267-272): r = 1 / sqrt(sum(x^2)/n + eps), tree256 order.
-__device__ __forceinline__ float norm_factor(const float* xr, int cols, const float* norm_w, float eps,
-                                             float* red) {
-    if (!norm_w) return 1.0f;
-    float p = 0.0f;
-    for (int i = threadIdx.x; i < cols; i += kThreads) p = __builtin_fmaf(xr[i], xr[i], p);
-    float ss = block_tree256(p, red);
-    float mean = ss / (float)cols;
-    return 1.0f / __builtin_sqrtf(mean + eps);
-}
 
 __device__ __forceinline__ float normed(const float* xr, const float* norm_w, float rr, int i) {
     return norm_w ? (xr[i] * rr) * norm_w[i] : xr[i];
@@ -68,7 +62,49 @@ __device__ __forceinline__ float act_scale(const float* xr, int cols, const floa
     return 127.0f / fmaxf(am, 1e-5f);
 }
 
-template <int T, int IN>
+// RMSNorm (optional) + ActQuant of one row into `dst` at positions pos(i);
+// returns s_a and sum(q) through sa/qs (written by thread 0).  Rows of up to
+// 256 * EPT values take one global pass with the values in registers; longer
+// rows re-read x (same arithmetic, same results).
+template <int EPT, typename Pos>
+__device__ __forceinline__ void quantize_row_block(const float* xr, int cols, int kp, const float* norm_w, float eps,
+                                                   int8_t* dst, Pos pos, float* sa, int* qs, float* red) {
+    int s = 0;
+    float scale;
+    if (cols <= EPT * kThreads) {
+        float v[EPT];
+        load_norm_row<EPT>(xr, cols, norm_w, eps, v, red);
+        float am = 0.0f;
+#pragma unroll
+        for (int e = 0; e < EPT; e++) am = fmaxf(am, fabsf(v[e]));
+        am = block_max(am, red);
+        scale = 127.0f / fmaxf(am, 1e-5f);
+#pragma unroll
+        for (int e = 0; e < EPT; e++) {
+            const int i = threadIdx.x + e * kThreads;
+            if (i < kp) {
+                const int qv = i < cols ? quant_one(v[e], scale) : 0;
+                dst[pos(i)] = (int8_t)qv;
+                s += qv;
+            }
+        }
+    } else {
+        const float rr = norm_factor_global(xr, cols, norm_w, eps, red);
+        scale = act_scale(xr, cols, norm_w, rr, red);
+        for (int i = threadIdx.x; i < kp; i += kThreads) {
+            const int qv = i < cols ? quant_one(normed(xr, norm_w, rr, i), scale) : 0;
+            dst[pos(i)] = (int8_t)qv;
+            s += qv;
+        }
+    }
+    s = block_sum_i(s, (int*)red);
+    if (threadIdx.x == 0) {
+        *sa = scale;
+        *qs = s;
+    }
+}
+
+template <int T, int IN, int EPT>
 __device__ __forceinline__ void build_acts(const GemvArgs& a, int t0, int8_t* xq, float* sa, int* qs,
                                            float* red) {
     const int kp = a.kp, C = a.C;
@@ -87,25 +123,36 @@ __device__ __forceinline__ void build_acts(const GemvArgs& a, int t0, int8_t* xq
                 *(int4*)(dst + perm_pos(u << 4, C)) = *(const int4*)(src + (u << 4));
             if (threadIdx.x == 0) { sa[t] = a.qscale ? a.qscale[tok] : 1.0f; qs[t] = a.qsum[tok]; }
         } else {
-            const float* xr = a.x + (size_t)tok * a.cols;
-            const float rr = norm_factor(xr, a.cols, a.norm_w, a.eps, red);
-            const float scale = act_scale(xr, a.cols, a.norm_w, rr, red);
-            int s = 0;
-            for (int i = threadIdx.x; i < kp; i += kThreads) {
-                int qv = i < a.cols ? quant_one(normed(xr, a.norm_w, rr, i), scale) : 0;
-                dst[perm_pos(i, C)] = (int8_t)qv;
-                s += qv;
-            }
-            s = block_sum_i(s, (int*)red);
-            if (threadIdx.x == 0) { sa[t] = scale; qs[t] = s; }
+            quantize_row_block<EPT>(a.x + (size_t)tok * a.cols, a.cols, kp, a.norm_w, a.eps, dst,
+                                    [C](int i) { return perm_pos(i, C); }, &sa[t], &qs[t], red);
         }
     }
 }
 
-__device__ __forceinline__ void resolve_row(const GemvArgs& a, int vr, bool pair, int& mat, int& r) {
-    if (pair) {
+// Virtual row -> (matrix, row).  kOutRelu2 interleaves gate/up rows
+// (2r, 2r+1) = (gate r, up r).  kOutQKV interleaves RoPE partners: for q and
+// k, virtual rows (2p, 2p+1) are rows (d, d + hd/2) of one head; v keeps its
+// order.  Otherwise rows of the matrices follow one another.
+template <int OUT>
+__device__ __forceinline__ void resolve_row(const GemvArgs& a, int vr, int& mat, int& r) {
+    if (OUT == kOutRelu2) {
         mat = vr & 1;
         r = vr >> 1;
+        return;
+    }
+    if (OUT == kOutQKV) {
+        int p = vr >> 1;
+        const int s = vr & 1, h2 = a.hd >> 1;
+        mat = 0;
+        if (p >= a.rows[0] >> 1) {
+            p -= a.rows[0] >> 1;
+            mat = 1;
+            if (p >= a.rows[1] >> 1) {
+                p -= a.rows[1] >> 1;
+                mat = 2;
+            }
+        }
+        r = mat == 2 ? 2 * p + s : (p / h2) * a.hd + (p % h2) + s * h2;
         return;
     }
     mat = 0;
@@ -120,120 +167,163 @@ __device__ __forceinline__ void resolve_row(const GemvArgs& a, int vr, bool pair
     }
 }
 
-template <int L, int T, int NCH, int IN, int OUT>
+template <int R, int T>
+__device__ __forceinline__ int row_dot(const int (&part)[4][R][T], int rr, int t, int qsum) {
+    return part[0][rr][t] + part[1][rr][t] + part[2][rr][t] + part[3][rr][t] - qsum;
+}
+
+template <int R, int T, int OUT>
+__device__ __forceinline__ void epilogue(const GemvArgs& a, int vr0, int t0, const int (&part)[4][R][T],
+                                         const float* sa, const int* qs) {
+    const int tid = threadIdx.x;
+    if (OUT == kOutRelu2 || OUT == kOutQKV) {
+        if (tid >= (R / 2) * T) return;
+        const int p = tid / T, t = tid % T;
+        const int v0 = vr0 + 2 * p, tok = t0 + t;
+        if (v0 >= a.total_rows || tok >= a.m) return;
+        const int d0 = row_dot(part, 2 * p, t, qs[t]);
+        const int d1 = row_dot(part, 2 * p + 1, t, qs[t]);
+        int mat, r0;
+        resolve_row<OUT>(a, v0, mat, r0);
+        const float inv = 1.0f / (sa[t] * a.sw[mat]);
+        const float y0 = (float)d0 * inv;
+        if (OUT == kOutRelu2) {
+            // relu(g)^2 * u (model.rs:363); gate and up have their own scales
+            const float u = (float)d1 * (1.0f / (sa[t] * a.sw[1]));
+            const float rl = y0 > 0.0f ? y0 : 0.0f;
+            ((float*)a.out[0])[(size_t)tok * a.rows[0] + r0] = (rl * rl) * u;
+            return;
+        }
+        const float y1 = (float)d1 * inv;
+        const int pos = (a.pos_dev ? *a.pos_dev : a.pos0) + tok;
+        if (mat == 2) {  // v: bf16 append, rows r0, r0 + 1 of head r0 / hd
+            const int g = r0 / a.hd, d = r0 % a.hd;
+            uint16_t* dst = a.vc + ((size_t)g * a.cap + pos) * a.hd + d;
+            dst[0] = f32_to_bf16(y0);
+            dst[1] = f32_to_bf16(y1);
+            return;
+        }
+        // apply_rope (model.rs:295-301) on the pair (d, d + hd/2)
+        const int h2 = a.hd >> 1, g = r0 / a.hd, d = r0 % a.hd;
+        const float c = a.cos_t[(size_t)pos * h2 + d], sn = a.sin_t[(size_t)pos * h2 + d];
+        const float z0 = y0 * c + (-y1) * sn;
+        const float z1 = y1 * c + y0 * sn;
+        if (mat == 0) {
+            float* q = (float*)a.out[0] + (size_t)tok * a.rows[0];
+            q[r0] = z0;
+            q[r0 + h2] = z1;
+        } else {
+            uint16_t* dst = a.kc + ((size_t)g * a.cap + pos) * a.hd + d;
+            dst[0] = f32_to_bf16(z0);
+            dst[h2] = f32_to_bf16(z1);
+        }
+        return;
+    }
+    if (tid >= R * T) return;
+    const int rr = tid / T, t = tid % T;
+    const int v = vr0 + rr, tok = t0 + t;
+    if (v >= a.total_rows || tok >= a.m) return;
+    int mt, ro;
+    resolve_row<OUT>(a, v, mt, ro);
+    const int dot = row_dot(part, rr, t, qs[t]);
+    const size_t o = (size_t)tok * a.rows[mt] + ro;
+    if (OUT == kOutI32) {
+        ((int32_t*)a.out[mt])[o] = dot;
+    } else {
+        const float y = (float)dot * (1.0f / (sa[t] * a.sw[mt]));
+        float* dst = (float*)a.out[mt];
+        if (OUT == kOutF32Add) dst[o] = dst[o] + y;
+        else dst[o] = y;
+    }
+}
+
+// One workgroup handles TILES consecutive tiles of R rows; all their weight
+// loads are issued before the activation prologue.  Rows longer than one
+// round (NCH * 4 * L chunks) reload per round (TILES == 1 only).
+template <int L, int T, int NCH, int TILES, int IN, int OUT>
 __global__ __launch_bounds__(kThreads) void tgemv_kernel(GemvArgs a) {
     constexpr int R = 64 / L;
     extern __shared__ __align__(16) int8_t xq[];  // T * kp, permuted
-    __shared__ float red[kThreads];
+    __shared__ float red[8];
     __shared__ float sa[T];
     __shared__ int qs[T];
     __shared__ int part[4][R][T];
 
     const int tid = threadIdx.x, w = tid >> 6, ln = tid & 63;
     const int rg = ln / L, j = ln % L;
-    const int vr = blockIdx.x * R + rg;
     const int t0 = blockIdx.y * T;
     const int C = a.C;
-    const bool valid = vr < a.total_rows;
-    int mat, r;
-    resolve_row(a, valid ? vr : 0, OUT == kOutRelu2, mat, r);
-    const uint4* rowp = (const uint4*)(a.w[mat] + (size_t)r * (size_t)(a.kp >> 2));
 
-    // First round of weight loads goes out before the prologue.
-    uint4 wv[NCH];
+    const uint4* rowp[TILES];
+    bool valid[TILES];
+    uint4 wv[TILES][NCH];
 #pragma unroll
-    for (int i = 0; i < NCH; i++) {
-        const int c = (i * 4 + w) * L + j;
-        wv[i] = (valid && c < C) ? rowp[c] : make_uint4(0, 0, 0, 0);
-    }
-
-    build_acts<T, IN>(a, t0, xq, sa, qs, red);
-    __syncthreads();
-
-    int acc[T];
-#pragma unroll
-    for (int t = 0; t < T; t++) acc[t] = 0;
-
-    for (int base = 0;; base += NCH * 4 * L) {
+    for (int k = 0; k < TILES; k++) {
+        const int vr = (blockIdx.x * TILES + k) * R + rg;
+        valid[k] = vr < a.total_rows;
+        int mat, r;
+        resolve_row<OUT>(a, valid[k] ? vr : 0, mat, r);
+        rowp[k] = (const uint4*)(a.w[mat] + (size_t)r * (size_t)(a.kp >> 2));
 #pragma unroll
         for (int i = 0; i < NCH; i++) {
-            const int c = base + (i * 4 + w) * L + j;
-            if (c < C) {
-                const uint32_t d0 = wv[i].x, d1 = wv[i].y, d2 = wv[i].z, d3 = wv[i].w;
+            const int c = (i * 4 + w) * L + j;
+            wv[k][i] = (valid[k] && c < C) ? ld_stream(rowp[k] + c) : make_uint4(0, 0, 0, 0);
+        }
+    }
+
+    build_acts<T, IN, NCH * 8>(a, t0, xq, sa, qs, red);
+    __syncthreads();
+
 #pragma unroll
-                for (int kk = 0; kk < 4; kk++) {
-                    const int off = (kk * C + c) << 4;
-                    const int s = 2 * kk;
-                    const int c0 = (int)((d0 >> s) & 0x03030303u);
-                    const int c1 = (int)((d1 >> s) & 0x03030303u);
-                    const int c2 = (int)((d2 >> s) & 0x03030303u);
-                    const int c3 = (int)((d3 >> s) & 0x03030303u);
+    for (int k = 0; k < TILES; k++) {
+        int acc[T];
 #pragma unroll
-                    for (int t = 0; t < T; t++) {
-                        const int4 xv = *(const int4*)(xq + t * a.kp + off);
-                        int s0 = __builtin_amdgcn_sdot4(c0, xv.x, acc[t], false);
-                        s0 = __builtin_amdgcn_sdot4(c1, xv.y, s0, false);
-                        s0 = __builtin_amdgcn_sdot4(c2, xv.z, s0, false);
-                        acc[t] = __builtin_amdgcn_sdot4(c3, xv.w, s0, false);
+        for (int t = 0; t < T; t++) acc[t] = 0;
+        for (int base = 0;; base += NCH * 4 * L) {
+#pragma unroll
+            for (int i = 0; i < NCH; i++) {
+                const int c = base + (i * 4 + w) * L + j;
+                if (c < C) {
+                    const uint32_t d0 = wv[k][i].x, d1 = wv[k][i].y, d2 = wv[k][i].z, d3 = wv[k][i].w;
+#pragma unroll
+                    for (int kk = 0; kk < 4; kk++) {
+                        const int off = (kk * C + c) << 4;
+                        const int sh = 2 * kk;
+                        const int c0 = (int)((d0 >> sh) & 0x03030303u);
+                        const int c1 = (int)((d1 >> sh) & 0x03030303u);
+                        const int c2 = (int)((d2 >> sh) & 0x03030303u);
+                        const int c3 = (int)((d3 >> sh) & 0x03030303u);
+#pragma unroll
+                        for (int t = 0; t < T; t++) {
+                            const int4 xv = *(const int4*)(xq + t * a.kp + off);
+                            int s0 = __builtin_amdgcn_sdot4(c0, xv.x, acc[t], false);
+                            s0 = __builtin_amdgcn_sdot4(c1, xv.y, s0, false);
+                            s0 = __builtin_amdgcn_sdot4(c2, xv.z, s0, false);
+                            acc[t] = __builtin_amdgcn_sdot4(c3, xv.w, s0, false);
+                        }
                     }
                 }
             }
-        }
-        const int nbase = base + NCH * 4 * L;
-        if (nbase >= C) break;
+            const int nbase = base + NCH * 4 * L;
+            if (TILES > 1 || nbase >= C) break;
 #pragma unroll
-        for (int i = 0; i < NCH; i++) {
-            const int c = nbase + (i * 4 + w) * L + j;
-            wv[i] = (valid && c < C) ? rowp[c] : make_uint4(0, 0, 0, 0);
-        }
-    }
-
-#pragma unroll
-    for (int t = 0; t < T; t++) {
-#pragma unroll
-        for (int o = L / 2; o >= 1; o >>= 1) acc[t] += __shfl_xor(acc[t], o);
-    }
-    if (j == 0) {
-#pragma unroll
-        for (int t = 0; t < T; t++) part[w][rg][t] = acc[t];
-    }
-    __syncthreads();
-
-    if (OUT == kOutRelu2) {
-        if (tid < (R / 2) * T) {
-            const int p = tid / T, t = tid % T;
-            const int vg = blockIdx.x * R + 2 * p;
-            const int tok = t0 + t;
-            if (vg < a.total_rows && tok < a.m) {
-                const int dg = part[0][2 * p][t] + part[1][2 * p][t] + part[2][2 * p][t] + part[3][2 * p][t] - qs[t];
-                const int du = part[0][2 * p + 1][t] + part[1][2 * p + 1][t] + part[2][2 * p + 1][t] +
-                               part[3][2 * p + 1][t] - qs[t];
-                const float g = (float)dg * (1.0f / (sa[t] * a.sw[0]));
-                const float u = (float)du * (1.0f / (sa[t] * a.sw[1]));
-                const float rl = g > 0.0f ? g : 0.0f;
-                ((float*)a.out[0])[(size_t)tok * a.rows[0] + (vg >> 1)] = (rl * rl) * u;
+            for (int i = 0; i < NCH; i++) {
+                const int c = nbase + (i * 4 + w) * L + j;
+                wv[k][i] = (valid[k] && c < C) ? ld_stream(rowp[k] + c) : make_uint4(0, 0, 0, 0);
             }
         }
-        return;
-    }
-    if (tid < R * T) {
-        const int rr = tid / T, t = tid % T;
-        const int v = blockIdx.x * R + rr;
-        const int tok = t0 + t;
-        if (v < a.total_rows && tok < a.m) {
-            int mt, ro;
-            resolve_row(a, v, false, mt, ro);
-            const int dot = part[0][rr][t] + part[1][rr][t] + part[2][rr][t] + part[3][rr][t] - qs[t];
-            const size_t o = (size_t)tok * a.rows[mt] + ro;
-            if (OUT == kOutI32) {
-                ((int32_t*)a.out[mt])[o] = dot;
-            } else {
-                const float y = (float)dot * (1.0f / (sa[t] * a.sw[mt]));
-                float* dst = (float*)a.out[mt];
-                if (OUT == kOutF32Add) dst[o] = dst[o] + y;
-                else dst[o] = y;
-            }
+#pragma unroll
+        for (int t = 0; t < T; t++) {
+#pragma unroll
+            for (int o = L / 2; o >= 1; o >>= 1) acc[t] += __shfl_xor(acc[t], o);
         }
+        if (j == 0) {
+#pragma unroll
+            for (int t = 0; t < T; t++) part[w][rg][t] = acc[t];
+        }
+        __syncthreads();
+        epilogue<R, T, OUT>(a, (blockIdx.x * TILES + k) * R, t0, part, sa, qs);
+        if (k + 1 < TILES) __syncthreads();
     }
 }
 
@@ -242,51 +332,54 @@ __global__ __launch_bounds__(kThreads) void tgemv_kernel(GemvArgs a) {
 __global__ __launch_bounds__(kThreads) void quantize_kernel(const float* x, const float* norm_w, float eps,
                                                             int k, int kp, int8_t* q, float* scale,
                                                             int32_t* sum) {
-    __shared__ float red[kThreads];
+    __shared__ float red[8];
     const int row = blockIdx.x;
-    const float* xr = x + (size_t)row * k;
-    const float rr = norm_factor(xr, k, norm_w, eps, red);
-    const float s = act_scale(xr, k, norm_w, rr, red);
-    int acc = 0;
-    for (int i = threadIdx.x; i < kp; i += kThreads) {
-        int qv = i < k ? quant_one(normed(xr, norm_w, rr, i), s) : 0;
-        q[(size_t)row * kp + i] = (int8_t)qv;
-        acc += qv;
-    }
-    acc = block_sum_i(acc, (int*)red);
-    if (threadIdx.x == 0) {
-        scale[row] = s;
-        sum[row] = acc;
-    }
+    quantize_row_block<32>(x + (size_t)row * k, k, kp, norm_w, eps, q + (size_t)row * kp, [](int i) { return i; },
+                           &scale[row], &sum[row], red);
 }
 
 namespace {
 
 constexpr int kL = 8;
 
-template <int T, int NCH, int IN>
+template <int T, int NCH, int TILES, int IN>
 hipError_t launch_out(const GemvArgs& a, int out_mode, dim3 grid, size_t lds, hipStream_t s) {
     switch (out_mode) {
         case kOutI32:
-            hipLaunchKernelGGL((tgemv_kernel<kL, T, NCH, IN, kOutI32>), grid, dim3(kThreads), lds, s, a);
+            hipLaunchKernelGGL((tgemv_kernel<kL, T, NCH, TILES, IN, kOutI32>), grid, dim3(kThreads), lds, s, a);
             break;
         case kOutF32:
-            hipLaunchKernelGGL((tgemv_kernel<kL, T, NCH, IN, kOutF32>), grid, dim3(kThreads), lds, s, a);
+            hipLaunchKernelGGL((tgemv_kernel<kL, T, NCH, TILES, IN, kOutF32>), grid, dim3(kThreads), lds, s, a);
             break;
         case kOutF32Add:
-            hipLaunchKernelGGL((tgemv_kernel<kL, T, NCH, IN, kOutF32Add>), grid, dim3(kThreads), lds, s, a);
+            hipLaunchKernelGGL((tgemv_kernel<kL, T, NCH, TILES, IN, kOutF32Add>), grid, dim3(kThreads), lds, s, a);
+            break;
+        case kOutRelu2:
+            hipLaunchKernelGGL((tgemv_kernel<kL, T, NCH, TILES, IN, kOutRelu2>), grid, dim3(kThreads), lds, s, a);
             break;
         default:
-            hipLaunchKernelGGL((tgemv_kernel<kL, T, NCH, IN, kOutRelu2>), grid, dim3(kThreads), lds, s, a);
+            hipLaunchKernelGGL((tgemv_kernel<kL, T, NCH, TILES, IN, kOutQKV>), grid, dim3(kThreads), lds, s, a);
             break;
     }
     return hipGetLastError();
 }
 
-template <int T, int NCH>
+template <int T, int NCH, int TILES>
 hipError_t launch_in(const GemvArgs& a, int in_mode, int out_mode, dim3 grid, size_t lds, hipStream_t s) {
-    return in_mode == kInPreQ ? launch_out<T, NCH, kInPreQ>(a, out_mode, grid, lds, s)
-                              : launch_out<T, NCH, kInF32>(a, out_mode, grid, lds, s);
+    return in_mode == kInPreQ ? launch_out<T, NCH, TILES, kInPreQ>(a, out_mode, grid, lds, s)
+                              : launch_out<T, NCH, TILES, kInF32>(a, out_mode, grid, lds, s);
+}
+
+template <int T>
+hipError_t launch_t(const GemvArgs& a, int nch, int tiles, int in_mode, int out_mode, dim3 grid, size_t lds,
+                    hipStream_t s) {
+    if (nch == 2) {
+        if (tiles == 4) return launch_in<T, 2, 4>(a, in_mode, out_mode, grid, lds, s);
+        if (tiles == 2) return launch_in<T, 2, 2>(a, in_mode, out_mode, grid, lds, s);
+        return launch_in<T, 2, 1>(a, in_mode, out_mode, grid, lds, s);
+    }
+    if (tiles == 2) return launch_in<T, 4, 2>(a, in_mode, out_mode, grid, lds, s);
+    return launch_in<T, 4, 1>(a, in_mode, out_mode, grid, lds, s);
 }
 
 }  // namespace
@@ -299,6 +392,9 @@ int launch_ternary_gemv(lbt_ctx* ctx, const TernaryOp& op) {
         return set_err(ctx, LBT_E_INVALID, "ternary: gate/up fusion needs two matrices of equal rows");
     if (op.out_mode == kOutF32Add && nmat != 1)
         return set_err(ctx, LBT_E_INVALID, "ternary: residual epilogue takes one matrix");
+    if (op.out_mode == kOutQKV &&
+        (nmat != 3 || op.hd <= 0 || op.hd % 2 || op.rows[0] % op.hd || op.rows[1] % op.hd || op.rows[1] != op.rows[2]))
+        return set_err(ctx, LBT_E_INVALID, "ternary: q/k/v fusion needs head-aligned q, k, v");
     int total = 0;
     for (int i = 0; i < 3; i++) {
         a.w[i] = i < nmat ? op.w[i] : op.w[0];
@@ -318,24 +414,34 @@ int launch_ternary_gemv(lbt_ctx* ctx, const TernaryOp& op) {
     a.x = op.x;
     a.norm_w = op.norm_w;
     a.eps = op.eps;
+    a.hd = op.hd;
+    a.pos0 = op.pos0;
+    a.pos_dev = op.pos_dev;
+    a.cap = op.cap;
+    a.cos_t = op.cos_t;
+    a.sin_t = op.sin_t;
+    a.kc = op.kc;
+    a.vc = op.vc;
     constexpr int R = 64 / kL;
     const int T = op.m == 1 ? 1 : 4;
     const int per_lane = (a.C + 4 * kL - 1) / (4 * kL);
     const int nch = per_lane <= 2 ? 2 : 4;
-    dim3 grid((unsigned)((total + R - 1) / R), (unsigned)((op.m + T - 1) / T));
+    const int ntiles = (total + R - 1) / R;
+    // several tiles per workgroup amortise the activation prologue once the
+    // grid already covers the chip (rows > 1 round only with one tile)
+    int tiles = 1;
+    if (per_lane <= 4) {
+        while (tiles < (nch == 2 ? 4 : 2) && ntiles / (tiles * 2) >= 384) tiles *= 2;
+    }
+    dim3 grid((unsigned)((ntiles + tiles - 1) / tiles), (unsigned)((op.m + T - 1) / T));
     const size_t lds = (size_t)T * a.kp;
     if (lds > 64 * 1024) return set_err(ctx, LBT_E_INVALID, "ternary: activation image exceeds LDS budget");
     hipEvent_t ev = nullptr;
     prof_begin(ctx, &ev);
-    hipError_t e;
-    if (T == 1)
-        e = nch == 2 ? launch_in<1, 2>(a, op.in_mode, op.out_mode, grid, lds, ctx->stream)
-                     : launch_in<1, 4>(a, op.in_mode, op.out_mode, grid, lds, ctx->stream);
-    else
-        e = nch == 2 ? launch_in<4, 2>(a, op.in_mode, op.out_mode, grid, lds, ctx->stream)
-                     : launch_in<4, 4>(a, op.in_mode, op.out_mode, grid, lds, ctx->stream);
+    hipError_t e = T == 1 ? launch_t<1>(a, nch, tiles, op.in_mode, op.out_mode, grid, lds, ctx->stream)
+                          : launch_t<4>(a, nch, tiles, op.in_mode, op.out_mode, grid, lds, ctx->stream);
     if (e != hipSuccess) return hip_err(ctx, e, "tgemv_kernel launch");
-    const double bytes = (double)total * (a.kp / 4);
+    const double bytes = (double)total * (a.kp / 4) + (double)op.m * op.cols * 4.0;
     prof_end(ctx, ev, kProfGemv, bytes);
     return LBT_OK;
 }

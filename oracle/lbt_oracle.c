@@ -254,16 +254,21 @@ void or_bf16_gemv_lanes(const uint16_t* w, size_t rows, size_t cols, const float
 /* device-order float building blocks                                        */
 /* ------------------------------------------------------------------------ */
 
-/* 256 partials reduced in LDS: p[t] += p[t + s] for s = 128, 64, ..., 1. */
-float or_tree256(const float* partials) {
-    float p[256];
-    memcpy(p, partials, sizeof(p));
-    for (int s = 128; s >= 1; s >>= 1)
-        for (int t = 0; t < s; t++) p[t] = p[t] + p[t + s];
-    return p[0];
+/* Block sum of 256 per-thread partials as the device reduces them: each
+ * wavefront of 64 reduces with the xor butterfly, then the four wave sums are
+ * added as (w0 + w1) + (w2 + w3). */
+float or_block_sum256(const float* partials) {
+    float w[4];
+    for (int k = 0; k < 4; k++) {
+        float v[64];
+        memcpy(v, partials + 64 * k, sizeof(v));
+        w[k] = butterfly64(v);
+    }
+    return (w[0] + w[1]) + (w[2] + w[3]);
 }
 
-/* Thread t of 256 accumulates x[i]^2 (fma) over i = t, t+256, ... ascending. */
+/* Thread t of 256 accumulates x[i]^2 (fma) over i = t, t+256, ... ascending,
+ * then the block sum above. */
 float or_sumsq256(const float* x, size_t n) {
     float p[256];
     for (int t = 0; t < 256; t++) {
@@ -271,7 +276,7 @@ float or_sumsq256(const float* x, size_t n) {
         for (size_t i = (size_t)t; i < n; i += 256) a = fmaf(x[i], x[i], a);
         p[t] = a;
     }
-    return or_tree256(p);
+    return or_block_sum256(p);
 }
 
 /* rms_norm (model.rs:267-272): x * (mean(x^2) + eps).sqrt().recip() * w */
@@ -527,6 +532,57 @@ static void linear(const or_model* m, const float* x, size_t n, size_t k, int la
     free(q); free(sa); free(qs); free(d);
 }
 
+/* xor butterfly over n values (n a power of two): step m = n/2 .. 1 adds
+ * v[l ^ m] to v[l]; returns v[0]. */
+static float butterfly_n(float* v, int n) {
+    float t[64];
+    for (int m = n / 2; m >= 1; m >>= 1) {
+        for (int l = 0; l < n; l++) t[l] = v[l] + v[l ^ m];
+        memcpy(v, t, (size_t)n * sizeof(float));
+    }
+    return v[0];
+}
+
+/* q.k in the device order: LK = hd/8 lanes, lane c sums dims 8c..8c+7 by
+ * fused multiply-adds, lanes combine by butterfly_n. */
+static float attn_score(const float* q, const uint16_t* k, size_t hd) {
+    int lk = (int)(hd / 8);
+    float part[64];
+    for (int c = 0; c < lk; c++) {
+        float a = 0.0f;
+        for (int e = 0; e < 8; e++) a = fmaf(q[8 * c + e], or_bf16_to_f32(k[8 * c + e]), a);
+        part[c] = a;
+    }
+    return butterfly_n(part, lk);
+}
+
+/* probs @ V in the device order: 256/LK key groups, group g accumulates keys
+ * j = g, g + 256/LK, ... by fused multiply-adds; the 64/LK groups of each
+ * wavefront combine by xor over the group index (m = 1, 2, ...), then the four
+ * wave sums as (w0 + w1) + (w2 + w3). */
+static void attn_pv(const float* p, const uint16_t* V, size_t vis, size_t hd, float* out) {
+    int lk = (int)(hd / 8), gw = 64 / lk, ng = 256 / lk;
+    float acc[256];
+    for (size_t d = 0; d < hd; d++) {
+        for (int g = 0; g < ng; g++) {
+            float a = 0.0f;
+            for (size_t j = (size_t)g; j < vis; j += (size_t)ng) a = fmaf(p[j], or_bf16_to_f32(V[j * hd + d]), a);
+            acc[g] = a;
+        }
+        float wsum[4];
+        for (int w = 0; w < 4; w++) {
+            float v[64], t[64];
+            memcpy(v, acc + w * gw, (size_t)gw * sizeof(float));
+            for (int m = 1; m < gw; m <<= 1) {
+                for (int l = 0; l < gw; l++) t[l] = v[l] + v[l ^ m];
+                memcpy(v, t, (size_t)gw * sizeof(float));
+            }
+            wsum[w] = v[0];
+        }
+        out[d] = (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
+    }
+}
+
 /* apply_rope (model.rs:295-301): x*cos + rot*sin, rot = cat(-x2, x1). */
 static void rope(float* v, size_t hd, const float* c, const float* s) {
     size_t h2 = hd / 2;
@@ -594,9 +650,7 @@ int or_model_forward(or_model* m, const uint32_t* tokens, size_t n, int all_logi
                 const uint16_t* Vh = V + (h / group) * cap * hd;
                 float mx = -INFINITY;
                 for (size_t j = 0; j < vis; j++) {
-                    float a = 0.0f;
-                    for (size_t d = 0; d < hd; d++) a = fmaf(qh[d], or_bf16_to_f32(Kh[j * hd + d]), a);
-                    e[j] = a * scaling;
+                    e[j] = attn_score(qh, Kh + j * hd, hd) * scaling;
                     mx = fmaxf(mx, e[j]);
                 }
                 float part[256];
@@ -605,13 +659,9 @@ int or_model_forward(or_model* m, const uint32_t* tokens, size_t n, int all_logi
                     for (size_t j = (size_t)th; j < vis; j += 256) s = s + or_expf(e[j] - mx);
                     part[th] = s;
                 }
-                float sum = or_tree256(part);
+                float sum = or_block_sum256(part);
                 for (size_t j = 0; j < vis; j++) e[j] = or_expf(e[j] - mx) / sum;
-                for (size_t d = 0; d < hd; d++) {
-                    float a = 0.0f;
-                    for (size_t j = 0; j < vis; j++) a = fmaf(e[j], or_bf16_to_f32(Vh[j * hd + d]), a);
-                    att[t * H + h * hd + d] = a;
-                }
+                attn_pv(e, Vh, vis, hd, att + t * H + h * hd);
             }
         }
         for (size_t t = 0; t < n; t++) or_rmsnorm(att + t * H, nw[2], H, eps, nrm + t * H);

@@ -61,8 +61,8 @@ float or_bf16_dot_lanes(const uint16_t* w, const float* x, size_t n);
 void or_bf16_gemv_lanes(const uint16_t* w, size_t rows, size_t cols, const float* x, float* out);
 
 /* ---- float building blocks in the device order ------------------------- */
-float or_tree256(const float* partials);                      /* LDS tree over 256 slots */
-float or_sumsq256(const float* x, size_t n);                  /* strided fma partials + tree */
+float or_block_sum256(const float* partials);                 /* wave butterflies, then (w0+w1)+(w2+w3) */
+float or_sumsq256(const float* x, size_t n);                  /* strided fma partials + block sum */
 /* rms_norm (crates/lb-model/src/model.rs:267-272): x * (mean(x^2)+eps).sqrt().recip() * w */
 void or_rmsnorm(const float* x, const float* w, size_t n, float eps, float* out);
 float or_expf(float x);                                       /* Cody-Waite + Taylor(7) */

@@ -194,3 +194,45 @@ def test_full_2b_prompt64_decode_matches_oracle(ctx):
     finally:
         orc.set_fast(old)
     m.free()
+
+
+def test_graph_decode_replays_match_eager_and_oracle(ctx, monkeypatch):
+    """Decode steps run as a replayed HIP graph; replays interleaved with eager
+    forwards and a cache regrowth (re-capture) give the oracle's tokens, and
+    the same tokens as the eager path (LBT_NO_GRAPH)."""
+    hip_cfg, or_cfg = cfgs(layers=1)
+    announce("graph decode replays")
+    m = lbt_hip.Model.synthetic(ctx, hip_cfg, 12)
+    om = orc.OracleModel(or_cfg, 12)
+    prompt = np.array([4, 8, 15, 16, 23, 42], np.uint32)
+
+    def oracle_run(first, steps):
+        out, tok = [], first
+        for _ in range(steps):
+            tok = int(om.forward([tok])[0].argmax())
+            out.append(tok)
+        return out
+
+    cache = m.new_cache()
+    first = m.forward_argmax(prompt, cache)
+    assert first == int(om.forward(prompt)[0].argmax())
+    toks, _ = m.decode_greedy(cache, first, 12)
+    assert list(toks) == oracle_run(first, 12)
+    # eager forward between graph replays
+    g = m.forward([int(toks[-1])], cache)
+    e = om.forward([int(toks[-1])])
+    assert np.array_equal(g, e)
+    nxt = int(e[0].argmax())
+    # crosses the 256-position capacity: the cache grows and the step is re-captured
+    toks2, _ = m.decode_greedy(cache, nxt, 250)
+    assert list(toks2) == oracle_run(nxt, 250)
+    assert len(cache) == len(prompt) + 12 + 1 + 250
+    cache.free()
+    c2 = m.new_cache()
+    monkeypatch.setenv("LBT_NO_GRAPH", "1")
+    f2 = m.forward_argmax(prompt, c2)
+    t_eager, _ = m.decode_greedy(c2, f2, 12)
+    assert list(t_eager) == list(toks)
+    c2.free()
+    m.free()
+    om.free()
