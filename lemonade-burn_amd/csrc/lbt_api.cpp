@@ -144,6 +144,7 @@ void lbt_ctx_destroy(lbt_ctx* ctx) {
     }
     for (auto e : ctx->free_events) hipEventDestroy(e);
     if (ctx->ws) hipFree(ctx->ws);
+    if (ctx->qws) hipFree(ctx->qws);
     hipStreamDestroy(ctx->stream);
     delete ctx;
 }

@@ -26,6 +26,9 @@ struct lbt_ctx {
     std::vector<Pending> pending;
     std::vector<hipEvent_t> free_events;
     lbt_prof acc{};
+    // grow-only device scratch of the prefill GEMM (quantized activations)
+    void* qws = nullptr;
+    size_t qws_bytes = 0;
 };
 
 struct lbt_weight {
@@ -94,6 +97,7 @@ struct TernaryOp {
     uint16_t* vc = nullptr;
 };
 // Dispatches decode GEMV (small m) or the int8-MFMA prefill GEMM (large m).
+constexpr int kMfmaMinTokens = 16;
 int launch_ternary(lbt_ctx* ctx, const TernaryOp& op);
 int launch_ternary_gemv(lbt_ctx* ctx, const TernaryOp& op);
 int launch_ternary_mfma(lbt_ctx* ctx, const TernaryOp& op);

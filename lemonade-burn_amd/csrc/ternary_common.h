@@ -1,0 +1,132 @@
+// ternary_common.h -- shared by the ternary decode GEMV and the int8-MFMA
+// prefill GEMM: kernel arguments, the virtual-row mapping of the fused
+// matrices, and the output epilogues, so both kernels write identical values.
+#pragma once
+#include "lbt_device.h"
+#include "lbt_internal.h"
+
+namespace lbt {
+
+struct GemvArgs {
+    const uint8_t* w[3];
+    int rows[3];
+    float sw[3];
+    int total_rows;  // virtual rows (2*rows for the gate/up interleave)
+    int cols, kp, C;
+    int m;
+    const int8_t* q;
+    const float* qscale;
+    const int32_t* qsum;
+    const float* x;
+    const float* norm_w;
+    float eps;
+    void* out[3];
+    // kOutQKV: RoPE at positions pos0 + token and bf16 K/V cache append
+    int hd, pos0, cap;
+    const int* pos_dev;  // if set, *pos_dev replaces pos0 (graph-replayed steps)
+    const float* cos_t;
+    const float* sin_t;
+    uint16_t* kc;
+    uint16_t* vc;
+};
+
+// Virtual row -> (matrix, row).  kOutRelu2 interleaves gate/up rows
+// (2r, 2r+1) = (gate r, up r).  kOutQKV interleaves RoPE partners: for q and
+// k, virtual rows (2p, 2p+1) are rows (d, d + hd/2) of one head; v keeps its
+// order.  Otherwise rows of the matrices follow one another.
+template <int OUT>
+__device__ __forceinline__ void resolve_row(const GemvArgs& a, int vr, int& mat, int& r) {
+    if (OUT == kOutRelu2) {
+        mat = vr & 1;
+        r = vr >> 1;
+        return;
+    }
+    if (OUT == kOutQKV) {
+        int p = vr >> 1;
+        const int s = vr & 1, h2 = a.hd >> 1;
+        mat = 0;
+        if (p >= a.rows[0] >> 1) {
+            p -= a.rows[0] >> 1;
+            mat = 1;
+            if (p >= a.rows[1] >> 1) {
+                p -= a.rows[1] >> 1;
+                mat = 2;
+            }
+        }
+        r = mat == 2 ? 2 * p + s : (p / h2) * a.hd + (p % h2) + s * h2;
+        return;
+    }
+    mat = 0;
+    r = vr;
+    if (r >= a.rows[0]) {
+        r -= a.rows[0];
+        mat = 1;
+        if (r >= a.rows[1]) {
+            r -= a.rows[1];
+            mat = 2;
+        }
+    }
+}
+
+// Output of one (token, virtual row) for the unpaired modes:
+// i32 dot; f32 y = dot * (1/(s_a*s_w)) (gemm.rs:141,150); or the residual
+// x += y (model.rs:359,365).
+template <int OUT>
+__device__ __forceinline__ void store_single(const GemvArgs& a, int tok, int v, int dot, float sa) {
+    int mt, ro;
+    resolve_row<OUT>(a, v, mt, ro);
+    const size_t o = (size_t)tok * a.rows[mt] + ro;
+    if (OUT == kOutI32) {
+        ((int32_t*)a.out[mt])[o] = dot;
+    } else {
+        const float y = (float)dot * (1.0f / (sa * a.sw[mt]));
+        float* dst = (float*)a.out[mt];
+        if (OUT == kOutF32Add) dst[o] = dst[o] + y;
+        else dst[o] = y;
+    }
+}
+
+// Output of the virtual-row pair (v0, v0 + 1) for the paired modes:
+// kOutRelu2: relu(gate)^2 * up (model.rs:362-363);
+// kOutQKV:   q/k get apply_rope (model.rs:295-301) at position pos + tok, q is
+//            stored f32, k and v are rounded to bf16 into the cache.
+template <int OUT>
+__device__ __forceinline__ void store_pair(const GemvArgs& a, int tok, int v0, int d0, int d1, float sa) {
+    int mat, r0;
+    resolve_row<OUT>(a, v0, mat, r0);
+    const float inv = 1.0f / (sa * a.sw[mat]);
+    const float y0 = (float)d0 * inv;
+    if (OUT == kOutRelu2) {
+        const float u = (float)d1 * (1.0f / (sa * a.sw[1]));
+        const float rl = y0 > 0.0f ? y0 : 0.0f;
+        ((float*)a.out[0])[(size_t)tok * a.rows[0] + r0] = (rl * rl) * u;
+        return;
+    }
+    const float y1 = (float)d1 * inv;
+    const int pos = (a.pos_dev ? *a.pos_dev : a.pos0) + tok;
+    if (mat == 2) {  // v: rows r0, r0 + 1 of head r0 / hd
+        const int g = r0 / a.hd, d = r0 % a.hd;
+        uint16_t* dst = a.vc + ((size_t)g * a.cap + pos) * a.hd + d;
+        dst[0] = f32_to_bf16(y0);
+        dst[1] = f32_to_bf16(y1);
+        return;
+    }
+    const int h2 = a.hd >> 1, g = r0 / a.hd, d = r0 % a.hd;
+    const float c = a.cos_t[(size_t)pos * h2 + d], sn = a.sin_t[(size_t)pos * h2 + d];
+    const float z0 = y0 * c + (-y1) * sn;
+    const float z1 = y1 * c + y0 * sn;
+    if (mat == 0) {
+        float* q = (float*)a.out[0] + (size_t)tok * a.rows[0];
+        q[r0] = z0;
+        q[r0 + h2] = z1;
+    } else {
+        uint16_t* dst = a.kc + ((size_t)g * a.cap + pos) * a.hd + d;
+        dst[0] = f32_to_bf16(z0);
+        dst[h2] = f32_to_bf16(z1);
+    }
+}
+
+// Fills GemvArgs from a TernaryOp (shared host-side setup).
+int make_gemv_args(lbt_ctx* ctx, const TernaryOp& op, GemvArgs& a);
+
+}  // namespace lbt

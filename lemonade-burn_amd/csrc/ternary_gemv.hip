@@ -24,31 +24,12 @@
 //     gate/up rows (model.rs:362-363).
 #include "lbt_device.h"
 #include "lbt_internal.h"
+#include "ternary_common.h"
+
+#include <stdlib.h>
 
 namespace lbt {
 
-struct GemvArgs {
-    const uint8_t* w[3];
-    int rows[3];
-    float sw[3];
-    int total_rows;  // virtual rows (2*rows for the gate/up interleave)
-    int cols, kp, C;
-    int m;
-    const int8_t* q;
-    const float* qscale;
-    const int32_t* qsum;
-    const float* x;
-    const float* norm_w;
-    float eps;
-    void* out[3];
-    // kOutQKV: RoPE at positions pos0 + token and bf16 K/V cache append
-    int hd, pos0, cap;
-    const int* pos_dev;  // if set, *pos_dev replaces pos0 (graph-replayed steps)
-    const float* cos_t;
-    const float* sin_t;
-    uint16_t* kc;
-    uint16_t* vc;
-};
 
 __device__ __forceinline__ float normed(const float* xr, const float* norm_w, float rr, int i) {
     return norm_w ? (xr[i] * rr) * norm_w[i] : xr[i];
@@ -129,44 +110,6 @@ __device__ __forceinline__ void build_acts(const GemvArgs& a, int t0, int8_t* xq
     }
 }
 
-// Virtual row -> (matrix, row).  kOutRelu2 interleaves gate/up rows
-// (2r, 2r+1) = (gate r, up r).  kOutQKV interleaves RoPE partners: for q and
-// k, virtual rows (2p, 2p+1) are rows (d, d + hd/2) of one head; v keeps its
-// order.  Otherwise rows of the matrices follow one another.
-template <int OUT>
-__device__ __forceinline__ void resolve_row(const GemvArgs& a, int vr, int& mat, int& r) {
-    if (OUT == kOutRelu2) {
-        mat = vr & 1;
-        r = vr >> 1;
-        return;
-    }
-    if (OUT == kOutQKV) {
-        int p = vr >> 1;
-        const int s = vr & 1, h2 = a.hd >> 1;
-        mat = 0;
-        if (p >= a.rows[0] >> 1) {
-            p -= a.rows[0] >> 1;
-            mat = 1;
-            if (p >= a.rows[1] >> 1) {
-                p -= a.rows[1] >> 1;
-                mat = 2;
-            }
-        }
-        r = mat == 2 ? 2 * p + s : (p / h2) * a.hd + (p % h2) + s * h2;
-        return;
-    }
-    mat = 0;
-    r = vr;
-    if (r >= a.rows[0]) {
-        r -= a.rows[0];
-        mat = 1;
-        if (r >= a.rows[1]) {
-            r -= a.rows[1];
-            mat = 2;
-        }
-    }
-}
-
 template <int R, int T>
 __device__ __forceinline__ int row_dot(const int (&part)[4][R][T], int rr, int t, int qsum) {
     return part[0][rr][t] + part[1][rr][t] + part[2][rr][t] + part[3][rr][t] - qsum;
@@ -181,60 +124,14 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, int vr0, int t0, con
         const int p = tid / T, t = tid % T;
         const int v0 = vr0 + 2 * p, tok = t0 + t;
         if (v0 >= a.total_rows || tok >= a.m) return;
-        const int d0 = row_dot(part, 2 * p, t, qs[t]);
-        const int d1 = row_dot(part, 2 * p + 1, t, qs[t]);
-        int mat, r0;
-        resolve_row<OUT>(a, v0, mat, r0);
-        const float inv = 1.0f / (sa[t] * a.sw[mat]);
-        const float y0 = (float)d0 * inv;
-        if (OUT == kOutRelu2) {
-            // relu(g)^2 * u (model.rs:363); gate and up have their own scales
-            const float u = (float)d1 * (1.0f / (sa[t] * a.sw[1]));
-            const float rl = y0 > 0.0f ? y0 : 0.0f;
-            ((float*)a.out[0])[(size_t)tok * a.rows[0] + r0] = (rl * rl) * u;
-            return;
-        }
-        const float y1 = (float)d1 * inv;
-        const int pos = (a.pos_dev ? *a.pos_dev : a.pos0) + tok;
-        if (mat == 2) {  // v: bf16 append, rows r0, r0 + 1 of head r0 / hd
-            const int g = r0 / a.hd, d = r0 % a.hd;
-            uint16_t* dst = a.vc + ((size_t)g * a.cap + pos) * a.hd + d;
-            dst[0] = f32_to_bf16(y0);
-            dst[1] = f32_to_bf16(y1);
-            return;
-        }
-        // apply_rope (model.rs:295-301) on the pair (d, d + hd/2)
-        const int h2 = a.hd >> 1, g = r0 / a.hd, d = r0 % a.hd;
-        const float c = a.cos_t[(size_t)pos * h2 + d], sn = a.sin_t[(size_t)pos * h2 + d];
-        const float z0 = y0 * c + (-y1) * sn;
-        const float z1 = y1 * c + y0 * sn;
-        if (mat == 0) {
-            float* q = (float*)a.out[0] + (size_t)tok * a.rows[0];
-            q[r0] = z0;
-            q[r0 + h2] = z1;
-        } else {
-            uint16_t* dst = a.kc + ((size_t)g * a.cap + pos) * a.hd + d;
-            dst[0] = f32_to_bf16(z0);
-            dst[h2] = f32_to_bf16(z1);
-        }
+        store_pair<OUT>(a, tok, v0, row_dot(part, 2 * p, t, qs[t]), row_dot(part, 2 * p + 1, t, qs[t]), sa[t]);
         return;
     }
     if (tid >= R * T) return;
     const int rr = tid / T, t = tid % T;
     const int v = vr0 + rr, tok = t0 + t;
     if (v >= a.total_rows || tok >= a.m) return;
-    int mt, ro;
-    resolve_row<OUT>(a, v, mt, ro);
-    const int dot = row_dot(part, rr, t, qs[t]);
-    const size_t o = (size_t)tok * a.rows[mt] + ro;
-    if (OUT == kOutI32) {
-        ((int32_t*)a.out[mt])[o] = dot;
-    } else {
-        const float y = (float)dot * (1.0f / (sa[t] * a.sw[mt]));
-        float* dst = (float*)a.out[mt];
-        if (OUT == kOutF32Add) dst[o] = dst[o] + y;
-        else dst[o] = y;
-    }
+    store_single<OUT>(a, tok, v, row_dot(part, rr, t, qs[t]), sa[t]);
 }
 
 // One workgroup handles TILES consecutive tiles of R rows; all their weight
@@ -384,8 +281,8 @@ hipError_t launch_t(const GemvArgs& a, int nch, int tiles, int in_mode, int out_
 
 }  // namespace
 
-int launch_ternary_gemv(lbt_ctx* ctx, const TernaryOp& op) {
-    GemvArgs a{};
+int make_gemv_args(lbt_ctx* ctx, const TernaryOp& op, GemvArgs& a) {
+    a = GemvArgs{};
     const int nmat = op.nmat;
     if (nmat < 1 || nmat > 3 || op.cols <= 0 || op.m <= 0) return set_err(ctx, LBT_E_INVALID, "ternary: bad shape");
     if (op.out_mode == kOutRelu2 && (nmat != 2 || op.rows[0] != op.rows[1]))
@@ -422,6 +319,14 @@ int launch_ternary_gemv(lbt_ctx* ctx, const TernaryOp& op) {
     a.sin_t = op.sin_t;
     a.kc = op.kc;
     a.vc = op.vc;
+    return LBT_OK;
+}
+
+int launch_ternary_gemv(lbt_ctx* ctx, const TernaryOp& op) {
+    GemvArgs a;
+    int rc = make_gemv_args(ctx, op, a);
+    if (rc) return rc;
+    const int total = a.total_rows;
     constexpr int R = 64 / kL;
     const int T = op.m == 1 ? 1 : 4;
     const int per_lane = (a.C + 4 * kL - 1) / (4 * kL);
@@ -456,7 +361,9 @@ int launch_quantize(lbt_ctx* ctx, const float* x, const float* norm_w, float eps
     return LBT_OK;
 }
 
+// Decode GEMV for a few tokens, the int8-MFMA GEMM from kMfmaMinTokens up.
 int launch_ternary(lbt_ctx* ctx, const TernaryOp& op) {
+    if (op.m >= kMfmaMinTokens && !getenv("LBT_NO_MFMA")) return launch_ternary_mfma(ctx, op);
     return launch_ternary_gemv(ctx, op);
 }
 

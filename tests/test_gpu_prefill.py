@@ -1,0 +1,95 @@
+"""Prefill GEMM on the int8 matrix cores (v_mfma_i32_16x16x64_i8): exact
+integers and bit-identical f32 outputs vs the oracle at BASELINE config 3
+(FFN shapes 2560->6912 and 6912->2560 at M = 128, 512, 2048), ragged tiles,
+the reference's prefill overflow case, and the model prefill through the
+MFMA path equal to the decode GEMV path."""
+import numpy as np
+import pytest
+
+import lbt_hip
+import lbt_oracle as orc
+from conftest import announce
+from refgen import golden_case, ternary_iid
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("rows,cols", [(6912, 2560), (2560, 6912)])
+@pytest.mark.parametrize("m", [128, 512, 2048])
+def test_config3_ffn_shapes_bitexact(ctx, rows, cols, m):
+    announce(f"prefill {rows}x{cols} m={m}")
+    rng = np.random.default_rng(rows + cols + m)
+    t = ternary_iid(rng, rows, cols)
+    p = orc.pack(t)
+    x = rng.standard_normal((m, cols)).astype(np.float32)
+    q, sa, su = orc.quantize_acts(x)
+    sw = float(np.float32(1.7))
+    w = ctx.upload(p, rows, cols, sw)
+    d = orc.port_gemm_i32(p, rows, cols, q, su)
+    assert np.array_equal(ctx.gemm_i32(w, q, su), d)
+    (y,) = ctx.ternary_linear([w], x)
+    inv = (np.float32(1.0) / (sa * np.float32(sw))).astype(np.float32)
+    assert np.array_equal(y, (d.astype(np.float32) * inv[:, None]).astype(np.float32))
+    w.free()
+
+
+@pytest.mark.parametrize("rows,cols,m", [(23, 384, 17), (37, 2560, 33), (130, 300, 65), (5, 129, 16), (100, 1000, 200)])
+def test_ragged_tiles(ctx, rows, cols, m):
+    announce(f"prefill ragged {rows}x{cols} m={m}")
+    t, scale, x = golden_case(rows, cols, m, rows + cols + m)
+    p = orc.pack(t)
+    q, sa, su = orc.quantize_acts(x)
+    w = ctx.upload(p, rows, cols, float(scale))
+    assert np.array_equal(ctx.gemm_i32(w, q, su), q[:, :cols].astype(np.int64) @ t.T.astype(np.int64))
+    (y,) = ctx.ternary_linear([w], x)
+    assert np.array_equal(y, orc.gemm_f32(p, rows, cols, scale, q, sa, su))
+    w.free()
+
+
+def test_prefill_extreme_long_rows_mfma(ctx):
+    # golden.rs:181-194 at an MFMA-sized token count
+    rows, cols, m = 3, 6912 * 2, 32
+    announce("prefill extreme")
+    w = ctx.upload(orc.pack(np.ones((rows, cols), np.int8)), rows, cols, 1.0)
+    for sign in (1.0, -1.0):
+        x = np.full((m, cols), sign, np.float32)
+        q, sa, su = ctx.quantize_acts(x)
+        assert np.all(ctx.gemm_i32(w, q, su) == int(sign) * 127 * cols)
+        (y,) = ctx.ternary_linear([w], x)
+        assert np.all(y == np.float32(sign * cols))
+    w.free()
+
+
+def test_fused_multi_mfma_equals_separate(ctx):
+    cols = 2560
+    rng = np.random.default_rng(77)
+    ws = [ctx.upload(orc.pack(ternary_iid(rng, r, cols)), r, cols, s) for r, s in [(2560, 0.9), (640, 1.1), (640, 1.3)]]
+    x = rng.standard_normal((96, cols)).astype(np.float32)
+    announce("prefill fused multi")
+    fused = ctx.ternary_linear(ws, x)
+    for i, w in enumerate(ws):
+        (single,) = ctx.ternary_linear([w], x)
+        assert np.array_equal(fused[i], single)
+    for w in ws:
+        w.free()
+
+
+@pytest.mark.parametrize("n", [16, 40, 130])
+def test_model_prefill_mfma_matches_oracle_and_gemv(ctx, monkeypatch, n):
+    cfg = dict(hidden=512, intermediate=1536, heads=4, kv_heads=1, layers=2, vocab=1000, max_pos=1024)
+    hip_cfg = lbt_hip.make_config(**cfg)
+    or_cfg = orc.config(**cfg)
+    announce(f"model prefill mfma n={n}")
+    m = lbt_hip.Model.synthetic(ctx, hip_cfg, 3)
+    om = orc.OracleModel(or_cfg, 3)
+    toks = (np.arange(n) * 31 % cfg["vocab"]).astype(np.uint32)
+    c = m.new_cache()
+    got = m.forward(toks, c, all_logits=True)
+    assert np.array_equal(got, om.forward(toks, all_logits=True))
+    c.free()
+    monkeypatch.setenv("LBT_NO_MFMA", "1")
+    c = m.new_cache()
+    assert np.array_equal(m.forward(toks, c, all_logits=True), got)
+    c.free()
+    m.free()
+    om.free()
