@@ -311,20 +311,20 @@ int launch_attention(lbt_ctx* ctx, const float* q, int m, int nh, int kvh, int h
     // a graph-replayed step reads its position on the device: size for the cache
     const size_t lds = (size_t)(pos_dev ? cap : pos0 + m) * sizeof(float);
     if (lds > 64 * 1024) return set_err(ctx, LBT_E_RANGE, "attention: context too long for the LDS score buffer");
-    hipEvent_t ev = nullptr;
-    prof_begin(ctx, &ev);
+    hipEvent_t e0, e1;
+    prof_pair(ctx, &e0, &e1);
     dim3 grid(nh, m);
     switch (hd) {
         case 64:
-            hipLaunchKernelGGL(attention_kernel<8>, grid, dim3(kThreads), lds, ctx->stream, q, nh, kvh, pos0, kc, vc,
+            hipExtLaunchKernelGGL(attention_kernel<8>, grid, dim3(kThreads), lds, ctx->stream, e0, e1, 0, q, nh, kvh, pos0, kc, vc,
                                cap, scaling, out, pos_dev);
             break;
         case 128:
-            hipLaunchKernelGGL(attention_kernel<16>, grid, dim3(kThreads), lds, ctx->stream, q, nh, kvh, pos0, kc, vc,
+            hipExtLaunchKernelGGL(attention_kernel<16>, grid, dim3(kThreads), lds, ctx->stream, e0, e1, 0, q, nh, kvh, pos0, kc, vc,
                                cap, scaling, out, pos_dev);
             break;
         case 256:
-            hipLaunchKernelGGL(attention_kernel<32>, grid, dim3(kThreads), lds, ctx->stream, q, nh, kvh, pos0, kc, vc,
+            hipExtLaunchKernelGGL(attention_kernel<32>, grid, dim3(kThreads), lds, ctx->stream, e0, e1, 0, q, nh, kvh, pos0, kc, vc,
                                cap, scaling, out, pos_dev);
             break;
         default:
@@ -332,7 +332,7 @@ int launch_attention(lbt_ctx* ctx, const float* q, int m, int nh, int kvh, int h
     }
     LBT_HIP(ctx, hipGetLastError());
     const double kv_bytes = 2.0 * kvh * (double)(pos0 + m) * hd * 2.0;
-    prof_end(ctx, ev, kProfAttn, kv_bytes);
+    prof_commit(ctx, e0, e1, kProfAttn, kv_bytes);
     return LBT_OK;
 }
 
@@ -345,12 +345,12 @@ int launch_bf16_linear(lbt_ctx* ctx, const uint16_t* w, int rows, int cols, cons
     int blocks = (rows + 31) / 32;
     if (blocks > 2048) blocks = 2048;
     if (blocks < 1) blocks = 1;
-    hipEvent_t ev = nullptr;
-    prof_begin(ctx, &ev);
-    hipLaunchKernelGGL(lmhead_kernel, dim3(blocks, m), dim3(kThreads), lds, ctx->stream, w, rows, cols, x, norm_w,
+    hipEvent_t e0, e1;
+    prof_pair(ctx, &e0, &e1);
+    hipExtLaunchKernelGGL(lmhead_kernel, dim3(blocks, m), dim3(kThreads), lds, ctx->stream, e0, e1, 0, w, rows, cols, x, norm_w,
                        eps, logits, key);
     LBT_HIP(ctx, hipGetLastError());
-    prof_end(ctx, ev, kProfHead, (double)rows * cols * 2.0 * m);
+    prof_commit(ctx, e0, e1, kProfHead, (double)rows * cols * 2.0 * m);
     return LBT_OK;
 }
 

@@ -37,31 +37,32 @@ int ws_reserve(lbt_ctx* ctx, size_t bytes, void** out) {
     return LBT_OK;
 }
 
-void prof_begin(lbt_ctx* ctx, hipEvent_t* ev) {
-    *ev = nullptr;
-    if (!ctx->prof) return;
-    hipEvent_t e;
+static hipEvent_t take_event(lbt_ctx* ctx) {
+    hipEvent_t e = nullptr;
     if (!ctx->free_events.empty()) {
         e = ctx->free_events.back();
         ctx->free_events.pop_back();
     } else if (hipEventCreate(&e) != hipSuccess) {
-        return;
+        e = nullptr;
     }
-    hipEventRecord(e, ctx->stream);
-    *ev = e;
+    return e;
 }
 
-void prof_end(lbt_ctx* ctx, hipEvent_t ev, int cls, double bytes) {
-    if (!ctx->prof || !ev) return;
-    hipEvent_t e;
-    if (!ctx->free_events.empty()) {
-        e = ctx->free_events.back();
-        ctx->free_events.pop_back();
-    } else if (hipEventCreate(&e) != hipSuccess) {
-        return;
+void prof_pair(lbt_ctx* ctx, hipEvent_t* a, hipEvent_t* b) {
+    *a = *b = nullptr;
+    if (!ctx->prof) return;
+    *a = take_event(ctx);
+    *b = take_event(ctx);
+    if (!*a || !*b) {
+        if (*a) ctx->free_events.push_back(*a);
+        if (*b) ctx->free_events.push_back(*b);
+        *a = *b = nullptr;
     }
-    hipEventRecord(e, ctx->stream);
-    ctx->pending.push_back({cls, bytes, ev, e});
+}
+
+void prof_commit(lbt_ctx* ctx, hipEvent_t a, hipEvent_t b, int cls, double bytes) {
+    if (!ctx->prof || !a || !b) return;
+    ctx->pending.push_back({cls, bytes, a, b});
 }
 
 }  // namespace lbt

@@ -1,6 +1,7 @@
 // lbt_internal.h -- host-side internals shared by the C ABI, the model loop
 // and the kernel launchers.
 #pragma once
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -62,8 +63,11 @@ int ws_reserve(lbt_ctx* ctx, size_t bytes, void** out);
 
 // Profiling brackets around one launch (no-ops unless ctx->prof).
 enum ProfClass { kProfGemv = 0, kProfGemm = 1, kProfHead = 2, kProfAttn = 3, kProfOther = 4 };
-void prof_begin(lbt_ctx* ctx, hipEvent_t* ev);
-void prof_end(lbt_ctx* ctx, hipEvent_t ev, int cls, double bytes);
+// prof_pair hands out a start/stop event pair (null when profiling is off)
+// for hipExtLaunchKernelGGL, which timestamps the dispatch itself, so the
+// measured time is the kernel's execution (as rocprofv3 reports it).
+void prof_pair(lbt_ctx* ctx, hipEvent_t* a, hipEvent_t* b);
+void prof_commit(lbt_ctx* ctx, hipEvent_t a, hipEvent_t b, int cls, double bytes);
 
 // ---- ternary GEMV / GEMM ------------------------------------------------
 enum InMode { kInPreQ = 0, kInF32 = 1 };

@@ -240,43 +240,45 @@ namespace {
 constexpr int kL = 8;
 
 template <int T, int NCH, int TILES, int IN>
-hipError_t launch_out(const GemvArgs& a, int out_mode, dim3 grid, size_t lds, hipStream_t s) {
+hipError_t launch_out(const GemvArgs& a, int out_mode, dim3 grid, size_t lds, hipStream_t s, hipEvent_t e0,
+                      hipEvent_t e1) {
     switch (out_mode) {
         case kOutI32:
-            hipLaunchKernelGGL((tgemv_kernel<kL, T, NCH, TILES, IN, kOutI32>), grid, dim3(kThreads), lds, s, a);
+            hipExtLaunchKernelGGL((tgemv_kernel<kL, T, NCH, TILES, IN, kOutI32>), grid, dim3(kThreads), lds, s, e0, e1, 0, a);
             break;
         case kOutF32:
-            hipLaunchKernelGGL((tgemv_kernel<kL, T, NCH, TILES, IN, kOutF32>), grid, dim3(kThreads), lds, s, a);
+            hipExtLaunchKernelGGL((tgemv_kernel<kL, T, NCH, TILES, IN, kOutF32>), grid, dim3(kThreads), lds, s, e0, e1, 0, a);
             break;
         case kOutF32Add:
-            hipLaunchKernelGGL((tgemv_kernel<kL, T, NCH, TILES, IN, kOutF32Add>), grid, dim3(kThreads), lds, s, a);
+            hipExtLaunchKernelGGL((tgemv_kernel<kL, T, NCH, TILES, IN, kOutF32Add>), grid, dim3(kThreads), lds, s, e0, e1, 0, a);
             break;
         case kOutRelu2:
-            hipLaunchKernelGGL((tgemv_kernel<kL, T, NCH, TILES, IN, kOutRelu2>), grid, dim3(kThreads), lds, s, a);
+            hipExtLaunchKernelGGL((tgemv_kernel<kL, T, NCH, TILES, IN, kOutRelu2>), grid, dim3(kThreads), lds, s, e0, e1, 0, a);
             break;
         default:
-            hipLaunchKernelGGL((tgemv_kernel<kL, T, NCH, TILES, IN, kOutQKV>), grid, dim3(kThreads), lds, s, a);
+            hipExtLaunchKernelGGL((tgemv_kernel<kL, T, NCH, TILES, IN, kOutQKV>), grid, dim3(kThreads), lds, s, e0, e1, 0, a);
             break;
     }
     return hipGetLastError();
 }
 
 template <int T, int NCH, int TILES>
-hipError_t launch_in(const GemvArgs& a, int in_mode, int out_mode, dim3 grid, size_t lds, hipStream_t s) {
-    return in_mode == kInPreQ ? launch_out<T, NCH, TILES, kInPreQ>(a, out_mode, grid, lds, s)
-                              : launch_out<T, NCH, TILES, kInF32>(a, out_mode, grid, lds, s);
+hipError_t launch_in(const GemvArgs& a, int in_mode, int out_mode, dim3 grid, size_t lds, hipStream_t s,
+                     hipEvent_t e0, hipEvent_t e1) {
+    return in_mode == kInPreQ ? launch_out<T, NCH, TILES, kInPreQ>(a, out_mode, grid, lds, s, e0, e1)
+                              : launch_out<T, NCH, TILES, kInF32>(a, out_mode, grid, lds, s, e0, e1);
 }
 
 template <int T>
 hipError_t launch_t(const GemvArgs& a, int nch, int tiles, int in_mode, int out_mode, dim3 grid, size_t lds,
-                    hipStream_t s) {
+                    hipStream_t s, hipEvent_t e0, hipEvent_t e1) {
     if (nch == 2) {
-        if (tiles == 4) return launch_in<T, 2, 4>(a, in_mode, out_mode, grid, lds, s);
-        if (tiles == 2) return launch_in<T, 2, 2>(a, in_mode, out_mode, grid, lds, s);
-        return launch_in<T, 2, 1>(a, in_mode, out_mode, grid, lds, s);
+        if (tiles == 4) return launch_in<T, 2, 4>(a, in_mode, out_mode, grid, lds, s, e0, e1);
+        if (tiles == 2) return launch_in<T, 2, 2>(a, in_mode, out_mode, grid, lds, s, e0, e1);
+        return launch_in<T, 2, 1>(a, in_mode, out_mode, grid, lds, s, e0, e1);
     }
-    if (tiles == 2) return launch_in<T, 4, 2>(a, in_mode, out_mode, grid, lds, s);
-    return launch_in<T, 4, 1>(a, in_mode, out_mode, grid, lds, s);
+    if (tiles == 2) return launch_in<T, 4, 2>(a, in_mode, out_mode, grid, lds, s, e0, e1);
+    return launch_in<T, 4, 1>(a, in_mode, out_mode, grid, lds, s, e0, e1);
 }
 
 }  // namespace
@@ -341,13 +343,13 @@ int launch_ternary_gemv(lbt_ctx* ctx, const TernaryOp& op) {
     dim3 grid((unsigned)((ntiles + tiles - 1) / tiles), (unsigned)((op.m + T - 1) / T));
     const size_t lds = (size_t)T * a.kp;
     if (lds > 64 * 1024) return set_err(ctx, LBT_E_INVALID, "ternary: activation image exceeds LDS budget");
-    hipEvent_t ev = nullptr;
-    prof_begin(ctx, &ev);
-    hipError_t e = T == 1 ? launch_t<1>(a, nch, tiles, op.in_mode, op.out_mode, grid, lds, ctx->stream)
-                          : launch_t<4>(a, nch, tiles, op.in_mode, op.out_mode, grid, lds, ctx->stream);
+    hipEvent_t e0, e1;
+    prof_pair(ctx, &e0, &e1);
+    hipError_t e = T == 1 ? launch_t<1>(a, nch, tiles, op.in_mode, op.out_mode, grid, lds, ctx->stream, e0, e1)
+                          : launch_t<4>(a, nch, tiles, op.in_mode, op.out_mode, grid, lds, ctx->stream, e0, e1);
     if (e != hipSuccess) return hip_err(ctx, e, "tgemv_kernel launch");
     const double bytes = (double)total * (a.kp / 4) + (double)op.m * op.cols * 4.0;
-    prof_end(ctx, ev, kProfGemv, bytes);
+    prof_commit(ctx, e0, e1, kProfGemv, bytes);
     return LBT_OK;
 }
 

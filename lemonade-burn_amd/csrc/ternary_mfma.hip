@@ -140,13 +140,13 @@ __global__ __launch_bounds__(kThreads) void tgemm_kernel(GemvArgs a) {
 namespace {
 
 template <int MS, int NS>
-hipError_t launch_tiles(const GemvArgs& a, int out_mode, dim3 grid, hipStream_t s) {
+hipError_t launch_tiles(const GemvArgs& a, int out_mode, dim3 grid, hipStream_t s, hipEvent_t e0, hipEvent_t e1) {
     switch (out_mode) {
-        case kOutI32: hipLaunchKernelGGL((tgemm_kernel<MS, NS, kOutI32>), grid, dim3(kThreads), 0, s, a); break;
-        case kOutF32: hipLaunchKernelGGL((tgemm_kernel<MS, NS, kOutF32>), grid, dim3(kThreads), 0, s, a); break;
-        case kOutF32Add: hipLaunchKernelGGL((tgemm_kernel<MS, NS, kOutF32Add>), grid, dim3(kThreads), 0, s, a); break;
-        case kOutRelu2: hipLaunchKernelGGL((tgemm_kernel<MS, NS, kOutRelu2>), grid, dim3(kThreads), 0, s, a); break;
-        default: hipLaunchKernelGGL((tgemm_kernel<MS, NS, kOutQKV>), grid, dim3(kThreads), 0, s, a); break;
+        case kOutI32: hipExtLaunchKernelGGL((tgemm_kernel<MS, NS, kOutI32>), grid, dim3(kThreads), 0, s, e0, e1, 0, a); break;
+        case kOutF32: hipExtLaunchKernelGGL((tgemm_kernel<MS, NS, kOutF32>), grid, dim3(kThreads), 0, s, e0, e1, 0, a); break;
+        case kOutF32Add: hipExtLaunchKernelGGL((tgemm_kernel<MS, NS, kOutF32Add>), grid, dim3(kThreads), 0, s, e0, e1, 0, a); break;
+        case kOutRelu2: hipExtLaunchKernelGGL((tgemm_kernel<MS, NS, kOutRelu2>), grid, dim3(kThreads), 0, s, e0, e1, 0, a); break;
+        default: hipExtLaunchKernelGGL((tgemm_kernel<MS, NS, kOutQKV>), grid, dim3(kThreads), 0, s, e0, e1, 0, a); break;
     }
     return hipGetLastError();
 }
@@ -192,18 +192,18 @@ int launch_ternary_mfma(lbt_ctx* ctx, const TernaryOp& op_in) {
     if (rc) return rc;
     const int total = a.total_rows;
     const bool big = (long)((total + 127) / 128) * ((op.m + 127) / 128) >= 240;
-    hipEvent_t ev = nullptr;
-    prof_begin(ctx, &ev);
+    hipEvent_t e0, e1;
+    prof_pair(ctx, &e0, &e1);
     hipError_t e;
     if (big) {
         dim3 grid((unsigned)((total + 127) / 128), (unsigned)((op.m + 127) / 128));
-        e = launch_tiles<4, 4>(a, op.out_mode, grid, ctx->stream);
+        e = launch_tiles<4, 4>(a, op.out_mode, grid, ctx->stream, e0, e1);
     } else {
         dim3 grid((unsigned)((total + 63) / 64), (unsigned)((op.m + 63) / 64));
-        e = launch_tiles<2, 2>(a, op.out_mode, grid, ctx->stream);
+        e = launch_tiles<2, 2>(a, op.out_mode, grid, ctx->stream, e0, e1);
     }
     if (e != hipSuccess) return hip_err(ctx, e, "tgemm_kernel launch");
-    prof_end(ctx, ev, kProfGemm, 2.0 * op.m * (double)total * a.kp);
+    prof_commit(ctx, e0, e1, kProfGemm, 2.0 * op.m * (double)total * a.kp);
     return LBT_OK;
 }
 
