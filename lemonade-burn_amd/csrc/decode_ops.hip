@@ -9,6 +9,7 @@
 // Float order follows lbt_device.h; the oracle mirrors it.
 #include "lbt_device.h"
 #include "lbt_internal.h"
+#include "attn_common.h"
 
 namespace lbt {
 
@@ -41,98 +42,17 @@ __global__ __launch_bounds__(kThreads) void embed_kernel(const uint16_t* embed, 
 }
 
 // ---------------------------------------------------------------------------
-// GQA attention for query row t (absolute position p = pos0 + t) and head h,
-// over keys 0..p of the bf16 cache (the q/k/v GEMV has already rotated q and
-// appended the rotated k and v).  model.rs:349-357: scores = q.K^T * scaling,
-// softmax = exp(s - max) / sum, out = probs @ V; the causal mask of :316-328
-// is the visibility bound.  One workgroup per (head, row).  Float order (the
-// oracle mirrors it), with LK = hd/8 lanes per key and 8 dims per lane:
-//   score: lane c sums q[8c+e]*k[8c+e] over e = 0..7 by fused multiply-adds,
-//          the LK lanes combine with an xor butterfly (m = LK/2 .. 1), then
-//          * scaling;
-//   sum:   thread t adds exp(s_j - max) over j = t, t+256, ...; block_sum;
-//   p_j:   exp(s_j - max) / sum;
-//   out:   thread (group g = t/LK, chunk c = t%LK) accumulates
-//          p_j * v[j][8c+e] by fused multiply-adds over j = g, g+256/LK, ...;
-//          the 64/LK groups of a wave combine by xor over the group index
-//          (m = 1, 2, ...), the four waves as (w0 + w1) + (w2 + w3).
+// GQA attention, one workgroup per (head, query row); see attn_common.h.
 template <int LK>
 __global__ __launch_bounds__(kThreads) void attention_kernel(const float* q, int nh, int kvh, int pos0,
                                                              const uint16_t* kc, const uint16_t* vc, int cap,
                                                              float scaling, float* out, const int* pos_dev) {
-    constexpr int HD = LK * 8, GW = 64 / LK, NG = kThreads / LK;
     extern __shared__ float sc[];  // [p + 1]
-    __shared__ __align__(16) float qs[HD];
-    __shared__ float red[8];
-    __shared__ __align__(16) float pv[4][HD];
-    const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    __shared__ AttnShared<LK> sh;
     if (pos_dev) pos0 = *pos_dev;
-    const int H = nh * HD, p = pos0 + t, vis = p + 1, g = h / (nh / kvh);
-    if (tid < HD) qs[tid] = q[(size_t)t * H + (size_t)h * HD + tid];
-    __syncthreads();
-    const uint16_t* K = kc + (size_t)g * cap * HD;
-    const uint16_t* V = vc + (size_t)g * cap * HD;
-    const int ks = lane / LK, cc = lane % LK;
-    float q8[8];
-#pragma unroll
-    for (int e = 0; e < 8; e++) q8[e] = qs[8 * cc + e];
-    float mx = -__builtin_inff();
-    for (int j0 = w * GW; j0 < vis; j0 += 4 * GW) {
-        const int j = j0 + ks;
-        float a = 0.0f;
-        if (j < vis) {
-            const uint4 kv = *(const uint4*)(K + (size_t)j * HD + 8 * cc);
-            const uint32_t wv[4] = {kv.x, kv.y, kv.z, kv.w};
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                a = __builtin_fmaf(q8[2 * e], bf16_to_f32((uint16_t)(wv[e] & 0xffffu)), a);
-                a = __builtin_fmaf(q8[2 * e + 1], bf16_to_f32((uint16_t)(wv[e] >> 16)), a);
-            }
-        }
-#pragma unroll
-        for (int m = LK / 2; m >= 1; m >>= 1) a = a + __shfl_xor(a, m);
-        if (j < vis) {
-            const float s = a * scaling;
-            if (cc == 0) sc[j] = s;
-            mx = fmaxf(mx, s);
-        }
-    }
-    mx = block_max(mx, red);  // includes the barrier that publishes sc
-    float ps = 0.0f;
-    for (int j = tid; j < vis; j += kThreads) {
-        const float e = lbt_expf(sc[j] - mx);
-        sc[j] = e;
-        ps = ps + e;
-    }
-    const float sum = block_sum(ps, red);
-    for (int j = tid; j < vis; j += kThreads) sc[j] = sc[j] / sum;
-    __syncthreads();
-    const int grp = tid / LK, c = tid % LK;
-    float acc[8];
-#pragma unroll
-    for (int e = 0; e < 8; e++) acc[e] = 0.0f;
-    for (int j = grp; j < vis; j += NG) {
-        const float pj = sc[j];
-        const uint4 vv = *(const uint4*)(V + (size_t)j * HD + 8 * c);
-        const uint32_t wv[4] = {vv.x, vv.y, vv.z, vv.w};
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            acc[2 * e] = __builtin_fmaf(pj, bf16_to_f32((uint16_t)(wv[e] & 0xffffu)), acc[2 * e]);
-            acc[2 * e + 1] = __builtin_fmaf(pj, bf16_to_f32((uint16_t)(wv[e] >> 16)), acc[2 * e + 1]);
-        }
-    }
-#pragma unroll
-    for (int m = 1; m < GW; m <<= 1) {
-#pragma unroll
-        for (int e = 0; e < 8; e++) acc[e] = acc[e] + __shfl_xor(acc[e], m * LK);
-    }
-    if (lane < LK) {
-#pragma unroll
-        for (int e = 0; e < 8; e++) pv[w][8 * c + e] = acc[e];
-    }
-    __syncthreads();
-    if (tid < HD)
-        out[(size_t)t * H + (size_t)h * HD + tid] = (pv[0][tid] + pv[1][tid]) + (pv[2][tid] + pv[3][tid]);
+    const int h = blockIdx.x, t = blockIdx.y;
+    attention_head<LK>(q + (size_t)t * nh * LK * 8, h, nh, kvh, pos0 + t, kc, vc, cap, scaling,
+                       out + (size_t)t * nh * LK * 8, sc, sh);
 }
 
 // ---------------------------------------------------------------------------
@@ -165,17 +85,17 @@ __global__ __launch_bounds__(kThreads) void lmhead_kernel(const uint16_t* W, int
                                                           const float* norm_w, float eps, float* logits,
                                                           unsigned long long* key) {
     extern __shared__ __align__(16) float xs[];  // cols
-    __shared__ float red[kThreads];
+    __shared__ float red[16];
     const int t = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
     const float* xr = x + (size_t)t * cols;
     if (cols <= 16 * kThreads) {
         float v[16];
-        load_norm_row<16>(xr, cols, norm_w, eps, v, red);
+        load_norm_row<16>(SrcF32{xr}, cols, norm_w, eps, v, red);
 #pragma unroll
         for (int e = 0; e < 16; e++)
             if (tid + e * kThreads < cols) xs[tid + e * kThreads] = v[e];
     } else {
-        const float rr = norm_factor_global(xr, cols, norm_w, eps, red);
+        const float rr = norm_factor_global(SrcF32{xr}, cols, norm_w, eps, red);
         for (int i = tid; i < cols; i += kThreads) xs[i] = norm_w ? (xr[i] * rr) * norm_w[i] : xr[i];
     }
     __syncthreads();

@@ -79,7 +79,8 @@ __device__ __forceinline__ float wave_sum(float v) {
 }
 
 // Block sum of one value per thread (blockDim.x == 256): wave butterflies,
-// then (w0 + w1) + (w2 + w3).  `red` >= 4 floats of LDS.
+// then (w0 + w1) + (w2 + w3).  `red` >= 16 floats of LDS (workgroups of up
+// to 1024 threads; only the first four waves' sums are used).
 __device__ __forceinline__ float block_sum(float v, float* red) {
     v = wave_sum(v);
     const int w = threadIdx.x >> 6;
@@ -102,7 +103,7 @@ __device__ __forceinline__ int wave_sum_i(int v) {
     return v;
 }
 
-// Order-independent block max (blockDim.x == 256); `red` >= 4 floats of LDS.
+// Block max over the first 256 threads; `red` >= 16 floats of LDS.
 __device__ __forceinline__ float block_max(float v, float* red) {
     v = wave_max(v);
     const int w = threadIdx.x >> 6;
@@ -123,26 +124,64 @@ __device__ __forceinline__ int block_sum_i(int v, int* red) {
     return r;
 }
 
-// Loads row xr[0..cols) into registers, v[e] = x[threadIdx.x + 256 e] (0 past
+// Hides a uniform pointer's value from the optimizer, so per-element
+// addresses derived from it are recomputed where they are used instead of
+// being hoisted out of long loops (which exhausts registers in the
+// persistent decode kernel).
+// The pointer must be uniform across the wavefront.
+template <typename T>
+__device__ __forceinline__ T* launder(T* p) {
+    const unsigned long long v = (unsigned long long)p;
+    unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)v);
+    unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)(v >> 32));
+    asm volatile("" : "+s"(lo), "+s"(hi));
+    return (T*)(((unsigned long long)hi << 32) | lo);
+}
+
+// threadIdx.x hidden from the optimizer (same purpose as launder: per-lane
+// values are recomputed in each phase instead of living across a long loop).
+__device__ __forceinline__ int fresh_tid() {
+    int t = (int)threadIdx.x;
+    asm volatile("" : "+v"(t));
+    return t;
+}
+
+// Row sources for the activation prologues: f32 rows, or bf16 rows (the
+// embedding, widened exactly).
+struct SrcF32 {
+    const float* p;
+    __device__ __forceinline__ float operator()(int i) const { return p[i]; }
+    __device__ __forceinline__ SrcF32 fresh() const { return SrcF32{launder(p)}; }
+};
+struct SrcBf16 {
+    const uint16_t* p;
+    __device__ __forceinline__ float operator()(int i) const { return bf16_to_f32(p[i]); }
+    __device__ __forceinline__ SrcBf16 fresh() const { return SrcBf16{launder(p)}; }
+};
+
+// Loads row x[0..cols) into registers, v[e] = x[threadIdx.x + 256 e] (0 past
 // cols), and if norm_w is set applies rms_norm (crates/lb-model/src/model.rs:
 // 267-272) in place: r = 1 / sqrt(sum(x^2)/cols + eps) with the sum of squares
 // accumulated per thread by fused multiply-adds in ascending i and combined by
 // block_sum; v = (x * r) * w.  Requires cols <= 256 * EPT.  One global pass.
-template <int EPT>
-__device__ __forceinline__ void load_norm_row(const float* xr, int cols, const float* norm_w, float eps,
-                                              float (&v)[EPT], float* red) {
+// Only the first 256 threads of the workgroup take part; larger workgroups
+// call it with all threads (the barriers are shared) and get zeros elsewhere.
+template <int EPT, typename Src>
+__device__ __forceinline__ void load_norm_row(Src x, int cols, const float* norm_w, float eps, float (&v)[EPT],
+                                              float* red) {
+    const bool act = threadIdx.x < kThreads;
     float nw[EPT];
 #pragma unroll
     for (int e = 0; e < EPT; e++) {
         const int i = threadIdx.x + e * kThreads;
-        v[e] = i < cols ? xr[i] : 0.0f;
-        nw[e] = (norm_w && i < cols) ? norm_w[i] : 0.0f;
+        v[e] = (act && i < cols) ? x(i) : 0.0f;
+        nw[e] = (act && norm_w && i < cols) ? norm_w[i] : 0.0f;
     }
     if (!norm_w) return;
     float p = 0.0f;
 #pragma unroll
     for (int e = 0; e < EPT; e++)
-        if (threadIdx.x + e * kThreads < cols) p = __builtin_fmaf(v[e], v[e], p);
+        if (act && threadIdx.x + e * kThreads < cols) p = __builtin_fmaf(v[e], v[e], p);
     const float ss = block_sum(p, red);
     const float r = 1.0f / __builtin_sqrtf(ss / (float)cols + eps);
 #pragma unroll
@@ -150,11 +189,12 @@ __device__ __forceinline__ void load_norm_row(const float* xr, int cols, const f
 }
 
 // Same result for rows longer than 256 * EPT, re-reading x from memory.
-__device__ __forceinline__ float norm_factor_global(const float* xr, int cols, const float* norm_w, float eps,
-                                                    float* red) {
+template <typename Src>
+__device__ __forceinline__ float norm_factor_global(Src x, int cols, const float* norm_w, float eps, float* red) {
     if (!norm_w) return 1.0f;
     float p = 0.0f;
-    for (int i = threadIdx.x; i < cols; i += kThreads) p = __builtin_fmaf(xr[i], xr[i], p);
+    if (threadIdx.x < kThreads)
+        for (int i = threadIdx.x; i < cols; i += kThreads) p = __builtin_fmaf(x(i), x(i), p);
     const float ss = block_sum(p, red);
     return 1.0f / __builtin_sqrtf(ss / (float)cols + eps);
 }

@@ -236,9 +236,14 @@ struct lbt_model {
     int last_n = 0;
     // graph of one decode step (embed from the argmax key .. LM head), valid
     // for the cache buffers and workspace it was captured with
-    int* state = nullptr;  // device {position, output slot}
+    int* state = nullptr;  // device {position - 1, output slot, barrier epoch, spare}
     hipGraphExec_t step_exec = nullptr;
     const void* step_key[6] = {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
+    // persistent decode step: device tables of the layers and the barrier words
+    void* ptab = nullptr;  // [layers*7] weight ptrs, [layers*7] scales, [layers*4] norm ptrs
+    unsigned long long* trace = nullptr;
+    unsigned* bar = nullptr;  // flags [G*16], go, err
+    int bar_g = 0;
 };
 
 struct lbt_cache {
@@ -497,6 +502,128 @@ int forward_dev(lbt_model* m, lbt_cache* cc, const uint32_t* toks_dev, int n, bo
                               (all_logits || want_logits) ? m->logits : nullptr, all_logits ? nullptr : m->key);
 }
 
+int ensure_state(lbt_model* m) {
+    if (m->state) return LBT_OK;
+    lbt_ctx* ctx = m->ctx;
+    LBT_HIP(ctx, hipMalloc(&m->state, 4 * sizeof(int)));
+    LBT_HIP(ctx, hipMemsetAsync(m->state, 0, 4 * sizeof(int), ctx->stream));
+    return LBT_OK;
+}
+
+// Persistent-grid workgroups (LBT_PERSIST_G overrides) or 0 when the
+// persistent step is off or the shape does not fit.  The persistent step is
+// opt-in (LBT_DECODE=persistent): on the 2B shape it is still slower than the
+// graph-replayed per-kernel step.
+int persist_grid(lbt_model* m, lbt_cache* c, int* rpw) {
+    const char* mode = getenv("LBT_DECODE");
+    if (!mode || strcmp(mode, "persistent") != 0) return 0;
+    int G = 64;
+    if (const char* g = getenv("LBT_PERSIST_G")) G = atoi(g);
+    if (G < 1 || G > 256) return 0;
+    const char* why = nullptr;
+    return persistent_supported(m->cfg, c->cap, G, rpw, &why) ? G : 0;
+}
+
+int persist_prepare(lbt_model* m, lbt_cache* c, int G, const int* rpw, PersistHost& h) {
+    lbt_ctx* ctx = m->ctx;
+    const lbt_config& cf = m->cfg;
+    const int L = cf.num_hidden_layers;
+    int rc;
+    if ((rc = ensure_state(m))) return rc;
+    if (!m->ptab) {
+        std::vector<const void*> wp(L * 7), np(L * 4);
+        std::vector<float> ws(L * 7);
+        for (int i = 0; i < L * 7; i++) {
+            wp[i] = m->lin[i].d;
+            ws[i] = m->lin[i].scale;
+        }
+        for (int i = 0; i < L * 4; i++) np[i] = m->norm[i];
+        const size_t b0 = wp.size() * 8, b1 = ws.size() * 4, b2 = np.size() * 8;
+        LBT_HIP(ctx, hipMalloc(&m->ptab, b0 + b1 + b2 + 64));
+        char* t = (char*)m->ptab;
+        LBT_HIP(ctx, hipMemcpy(t, wp.data(), b0, hipMemcpyHostToDevice));
+        LBT_HIP(ctx, hipMemcpy(t + b0, ws.data(), b1, hipMemcpyHostToDevice));
+        LBT_HIP(ctx, hipMemcpy(t + ((b0 + b1 + 7) & ~(size_t)7), np.data(), b2, hipMemcpyHostToDevice));
+    }
+    if (m->bar_g < G) {
+        // flags are monotonic epochs; fresh buffers start at 0 with the epoch
+        if (m->bar) hipFree(m->bar);
+        m->bar = nullptr;
+        LBT_HIP(ctx, hipMalloc(&m->bar, ((size_t)G * 16 + 32) * 4));
+        LBT_HIP(ctx, hipMemset(m->bar, 0, ((size_t)G * 16 + 32) * 4));
+        LBT_HIP(ctx, hipMemset(m->state + 2, 0, sizeof(int)));
+        m->bar_g = G;
+    }
+    const size_t b0 = (size_t)L * 7 * 8, b1 = (size_t)L * 7 * 4;
+    h.cfg = cf;
+    h.w = (const uint8_t* const*)m->ptab;
+    h.wscale = (const float*)((char*)m->ptab + b0);
+    h.norm = (const float* const*)((char*)m->ptab + ((b0 + b1 + 7) & ~(size_t)7));
+    h.embed = m->embed;
+    h.cos_t = m->cos_t;
+    h.sin_t = m->sin_t;
+    h.kc = c->k;
+    h.vc = c->v;
+    h.cap = c->cap;
+    h.layer_kv = (size_t)cf.num_key_value_heads * c->cap * m->hd;
+    h.scaling = m->scaling;
+    h.state = m->state;
+    h.key = m->key;
+    h.tok_out = m->tok_out;
+    h.x = m->x;
+    h.q = m->q;
+    h.att = m->att;
+    h.h = m->h;
+    h.flags = m->bar;
+    h.go = m->bar + (size_t)G * 16;
+    h.err = m->bar + (size_t)G * 16 + 16;
+    for (int i = 0; i < 4; i++) h.rpw[i] = rpw[i];
+    h.trace = nullptr;
+    if (getenv("LBT_PERSIST_TRACE")) {
+        if (!m->trace) LBT_HIP(ctx, hipMalloc(&m->trace, 8192 * 8));
+        h.trace = m->trace;
+    }
+    return LBT_OK;
+}
+
+// After a synchronize: a barrier timeout inside the persistent step is an error.
+int persist_check(lbt_model* m) {
+    if (!m->bar) return LBT_OK;
+    lbt_ctx* ctx = m->ctx;
+    unsigned err = 0;
+    unsigned* e = m->bar + (size_t)m->bar_g * 16 + 16;
+    LBT_HIP(ctx, hipMemcpy(&err, e, 4, hipMemcpyDeviceToHost));
+    if (err) {
+        hipMemset(e, 0, 4);
+        return set_err(ctx, LBT_E_DEVICE, "persistent decode: grid barrier timed out");
+    }
+    if (m->trace && getenv("LBT_PERSIST_TRACE")) {
+        // debugging aid: mean duration of each traced segment of the last step
+        std::vector<unsigned long long> t(8192);
+        LBT_HIP(ctx, hipMemcpy(t.data(), m->trace, 8192 * 8, hipMemcpyDeviceToHost));
+        const int L = m->cfg.num_hidden_layers;
+        for (int half = 0; half < 2; half++) {
+            double seg[16] = {0};
+            for (int l = 0; l < L; l++)
+                for (int k = 1; k < 16; k++) {
+                    const unsigned long long* r = &t[half * 4096 + l * 16];
+                    seg[k] += (double)(r[k] - r[k - 1]) / L;
+                }
+            fprintf(stderr, "persistent trace wg%s (us, 100 MHz ticks/100):", half ? "-last" : "0");
+            for (int k = 1; k < 16; k++) fprintf(stderr, " %d:%.2f", k, seg[k] / 100.0);
+            double wg = 0, wd = 0;
+            for (int l = 0; l < L; l++) {
+                const unsigned long long* r = &t[half * 4096 + l * 16];
+                const unsigned long long* x = &t[half * 4096 + 2048 + l * 4];
+                wg += (double)(x[0] - r[10]) / L;
+                wd += (double)(x[1] - r[13]) / L;
+            }
+            fprintf(stderr, " | weights-wait gu %.2f down %.2f\n", wg / 100.0, wd / 100.0);
+        }
+    }
+    return LBT_OK;
+}
+
 // Runs n decode steps, each fed with the previous step's argmax (the key);
 // the token consumed by step s goes to m->tok_out[slot0 + s].  Outside
 // profiling one captured step is replayed as a HIP graph (positions and
@@ -506,12 +633,29 @@ int decode_steps(lbt_model* m, lbt_cache* c, int n, int slot0) {
     lbt_ctx* ctx = m->ctx;
     if (n <= 0) return LBT_OK;
     int rc;
+    int rpw[4];
+    const int G = persist_grid(m, c, rpw);
+    if (G > 0) {
+        PersistHost h;
+        if ((rc = persist_prepare(m, c, G, rpw, h))) return rc;
+        if ((rc = launch_set_state(ctx, m->state, c->len - 1, slot0))) return rc;
+        const lbt_config& cf = m->cfg;
+        for (int s = 0; s < n; s++) {
+            if ((rc = launch_decode_persistent(ctx, h, G, ctx->stream))) return rc;
+            if ((rc = launch_bf16_linear(ctx, m->embed, cf.vocab_size, cf.hidden_size, m->x, 1, m->final_norm,
+                                         (float)cf.rms_norm_eps, nullptr, m->key)))
+                return rc;
+        }
+        c->len += n;
+        m->last_n = 1;
+        return LBT_OK;
+    }
     if (ctx->prof || getenv("LBT_NO_GRAPH")) {
         for (int s = 0; s < n; s++)
             if ((rc = forward_dev(m, c, nullptr, 1, false, false, m->tok_out + slot0 + s))) return rc;
         return LBT_OK;
     }
-    if (!m->state) LBT_HIP(ctx, hipMalloc(&m->state, 2 * sizeof(int)));
+    if ((rc = ensure_state(m))) return rc;
     const void* key[6] = {c->k, c->v, (const void*)(intptr_t)c->cap, m->tok_out, m->x, m->key};
     if (!m->step_exec || memcmp(key, m->step_key, sizeof(key)) != 0) {
         if (m->step_exec) {
@@ -740,6 +884,8 @@ void lbt_model_free(lbt_model* m) {
     if (!m) return;
     hipStreamSynchronize(m->ctx->stream);
     if (m->step_exec) hipGraphExecDestroy(m->step_exec);
+    if (m->ptab) hipFree(m->ptab);
+    if (m->bar) hipFree(m->bar);
     void* bufs[] = {m->wbuf, m->fbuf, m->embed, m->cos_t, m->sin_t, m->x,   m->q,       m->k,
                     m->v,    m->att,  m->h,     m->logits, m->toks, m->key, m->tok_out, m->state};
     for (void* b : bufs)
@@ -858,6 +1004,7 @@ int lbt_model_generate_greedy(lbt_model* m, const uint32_t* prompt, size_t n, si
     }
     hipError_t e = hipStreamSynchronize(ctx->stream);
     if (!rc && e != hipSuccess) rc = hip_err(ctx, e, "generate");
+    if (!rc) rc = persist_check(m);
     if (!rc) {
         float a = 0, b = 0;
         hipEventElapsedTime(&a, e0, e1);
@@ -898,6 +1045,7 @@ int lbt_model_decode_greedy(lbt_model* m, lbt_cache* c, uint32_t first, size_t s
     hipEventRecord(e1, ctx->stream);
     hipError_t e = hipStreamSynchronize(ctx->stream);
     if (!rc && e != hipSuccess) rc = hip_err(ctx, e, "decode");
+    if (!rc) rc = persist_check(m);
     if (!rc) {
         float a = 0;
         hipEventElapsedTime(&a, e0, e1);

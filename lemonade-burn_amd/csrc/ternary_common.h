@@ -30,6 +30,13 @@ struct GemvArgs {
     uint16_t* vc;
 };
 
+// Element i (0..2) of a 3-array by selects: a runtime index into a local
+// struct would put the struct in scratch memory.
+template <typename T>
+__device__ __forceinline__ T sel3(const T (&v)[3], int i) {
+    return i == 0 ? v[0] : (i == 1 ? v[1] : v[2]);
+}
+
 // Virtual row -> (matrix, row).  kOutRelu2 interleaves gate/up rows
 // (2r, 2r+1) = (gate r, up r).  kOutQKV interleaves RoPE partners: for q and
 // k, virtual rows (2p, 2p+1) are rows (d, d + hd/2) of one head; v keeps its
@@ -75,12 +82,12 @@ template <int OUT>
 __device__ __forceinline__ void store_single(const GemvArgs& a, int tok, int v, int dot, float sa) {
     int mt, ro;
     resolve_row<OUT>(a, v, mt, ro);
-    const size_t o = (size_t)tok * a.rows[mt] + ro;
+    const size_t o = (size_t)tok * sel3(a.rows, mt) + ro;
     if (OUT == kOutI32) {
-        ((int32_t*)a.out[mt])[o] = dot;
+        ((int32_t*)sel3(a.out, mt))[o] = dot;
     } else {
-        const float y = (float)dot * (1.0f / (sa * a.sw[mt]));
-        float* dst = (float*)a.out[mt];
+        const float y = (float)dot * (1.0f / (sa * sel3(a.sw, mt)));
+        float* dst = (float*)sel3(a.out, mt);
         if (OUT == kOutF32Add) dst[o] = dst[o] + y;
         else dst[o] = y;
     }
@@ -94,7 +101,7 @@ template <int OUT>
 __device__ __forceinline__ void store_pair(const GemvArgs& a, int tok, int v0, int d0, int d1, float sa) {
     int mat, r0;
     resolve_row<OUT>(a, v0, mat, r0);
-    const float inv = 1.0f / (sa * a.sw[mat]);
+    const float inv = 1.0f / (sa * sel3(a.sw, mat));
     const float y0 = (float)d0 * inv;
     if (OUT == kOutRelu2) {
         const float u = (float)d1 * (1.0f / (sa * a.sw[1]));
@@ -123,6 +130,64 @@ __device__ __forceinline__ void store_pair(const GemvArgs& a, int tok, int v0, i
         uint16_t* dst = a.kc + ((size_t)g * a.cap + pos) * a.hd + d;
         dst[0] = f32_to_bf16(z0);
         dst[h2] = f32_to_bf16(z1);
+    }
+}
+
+// amax over the (normed) row, then s_a = 127 / max(amax, 1e-5) (quant.rs:100-113).
+template <typename Src>
+__device__ __forceinline__ float act_scale(Src x, int cols, const float* norm_w, float rr, float* red) {
+    float am = 0.0f;
+    if (threadIdx.x < kThreads)
+        for (int i = threadIdx.x; i < cols; i += kThreads)
+            am = fmaxf(am, fabsf(norm_w ? (x(i) * rr) * norm_w[i] : x(i)));
+    am = block_max(am, red);
+    return 127.0f / fmaxf(am, 1e-5f);
+}
+
+// RMSNorm (optional) + ActQuant (quant.rs:100-118) of one row into `dst` at
+// positions pos(i); s_a and sum(q) go to *sa / *qs (written by thread 0).
+// Rows of up to 256 * EPT values take one global pass with the values in
+// registers; longer rows re-read x (same arithmetic, same results).  Work is
+// done by the first 256 threads; every thread must call it (shared barriers).
+template <int EPT, typename Src, typename Pos>
+__device__ __forceinline__ void quantize_row_block(Src x0, int cols, int kp, const float* norm_w0, float eps,
+                                                   int8_t* dst, Pos pos, float* sa, int* qs, float* red) {
+    const Src x = x0.fresh();
+    const float* norm_w = norm_w0 ? launder(norm_w0) : nullptr;
+    const bool act = threadIdx.x < kThreads;
+    int s = 0;
+    float scale;
+    if (cols <= EPT * kThreads) {
+        float v[EPT];
+        load_norm_row<EPT>(x, cols, norm_w, eps, v, red);
+        float am = 0.0f;
+#pragma unroll
+        for (int e = 0; e < EPT; e++) am = fmaxf(am, fabsf(v[e]));
+        am = block_max(am, red);
+        scale = 127.0f / fmaxf(am, 1e-5f);
+#pragma unroll
+        for (int e = 0; e < EPT; e++) {
+            const int i = threadIdx.x + e * kThreads;
+            if (act && i < kp) {
+                const int qv = i < cols ? quant_one(v[e], scale) : 0;
+                dst[pos(i)] = (int8_t)qv;
+                s += qv;
+            }
+        }
+    } else {
+        const float rr = norm_factor_global(x, cols, norm_w, eps, red);
+        scale = act_scale(x, cols, norm_w, rr, red);
+        if (act)
+            for (int i = threadIdx.x; i < kp; i += kThreads) {
+                const int qv = i < cols ? quant_one(norm_w ? (x(i) * rr) * norm_w[i] : x(i), scale) : 0;
+                dst[pos(i)] = (int8_t)qv;
+                s += qv;
+            }
+    }
+    s = block_sum_i(s, (int*)red);
+    if (threadIdx.x == 0) {
+        *sa = scale;
+        *qs = s;
     }
 }
 

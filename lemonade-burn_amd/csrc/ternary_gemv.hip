@@ -31,60 +31,6 @@
 namespace lbt {
 
 
-__device__ __forceinline__ float normed(const float* xr, const float* norm_w, float rr, int i) {
-    return norm_w ? (xr[i] * rr) * norm_w[i] : xr[i];
-}
-
-// amax over the (normed) row, then s_a = 127 / max(amax, 1e-5) (quant.rs:100-113).
-__device__ __forceinline__ float act_scale(const float* xr, int cols, const float* norm_w, float rr, float* red) {
-    float am = 0.0f;
-    for (int i = threadIdx.x; i < cols; i += kThreads) am = fmaxf(am, fabsf(normed(xr, norm_w, rr, i)));
-    am = block_max(am, red);
-    return 127.0f / fmaxf(am, 1e-5f);
-}
-
-// RMSNorm (optional) + ActQuant of one row into `dst` at positions pos(i);
-// returns s_a and sum(q) through sa/qs (written by thread 0).  Rows of up to
-// 256 * EPT values take one global pass with the values in registers; longer
-// rows re-read x (same arithmetic, same results).
-template <int EPT, typename Pos>
-__device__ __forceinline__ void quantize_row_block(const float* xr, int cols, int kp, const float* norm_w, float eps,
-                                                   int8_t* dst, Pos pos, float* sa, int* qs, float* red) {
-    int s = 0;
-    float scale;
-    if (cols <= EPT * kThreads) {
-        float v[EPT];
-        load_norm_row<EPT>(xr, cols, norm_w, eps, v, red);
-        float am = 0.0f;
-#pragma unroll
-        for (int e = 0; e < EPT; e++) am = fmaxf(am, fabsf(v[e]));
-        am = block_max(am, red);
-        scale = 127.0f / fmaxf(am, 1e-5f);
-#pragma unroll
-        for (int e = 0; e < EPT; e++) {
-            const int i = threadIdx.x + e * kThreads;
-            if (i < kp) {
-                const int qv = i < cols ? quant_one(v[e], scale) : 0;
-                dst[pos(i)] = (int8_t)qv;
-                s += qv;
-            }
-        }
-    } else {
-        const float rr = norm_factor_global(xr, cols, norm_w, eps, red);
-        scale = act_scale(xr, cols, norm_w, rr, red);
-        for (int i = threadIdx.x; i < kp; i += kThreads) {
-            const int qv = i < cols ? quant_one(normed(xr, norm_w, rr, i), scale) : 0;
-            dst[pos(i)] = (int8_t)qv;
-            s += qv;
-        }
-    }
-    s = block_sum_i(s, (int*)red);
-    if (threadIdx.x == 0) {
-        *sa = scale;
-        *qs = s;
-    }
-}
-
 template <int T, int IN, int EPT>
 __device__ __forceinline__ void build_acts(const GemvArgs& a, int t0, int8_t* xq, float* sa, int* qs,
                                            float* red) {
@@ -104,7 +50,7 @@ __device__ __forceinline__ void build_acts(const GemvArgs& a, int t0, int8_t* xq
                 *(int4*)(dst + perm_pos(u << 4, C)) = *(const int4*)(src + (u << 4));
             if (threadIdx.x == 0) { sa[t] = a.qscale ? a.qscale[tok] : 1.0f; qs[t] = a.qsum[tok]; }
         } else {
-            quantize_row_block<EPT>(a.x + (size_t)tok * a.cols, a.cols, kp, a.norm_w, a.eps, dst,
+            quantize_row_block<EPT>(SrcF32{a.x + (size_t)tok * a.cols}, a.cols, kp, a.norm_w, a.eps, dst,
                                     [C](int i) { return perm_pos(i, C); }, &sa[t], &qs[t], red);
         }
     }
@@ -141,7 +87,7 @@ template <int L, int T, int NCH, int TILES, int IN, int OUT>
 __global__ __launch_bounds__(kThreads) void tgemv_kernel(GemvArgs a) {
     constexpr int R = 64 / L;
     extern __shared__ __align__(16) int8_t xq[];  // T * kp, permuted
-    __shared__ float red[8];
+    __shared__ float red[16];
     __shared__ float sa[T];
     __shared__ int qs[T];
     __shared__ int part[4][R][T];
@@ -160,7 +106,7 @@ __global__ __launch_bounds__(kThreads) void tgemv_kernel(GemvArgs a) {
         valid[k] = vr < a.total_rows;
         int mat, r;
         resolve_row<OUT>(a, valid[k] ? vr : 0, mat, r);
-        rowp[k] = (const uint4*)(a.w[mat] + (size_t)r * (size_t)(a.kp >> 2));
+        rowp[k] = (const uint4*)(sel3(a.w, mat) + (size_t)r * (size_t)(a.kp >> 2));
 #pragma unroll
         for (int i = 0; i < NCH; i++) {
             const int c = (i * 4 + w) * L + j;
@@ -229,9 +175,9 @@ __global__ __launch_bounds__(kThreads) void tgemv_kernel(GemvArgs a) {
 __global__ __launch_bounds__(kThreads) void quantize_kernel(const float* x, const float* norm_w, float eps,
                                                             int k, int kp, int8_t* q, float* scale,
                                                             int32_t* sum) {
-    __shared__ float red[8];
+    __shared__ float red[16];
     const int row = blockIdx.x;
-    quantize_row_block<32>(x + (size_t)row * k, k, kp, norm_w, eps, q + (size_t)row * kp, [](int i) { return i; },
+    quantize_row_block<32>(SrcF32{x + (size_t)row * k}, k, kp, norm_w, eps, q + (size_t)row * kp, [](int i) { return i; },
                            &scale[row], &sum[row], red);
 }
 

@@ -48,7 +48,7 @@ __global__ __launch_bounds__(kThreads) void tgemm_kernel(GemvArgs a) {
         bval[s] = vr < a.total_rows;
         int mat, r;
         resolve_row<OUT>(a, bval[s] ? vr : 0, mat, r);
-        brow[s] = (const uint4*)(a.w[mat] + (size_t)r * (size_t)(kp >> 2));
+        brow[s] = (const uint4*)(sel3(a.w, mat) + (size_t)r * (size_t)(kp >> 2));
     }
 
     int4 ast[APT];
