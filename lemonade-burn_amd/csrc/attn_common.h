@@ -61,8 +61,7 @@ __device__ __forceinline__ void attention_head(const float* q, int h, int nh, in
                     a = __builtin_fmaf(q8[2 * e + 1], bf16_to_f32((uint16_t)(wv[e] >> 16)), a);
                 }
             }
-#pragma unroll
-            for (int m = LK / 2; m >= 1; m >>= 1) a = a + __shfl_xor(a, m);
+            a = xor_sum_down<LK / 2>(a);
             if (j < vis) {
                 const float s = a * scaling;
                 if (cc == 0) sc[j] = s;
@@ -97,10 +96,9 @@ __device__ __forceinline__ void attention_head(const float* q, int h, int nh, in
                 acc[2 * e + 1] = __builtin_fmaf(pj, bf16_to_f32((uint16_t)(wv[e] >> 16)), acc[2 * e + 1]);
             }
         }
+    if constexpr (GW > 1) {
 #pragma unroll
-    for (int m = 1; m < GW; m <<= 1) {
-#pragma unroll
-        for (int e = 0; e < 8; e++) acc[e] = acc[e] + __shfl_xor(acc[e], m * LK);
+        for (int e = 0; e < 8; e++) acc[e] = xor_sum_up<LK>(acc[e]);
     }
     if (act && lane < LK) {
 #pragma unroll

@@ -125,11 +125,8 @@ __global__ __launch_bounds__(kThreads) void lmhead_kernel(const uint16_t* W, int
                     acc1 = dot8(a1[i], xs + 8 * c, acc1);
                 }
             }
-#pragma unroll
-            for (int m = 32; m >= 1; m >>= 1) {
-                acc0 = acc0 + __shfl_xor(acc0, m);
-                acc1 = acc1 + __shfl_xor(acc1, m);
-            }
+            acc0 = wave_sum(acc0);
+            acc1 = wave_sum(acc1);
             if (lane == 0) {
                 if (logits) logits[(size_t)t * rows + r] = acc0;
                 unsigned long long k = argmax_key(acc0, (uint32_t)r);
@@ -146,8 +143,7 @@ __global__ __launch_bounds__(kThreads) void lmhead_kernel(const uint16_t* W, int
             const uint4* wr = (const uint4*)(W + (size_t)r * cols);
             float acc = 0.0f;
             for (int c = lane; c < nchunks; c += 64) acc = dot8(ld_stream(wr + c), xs + 8 * c, acc);
-#pragma unroll
-            for (int m = 32; m >= 1; m >>= 1) acc = acc + __shfl_xor(acc, m);
+            acc = wave_sum(acc);
             if (lane == 0) {
                 if (logits) logits[(size_t)t * rows + r] = acc;
                 const unsigned long long k = argmax_key(acc, (uint32_t)r);

@@ -165,8 +165,7 @@ __device__ __forceinline__ void phase_compute(const GemvArgs& g, int vr0, int nr
                 }
             }
         }
-#pragma unroll
-        for (int o = L / 2; o >= 1; o >>= 1) acc += __shfl_xor(acc, o);
+        acc = xor_sum_down_i<L / 2>(acc);
         const int dot = acc - qs;
         const int lr = t * R + rg, vr = vr0 + lr;
         const bool ok = lr < nrows && vr < g.total_rows;

@@ -20,9 +20,18 @@ constexpr int kThreads = 256;    // threads per workgroup everywhere
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+#define LBT_GLOBAL __attribute__((address_space(1)))
+
+// Load through the global address space (global_load rather than flat_load,
+// which also occupies the LDS counter); p must point to device memory.
+template <typename T>
+__device__ __forceinline__ T gload(const T* p) {
+    return *(const LBT_GLOBAL T*)p;
+}
+
 // 16-byte streaming load (nontemporal: the weights are read once per token).
 __device__ __forceinline__ uint4 ld_stream(const uint4* p) {
-    const u32x4 v = __builtin_nontemporal_load((const u32x4*)p);
+    const u32x4 v = __builtin_nontemporal_load((const LBT_GLOBAL u32x4*)p);
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
@@ -70,56 +79,151 @@ __device__ __forceinline__ float lbt_expf(float x) {
     return p * __uint_as_float((uint32_t)(ni + 127) << 23);
 }
 
+// Cross-lane exchange without LDS: xor_pair<M>(v) returns (a, b) with
+// {a, b} = {v[l], v[l ^ M]} at every lane l (the order within the pair may
+// differ between lanes, which commutative combines do not see).
+//   M = 1, 2:  DPP quad_perm;      M = 4: two DPP row rotates (row_ror:n
+//   reads lane (i - n) mod 16: by 12 for lane banks 0 and 2, by 4 for banks
+//   1 and 3);   M = 8: DPP row_ror:8;
+//   M = 16, 32: v_permlane16_swap / v_permlane32_swap (gfx950).
+// Every lane of the wavefront must be active.
+template <int M>
+__device__ __forceinline__ void xor_pair(uint32_t v, uint32_t& a, uint32_t& b) {
+    static_assert(M == 1 || M == 2 || M == 4 || M == 8 || M == 16 || M == 32, "xor distance");
+    if constexpr (M == 32) {
+        const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        a = r[0];
+        b = r[1];
+    } else if constexpr (M == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        a = r[0];
+        b = r[1];
+    } else {
+        const int iv = (int)v;
+        int p;
+        if constexpr (M == 1) p = __builtin_amdgcn_update_dpp(0, iv, 0xB1, 0xf, 0xf, false);
+        else if constexpr (M == 2) p = __builtin_amdgcn_update_dpp(0, iv, 0x4E, 0xf, 0xf, false);
+        else if constexpr (M == 8) p = __builtin_amdgcn_update_dpp(0, iv, 0x128, 0xf, 0xf, false);
+        else {
+            p = __builtin_amdgcn_update_dpp(0, iv, 0x12C, 0xf, 0x5, false);
+            p = __builtin_amdgcn_update_dpp(p, iv, 0x124, 0xf, 0xA, false);
+        }
+        a = v;
+        b = (uint32_t)p;
+    }
+}
+
+// v[l] + v[l ^ M] (bit-identical to v + __shfl_xor(v, M)).
+template <int M>
+__device__ __forceinline__ float xor_add(float v) {
+    uint32_t a, b;
+    xor_pair<M>(__float_as_uint(v), a, b);
+    return __uint_as_float(a) + __uint_as_float(b);
+}
+template <int M>
+__device__ __forceinline__ int xor_add_i(int v) {
+    uint32_t a, b;
+    xor_pair<M>((uint32_t)v, a, b);
+    return (int)a + (int)b;
+}
+template <int M>
+__device__ __forceinline__ float xor_max(float v) {
+    uint32_t a, b;
+    xor_pair<M>(__float_as_uint(v), a, b);
+    return fmaxf(__uint_as_float(a), __uint_as_float(b));
+}
+
+// Butterfly steps M, M/2, ..., 1 (descending), as
+// `for (m = M; m >= 1; m >>= 1) v = v + __shfl_xor(v, m)`.
+template <int M>
+__device__ __forceinline__ float xor_sum_down(float v) {
+    if constexpr (M >= 1) {
+        v = xor_add<M>(v);
+        return xor_sum_down<M / 2>(v);
+    }
+    return v;
+}
+template <int M>
+__device__ __forceinline__ int xor_sum_down_i(int v) {
+    if constexpr (M >= 1) {
+        v = xor_add_i<M>(v);
+        return xor_sum_down_i<M / 2>(v);
+    }
+    return v;
+}
+
+// Butterfly steps M, 2M, ..., 32 (ascending), as
+// `for (m = M; m <= 32; m <<= 1) v = v + __shfl_xor(v, m)`.
+template <int M>
+__device__ __forceinline__ float xor_sum_up(float v) {
+    if constexpr (M <= 32) {
+        v = xor_add<M>(v);
+        return xor_sum_up<M * 2>(v);
+    }
+    return v;
+}
+
 // xor butterfly over the 64 lanes of a wavefront: every lane ends with the
 // same value, lane l having added v[l] + v[l ^ m] for m = 32, 16, ..., 1.
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v = v + __shfl_xor(v, m);
-    return v;
-}
-
-// Block sum of one value per thread (blockDim.x == 256): wave butterflies,
-// then (w0 + w1) + (w2 + w3).  `red` >= 16 floats of LDS (workgroups of up
-// to 1024 threads; only the first four waves' sums are used).
-__device__ __forceinline__ float block_sum(float v, float* red) {
-    v = wave_sum(v);
-    const int w = threadIdx.x >> 6;
-    if ((threadIdx.x & 63) == 0) red[w] = v;
-    __syncthreads();
-    float r = (red[0] + red[1]) + (red[2] + red[3]);
-    __syncthreads();
-    return r;
-}
+__device__ __forceinline__ float wave_sum(float v) { return xor_sum_down<32>(v); }
 
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m));
-    return v;
+    v = xor_max<32>(v);
+    v = xor_max<16>(v);
+    v = xor_max<8>(v);
+    v = xor_max<4>(v);
+    v = xor_max<2>(v);
+    return xor_max<1>(v);
 }
 
-__device__ __forceinline__ int wave_sum_i(int v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
-    return v;
-}
+__device__ __forceinline__ int wave_sum_i(int v) { return xor_sum_down_i<32>(v); }
 
-// Block max over the first 256 threads; `red` >= 16 floats of LDS.
-__device__ __forceinline__ float block_max(float v, float* red) {
+// Block reductions over the first 256 threads (four wavefronts): wavefront
+// results of waves 0..3 go to red[4*slot .. 4*slot+3], one barrier, then
+// sum (w0 + w1) + (w2 + w3) / max / integer sum.  No trailing barrier: a slot
+// may be written again only after two further barriers, which holds when
+// successive reductions rotate through slots 0, 1, 2 or a barrier separates
+// them from the next use.  `red` >= 16 floats of LDS; larger workgroups call
+// with all threads (the barrier is shared) and get the first four waves'
+// result.
+__device__ __forceinline__ float block_sum_slot(float v, float* red, int slot) {
+    v = wave_sum(v);
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0 && w < 4) red[4 * slot + w] = v;
+    __syncthreads();
+    const float* r = red + 4 * slot;
+    return (r[0] + r[1]) + (r[2] + r[3]);
+}
+__device__ __forceinline__ float block_max_slot(float v, float* red, int slot) {
     v = wave_max(v);
     const int w = threadIdx.x >> 6;
-    if ((threadIdx.x & 63) == 0) red[w] = v;
+    if ((threadIdx.x & 63) == 0 && w < 4) red[4 * slot + w] = v;
     __syncthreads();
-    float r = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const float* r = red + 4 * slot;
+    return fmaxf(fmaxf(r[0], r[1]), fmaxf(r[2], r[3]));
+}
+__device__ __forceinline__ int block_sum_i_slot(int v, int* red, int slot) {
+    v = wave_sum_i(v);
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0 && w < 4) red[4 * slot + w] = v;
+    __syncthreads();
+    const int* r = red + 4 * slot;
+    return r[0] + r[1] + r[2] + r[3];
+}
+
+// The same reductions followed by a barrier, so `red` is free on return.
+__device__ __forceinline__ float block_sum(float v, float* red) {
+    const float r = block_sum_slot(v, red, 0);
     __syncthreads();
     return r;
 }
-
-__device__ __forceinline__ int block_sum_i(int v, int* red) {
-    v = wave_sum_i(v);
-    const int w = threadIdx.x >> 6;
-    if ((threadIdx.x & 63) == 0) red[w] = v;
+__device__ __forceinline__ float block_max(float v, float* red) {
+    const float r = block_max_slot(v, red, 0);
     __syncthreads();
-    int r = red[0] + red[1] + red[2] + red[3];
+    return r;
+}
+__device__ __forceinline__ int block_sum_i(int v, int* red) {
+    const int r = block_sum_i_slot(v, red, 0);
     __syncthreads();
     return r;
 }
@@ -150,12 +254,12 @@ __device__ __forceinline__ int fresh_tid() {
 // embedding, widened exactly).
 struct SrcF32 {
     const float* p;
-    __device__ __forceinline__ float operator()(int i) const { return p[i]; }
+    __device__ __forceinline__ float operator()(int i) const { return gload(p + i); }
     __device__ __forceinline__ SrcF32 fresh() const { return SrcF32{launder(p)}; }
 };
 struct SrcBf16 {
     const uint16_t* p;
-    __device__ __forceinline__ float operator()(int i) const { return bf16_to_f32(p[i]); }
+    __device__ __forceinline__ float operator()(int i) const { return bf16_to_f32(gload(p + i)); }
     __device__ __forceinline__ SrcBf16 fresh() const { return SrcBf16{launder(p)}; }
 };
 
@@ -164,6 +268,7 @@ struct SrcBf16 {
 // 267-272) in place: r = 1 / sqrt(sum(x^2)/cols + eps) with the sum of squares
 // accumulated per thread by fused multiply-adds in ascending i and combined by
 // block_sum; v = (x * r) * w.  Requires cols <= 256 * EPT.  One global pass.
+// Uses reduction slot 0 of `red` (see block_sum_slot).
 // Only the first 256 threads of the workgroup take part; larger workgroups
 // call it with all threads (the barriers are shared) and get zeros elsewhere.
 template <int EPT, typename Src>
@@ -175,14 +280,14 @@ __device__ __forceinline__ void load_norm_row(Src x, int cols, const float* norm
     for (int e = 0; e < EPT; e++) {
         const int i = threadIdx.x + e * kThreads;
         v[e] = (act && i < cols) ? x(i) : 0.0f;
-        nw[e] = (act && norm_w && i < cols) ? norm_w[i] : 0.0f;
+        nw[e] = (act && norm_w && i < cols) ? gload(norm_w + i) : 0.0f;
     }
     if (!norm_w) return;
     float p = 0.0f;
 #pragma unroll
     for (int e = 0; e < EPT; e++)
         if (act && threadIdx.x + e * kThreads < cols) p = __builtin_fmaf(v[e], v[e], p);
-    const float ss = block_sum(p, red);
+    const float ss = block_sum_slot(p, red, 0);
     const float r = 1.0f / __builtin_sqrtf(ss / (float)cols + eps);
 #pragma unroll
     for (int e = 0; e < EPT; e++) v[e] = (v[e] * r) * nw[e];

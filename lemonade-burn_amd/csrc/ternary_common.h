@@ -30,11 +30,32 @@ struct GemvArgs {
     uint16_t* vc;
 };
 
-// Element i (0..2) of a 3-array by selects: a runtime index into a local
-// struct would put the struct in scratch memory.
+// Element i (0..2) of a 3-array of uniform values by selects between scalar
+// registers.  A runtime index into a local struct would put the struct in
+// scratch memory, and a plain select of kernel-argument fields is turned into
+// a vector load from the argument segment (one memory round trip before the
+// first weight load); the elements are pinned to scalar registers first.
+__device__ __forceinline__ uint32_t pin_s(uint32_t v) {
+    v = __builtin_amdgcn_readfirstlane(v);
+    asm volatile("" : "+s"(v));
+    return v;
+}
 template <typename T>
-__device__ __forceinline__ T sel3(const T (&v)[3], int i) {
-    return i == 0 ? v[0] : (i == 1 ? v[1] : v[2]);
+__device__ __forceinline__ T* sel3(T* const (&v)[3], int i) {
+    T* a = launder(v[0]);
+    T* b = launder(v[1]);
+    T* c = launder(v[2]);
+    return i == 0 ? a : (i == 1 ? b : c);
+}
+__device__ __forceinline__ int sel3(const int (&v)[3], int i) {
+    const int a = (int)pin_s((uint32_t)v[0]), b = (int)pin_s((uint32_t)v[1]), c = (int)pin_s((uint32_t)v[2]);
+    return i == 0 ? a : (i == 1 ? b : c);
+}
+__device__ __forceinline__ float sel3(const float (&v)[3], int i) {
+    const float a = __uint_as_float(pin_s(__float_as_uint(v[0])));
+    const float b = __uint_as_float(pin_s(__float_as_uint(v[1])));
+    const float c = __uint_as_float(pin_s(__float_as_uint(v[2])));
+    return i == 0 ? a : (i == 1 ? b : c);
 }
 
 // Virtual row -> (matrix, row).  kOutRelu2 interleaves gate/up rows
@@ -149,6 +170,8 @@ __device__ __forceinline__ float act_scale(Src x, int cols, const float* norm_w,
 // Rows of up to 256 * EPT values take one global pass with the values in
 // registers; longer rows re-read x (same arithmetic, same results).  Work is
 // done by the first 256 threads; every thread must call it (shared barriers).
+// Reduction slots 0..2 of `red` are in use until two more barriers have
+// passed (successive calls are safe; see block_sum_slot).
 template <int EPT, typename Src, typename Pos>
 __device__ __forceinline__ void quantize_row_block(Src x0, int cols, int kp, const float* norm_w0, float eps,
                                                    int8_t* dst, Pos pos, float* sa, int* qs, float* red) {
@@ -163,7 +186,7 @@ __device__ __forceinline__ void quantize_row_block(Src x0, int cols, int kp, con
         float am = 0.0f;
 #pragma unroll
         for (int e = 0; e < EPT; e++) am = fmaxf(am, fabsf(v[e]));
-        am = block_max(am, red);
+        am = block_max_slot(am, red, 1);
         scale = 127.0f / fmaxf(am, 1e-5f);
 #pragma unroll
         for (int e = 0; e < EPT; e++) {
@@ -184,7 +207,7 @@ __device__ __forceinline__ void quantize_row_block(Src x0, int cols, int kp, con
                 s += qv;
             }
     }
-    s = block_sum_i(s, (int*)red);
+    s = block_sum_i_slot(s, (int*)red, 2);
     if (threadIdx.x == 0) {
         *sa = scale;
         *qs = s;

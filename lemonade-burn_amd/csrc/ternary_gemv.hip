@@ -28,6 +28,18 @@
 
 #include <stdlib.h>
 
+#ifdef LBT_GEMV_TRACE
+// Debug build only: per-workgroup wall-clock stamps of the GEMV phases.
+__device__ unsigned long long lbt_gemv_trace[4096 * 8];
+#define GTR(i) \
+    if (threadIdx.x == 0 && blockIdx.y == 0 && blockIdx.x < 4096) lbt_gemv_trace[blockIdx.x * 8 + (i)] = wall_clock64();
+extern "C" int lbt_debug_gemv_trace(unsigned long long* out) {
+    return (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(lbt_gemv_trace), sizeof(lbt_gemv_trace));
+}
+#else
+#define GTR(i)
+#endif
+
 namespace lbt {
 
 
@@ -61,10 +73,12 @@ __device__ __forceinline__ int row_dot(const int (&part)[4][R][T], int rr, int t
     return part[0][rr][t] + part[1][rr][t] + part[2][rr][t] + part[3][rr][t] - qsum;
 }
 
+// Outputs of one tile; thread `tid` (0 .. R*T-1, others return) writes one
+// (row, token) or one row pair.
 template <int R, int T, int OUT>
 __device__ __forceinline__ void epilogue(const GemvArgs& a, int vr0, int t0, const int (&part)[4][R][T],
-                                         const float* sa, const int* qs) {
-    const int tid = threadIdx.x;
+                                         const float* sa, const int* qs, int tid) {
+    if (tid < 0) return;
     if (OUT == kOutRelu2 || OUT == kOutQKV) {
         if (tid >= (R / 2) * T) return;
         const int p = tid / T, t = tid % T;
@@ -90,8 +104,9 @@ __global__ __launch_bounds__(kThreads) void tgemv_kernel(GemvArgs a) {
     __shared__ float red[16];
     __shared__ float sa[T];
     __shared__ int qs[T];
-    __shared__ int part[4][R][T];
+    __shared__ int part[TILES][4][R][T];
 
+    GTR(0)
     const int tid = threadIdx.x, w = tid >> 6, ln = tid & 63;
     const int rg = ln / L, j = ln % L;
     const int t0 = blockIdx.y * T;
@@ -114,8 +129,10 @@ __global__ __launch_bounds__(kThreads) void tgemv_kernel(GemvArgs a) {
         }
     }
 
+    GTR(1)
     build_acts<T, IN, NCH * 8>(a, t0, xq, sa, qs, red);
     __syncthreads();
+    GTR(2)
 
 #pragma unroll
     for (int k = 0; k < TILES; k++) {
@@ -155,19 +172,20 @@ __global__ __launch_bounds__(kThreads) void tgemv_kernel(GemvArgs a) {
                 wv[k][i] = (valid[k] && c < C) ? ld_stream(rowp[k] + c) : make_uint4(0, 0, 0, 0);
             }
         }
+        if (k == 0) { GTR(3) }
 #pragma unroll
-        for (int t = 0; t < T; t++) {
-#pragma unroll
-            for (int o = L / 2; o >= 1; o >>= 1) acc[t] += __shfl_xor(acc[t], o);
-        }
+        for (int t = 0; t < T; t++) acc[t] = xor_sum_down_i<L / 2>(acc[t]);
         if (j == 0) {
 #pragma unroll
-            for (int t = 0; t < T; t++) part[w][rg][t] = acc[t];
+            for (int t = 0; t < T; t++) part[k][w][rg][t] = acc[t];
         }
-        __syncthreads();
-        epilogue<R, T, OUT>(a, (blockIdx.x * TILES + k) * R, t0, part, sa, qs);
-        if (k + 1 < TILES) __syncthreads();
     }
+    __syncthreads();
+    // one barrier for all tiles: tile k's outputs go to threads k*R*T ..
+#pragma unroll
+    for (int k = 0; k < TILES; k++)
+        epilogue<R, T, OUT>(a, (blockIdx.x * TILES + k) * R, t0, part[k], sa, qs, tid - k * R * T);
+    GTR(4)
 }
 
 // Standalone quantizer: one workgroup per row, writes q [m, kp] (zero padded),
