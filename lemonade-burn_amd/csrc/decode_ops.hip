@@ -93,7 +93,7 @@ __global__ __launch_bounds__(kThreads) void lmhead_kernel(const uint16_t* W, int
         load_norm_row<16>(SrcF32{xr}, cols, norm_w, eps, v, red);
 #pragma unroll
         for (int e = 0; e < 16; e++)
-            if (tid + e * kThreads < cols) xs[tid + e * kThreads] = v[e];
+            if (tid < kThreads && row_elem(tid, e) < cols) xs[row_elem(tid, e)] = v[e];
     } else {
         const float rr = norm_factor_global(SrcF32{xr}, cols, norm_w, eps, red);
         for (int i = tid; i < cols; i += kThreads) xs[i] = norm_w ? (xr[i] * rr) * norm_w[i] : xr[i];

@@ -19,6 +19,8 @@ constexpr int kBlockBytes = 32;  // bytes per LB2 block (pack.rs:19)
 constexpr int kThreads = 256;    // threads per workgroup everywhere
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 #define LBT_GLOBAL __attribute__((address_space(1)))
 
@@ -48,11 +50,9 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
 // quant_one (crates/lb-ternary/src/quant.rs:116-118):
 // (v*scale).round_ties_even().clamp(-128, 127) as i8, NaN -> 0.
 __device__ __forceinline__ int quant_one(float v, float scale) {
-    float y = __builtin_rintf(v * scale);
+    const float y = __builtin_rintf(v * scale);
     if (y != y) return 0;
-    y = y < -128.0f ? -128.0f : y;
-    y = y > 127.0f ? 127.0f : y;
-    return (int)y;
+    return (int)__builtin_amdgcn_fmed3f(y, -128.0f, 127.0f);
 }
 
 // exp(x) for the softmax: Cody & Waite two-constant reduction x = n ln2 + r,
@@ -255,51 +255,125 @@ __device__ __forceinline__ int fresh_tid() {
 struct SrcF32 {
     const float* p;
     __device__ __forceinline__ float operator()(int i) const { return gload(p + i); }
+    // four elements i..i+3 at once when vec_ok (16-byte aligned groups)
+    __device__ __forceinline__ bool vec_ok(int cols) const {
+        return (cols & 3) == 0 && ((uintptr_t)p & 15) == 0;
+    }
+    __device__ __forceinline__ void load4(int i, float* o) const {
+        const f32x4 v = gload((const f32x4*)(p + i));
+        o[0] = v.x;
+        o[1] = v.y;
+        o[2] = v.z;
+        o[3] = v.w;
+    }
     __device__ __forceinline__ SrcF32 fresh() const { return SrcF32{launder(p)}; }
 };
 struct SrcBf16 {
     const uint16_t* p;
     __device__ __forceinline__ float operator()(int i) const { return bf16_to_f32(gload(p + i)); }
+    __device__ __forceinline__ bool vec_ok(int cols) const {
+        return (cols & 3) == 0 && ((uintptr_t)p & 7) == 0;
+    }
+    __device__ __forceinline__ void load4(int i, float* o) const {
+        const u32x2 v = gload((const u32x2*)(p + i));
+        o[0] = __uint_as_float(v.x << 16);
+        o[1] = __uint_as_float(v.x & 0xffff0000u);
+        o[2] = __uint_as_float(v.y << 16);
+        o[3] = __uint_as_float(v.y & 0xffff0000u);
+    }
     __device__ __forceinline__ SrcBf16 fresh() const { return SrcBf16{launder(p)}; }
 };
 
-// Loads row x[0..cols) into registers, v[e] = x[threadIdx.x + 256 e] (0 past
-// cols), and if norm_w is set applies rms_norm (crates/lb-model/src/model.rs:
-// 267-272) in place: r = 1 / sqrt(sum(x^2)/cols + eps) with the sum of squares
-// accumulated per thread by fused multiply-adds in ascending i and combined by
-// block_sum; v = (x * r) * w.  Requires cols <= 256 * EPT.  One global pass.
-// Uses reduction slot 0 of `red` (see block_sum_slot).
-// Only the first 256 threads of the workgroup take part; larger workgroups
-// call it with all threads (the barriers are shared) and get zeros elsewhere.
-template <int EPT, typename Src>
-__device__ __forceinline__ void load_norm_row(Src x, int cols, const float* norm_w, float eps, float (&v)[EPT],
-                                              float* red) {
-    const bool act = threadIdx.x < kThreads;
+// Element layout of the row prologues: thread t (< 256) holds EPT/4 groups of
+// four consecutive elements, v[4g + k] = x[1024 g + 4 t + k].  Rows of up to
+// 256 * EPT elements are held in registers (one global pass).
+__device__ __forceinline__ int row_elem(int tid, int e) { return 1024 * (e >> 2) + 4 * tid + (e & 3); }
+
+template <int EPT>
+struct RowRegs {
+    static_assert(EPT % 4 == 0, "groups of four");
+    float v[EPT];
     float nw[EPT];
+};
+
+// Issues the loads of row x[0..cols) (0 past cols) and, if norm_w is set, of
+// the norm weights, into r.  Only the first 256 threads load.
+template <int EPT, typename Src>
+__device__ __forceinline__ void row_load(Src x, int cols, const float* norm_w, RowRegs<EPT>& r) {
+    const int tid = (int)threadIdx.x;
+    const bool act = tid < kThreads;
+    const bool vec = x.vec_ok(cols) && (!norm_w || ((uintptr_t)norm_w & 15) == 0);
 #pragma unroll
-    for (int e = 0; e < EPT; e++) {
-        const int i = threadIdx.x + e * kThreads;
-        v[e] = (act && i < cols) ? x(i) : 0.0f;
-        nw[e] = (act && norm_w && i < cols) ? gload(norm_w + i) : 0.0f;
+    for (int g = 0; g < EPT / 4; g++) {
+        const int i0 = 1024 * g + 4 * tid;
+        if (vec && act && i0 < cols) {
+            x.load4(i0, &r.v[4 * g]);
+            if (norm_w) {
+                const f32x4 w = gload((const f32x4*)(norm_w + i0));
+                r.nw[4 * g] = w.x;
+                r.nw[4 * g + 1] = w.y;
+                r.nw[4 * g + 2] = w.z;
+                r.nw[4 * g + 3] = w.w;
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int i = i0 + k;
+                r.v[4 * g + k] = (!vec && act && i < cols) ? x(i) : 0.0f;
+                r.nw[4 * g + k] = (!vec && act && norm_w && i < cols) ? gload(norm_w + i) : 0.0f;
+            }
+        }
+        if (!norm_w) {
+#pragma unroll
+            for (int k = 0; k < 4; k++) r.nw[4 * g + k] = 0.0f;
+        }
     }
+}
+
+// rms_norm (crates/lb-model/src/model.rs:267-272) of the loaded row, in place,
+// when norm_w is set: r = 1 / sqrt(sum(x^2)/cols + eps), with each thread's
+// sum of squares accumulated by fused multiply-adds over its elements in the
+// order v[0], v[1], ... (ascending i) and combined by block_sum; then
+// v = (x * r) * w.  Uses reduction slot 0 of `red` (see block_sum_slot).
+template <int EPT>
+__device__ __forceinline__ void row_norm(RowRegs<EPT>& r, int cols, const float* norm_w, float eps, float* red) {
     if (!norm_w) return;
+    const int tid = (int)threadIdx.x;
+    const bool act = tid < kThreads;
     float p = 0.0f;
 #pragma unroll
     for (int e = 0; e < EPT; e++)
-        if (act && threadIdx.x + e * kThreads < cols) p = __builtin_fmaf(v[e], v[e], p);
+        if (act && row_elem(tid, e) < cols) p = __builtin_fmaf(r.v[e], r.v[e], p);
     const float ss = block_sum_slot(p, red, 0);
-    const float r = 1.0f / __builtin_sqrtf(ss / (float)cols + eps);
+    const float f = 1.0f / __builtin_sqrtf(ss / (float)cols + eps);
 #pragma unroll
-    for (int e = 0; e < EPT; e++) v[e] = (v[e] * r) * nw[e];
+    for (int e = 0; e < EPT; e++) r.v[e] = (r.v[e] * f) * r.nw[e];
 }
 
-// Same result for rows longer than 256 * EPT, re-reading x from memory.
+// row_load + row_norm: v[e] = normed x[row_elem(threadIdx.x, e)].  Requires
+// cols <= 256 * EPT.  Only the first 256 threads of the workgroup take part;
+// larger workgroups call it with all threads (the barriers are shared) and get
+// zeros elsewhere.
+template <int EPT, typename Src>
+__device__ __forceinline__ void load_norm_row(Src x, int cols, const float* norm_w, float eps, float (&v)[EPT],
+                                              float* red) {
+    RowRegs<EPT> r;
+    row_load<EPT>(x, cols, norm_w, r);
+    row_norm<EPT>(r, cols, norm_w, eps, red);
+#pragma unroll
+    for (int e = 0; e < EPT; e++) v[e] = r.v[e];
+}
+
+// Same result for rows longer than 256 * EPT, re-reading x from memory (same
+// per-thread element order).
 template <typename Src>
 __device__ __forceinline__ float norm_factor_global(Src x, int cols, const float* norm_w, float eps, float* red) {
     if (!norm_w) return 1.0f;
     float p = 0.0f;
-    if (threadIdx.x < kThreads)
-        for (int i = threadIdx.x; i < cols; i += kThreads) p = __builtin_fmaf(x(i), x(i), p);
+    const int tid = (int)threadIdx.x;
+    if (tid < kThreads)
+        for (int i0 = 4 * tid; i0 < cols; i0 += 1024)
+            for (int i = i0; i < i0 + 4 && i < cols; i++) p = __builtin_fmaf(x(i), x(i), p);
     const float ss = block_sum(p, red);
     return 1.0f / __builtin_sqrtf(ss / (float)cols + eps);
 }

@@ -5,6 +5,11 @@
 #include "lbt_device.h"
 #include "lbt_internal.h"
 
+// Optional phase stamps of the activation prologue (debug builds of the GEMV).
+#ifndef LBT_QTR
+#define LBT_QTR(i)
+#endif
+
 namespace lbt {
 
 struct GemvArgs {
@@ -165,48 +170,76 @@ __device__ __forceinline__ float act_scale(Src x, int cols, const float* norm_w,
     return 127.0f / fmaxf(am, 1e-5f);
 }
 
-// RMSNorm (optional) + ActQuant (quant.rs:100-118) of one row into `dst` at
-// positions pos(i); s_a and sum(q) go to *sa / *qs (written by thread 0).
-// Rows of up to 256 * EPT values take one global pass with the values in
-// registers; longer rows re-read x (same arithmetic, same results).  Work is
-// done by the first 256 threads; every thread must call it (shared barriers).
-// Reduction slots 0..2 of `red` are in use until two more barriers have
-// passed (successive calls are safe; see block_sum_slot).
+// ActQuant (quant.rs:100-118) of a row already in registers (row_load, and
+// row_norm applied here when norm_w is set) into `dst` at positions pos(i),
+// four bytes per store (pos keeps each 4-aligned group contiguous); zeros
+// fill [cols, kp).  s_a and sum(q) go to *sa / *qs (written by thread 0).
+// Requires kp <= 256 * EPT.  Work is done by the first 256 threads; every
+// thread must call it (shared barriers).  Reduction slots 0..2 of `red` are
+// in use until two more barriers have passed (successive calls are safe; see
+// block_sum_slot).
+template <int EPT, typename Pos>
+__device__ __forceinline__ void quantize_row_regs(RowRegs<EPT>& r, int cols, int kp, const float* norm_w, float eps,
+                                                  int8_t* dst, Pos pos, float* sa, int* qs, float* red) {
+    const int tid = (int)threadIdx.x;
+    const bool act = tid < kThreads;
+    row_norm<EPT>(r, cols, norm_w, eps, red);
+    float am = 0.0f;
+#pragma unroll
+    for (int e = 0; e < EPT; e++) am = fmaxf(am, fabsf(r.v[e]));
+    LBT_QTR(5)
+    am = block_max_slot(am, red, 1);
+    const float scale = 127.0f / fmaxf(am, 1e-5f);
+    LBT_QTR(6)
+    int s = 0;
+#pragma unroll
+    for (int g = 0; g < EPT / 4; g++) {
+        const int i0 = 1024 * g + 4 * tid;
+        if (act && i0 < kp) {
+            uint32_t word = 0;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int qv = i0 + k < cols ? quant_one(r.v[4 * g + k], scale) : 0;
+                s += qv;
+                word |= ((uint32_t)qv & 0xffu) << (8 * k);
+            }
+            *(uint32_t*)(dst + pos(i0)) = word;
+        }
+    }
+    LBT_QTR(7)
+    s = block_sum_i_slot(s, (int*)red, 2);
+    LBT_QTR(8)
+    if (tid == 0) {
+        *sa = scale;
+        *qs = s;
+    }
+}
+
+// RMSNorm (optional) + ActQuant of one row (loads it first).  Rows of up to
+// 256 * EPT values take one global pass with the values in registers; longer
+// rows re-read x (same arithmetic, same results).  Same contract as
+// quantize_row_regs.
 template <int EPT, typename Src, typename Pos>
 __device__ __forceinline__ void quantize_row_block(Src x0, int cols, int kp, const float* norm_w0, float eps,
                                                    int8_t* dst, Pos pos, float* sa, int* qs, float* red) {
     const Src x = x0.fresh();
     const float* norm_w = norm_w0 ? launder(norm_w0) : nullptr;
+    if (kp <= EPT * kThreads) {
+        RowRegs<EPT> r;
+        row_load<EPT>(x, cols, norm_w, r);
+        quantize_row_regs<EPT>(r, cols, kp, norm_w, eps, dst, pos, sa, qs, red);
+        return;
+    }
     const bool act = threadIdx.x < kThreads;
     int s = 0;
-    float scale;
-    if (cols <= EPT * kThreads) {
-        float v[EPT];
-        load_norm_row<EPT>(x, cols, norm_w, eps, v, red);
-        float am = 0.0f;
-#pragma unroll
-        for (int e = 0; e < EPT; e++) am = fmaxf(am, fabsf(v[e]));
-        am = block_max_slot(am, red, 1);
-        scale = 127.0f / fmaxf(am, 1e-5f);
-#pragma unroll
-        for (int e = 0; e < EPT; e++) {
-            const int i = threadIdx.x + e * kThreads;
-            if (act && i < kp) {
-                const int qv = i < cols ? quant_one(v[e], scale) : 0;
-                dst[pos(i)] = (int8_t)qv;
-                s += qv;
-            }
+    const float rr = norm_factor_global(x, cols, norm_w, eps, red);
+    const float scale = act_scale(x, cols, norm_w, rr, red);
+    if (act)
+        for (int i = threadIdx.x; i < kp; i += kThreads) {
+            const int qv = i < cols ? quant_one(norm_w ? (x(i) * rr) * norm_w[i] : x(i), scale) : 0;
+            dst[pos(i)] = (int8_t)qv;
+            s += qv;
         }
-    } else {
-        const float rr = norm_factor_global(x, cols, norm_w, eps, red);
-        scale = act_scale(x, cols, norm_w, rr, red);
-        if (act)
-            for (int i = threadIdx.x; i < kp; i += kThreads) {
-                const int qv = i < cols ? quant_one(norm_w ? (x(i) * rr) * norm_w[i] : x(i), scale) : 0;
-                dst[pos(i)] = (int8_t)qv;
-                s += qv;
-            }
-    }
     s = block_sum_i_slot(s, (int*)red, 2);
     if (threadIdx.x == 0) {
         *sa = scale;

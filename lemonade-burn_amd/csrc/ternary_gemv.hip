@@ -22,23 +22,32 @@
 //   * epilogues: i32 out, f32 y = dot * (1/(s_a*s_w)) (gemm.rs:141,150),
 //     residual add (model.rs:359,365), and relu(g)^2 * u for interleaved
 //     gate/up rows (model.rs:362-363).
+#include <hip/hip_runtime.h>
+
+#ifdef LBT_GEMV_TRACE
+// Debug build only: per-workgroup wall-clock stamps of the GEMV phases.
+__device__ unsigned long long lbt_gemv_trace[4096 * 16];
+#define GTR(i) \
+    if (threadIdx.x == 0 && blockIdx.y == 0 && blockIdx.x < 4096) lbt_gemv_trace[blockIdx.x * 16 + (i)] = wall_clock64();
+extern "C" int lbt_debug_gemv_trace(unsigned long long* out) {
+    return (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(lbt_gemv_trace), sizeof(lbt_gemv_trace));
+}
+extern "C" int lbt_debug_gemv_clear() {
+    void* p;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(lbt_gemv_trace)) != hipSuccess) return -1;
+    return (int)hipMemset(p, 0, sizeof(lbt_gemv_trace));
+}
+#define LBT_QTR(i) GTR(i)
+#else
+#define GTR(i)
+#endif
+
 #include "lbt_device.h"
 #include "lbt_internal.h"
 #include "ternary_common.h"
 
 #include <stdlib.h>
 
-#ifdef LBT_GEMV_TRACE
-// Debug build only: per-workgroup wall-clock stamps of the GEMV phases.
-__device__ unsigned long long lbt_gemv_trace[4096 * 8];
-#define GTR(i) \
-    if (threadIdx.x == 0 && blockIdx.y == 0 && blockIdx.x < 4096) lbt_gemv_trace[blockIdx.x * 8 + (i)] = wall_clock64();
-extern "C" int lbt_debug_gemv_trace(unsigned long long* out) {
-    return (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(lbt_gemv_trace), sizeof(lbt_gemv_trace));
-}
-#else
-#define GTR(i)
-#endif
 
 namespace lbt {
 
@@ -94,8 +103,9 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, int vr0, int t0, con
     store_single<OUT>(a, tok, v, row_dot(part, rr, t, qs[t]), sa[t]);
 }
 
-// One workgroup handles TILES consecutive tiles of R rows; all their weight
-// loads are issued before the activation prologue.  Rows longer than one
+// One workgroup handles TILES consecutive tiles of R rows; the loads of a
+// single f32 input row go out first, then all weight loads, then the
+// activation prologue runs while the weights are in flight.  Rows longer than one
 // round (NCH * 4 * L chunks) reload per round (TILES == 1 only).
 template <int L, int T, int NCH, int TILES, int IN, int OUT>
 __global__ __launch_bounds__(kThreads) void tgemv_kernel(GemvArgs a) {
@@ -111,6 +121,15 @@ __global__ __launch_bounds__(kThreads) void tgemv_kernel(GemvArgs a) {
     const int rg = ln / L, j = ln % L;
     const int t0 = blockIdx.y * T;
     const int C = a.C;
+
+    // Single-token f32 input held in registers: its loads go out first, so the
+    // prologue waits for them without waiting for the weight loads behind.
+    constexpr int EPT = NCH * 8;
+    constexpr bool kRegs = T == 1 && IN == kInF32;
+    const bool regs = kRegs && a.kp <= EPT * kThreads;
+    RowRegs<kRegs ? EPT : 4> rrow;
+    const float* norm_w = a.norm_w ? launder(a.norm_w) : nullptr;
+    if (regs) row_load(SrcF32{launder(a.x) + (size_t)t0 * a.cols}, a.cols, norm_w, rrow);
 
     const uint4* rowp[TILES];
     bool valid[TILES];
@@ -130,7 +149,15 @@ __global__ __launch_bounds__(kThreads) void tgemv_kernel(GemvArgs a) {
     }
 
     GTR(1)
-    build_acts<T, IN, NCH * 8>(a, t0, xq, sa, qs, red);
+    if constexpr (kRegs) {
+        if (regs)
+            quantize_row_regs(rrow, a.cols, a.kp, norm_w, a.eps, xq, [C](int i) { return perm_pos(i, C); }, &sa[0],
+                              &qs[0], red);
+        else
+            build_acts<T, IN, EPT>(a, t0, xq, sa, qs, red);
+    } else {
+        build_acts<T, IN, EPT>(a, t0, xq, sa, qs, red);
+    }
     __syncthreads();
     GTR(2)
 

@@ -267,13 +267,15 @@ float or_block_sum256(const float* partials) {
     return (w[0] + w[1]) + (w[2] + w[3]);
 }
 
-/* Thread t of 256 accumulates x[i]^2 (fma) over i = t, t+256, ... ascending,
- * then the block sum above. */
+/* Thread t of 256 holds the groups of four consecutive elements
+ * i = 1024 g + 4 t + k (k = 0..3) and accumulates x[i]^2 (fma) over them in
+ * ascending i, then the block sum above. */
 float or_sumsq256(const float* x, size_t n) {
     float p[256];
     for (int t = 0; t < 256; t++) {
         float a = 0.0f;
-        for (size_t i = (size_t)t; i < n; i += 256) a = fmaf(x[i], x[i], a);
+        for (size_t i0 = 4 * (size_t)t; i0 < n; i0 += 1024)
+            for (size_t i = i0; i < i0 + 4 && i < n; i++) a = fmaf(x[i], x[i], a);
         p[t] = a;
     }
     return or_block_sum256(p);
