@@ -55,6 +55,23 @@ __device__ __forceinline__ int quant_one(float v, float scale) {
     return (int)__builtin_amdgcn_fmed3f(y, -128.0f, 127.0f);
 }
 
+// Four quant_one values of consecutive elements, packed little-endian into
+// one word; *sum += their sum.  v_cvt_i32_f32 saturates out-of-range values
+// and converts NaN to 0, so rint -> convert -> clamp to [-128, 127] equals
+// quant_one for every input.
+__device__ __forceinline__ uint32_t quant4(const float* v, float scale, int& sum) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        int q;
+        asm("v_cvt_i32_f32 %0, %1" : "=v"(q) : "v"(__builtin_rintf(v[k] * scale)));
+        q = q < -128 ? -128 : (q > 127 ? 127 : q);
+        word |= ((uint32_t)q & 0xffu) << (8 * k);
+    }
+    sum = __builtin_amdgcn_sdot4((int)word, 0x01010101, sum, false);
+    return word;
+}
+
 // exp(x) for the softmax: Cody & Waite two-constant reduction x = n ln2 + r,
 // degree-7 Taylor polynomial of e^r (Horner, fused multiply-adds), scale by
 // 2^n through the exponent bits; below 2^-126 flushes to zero.

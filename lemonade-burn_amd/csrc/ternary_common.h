@@ -196,14 +196,8 @@ __device__ __forceinline__ void quantize_row_regs(RowRegs<EPT>& r, int cols, int
     for (int g = 0; g < EPT / 4; g++) {
         const int i0 = 1024 * g + 4 * tid;
         if (act && i0 < kp) {
-            uint32_t word = 0;
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const int qv = i0 + k < cols ? quant_one(r.v[4 * g + k], scale) : 0;
-                s += qv;
-                word |= ((uint32_t)qv & 0xffu) << (8 * k);
-            }
-            *(uint32_t*)(dst + pos(i0)) = word;
+            // elements past cols hold 0 and quantize to 0
+            *(uint32_t*)(dst + pos(i0)) = quant4(&r.v[4 * g], scale, s);
         }
     }
     LBT_QTR(7)

@@ -208,10 +208,12 @@ __global__ __launch_bounds__(kThreads) void tgemv_kernel(GemvArgs a) {
         }
     }
     __syncthreads();
-    // one barrier for all tiles: tile k's outputs go to threads k*R*T ..
+    // one barrier for all tiles: tile k's outputs go to wavefront k, so the
+    // tiles' epilogues run side by side
+    static_assert(TILES <= 4 && R * T <= 64, "one wavefront per tile epilogue");
 #pragma unroll
     for (int k = 0; k < TILES; k++)
-        epilogue<R, T, OUT>(a, (blockIdx.x * TILES + k) * R, t0, part[k], sa, qs, tid - k * R * T);
+        epilogue<R, T, OUT>(a, (blockIdx.x * TILES + k) * R, t0, part[k], sa, qs, tid - k * 64);
     GTR(4)
 }
 

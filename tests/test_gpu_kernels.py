@@ -198,3 +198,22 @@ def test_invalid_arguments_return_errors(ctx):
     with pytest.raises(lbt_hip.LbtError):
         ctx.ternary_linear([w], np.zeros((1, 64), np.float32))  # inner dimension mismatch
     w.free()
+
+
+@pytest.mark.gpu
+def test_fused_prologue_edge_cases_match_oracle(ctx):
+    # the reference's quantizer edge cases (NaN -> 0, +-inf, denormals, ties,
+    # all-zero rows) through the GEMV's fused quantize prologue
+    rng = np.random.default_rng(11)
+    for i, x in enumerate(quant_cases()):
+        cols = x.size
+        announce(f"fused prologue case {i} cols={cols}")
+        rows = 24
+        t = rng.integers(-1, 2, (rows, cols)).astype(np.int8)
+        p = orc.pack(t)
+        q, sa, su = orc.quantize_acts(x[None, :])
+        w = ctx.upload(p, rows, cols, 0.75)
+        (y,) = ctx.ternary_linear([w], x[None, :].copy())
+        exp = orc.gemm_f32(p, rows, cols, 0.75, q, sa, su)
+        assert np.array_equal(y, exp, equal_nan=True)
+        w.free()
