@@ -1,101 +1,184 @@
-// attn_common.h -- GQA attention for one (query row, head) over the bf16 KV
-// cache, shared by the standalone attention kernel and the persistent decode
-// kernel so both compute the same bits.
+// attn_common.h -- split-key GQA attention over the bf16 KV cache and the
+// combine of its splits, shared by the standalone kernels, the decode GEMV's
+// o-projection prologue and the persistent decode kernel, so all of them
+// compute the same bits.
+//
+// The reference (crates/lb-model/src/model.rs:349-357) computes, per query
+// row and head, scores = q.K^T * scaling over the visible keys 0..p (the
+// causal mask of :316-328), softmax = exp(s - max) / sum, out = probs @ V.
+// Here the vis = p + 1 keys are cut into
+//   ks = max(kAttnMinKeys, ceil(vis / kAttnSplits)) keys per split,
+//   ns = ceil(vis / ks) splits, split s holding keys s*ks .. s*ks + cnt - 1,
+// one workgroup per (query head, split).  A split writes its max m_s, its
+// exponential sum l_s and its unnormalised output o_s = sum_j exp(s_j - m_s) v_j;
+// the combine (flash-decoding form of the same softmax) is
+//   M = max_s m_s, f_s = exp(m_s - M), L = sum_s l_s f_s, out = (sum_s o_s f_s) / L.
+//
+// Float order (the oracle, oracle/lbt_oracle.c, mirrors it), LK = hd/8 lanes
+// per key, 8 dims per lane, u the key index inside the split:
+//   score:  lane c sums q[8c+e]*k[8c+e] over e = 0..7 by fused multiply-adds,
+//           the LK lanes combine by an xor butterfly (m = LK/2 .. 1), then
+//           * scaling;
+//   l_s:    thread t adds exp(s_u - m_s) over u = t, t+256, ...; block_sum;
+//   o_s:    thread (group G = t/LK, chunk c = t%LK) accumulates
+//           exp(s_u - m_s) * v_u[8c+e] by fused multiply-adds over
+//           u = G, G + 256/LK, ...; the 64/LK groups of a wavefront combine
+//           by xor over the group index (m = 1, 2, ...), the four wavefronts
+//           as (w0 + w1) + (w2 + w3);
+//   combine: L = L + l_s*f_s and O = O + o_s*f_s over s = 0, 1, ... (multiply
+//           then add), out = O / L.
+//
+// Partials of one query row (nh heads, hidden H = nh*hd):
+//   o  [kAttnSplits][H]          o_s of head h at [s][h*hd .. h*hd + hd)
+//   ml [kAttnSplits][nh][2]      (m_s, l_s)
 #pragma once
 #include "lbt_device.h"
+#include "lbt_internal.h"
 
 namespace lbt {
 
-// GQA attention for query row t (absolute position p = pos0 + t) and head h,
-// over keys 0..p of the bf16 cache (the q/k/v GEMV has already rotated q and
-// appended the rotated k and v).  model.rs:349-357: scores = q.K^T * scaling,
-// softmax = exp(s - max) / sum, out = probs @ V; the causal mask of :316-328
-// is the visibility bound.  One workgroup per (head, row).  Float order (the
-// oracle mirrors it), with LK = hd/8 lanes per key and 8 dims per lane:
-//   score: lane c sums q[8c+e]*k[8c+e] over e = 0..7 by fused multiply-adds,
-//          the LK lanes combine with an xor butterfly (m = LK/2 .. 1), then
-//          * scaling;
-//   sum:   thread t adds exp(s_j - max) over j = t, t+256, ...; block_sum;
-//   p_j:   exp(s_j - max) / sum;
-//   out:   thread (group g = t/LK, chunk c = t%LK) accumulates
-//          p_j * v[j][8c+e] by fused multiply-adds over j = g, g+256/LK, ...;
-//          the 64/LK groups of a wave combine by xor over the group index
-//          (m = 1, 2, ...), the four waves as (w0 + w1) + (w2 + w3).
 template <int LK>
 struct AttnShared {
     __align__(16) float qs[LK * 8];
-    float red[16];
+    float rmax[4];
+    float rsum[4];
     __align__(16) float pv[4][LK * 8];
 };
 
-// q: this row's q [nh * hd] (already rotated); p: absolute position (keys
-// 0..p are visible); out: this row's output [nh * hd].  The first 256 threads
-// do the work; every thread of the workgroup must call it (shared barriers).
-template <int LK>
-__device__ __forceinline__ void attention_head(const float* q, int h, int nh, int kvh, int p, const uint16_t* kc,
-                                               const uint16_t* vc, int cap, float scaling, float* out, float* sc,
-                                               AttnShared<LK>& sh) {
-    constexpr int HD = LK * 8, GW = 64 / LK, NG = kThreads / LK;
-    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+// Optional phase stamps (debug builds of the attention kernel).
+#ifndef LBT_ATR
+#define LBT_ATR(i)
+#endif
+
+// Splits of vis visible keys.
+__host__ __device__ __forceinline__ int attn_splits(int vis) {
+    const int ks = attn_split_keys(vis);
+    return (vis + ks - 1) / ks;
+}
+
+// Split s of query head h for one query row at absolute position p (keys
+// 0..p visible).  q: the row's q [nh * hd] (rotated); K0/V0: the cache rows
+// of h's KV head; o/ml: the row's partials (layout above); sc: LDS scores
+// [attn_split_keys(cap)].  KU: key passes whose K (and V) loads are in flight
+// together.  The first 256 threads do the work; every thread of the
+// workgroup must call it (shared barriers).  Splits past the last return at
+// once.
+template <int LK, int KU>
+__device__ __forceinline__ void attention_split_ku(const float* q, int h, int nh, int s, int p, const uint16_t* K0,
+                                                   const uint16_t* V0, float scaling, float* o, float* ml, float* sc,
+                                                   AttnShared<LK>& sh) {
+    constexpr int HD = LK * 8, GW = 64 / LK, NK = kThreads / LK;
+    const int vis = p + 1;
+    const int ks = attn_split_keys(vis);
+    const int ns = (vis + ks - 1) / ks;
+    if (s >= ns) return;
+    const int j0 = s * ks, cnt = vis - j0 < ks ? vis - j0 : ks;
+    const int tid = (int)threadIdx.x, w = tid >> 6, lane = tid & 63;
     const bool act = tid < kThreads;
-    const int vis = p + 1, g = h / (nh / kvh);
-    if (tid < HD) sh.qs[tid] = q[(size_t)h * HD + tid];
+    const uint16_t* K = K0 + (size_t)j0 * HD;
+    const uint16_t* V = V0 + (size_t)j0 * HD;
+    const int kslot = lane / LK, cc = lane % LK;  // score loop: key of this lane group, chunk
+    const int grp = tid / LK, c = tid % LK;       // PV loop: key group, chunk
+    // q, then the first batches of K and V rows, all in flight together
+    const float qv = (act && tid < HD) ? q[(size_t)h * HD + tid] : 0.0f;
+    uint4 kb[KU], vb[KU];
+#pragma unroll
+    for (int u = 0; u < KU; u++) {
+        const int k = u * NK + w * GW + kslot;
+        kb[u] = (act && k < cnt) ? *(const uint4*)(K + (size_t)k * HD + 8 * cc) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < KU; u++) {
+        const int k = grp + u * NK;
+        vb[u] = (act && k < cnt) ? *(const uint4*)(V + (size_t)k * HD + 8 * c) : make_uint4(0, 0, 0, 0);
+    }
+    LBT_ATR(1)
+    if (act && tid < HD) sh.qs[tid] = qv;
     __syncthreads();
-    const uint16_t* K = kc + (size_t)g * cap * HD;
-    const uint16_t* V = vc + (size_t)g * cap * HD;
-    const int ks = lane / LK, cc = lane % LK;
+    LBT_ATR(2)
     float q8[8];
 #pragma unroll
     for (int e = 0; e < 8; e++) q8[e] = sh.qs[8 * cc + e];
+
+    // ---- scores and the split max
     float mx = -__builtin_inff();
     if (act) {
-        for (int j0 = w * GW; j0 < vis; j0 += 4 * GW) {
-            const int j = j0 + ks;
-            float a = 0.0f;
-            if (j < vis) {
-                const uint4 kv = *(const uint4*)(K + (size_t)j * HD + 8 * cc);
-                const uint32_t wv[4] = {kv.x, kv.y, kv.z, kv.w};
+        for (int b0 = 0;; b0 += KU * NK) {
+            if (b0 > 0) {
+#pragma unroll
+                for (int u = 0; u < KU; u++) {
+                    const int k = b0 + u * NK + w * GW + kslot;
+                    kb[u] = k < cnt ? *(const uint4*)(K + (size_t)k * HD + 8 * cc) : make_uint4(0, 0, 0, 0);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < KU; u++) {
+                const int k = b0 + u * NK + w * GW + kslot;
+                const uint32_t wv[4] = {kb[u].x, kb[u].y, kb[u].z, kb[u].w};
+                float a = 0.0f;
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
                     a = __builtin_fmaf(q8[2 * e], bf16_to_f32((uint16_t)(wv[e] & 0xffffu)), a);
                     a = __builtin_fmaf(q8[2 * e + 1], bf16_to_f32((uint16_t)(wv[e] >> 16)), a);
                 }
+                a = xor_sum_down<LK / 2>(a);
+                if (k < cnt) {
+                    const float sv = a * scaling;
+                    if (cc == 0) sc[k] = sv;
+                    mx = fmaxf(mx, sv);
+                }
             }
-            a = xor_sum_down<LK / 2>(a);
-            if (j < vis) {
-                const float s = a * scaling;
-                if (cc == 0) sc[j] = s;
-                mx = fmaxf(mx, s);
-            }
+            if (b0 + KU * NK >= cnt) break;
         }
     }
-    mx = block_max(mx, sh.red);  // includes the barrier that publishes sc
+    mx = wave_max(mx);
+    if (lane == 0 && w < 4) sh.rmax[w] = mx;
+    LBT_ATR(3)
+    __syncthreads();  // publishes the scores and the wave maxima
+    LBT_ATR(4)
+    const float m = fmaxf(fmaxf(sh.rmax[0], sh.rmax[1]), fmaxf(sh.rmax[2], sh.rmax[3]));
     float ps = 0.0f;
     if (act)
-        for (int j = tid; j < vis; j += kThreads) {
-            const float e = lbt_expf(sc[j] - mx);
-            sc[j] = e;
+        for (int u = tid; u < cnt; u += kThreads) {
+            const float e = lbt_expf(sc[u] - m);
+            sc[u] = e;
             ps = ps + e;
         }
-    const float sum = block_sum(ps, sh.red);
-    if (act)
-        for (int j = tid; j < vis; j += kThreads) sc[j] = sc[j] / sum;
-    __syncthreads();
-    const int grp = tid / LK, c = tid % LK;
+    ps = wave_sum(ps);
+    if (lane == 0 && w < 4) sh.rsum[w] = ps;
+    __syncthreads();  // publishes the exponentials and the wave sums
+    LBT_ATR(5)
+
+    // ---- unnormalised probs @ V
     float acc[8];
 #pragma unroll
     for (int e = 0; e < 8; e++) acc[e] = 0.0f;
-    if (act)
-        for (int j = grp; j < vis; j += NG) {
-            const float pj = sc[j];
-            const uint4 vv = *(const uint4*)(V + (size_t)j * HD + 8 * c);
-            const uint32_t wv[4] = {vv.x, vv.y, vv.z, vv.w};
+    if (act) {
+        for (int b0 = 0;; b0 += KU * NK) {
+            if (b0 > 0) {
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                acc[2 * e] = __builtin_fmaf(pj, bf16_to_f32((uint16_t)(wv[e] & 0xffffu)), acc[2 * e]);
-                acc[2 * e + 1] = __builtin_fmaf(pj, bf16_to_f32((uint16_t)(wv[e] >> 16)), acc[2 * e + 1]);
+                for (int u = 0; u < KU; u++) {
+                    const int k = b0 + grp + u * NK;
+                    vb[u] = k < cnt ? *(const uint4*)(V + (size_t)k * HD + 8 * c) : make_uint4(0, 0, 0, 0);
+                }
             }
+#pragma unroll
+            for (int u = 0; u < KU; u++) {
+                const int k = b0 + grp + u * NK;
+                if (k < cnt) {
+                    const float pj = sc[k];
+                    const uint32_t wv[4] = {vb[u].x, vb[u].y, vb[u].z, vb[u].w};
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        acc[2 * e] = __builtin_fmaf(pj, bf16_to_f32((uint16_t)(wv[e] & 0xffffu)), acc[2 * e]);
+                        acc[2 * e + 1] = __builtin_fmaf(pj, bf16_to_f32((uint16_t)(wv[e] >> 16)), acc[2 * e + 1]);
+                    }
+                }
+            }
+            if (b0 + KU * NK >= cnt) break;
         }
+    }
+    LBT_ATR(6)
     if constexpr (GW > 1) {
 #pragma unroll
         for (int e = 0; e < 8; e++) acc[e] = xor_sum_up<LK>(acc[e]);
@@ -105,8 +188,163 @@ __device__ __forceinline__ void attention_head(const float* q, int h, int nh, in
         for (int e = 0; e < 8; e++) sh.pv[w][8 * c + e] = acc[e];
     }
     __syncthreads();
-    if (tid < HD) out[(size_t)h * HD + tid] = (sh.pv[0][tid] + sh.pv[1][tid]) + (sh.pv[2][tid] + sh.pv[3][tid]);
+    // ---- this split's partial
+    if (act && tid < HD)
+        o[(size_t)s * nh * HD + (size_t)h * HD + tid] =
+            (sh.pv[0][tid] + sh.pv[1][tid]) + (sh.pv[2][tid] + sh.pv[3][tid]);
+    if (tid == 0) {
+        ml[((size_t)s * nh + h) * 2] = m;
+        ml[((size_t)s * nh + h) * 2 + 1] = (sh.rsum[0] + sh.rsum[1]) + (sh.rsum[2] + sh.rsum[3]);
+    }
+    LBT_ATR(8)
+}
+
+// attention_split_ku with the load batch sized to the split: four key passes
+// for short splits, eight for long ones.
+template <int LK>
+__device__ __forceinline__ void attention_split(const float* q, int h, int nh, int s, int p, const uint16_t* K0,
+                                                const uint16_t* V0, float scaling, float* o, float* ml, float* sc,
+                                                AttnShared<LK>& sh) {
+    if (attn_split_keys(p + 1) <= 4 * (kThreads / LK))
+        attention_split_ku<LK, 4>(q, h, nh, s, p, K0, V0, scaling, o, ml, sc, sh);
+    else
+        attention_split_ku<LK, 8>(q, h, nh, s, p, K0, V0, scaling, o, ml, sc, sh);
+}
+
+// ---------------------------------------------------------------------------
+// Combine of one row's splits, as a row source for the activation prologues.
+// Thread t (< 256) produces the row elements of RowRegs (groups of four,
+// v[4g + k] = att[1024 g + 4 t + k]).  attn_row_issue starts the loads (the
+// first NSB splits of the outputs, the (m, l) pairs and the norm weights);
+// attn_row_finish builds the per-(head, split) factors in LDS and combines.
+// The issue does not depend on the split count (a.ns is read by the finish
+// only): the first NSB splits and all (m, l) slots are loaded (the partial
+// buffers hold kAttnSplits splits), entries past the row's splits unused.
+struct AttnRow {
+    const float* o;   // [kAttnSplits][H]
+    const float* ml;  // [kAttnSplits][nh][2]
+    int ns;           // splits of this row
+    int nh, hd, H;
+};
+
+constexpr int kAttnPairSlots = (kAttnMaxHeads * kAttnSplits + kThreads - 1) / kThreads;
+
+template <int EPT, int NSB>
+struct AttnRegs {
+    f32x4 ov[EPT / 4][NSB];
+    float mv[kAttnPairSlots];
+    float lv[kAttnPairSlots];
+};
+
+// LDS of the combine: m, l and f per (head, split), L per head.
+struct AttnTab {
+    float m[kAttnMaxHeads][kAttnSplits];
+    float l[kAttnMaxHeads][kAttnSplits];
+    float f[kAttnMaxHeads][kAttnSplits];
+    float L[kAttnMaxHeads];
+};
+
+template <int EPT, int NSB>
+__device__ __forceinline__ void attn_row_issue(const AttnRow& a, const float* norm_w, AttnRegs<EPT, NSB>& ar,
+                                               RowRegs<EPT>& r) {
+    const int tid = (int)threadIdx.x;
+    const bool act = tid < kThreads;
+#pragma unroll
+    for (int g = 0; g < EPT / 4; g++) {
+        const int i0 = 1024 * g + 4 * tid;
+#pragma unroll
+        for (int s = 0; s < NSB; s++)
+            ar.ov[g][s] = (act && i0 < a.H) ? gload((const f32x4*)(a.o + (size_t)s * a.H + i0))
+                                            : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        if (norm_w && act && i0 < a.H) {
+            const f32x4 wv = gload((const f32x4*)(norm_w + i0));
+            r.nw[4 * g] = wv.x;
+            r.nw[4 * g + 1] = wv.y;
+            r.nw[4 * g + 2] = wv.z;
+            r.nw[4 * g + 3] = wv.w;
+        } else {
+#pragma unroll
+            for (int k = 0; k < 4; k++) r.nw[4 * g + k] = 0.0f;
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < kAttnPairSlots; j++) {
+        const int pi = tid + j * kThreads, h = pi / kAttnSplits, s = pi % kAttnSplits;
+        const bool ok = act && h < a.nh;
+        ar.mv[j] = ok ? gload(a.ml + ((size_t)s * a.nh + h) * 2) : 0.0f;
+        ar.lv[j] = ok ? gload(a.ml + ((size_t)s * a.nh + h) * 2 + 1) : 0.0f;
+    }
+}
+
+template <int EPT, int NSB>
+__device__ __forceinline__ void attn_row_finish(const AttnRow& a, AttnRegs<EPT, NSB>& ar, RowRegs<EPT>& r,
+                                                AttnTab& tab) {
+    const int tid = (int)threadIdx.x;
+    const bool act = tid < kThreads;
+#pragma unroll
+    for (int j = 0; j < kAttnPairSlots; j++) {
+        const int pi = tid + j * kThreads, h = pi / kAttnSplits, s = pi % kAttnSplits;
+        if (act && h < a.nh) {
+            tab.m[h][s] = s < a.ns ? ar.mv[j] : -__builtin_inff();
+            tab.l[h][s] = ar.lv[j];
+        }
+    }
     __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kAttnPairSlots; j++) {
+        const int pi = tid + j * kThreads, h = pi / kAttnSplits, s = pi % kAttnSplits;
+        if (act && h < a.nh) {
+            float M = -__builtin_inff();
+            for (int t = 0; t < a.ns; t++) M = fmaxf(M, tab.m[h][t]);
+            tab.f[h][s] = s < a.ns ? lbt_expf(tab.m[h][s] - M) : 0.0f;
+        }
+    }
+    __syncthreads();
+    if (act && tid < a.nh) {
+        float L = 0.0f;
+        for (int t = 0; t < a.ns; t++) L = L + tab.l[tid][t] * tab.f[tid][t];
+        tab.L[tid] = L;
+    }
+    __syncthreads();
+    float O[EPT];
+#pragma unroll
+    for (int e = 0; e < EPT; e++) O[e] = 0.0f;
+    for (int s0 = 0; s0 < a.ns; s0 += NSB) {
+        if (s0 > 0) {
+#pragma unroll
+            for (int g = 0; g < EPT / 4; g++) {
+                const int i0 = 1024 * g + 4 * tid;
+#pragma unroll
+                for (int s = 0; s < NSB; s++)
+                    ar.ov[g][s] = (act && i0 < a.H && s0 + s < a.ns)
+                                      ? gload((const f32x4*)(a.o + (size_t)(s0 + s) * a.H + i0))
+                                      : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < EPT / 4; g++) {
+            const int i0 = 1024 * g + 4 * tid;
+            if (!act || i0 >= a.H) continue;
+            const int h = i0 / a.hd;
+#pragma unroll
+            for (int s = 0; s < NSB; s++)
+                if (s0 + s < a.ns) {
+                    const float f = tab.f[h][s0 + s];
+                    O[4 * g] = O[4 * g] + ar.ov[g][s].x * f;
+                    O[4 * g + 1] = O[4 * g + 1] + ar.ov[g][s].y * f;
+                    O[4 * g + 2] = O[4 * g + 2] + ar.ov[g][s].z * f;
+                    O[4 * g + 3] = O[4 * g + 3] + ar.ov[g][s].w * f;
+                }
+        }
+    }
+#pragma unroll
+    for (int g = 0; g < EPT / 4; g++) {
+        const int i0 = 1024 * g + 4 * tid;
+        const bool in = act && i0 < a.H;
+        const float L = in ? tab.L[i0 / a.hd] : 1.0f;
+#pragma unroll
+        for (int k = 0; k < 4; k++) r.v[4 * g + k] = in ? O[4 * g + k] / L : 0.0f;
+    }
 }
 
 }  // namespace lbt

@@ -7,6 +7,18 @@
 // KV cache :340-347, GQA attention :349-357, final norm + head :368-373),
 // crates/lb-ternary/src/bf16.rs (bf16_gemv :14-25), sample.rs:17-25 (argmax).
 // Float order follows lbt_device.h; the oracle mirrors it.
+#include <hip/hip_runtime.h>
+
+#ifdef LBT_ATTN_TRACE
+// Debug build only: wall-clock stamps of the attention phases per workgroup.
+__device__ unsigned long long lbt_attn_trace[256 * 16];
+#define LBT_ATR(i) \
+    if (threadIdx.x == 0 && blockIdx.y == 0 && blockIdx.x < 256) lbt_attn_trace[blockIdx.x * 16 + (i)] = wall_clock64();
+extern "C" int lbt_debug_attn_trace(unsigned long long* out) {
+    return (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(lbt_attn_trace), sizeof(lbt_attn_trace));
+}
+#endif
+
 #include "lbt_device.h"
 #include "lbt_internal.h"
 #include "attn_common.h"
@@ -42,17 +54,43 @@ __global__ __launch_bounds__(kThreads) void embed_kernel(const uint16_t* embed, 
 }
 
 // ---------------------------------------------------------------------------
-// GQA attention, one workgroup per (head, query row); see attn_common.h.
+// GQA attention splits, one workgroup per (query head, key split, query
+// row); see attn_common.h.  Grid (nh * kAttnSplits, m); splits past a row's
+// last one exit at once.
 template <int LK>
 __global__ __launch_bounds__(kThreads) void attention_kernel(const float* q, int nh, int kvh, int pos0,
                                                              const uint16_t* kc, const uint16_t* vc, int cap,
-                                                             float scaling, float* out, const int* pos_dev) {
-    extern __shared__ float sc[];  // [p + 1]
+                                                             float scaling, float* o, float* ml, const int* pos_dev) {
+    extern __shared__ float sc[];  // [attn_split_keys(visible keys)]
     __shared__ AttnShared<LK> sh;
+    LBT_ATR(0)
     if (pos_dev) pos0 = *pos_dev;
-    const int h = blockIdx.x, t = blockIdx.y;
-    attention_head<LK>(q + (size_t)t * nh * LK * 8, h, nh, kvh, pos0 + t, kc, vc, cap, scaling,
-                       out + (size_t)t * nh * LK * 8, sc, sh);
+    const int h = blockIdx.x / kAttnSplits, s = blockIdx.x % kAttnSplits, t = blockIdx.y;
+    const int H = nh * LK * 8, g = h / (nh / kvh);
+    const size_t kvoff = (size_t)g * cap * LK * 8;
+    attention_split<LK>(q + (size_t)t * H, h, nh, s, pos0 + t, kc + kvoff, vc + kvoff, scaling,
+                        o + (size_t)t * kAttnSplits * H, ml + (size_t)t * kAttnSplits * nh * 2, sc, sh);
+    LBT_ATR(7)
+}
+
+// Combine of the attention splits of row blockIdx.x into out (attn_common.h).
+template <int EPT>
+__global__ __launch_bounds__(kThreads) void attn_combine_kernel(const float* o, const float* ml, int nh, int hd,
+                                                                int pos0, float* out, const int* pos_dev) {
+    __shared__ AttnTab tab;
+    const int t = blockIdx.x, H = nh * hd;
+    AttnRow a{o + (size_t)t * kAttnSplits * H, ml + (size_t)t * kAttnSplits * nh * 2, 0, nh, hd, H};
+    RowRegs<EPT> r;
+    AttnRegs<EPT, 4> ar;
+    attn_row_issue(a, nullptr, ar, r);
+    a.ns = attn_splits((pos_dev ? *pos_dev : pos0) + t + 1);
+    attn_row_finish(a, ar, r, tab);
+    float* dst = out + (size_t)t * H;
+#pragma unroll
+    for (int g = 0; g < EPT / 4; g++) {
+        const int i0 = 1024 * g + 4 * (int)threadIdx.x;
+        if (i0 < H) *(float4*)(dst + i0) = make_float4(r.v[4 * g], r.v[4 * g + 1], r.v[4 * g + 2], r.v[4 * g + 3]);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -223,25 +261,27 @@ int launch_embed(lbt_ctx* ctx, const uint16_t* embed, int hidden, int vocab, con
 }
 
 int launch_attention(lbt_ctx* ctx, const float* q, int m, int nh, int kvh, int hd, int pos0, const uint16_t* kc,
-                     const uint16_t* vc, int cap, float scaling, float* out, const int* pos_dev) {
+                     const uint16_t* vc, int cap, float scaling, float* o, float* ml, const int* pos_dev) {
+    if (kvh <= 0 || nh % kvh) return set_err(ctx, LBT_E_INVALID, "attention: heads must be a multiple of kv heads");
     // a graph-replayed step reads its position on the device: size for the cache
-    const size_t lds = (size_t)(pos_dev ? cap : pos0 + m) * sizeof(float);
+    const int vis_max = pos_dev ? cap : pos0 + m;
+    const size_t lds = (size_t)attn_split_keys(vis_max) * sizeof(float);
     if (lds > 64 * 1024) return set_err(ctx, LBT_E_RANGE, "attention: context too long for the LDS score buffer");
     hipEvent_t e0, e1;
     prof_pair(ctx, &e0, &e1);
-    dim3 grid(nh, m);
+    dim3 grid(nh * kAttnSplits, m);
     switch (hd) {
         case 64:
-            hipExtLaunchKernelGGL(attention_kernel<8>, grid, dim3(kThreads), lds, ctx->stream, e0, e1, 0, q, nh, kvh, pos0, kc, vc,
-                               cap, scaling, out, pos_dev);
+            hipExtLaunchKernelGGL(attention_kernel<8>, grid, dim3(kThreads), lds, ctx->stream, e0, e1, 0, q, nh, kvh,
+                                  pos0, kc, vc, cap, scaling, o, ml, pos_dev);
             break;
         case 128:
-            hipExtLaunchKernelGGL(attention_kernel<16>, grid, dim3(kThreads), lds, ctx->stream, e0, e1, 0, q, nh, kvh, pos0, kc, vc,
-                               cap, scaling, out, pos_dev);
+            hipExtLaunchKernelGGL(attention_kernel<16>, grid, dim3(kThreads), lds, ctx->stream, e0, e1, 0, q, nh, kvh,
+                                  pos0, kc, vc, cap, scaling, o, ml, pos_dev);
             break;
         case 256:
-            hipExtLaunchKernelGGL(attention_kernel<32>, grid, dim3(kThreads), lds, ctx->stream, e0, e1, 0, q, nh, kvh, pos0, kc, vc,
-                               cap, scaling, out, pos_dev);
+            hipExtLaunchKernelGGL(attention_kernel<32>, grid, dim3(kThreads), lds, ctx->stream, e0, e1, 0, q, nh, kvh,
+                                  pos0, kc, vc, cap, scaling, o, ml, pos_dev);
             break;
         default:
             return set_err(ctx, LBT_E_INVALID, "attention: head_dim must be 64, 128 or 256");
@@ -249,6 +289,24 @@ int launch_attention(lbt_ctx* ctx, const float* q, int m, int nh, int kvh, int h
     LBT_HIP(ctx, hipGetLastError());
     const double kv_bytes = 2.0 * kvh * (double)(pos0 + m) * hd * 2.0;
     prof_commit(ctx, e0, e1, kProfAttn, kv_bytes);
+    return LBT_OK;
+}
+
+int launch_attn_combine(lbt_ctx* ctx, const float* o, const float* ml, int m, int nh, int hd, int pos0, float* out,
+                        const int* pos_dev) {
+    const int H = nh * hd;
+    if (nh <= 0 || nh > kAttnMaxHeads || hd % 4 || H > 8192)
+        return set_err(ctx, LBT_E_INVALID, "attention combine: at most 64 heads and 8192 columns");
+    hipEvent_t e0, e1;
+    prof_pair(ctx, &e0, &e1);
+    if (H <= 16 * kThreads)
+        hipExtLaunchKernelGGL(attn_combine_kernel<16>, dim3(m), dim3(kThreads), 0, ctx->stream, e0, e1, 0, o, ml, nh,
+                              hd, pos0, out, pos_dev);
+    else
+        hipExtLaunchKernelGGL(attn_combine_kernel<32>, dim3(m), dim3(kThreads), 0, ctx->stream, e0, e1, 0, o, ml, nh,
+                              hd, pos0, out, pos_dev);
+    LBT_HIP(ctx, hipGetLastError());
+    prof_commit(ctx, e0, e1, kProfAttn, 0.0);
     return LBT_OK;
 }
 

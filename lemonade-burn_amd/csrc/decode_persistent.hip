@@ -19,12 +19,15 @@
 #include "attn_common.h"
 #include "ternary_common.h"
 
+#include <map>
+#include <mutex>
+
 namespace lbt {
 
 constexpr int kPT = 512;       // threads per persistent workgroup (256 VGPRs per lane)
 constexpr int kWaves = kPT / 64;
 constexpr unsigned kSpinLimit = 1u << 20;  // ~1 s of polling
-constexpr size_t kPersistLds = 150 * 1024;
+constexpr size_t kCuLds = 160 * 1024;  // LDS per CU (gfx950)
 constexpr size_t kTraceStride = 16, kTraceHalf = 4096;  // dynamic LDS budget per workgroup (160 KB per CU)
 
 struct PersistArgs {
@@ -46,6 +49,8 @@ struct PersistArgs {
     float* x;
     float* q;
     float* att;
+    float* ao;   // attention split outputs [kAttnSplits][H]
+    float* aml;  // attention split (max, sum) [kAttnSplits][nh][2]
     float* h;
     unsigned* flags;  // [G * 16]
     unsigned* go;
@@ -190,6 +195,28 @@ __device__ __forceinline__ void phase_prologue(Src x, int cols, const float* nor
     __syncthreads();
 }
 
+// The o-projection input: the combine of the attention splits, then the
+// prologue's norm and quantization.
+__device__ __forceinline__ void phase_prologue_attn(const AttnRow& row, const float* norm_w, float eps, int8_t* xq,
+                                                    float* sa, int* qs, float* red, AttnTab& tab) {
+    const int kp = (row.H + 127) / 128 * 128, C = kp / 64;
+    auto pos = [C](int i) { return perm_pos(i, C); };
+    if (kp <= 16 * kThreads) {
+        RowRegs<16> r;
+        AttnRegs<16, 4> ar;
+        attn_row_issue(row, norm_w, ar, r);
+        attn_row_finish(row, ar, r, tab);
+        quantize_row_regs(r, row.H, kp, norm_w, eps, xq, pos, sa, qs, red);
+    } else {
+        RowRegs<32> r;
+        AttnRegs<32, 2> ar;
+        attn_row_issue(row, norm_w, ar, r);
+        attn_row_finish(row, ar, r, tab);
+        quantize_row_regs(r, row.H, kp, norm_w, eps, xq, pos, sa, qs, red);
+    }
+    __syncthreads();
+}
+
 __device__ __forceinline__ GemvArgs make_args(const PersistArgs& a, int layer, int first, int n, int cols) {
     GemvArgs g{};
     for (int i = 0; i < 3; i++) {
@@ -212,6 +239,7 @@ __global__ __launch_bounds__(kPT) void decode_persistent_kernel(PersistArgs a) {
     __shared__ float sa_s;
     __shared__ int qs_s;
     __shared__ AttnShared<LK> ash;
+    __shared__ AttnTab atab;
     const int G = gridDim.x, b = blockIdx.x;
     const int H = a.H, I = a.I, hd = a.hd, KV = a.kvh * hd;
     const int p = a.state[0] + 1;
@@ -307,16 +335,20 @@ __global__ __launch_bounds__(kPT) void decode_persistent_kernel(PersistArgs a) {
         LBT_TR(3)
         grid_wait(a, epoch);
         LBT_TR(4)
-        // ---- attention: head b (if any) on the first 256 threads
-        for (int hh = b; hh < a.nh; hh += G)
-            attention_head<LK>(a.q, hh, a.nh, a.kvh, p, a.kc + (size_t)l * a.layer_kv, a.vc + (size_t)l * a.layer_kv,
-                               a.cap, a.scaling, a.att, (float*)act, ash);
+        // ---- attention: (query head, key split) items b, b + G, ... on the first 256 threads
+        for (int it = b; it < a.nh * kAttnSplits; it += G) {
+            const int hq = it / kAttnSplits, g = hq / (a.nh / a.kvh);
+            const size_t kvoff = (size_t)l * a.layer_kv + (size_t)g * a.cap * hd;
+            attention_split_ku<LK, 4>(a.q, hq, a.nh, it % kAttnSplits, p, a.kc + kvoff, a.vc + kvoff, a.scaling, a.ao,
+                                      a.aml, (float*)act, ash);
+        }
         LBT_TR(5)
         grid_arrive(a, ++epoch);
         grid_wait(a, epoch);
         LBT_TR(6)
         // ---- o_proj(attn_sub_norm(attn)), x += y
-        phase_prologue(SrcF32{a.att}, H, nw[2], a.eps, act, &sa_s, &qs_s, red);
+        phase_prologue_attn(AttnRow{a.ao, a.aml, attn_splits(p + 1), a.nh, hd, H}, nw[2], a.eps, act, &sa_s,
+                            &qs_s, red, atab);
         LBT_TR(7)
         if (Lq == 8) phase_compute<8, kOutF32Add>(go_(l), vo0, no, cplH, wl, act, sa_s, qs_s);
         else phase_compute<16, kOutF32Add>(go_(l), vo0, no, cplH, wl, act, sa_s, qs_s);
@@ -376,14 +408,46 @@ static void persistent_lds(const lbt_config& c, int cap, const int* rpw, size_t*
         if (tiles * cpl * 1024 > w) w = tiles * cpl * 1024;
     }
     *wbytes = w;
-    const size_t sc = (size_t)cap * 4;
+    const size_t sc = (size_t)attn_split_keys(cap) * 4;
     *abytes = (size_t)(kpI > kpH ? kpI : kpH) > sc ? (size_t)(kpI > kpH ? kpI : kpH) : sc;
 }
+
+namespace {
+
+const void* persistent_fn(int hd) {
+    switch (hd) {
+        case 64: return (const void*)decode_persistent_kernel<8>;
+        case 128: return (const void*)decode_persistent_kernel<16>;
+        case 256: return (const void*)decode_persistent_kernel<32>;
+        default: return nullptr;
+    }
+}
+
+// Dynamic LDS available to an instantiation: the CU's LDS less its static
+// shared memory (the attention scratch grows with the head shape).
+size_t persistent_dyn_limit(const void* fn) {
+    static std::mutex mu;
+    static std::map<const void*, size_t> lim;
+    std::lock_guard<std::mutex> lk(mu);
+    auto it = lim.find(fn);
+    if (it != lim.end()) return it->second;
+    hipFuncAttributes at{};
+    size_t v = 0;
+    if (hipFuncGetAttributes(&at, fn) == hipSuccess && at.sharedSizeBytes < kCuLds) v = kCuLds - at.sharedSizeBytes;
+    (void)hipGetLastError();
+    if (v && hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)v) != hipSuccess) v = 0;
+    (void)hipGetLastError();
+    lim[fn] = v;
+    return v;
+}
+
+}  // namespace
 
 int persistent_supported(const lbt_config& c, int cap, int G, int* rpw, const char** why) {
     const int hd = c.hidden_size / c.num_attention_heads;
     const int H = c.hidden_size, I = c.intermediate_size, KV = c.num_key_value_heads * hd;
     if (hd != 64 && hd != 128 && hd != 256) return *why = "head_dim", 0;
+    if (c.num_attention_heads > kAttnMaxHeads) return *why = "heads", 0;
     const int kpH = (H + 127) / 128 * 128, kpI = (I + 127) / 128 * 128;
     if (kpH > 8192 || kpI > 8192) return *why = "hidden/intermediate > 8192", 0;
     const int tot[4] = {H + 2 * KV, H, 2 * I, H};
@@ -393,9 +457,12 @@ int persistent_supported(const lbt_config& c, int cap, int G, int* rpw, const ch
     }
     size_t wb, ab;
     persistent_lds(c, cap, rpw, &wb, &ab);
-    if (wb + ab > kPersistLds) return *why = "LDS", 0;
+    const void* fn = persistent_fn(hd);
+    if (!fn) return *why = "head shape", 0;
+    if (wb + ab > persistent_dyn_limit(fn)) return *why = "LDS", 0;
     return 1;
 }
+
 
 int launch_decode_persistent(lbt_ctx* ctx, const PersistHost& h, int G, hipStream_t s) {
     PersistArgs a{};
@@ -424,6 +491,8 @@ int launch_decode_persistent(lbt_ctx* ctx, const PersistHost& h, int G, hipStrea
     a.x = h.x;
     a.q = h.q;
     a.att = h.att;
+    a.ao = h.ao;
+    a.aml = h.aml;
     a.h = h.h;
     a.flags = h.flags;
     a.go = h.go;
@@ -435,25 +504,13 @@ int launch_decode_persistent(lbt_ctx* ctx, const PersistHost& h, int G, hipStrea
     a.trace = h.trace;
     const size_t lds = wb + ab;
     void* args[] = {&a};
-    static bool attr_set = false;
-    if (!attr_set) {
-        (void)hipFuncSetAttribute((const void*)decode_persistent_kernel<8>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            kPersistLds);
-        (void)hipFuncSetAttribute((const void*)decode_persistent_kernel<16>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            kPersistLds);
-        (void)hipFuncSetAttribute((const void*)decode_persistent_kernel<32>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            kPersistLds);
-        attr_set = true;
-    }
-    hipError_t e;
+    const void* fn = persistent_fn(a.hd);
+    if (!fn) return set_err(ctx, LBT_E_INVALID, "persistent decode: unsupported head shape");
+    if (lds > persistent_dyn_limit(fn)) return set_err(ctx, LBT_E_INVALID, "persistent decode: LDS budget");
     hipEvent_t e0, e1;
     prof_pair(ctx, &e0, &e1);
     if (e0) (void)hipEventRecord(e0, s);
-    switch (a.hd) {
-        case 64: e = hipLaunchCooperativeKernel((void*)decode_persistent_kernel<8>, dim3(G), dim3(kPT), args, lds, s); break;
-        case 128: e = hipLaunchCooperativeKernel((void*)decode_persistent_kernel<16>, dim3(G), dim3(kPT), args, lds, s); break;
-        default: e = hipLaunchCooperativeKernel((void*)decode_persistent_kernel<32>, dim3(G), dim3(kPT), args, lds, s); break;
-    }
+    const hipError_t e = hipLaunchCooperativeKernel(fn, dim3(G), dim3(kPT), args, lds, s);
     if (e1) (void)hipEventRecord(e1, s);
     if (e != hipSuccess) return hip_err(ctx, e, "persistent decode launch");
     prof_commit(ctx, e0, e1, kProfOther, 0.0);

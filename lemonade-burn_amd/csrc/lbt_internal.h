@@ -70,7 +70,9 @@ void prof_pair(lbt_ctx* ctx, hipEvent_t* a, hipEvent_t* b);
 void prof_commit(lbt_ctx* ctx, hipEvent_t a, hipEvent_t b, int cls, double bytes);
 
 // ---- ternary GEMV / GEMM ------------------------------------------------
-enum InMode { kInPreQ = 0, kInF32 = 1 };
+// kInAttn: one token whose input row is the combine of the attention splits
+// (o-projection of a decode step, attn_common.h), with the norm of kInF32.
+enum InMode { kInPreQ = 0, kInF32 = 1, kInAttn = 2 };
 enum OutMode { kOutI32 = 0, kOutF32 = 1, kOutF32Add = 2, kOutRelu2 = 3, kOutQKV = 4 };
 
 struct TernaryOp {
@@ -88,6 +90,10 @@ struct TernaryOp {
     const float* x = nullptr;
     const float* norm_w = nullptr;  // nullable: plain ActQuant
     float eps = 0.f;
+    // kInAttn (m == 1): split partials of the row, position from pos0 / pos_dev
+    const float* att_o = nullptr;
+    const float* att_ml = nullptr;
+    int att_nh = 0;
     int in_mode = kInPreQ;
     int out_mode = kOutF32;
     void* out[3] = {nullptr, nullptr, nullptr};
@@ -121,8 +127,23 @@ int launch_bf16_linear(lbt_ctx* ctx, const uint16_t* w, int rows, int cols, cons
 // advances the position by one and writes the token to tok_out[slot++].
 int launch_embed(lbt_ctx* ctx, const uint16_t* embed, int hidden, int vocab, const uint32_t* tokens,
                  const unsigned long long* key, uint32_t* tok_out, int m, float* x, int* state = nullptr);
+// Split-key attention (attn_common.h): keys per split for vis visible keys,
+// at most kAttnSplits splits per (row, query head).
+constexpr int kAttnSplits = 16;
+constexpr int kAttnMinKeys = 64;
+constexpr int kAttnMaxHeads = 64;  // heads of the split combine
+__host__ __device__ __forceinline__ int attn_split_keys(int vis) {
+    const int ks = (vis + kAttnSplits - 1) / kAttnSplits;
+    return ks < kAttnMinKeys ? kAttnMinKeys : ks;
+}
+
+// Attention splits of m query rows at positions pos0 + t (or *pos_dev + t):
+// partials o [m][kAttnSplits][nh*hd], ml [m][kAttnSplits][nh][2].
 int launch_attention(lbt_ctx* ctx, const float* q, int m, int nh, int kvh, int hd, int pos0, const uint16_t* kc,
-                     const uint16_t* vc, int cap, float scaling, float* out, const int* pos_dev = nullptr);
+                     const uint16_t* vc, int cap, float scaling, float* o, float* ml, const int* pos_dev = nullptr);
+// Combine of the splits into out [m][nh*hd].
+int launch_attn_combine(lbt_ctx* ctx, const float* o, const float* ml, int m, int nh, int hd, int pos0, float* out,
+                        const int* pos_dev = nullptr);
 int launch_fill_u64(lbt_ctx* ctx, unsigned long long* p, int n, unsigned long long v);
 int launch_set_state(lbt_ctx* ctx, int* state, int pos, int slot);
 
@@ -146,6 +167,8 @@ struct PersistHost {
     float* x;
     float* q;
     float* att;
+    float* ao;   // attention split outputs of one row [kAttnSplits][hidden]
+    float* aml;  // attention split (max, sum) of one row [kAttnSplits][heads][2]
     float* h;
     unsigned* flags;
     unsigned* go;

@@ -233,6 +233,8 @@ struct lbt_model {
     uint32_t* tok_out = nullptr;
     int tok_out_cap = 0;
     unsigned long long* key = nullptr;
+    float* ao = nullptr;   // attention split outputs [mcap][splits][hidden]
+    float* aml = nullptr;  // attention split (max, sum) [mcap][splits][heads][2]
     int last_n = 0;
     // graph of one decode step (embed from the argmax key .. LM head), valid
     // for the cache buffers and workspace it was captured with
@@ -350,6 +352,8 @@ int ensure_ws(lbt_model* m, int n) {
         }
     if (m->toks) hipFree(m->toks);
     if (m->key) hipFree(m->key);
+    if (m->ao) hipFree(m->ao);
+    if (m->aml) hipFree(m->aml);
     const lbt_config& c = m->cfg;
     const size_t H = (size_t)c.hidden_size, I = (size_t)c.intermediate_size;
     const size_t KV = (size_t)c.num_key_value_heads * m->hd;
@@ -362,6 +366,8 @@ int ensure_ws(lbt_model* m, int n) {
     LBT_HIP(ctx, hipMalloc(&m->logits, (size_t)n * c.vocab_size * 4));
     LBT_HIP(ctx, hipMalloc(&m->toks, n * 4));
     LBT_HIP(ctx, hipMalloc(&m->key, n * 8));
+    LBT_HIP(ctx, hipMalloc(&m->ao, n * kAttnSplits * H * 4));
+    LBT_HIP(ctx, hipMalloc(&m->aml, n * kAttnSplits * (size_t)c.num_attention_heads * 2 * 4));
     m->mcap = n;
     return LBT_OK;
 }
@@ -443,8 +449,12 @@ int forward_dev(lbt_model* m, lbt_cache* cc, const uint32_t* toks_dev, int n, bo
         op.kc = Kl;
         op.vc = Vl;
         if ((rc = launch_ternary(ctx, op))) return rc;
-        if ((rc = launch_attention(ctx, m->q, n, nh, kvh, hd, pos0, Kl, Vl, cc->cap, m->scaling, m->att, state)))
+        if ((rc = launch_attention(ctx, m->q, n, nh, kvh, hd, pos0, Kl, Vl, cc->cap, m->scaling, m->ao, m->aml,
+                                   state)))
             return rc;
+        // one token: the o-projection prologue combines the splits itself
+        const bool fused = n == 1 && nh <= kAttnMaxHeads && H <= 4096;
+        if (!fused && (rc = launch_attn_combine(ctx, m->ao, m->aml, n, nh, hd, pos0, m->att, state))) return rc;
         // o_proj on attn_sub_norm(attn), residual (model.rs:358-359)
         TernaryOp o;
         o.nmat = 1;
@@ -453,8 +463,14 @@ int forward_dev(lbt_model* m, lbt_cache* cc, const uint32_t* toks_dev, int n, bo
         o.sw[0] = W[3].scale;
         o.cols = H;
         o.m = n;
-        o.in_mode = kInF32;
+        o.in_mode = fused ? kInAttn : kInF32;
         o.x = m->att;
+        o.att_o = m->ao;
+        o.att_ml = m->aml;
+        o.att_nh = nh;
+        o.hd = hd;
+        o.pos0 = pos0;
+        o.pos_dev = state;
         o.norm_w = m->norm[l * 4 + 2];
         o.eps = eps;
         o.out_mode = kOutF32Add;
@@ -573,6 +589,8 @@ int persist_prepare(lbt_model* m, lbt_cache* c, int G, const int* rpw, PersistHo
     h.x = m->x;
     h.q = m->q;
     h.att = m->att;
+    h.ao = m->ao;
+    h.aml = m->aml;
     h.h = m->h;
     h.flags = m->bar;
     h.go = m->bar + (size_t)G * 16;
@@ -887,7 +905,8 @@ void lbt_model_free(lbt_model* m) {
     if (m->ptab) hipFree(m->ptab);
     if (m->bar) hipFree(m->bar);
     void* bufs[] = {m->wbuf, m->fbuf, m->embed, m->cos_t, m->sin_t, m->x,   m->q,       m->k,
-                    m->v,    m->att,  m->h,     m->logits, m->toks, m->key, m->tok_out, m->state};
+                    m->v,    m->att,  m->h,     m->logits, m->toks, m->key, m->tok_out, m->state,
+                    m->ao,   m->aml};
     for (void* b : bufs)
         if (b) hipFree(b);
     delete m;

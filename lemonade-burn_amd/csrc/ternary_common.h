@@ -25,6 +25,9 @@ struct GemvArgs {
     const float* x;
     const float* norm_w;
     float eps;
+    const float* att_o;  // kInAttn
+    const float* att_ml;
+    int att_nh;
     void* out[3];
     // kOutQKV: RoPE at positions pos0 + token and bf16 K/V cache append
     int hd, pos0, cap;

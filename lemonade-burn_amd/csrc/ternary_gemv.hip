@@ -29,6 +29,8 @@
 __device__ unsigned long long lbt_gemv_trace[4096 * 16];
 #define GTR(i) \
     if (threadIdx.x == 0 && blockIdx.y == 0 && blockIdx.x < 4096) lbt_gemv_trace[blockIdx.x * 16 + (i)] = wall_clock64();
+#define GCLK(i) \
+    if (threadIdx.x == 0 && blockIdx.y == 0 && blockIdx.x < 4096) lbt_gemv_trace[blockIdx.x * 16 + (i)] = clock64();
 extern "C" int lbt_debug_gemv_trace(unsigned long long* out) {
     return (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(lbt_gemv_trace), sizeof(lbt_gemv_trace));
 }
@@ -40,11 +42,13 @@ extern "C" int lbt_debug_gemv_clear() {
 #define LBT_QTR(i) GTR(i)
 #else
 #define GTR(i)
+#define GCLK(i)
 #endif
 
 #include "lbt_device.h"
 #include "lbt_internal.h"
 #include "ternary_common.h"
+#include "attn_common.h"
 
 #include <stdlib.h>
 
@@ -117,6 +121,7 @@ __global__ __launch_bounds__(kThreads) void tgemv_kernel(GemvArgs a) {
     __shared__ int part[TILES][4][R][T];
 
     GTR(0)
+    GCLK(10)
     const int tid = threadIdx.x, w = tid >> 6, ln = tid & 63;
     const int rg = ln / L, j = ln % L;
     const int t0 = blockIdx.y * T;
@@ -124,12 +129,21 @@ __global__ __launch_bounds__(kThreads) void tgemv_kernel(GemvArgs a) {
 
     // Single-token f32 input held in registers: its loads go out first, so the
     // prologue waits for them without waiting for the weight loads behind.
+    // kInAttn: the row is the combine of the attention splits (same order).
     constexpr int EPT = NCH * 8;
-    constexpr bool kRegs = T == 1 && IN == kInF32;
-    const bool regs = kRegs && a.kp <= EPT * kThreads;
+    constexpr bool kAttn = IN == kInAttn;
+    constexpr bool kRegs = T == 1 && (IN == kInF32 || kAttn);
+    static_assert(!kAttn || T == 1, "attention rows are single tokens");
+    const bool regs = kRegs && (kAttn || a.kp <= EPT * kThreads);
     RowRegs<kRegs ? EPT : 4> rrow;
+    AttnRegs<kAttn ? EPT : 4, kAttn ? 4 : 1> arow;
+    AttnRow attn{a.att_o, a.att_ml, 0, a.att_nh, a.hd, a.cols};
     const float* norm_w = a.norm_w ? launder(a.norm_w) : nullptr;
-    if (regs) row_load(SrcF32{launder(a.x) + (size_t)t0 * a.cols}, a.cols, norm_w, rrow);
+    if constexpr (kAttn) {
+        attn_row_issue(attn, norm_w, arow, rrow);
+    } else {
+        if (regs) row_load(SrcF32{launder(a.x) + (size_t)t0 * a.cols}, a.cols, norm_w, rrow);
+    }
 
     const uint4* rowp[TILES];
     bool valid[TILES];
@@ -149,7 +163,13 @@ __global__ __launch_bounds__(kThreads) void tgemv_kernel(GemvArgs a) {
     }
 
     GTR(1)
-    if constexpr (kRegs) {
+    if constexpr (kAttn) {
+        __shared__ AttnTab tab;
+        attn.ns = attn_splits((a.pos_dev ? *a.pos_dev : a.pos0) + 1);
+        attn_row_finish(attn, arow, rrow, tab);
+        quantize_row_regs(rrow, a.cols, a.kp, norm_w, a.eps, xq, [C](int i) { return perm_pos(i, C); }, &sa[0],
+                          &qs[0], red);
+    } else if constexpr (kRegs) {
         if (regs)
             quantize_row_regs(rrow, a.cols, a.kp, norm_w, a.eps, xq, [C](int i) { return perm_pos(i, C); }, &sa[0],
                               &qs[0], red);
@@ -215,6 +235,7 @@ __global__ __launch_bounds__(kThreads) void tgemv_kernel(GemvArgs a) {
     for (int k = 0; k < TILES; k++)
         epilogue<R, T, OUT>(a, (blockIdx.x * TILES + k) * R, t0, part[k], sa, qs, tid - k * 64);
     GTR(4)
+    GCLK(11)
 }
 
 // Standalone quantizer: one workgroup per row, writes q [m, kp] (zero padded),
@@ -258,6 +279,14 @@ hipError_t launch_out(const GemvArgs& a, int out_mode, dim3 grid, size_t lds, hi
 template <int T, int NCH, int TILES>
 hipError_t launch_in(const GemvArgs& a, int in_mode, int out_mode, dim3 grid, size_t lds, hipStream_t s,
                      hipEvent_t e0, hipEvent_t e1) {
+    if (in_mode == kInAttn) {
+        if constexpr (T == 1) {
+            hipExtLaunchKernelGGL((tgemv_kernel<kL, 1, NCH, TILES, kInAttn, kOutF32Add>), grid, dim3(kThreads), lds, s,
+                                  e0, e1, 0, a);
+            return hipGetLastError();
+        }
+        return hipErrorInvalidValue;
+    }
     return in_mode == kInPreQ ? launch_out<T, NCH, TILES, kInPreQ>(a, out_mode, grid, lds, s, e0, e1)
                               : launch_out<T, NCH, TILES, kInF32>(a, out_mode, grid, lds, s, e0, e1);
 }
@@ -287,6 +316,11 @@ int make_gemv_args(lbt_ctx* ctx, const TernaryOp& op, GemvArgs& a) {
     if (op.out_mode == kOutQKV &&
         (nmat != 3 || op.hd <= 0 || op.hd % 2 || op.rows[0] % op.hd || op.rows[1] % op.hd || op.rows[1] != op.rows[2]))
         return set_err(ctx, LBT_E_INVALID, "ternary: q/k/v fusion needs head-aligned q, k, v");
+    if (op.in_mode == kInAttn &&
+        (op.m != 1 || op.out_mode != kOutF32Add || !op.att_o || !op.att_ml || op.att_nh <= 0 ||
+         op.att_nh > kAttnMaxHeads || op.hd <= 0 || op.hd % 4 || op.att_nh * op.hd != op.cols || op.cols % 4 ||
+         op.cols > 4096))
+        return set_err(ctx, LBT_E_INVALID, "ternary: attention-combine input needs one token, nh*hd = cols <= 4096");
     int total = 0;
     for (int i = 0; i < 3; i++) {
         a.w[i] = i < nmat ? op.w[i] : op.w[0];
@@ -306,6 +340,9 @@ int make_gemv_args(lbt_ctx* ctx, const TernaryOp& op, GemvArgs& a) {
     a.x = op.x;
     a.norm_w = op.norm_w;
     a.eps = op.eps;
+    a.att_o = op.att_o;
+    a.att_ml = op.att_ml;
+    a.att_nh = op.att_nh;
     a.hd = op.hd;
     a.pos0 = op.pos0;
     a.pos_dev = op.pos_dev;

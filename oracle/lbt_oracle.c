@@ -597,6 +597,60 @@ static void rope(float* v, size_t hd, const float* c, const float* s) {
     memcpy(v, tmp, hd * sizeof(float));
 }
 
+/* Split-key attention of the gh query heads that read one KV head, in the
+ * device's float order (lemonade-burn_amd/csrc/attn_common.h):
+ * ks = max(64, ceil(vis/16)) keys per split; per split and head the max m_s,
+ * l_s = block sum of per-thread sums of exp(s_u - m_s) (thread t: u = t, t+256,
+ * ...), o_s = attn_pv of the exponentials; then in split order
+ * L += l_s f_s, O += o_s f_s with f_s = exp(m_s - M), out = O / L. */
+#define ATTN_SPLITS 16
+#define ATTN_MIN_KEYS 64
+static void attn_split_group(const float* qg, const uint16_t* K, const uint16_t* V, size_t vis, size_t hd,
+                             size_t gh, float scaling, float* out) {
+    size_t ks = (vis + ATTN_SPLITS - 1) / ATTN_SPLITS;
+    if (ks < ATTN_MIN_KEYS) ks = ATTN_MIN_KEYS;
+    size_t ns = (vis + ks - 1) / ks;
+    float* ms = (float*)malloc(ns * gh * sizeof(float));
+    float* ls = (float*)malloc(ns * gh * sizeof(float));
+    float* os = (float*)malloc(ns * gh * hd * sizeof(float));
+    float* e = (float*)malloc(ks * sizeof(float));
+    for (size_t s = 0; s < ns; s++) {
+        size_t j0 = s * ks, cnt = vis - j0 < ks ? vis - j0 : ks;
+        for (size_t h = 0; h < gh; h++) {
+            const float* qh = qg + h * hd;
+            float mx = -INFINITY;
+            for (size_t u = 0; u < cnt; u++) {
+                e[u] = attn_score(qh, K + (j0 + u) * hd, hd) * scaling;
+                mx = fmaxf(mx, e[u]);
+            }
+            for (size_t u = 0; u < cnt; u++) e[u] = or_expf(e[u] - mx);
+            float part[256];
+            for (int th = 0; th < 256; th++) {
+                float a = 0.0f;
+                for (size_t u = (size_t)th; u < cnt; u += 256) a = a + e[u];
+                part[th] = a;
+            }
+            ms[s * gh + h] = mx;
+            ls[s * gh + h] = or_block_sum256(part);
+            attn_pv(e, V + j0 * hd, cnt, hd, os + (s * gh + h) * hd);
+        }
+    }
+    for (size_t h = 0; h < gh; h++) {
+        float M = -INFINITY;
+        for (size_t s = 0; s < ns; s++) M = fmaxf(M, ms[s * gh + h]);
+        for (size_t d = 0; d < hd; d++) {
+            float L = 0.0f, O = 0.0f;
+            for (size_t s = 0; s < ns; s++) {
+                float f = or_expf(ms[s * gh + h] - M);
+                L = L + ls[s * gh + h] * f;
+                O = O + os[(s * gh + h) * hd + d] * f;
+            }
+            out[h * hd + d] = O / L;
+        }
+    }
+    free(ms); free(ls); free(os); free(e);
+}
+
 int or_model_forward(or_model* m, const uint32_t* tokens, size_t n, int all_logits, float* logits) {
     const or_config* c = &m->c;
     size_t H = (size_t)c->hidden, I = (size_t)c->intermediate;
@@ -616,7 +670,6 @@ int or_model_forward(or_model* m, const uint32_t* tokens, size_t n, int all_logi
     float* y = (float*)malloc(n * H * sizeof(float));
     float* g = (float*)malloc(n * I * sizeof(float));
     float* u = (float*)malloc(n * I * sizeof(float));
-    float* e = (float*)malloc(total * sizeof(float));
 
     /* embed (model.rs:274-282) */
     for (size_t t = 0; t < n; t++)
@@ -646,25 +699,9 @@ int or_model_forward(or_model* m, const uint32_t* tokens, size_t n, int all_logi
         /* GQA attention (model.rs:349-357): q head h reads kv head h / group. */
         for (size_t t = 0; t < n; t++) {
             size_t vis = pos0 + t + 1;
-            for (size_t h = 0; h < nh; h++) {
-                const float* qh = q + t * H + h * hd;
-                const uint16_t* Kh = K + (h / group) * cap * hd;
-                const uint16_t* Vh = V + (h / group) * cap * hd;
-                float mx = -INFINITY;
-                for (size_t j = 0; j < vis; j++) {
-                    e[j] = attn_score(qh, Kh + j * hd, hd) * scaling;
-                    mx = fmaxf(mx, e[j]);
-                }
-                float part[256];
-                for (int th = 0; th < 256; th++) {
-                    float s = 0.0f;
-                    for (size_t j = (size_t)th; j < vis; j += 256) s = s + or_expf(e[j] - mx);
-                    part[th] = s;
-                }
-                float sum = or_block_sum256(part);
-                for (size_t j = 0; j < vis; j++) e[j] = or_expf(e[j] - mx) / sum;
-                attn_pv(e, Vh, vis, hd, att + t * H + h * hd);
-            }
+            for (size_t h = 0; h < nh; h++)
+                attn_split_group(q + t * H + h * hd, K + (h / group) * cap * hd, V + (h / group) * cap * hd, vis, hd,
+                                 1, scaling, att + t * H + h * hd);
         }
         for (size_t t = 0; t < n; t++) or_rmsnorm(att + t * H, nw[2], H, eps, nrm + t * H);
         linear(m, nrm, n, H, l, 3, y);
@@ -695,6 +732,6 @@ int or_model_forward(or_model* m, const uint32_t* tokens, size_t n, int all_logi
         if (g_fast >= 2) port_bf16_gemv(m->embed, (size_t)c->vocab, H, nrm, lt, 0); /* reference order */
         else or_bf16_gemv_lanes(m->embed, (size_t)c->vocab, H, nrm, lt);
     }
-    free(x); free(nrm); free(q); free(kk); free(vv); free(att); free(y); free(g); free(u); free(e);
+    free(x); free(nrm); free(q); free(kk); free(vv); free(att); free(y); free(g); free(u);
     return 0;
 }
