@@ -25,8 +25,9 @@
 //           u = G, G + 256/LK, ...; the 64/LK groups of a wavefront combine
 //           by xor over the group index (m = 1, 2, ...), the four wavefronts
 //           as (w0 + w1) + (w2 + w3);
-//   combine: L = L + l_s*f_s and O = O + o_s*f_s over s = 0, 1, ... (multiply
-//           then add), out = O / L.
+//   combine: f_s = exp(m_s - M); L = xor butterfly (m = 8 .. 1) over the 16
+//           split slots of l_s * f_s (0 past ns); O = fma(o_s, f_s, O) over
+//           s = 0, 1, ...; out = O * (1 / L).
 //
 // Partials of one query row (nh heads, hidden H = nh*hd):
 //   o  [kAttnSplits][H]          o_s of head h at [s][h*hd .. h*hd + hd)
@@ -45,9 +46,13 @@ struct AttnShared {
     __align__(16) float pv[4][LK * 8];
 };
 
-// Optional phase stamps (debug builds of the attention kernel).
+// Optional phase stamps (debug builds of the attention kernel and of the
+// combine).
 #ifndef LBT_ATR
 #define LBT_ATR(i)
+#endif
+#ifndef LBT_CTR
+#define LBT_CTR(i)
 #endif
 
 // Splits of vis visible keys.
@@ -232,14 +237,11 @@ constexpr int kAttnPairSlots = (kAttnMaxHeads * kAttnSplits + kThreads - 1) / kT
 template <int EPT, int NSB>
 struct AttnRegs {
     f32x4 ov[EPT / 4][NSB];
-    float mv[kAttnPairSlots];
-    float lv[kAttnPairSlots];
+    f32x2 mlv[kAttnPairSlots];
 };
 
-// LDS of the combine: m, l and f per (head, split), L per head.
+// LDS of the combine: f per (head, split) and 1 / L per head.
 struct AttnTab {
-    float m[kAttnMaxHeads][kAttnSplits];
-    float l[kAttnMaxHeads][kAttnSplits];
     float f[kAttnMaxHeads][kAttnSplits];
     float L[kAttnMaxHeads];
 };
@@ -270,9 +272,8 @@ __device__ __forceinline__ void attn_row_issue(const AttnRow& a, const float* no
 #pragma unroll
     for (int j = 0; j < kAttnPairSlots; j++) {
         const int pi = tid + j * kThreads, h = pi / kAttnSplits, s = pi % kAttnSplits;
-        const bool ok = act && h < a.nh;
-        ar.mv[j] = ok ? gload(a.ml + ((size_t)s * a.nh + h) * 2) : 0.0f;
-        ar.lv[j] = ok ? gload(a.ml + ((size_t)s * a.nh + h) * 2 + 1) : 0.0f;
+        ar.mlv[j] = (act && h < a.nh) ? gload((const f32x2*)(a.ml + ((size_t)s * a.nh + h) * 2))
+                                      : f32x2{0.0f, 0.0f};
     }
 }
 
@@ -281,69 +282,72 @@ __device__ __forceinline__ void attn_row_finish(const AttnRow& a, AttnRegs<EPT, 
                                                 AttnTab& tab) {
     const int tid = (int)threadIdx.x;
     const bool act = tid < kThreads;
+    const int hs = __builtin_ctz((unsigned)a.hd);  // head_dim is a power of two
+    LBT_CTR(6)
+    // (head, split) pairs sit in 16 consecutive lanes per head: M, the split
+    // factors f_s and L come from lane butterflies, no LDS round trip
+    static_assert(kAttnSplits == 16 && kThreads % kAttnSplits == 0, "16-lane head segments");
 #pragma unroll
     for (int j = 0; j < kAttnPairSlots; j++) {
         const int pi = tid + j * kThreads, h = pi / kAttnSplits, s = pi % kAttnSplits;
+        if (j * kThreads >= a.nh * kAttnSplits) break;  // uniform
+        const bool live = act && h < a.nh && s < a.ns;
+        const float m = live ? ar.mlv[j].x : -__builtin_inff();
+        float M = xor_max<8>(m);
+        M = xor_max<4>(M);
+        M = xor_max<2>(M);
+        M = xor_max<1>(M);
+        const float f = live ? lbt_expf(m - M) : 0.0f;
+        const float L = xor_sum_down<8>(live ? ar.mlv[j].y * f : 0.0f);
         if (act && h < a.nh) {
-            tab.m[h][s] = s < a.ns ? ar.mv[j] : -__builtin_inff();
-            tab.l[h][s] = ar.lv[j];
+            tab.f[h][s] = f;
+            if (s == 0) tab.L[h] = 1.0f / L;
         }
     }
+    LBT_CTR(9)
     __syncthreads();
-#pragma unroll
-    for (int j = 0; j < kAttnPairSlots; j++) {
-        const int pi = tid + j * kThreads, h = pi / kAttnSplits, s = pi % kAttnSplits;
-        if (act && h < a.nh) {
-            float M = -__builtin_inff();
-            for (int t = 0; t < a.ns; t++) M = fmaxf(M, tab.m[h][t]);
-            tab.f[h][s] = s < a.ns ? lbt_expf(tab.m[h][s] - M) : 0.0f;
-        }
-    }
-    __syncthreads();
-    if (act && tid < a.nh) {
-        float L = 0.0f;
-        for (int t = 0; t < a.ns; t++) L = L + tab.l[tid][t] * tab.f[tid][t];
-        tab.L[tid] = L;
-    }
-    __syncthreads();
+    LBT_CTR(10)
     float O[EPT];
 #pragma unroll
     for (int e = 0; e < EPT; e++) O[e] = 0.0f;
-    for (int s0 = 0; s0 < a.ns; s0 += NSB) {
-        if (s0 > 0) {
-#pragma unroll
-            for (int g = 0; g < EPT / 4; g++) {
-                const int i0 = 1024 * g + 4 * tid;
-#pragma unroll
-                for (int s = 0; s < NSB; s++)
-                    ar.ov[g][s] = (act && i0 < a.H && s0 + s < a.ns)
-                                      ? gload((const f32x4*)(a.o + (size_t)(s0 + s) * a.H + i0))
-                                      : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-            }
-        }
+    auto accumulate = [&](const f32x4 (&ov)[EPT / 4][NSB], int s0) {
 #pragma unroll
         for (int g = 0; g < EPT / 4; g++) {
             const int i0 = 1024 * g + 4 * tid;
             if (!act || i0 >= a.H) continue;
-            const int h = i0 / a.hd;
+            const float* fh = tab.f[i0 >> hs];
+#pragma unroll
+            for (int s = 0; s < NSB; s++) {
+                // selects, not branches: splits past ns leave O unchanged
+                const bool live = s0 + s < a.ns;
+                const float f = fh[(s0 + s) & (kAttnSplits - 1)];
+                O[4 * g] = live ? __builtin_fmaf(ov[g][s].x, f, O[4 * g]) : O[4 * g];
+                O[4 * g + 1] = live ? __builtin_fmaf(ov[g][s].y, f, O[4 * g + 1]) : O[4 * g + 1];
+                O[4 * g + 2] = live ? __builtin_fmaf(ov[g][s].z, f, O[4 * g + 2]) : O[4 * g + 2];
+                O[4 * g + 3] = live ? __builtin_fmaf(ov[g][s].w, f, O[4 * g + 3]) : O[4 * g + 3];
+            }
+        }
+    };
+    accumulate(ar.ov, 0);  // the splits loaded by attn_row_issue
+    for (int s0 = NSB; s0 < a.ns; s0 += NSB) {
+        f32x4 ov[EPT / 4][NSB];
+#pragma unroll
+        for (int g = 0; g < EPT / 4; g++) {
+            const int i0 = 1024 * g + 4 * tid;
 #pragma unroll
             for (int s = 0; s < NSB; s++)
-                if (s0 + s < a.ns) {
-                    const float f = tab.f[h][s0 + s];
-                    O[4 * g] = O[4 * g] + ar.ov[g][s].x * f;
-                    O[4 * g + 1] = O[4 * g + 1] + ar.ov[g][s].y * f;
-                    O[4 * g + 2] = O[4 * g + 2] + ar.ov[g][s].z * f;
-                    O[4 * g + 3] = O[4 * g + 3] + ar.ov[g][s].w * f;
-                }
+                ov[g][s] = (act && i0 < a.H && s0 + s < a.ns) ? gload((const f32x4*)(a.o + (size_t)(s0 + s) * a.H + i0))
+                                                              : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         }
+        accumulate(ov, s0);
     }
 #pragma unroll
     for (int g = 0; g < EPT / 4; g++) {
         const int i0 = 1024 * g + 4 * tid;
         const bool in = act && i0 < a.H;
-        const float L = in ? tab.L[i0 / a.hd] : 1.0f;
+        const float rl = in ? tab.L[i0 >> hs] : 0.0f;
 #pragma unroll
-        for (int k = 0; k < 4; k++) r.v[4 * g + k] = in ? O[4 * g + k] / L : 0.0f;
+        for (int k = 0; k < 4; k++) r.v[4 * g + k] = O[4 * g + k] * rl;
     }
 }
 

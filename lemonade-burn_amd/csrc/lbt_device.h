@@ -21,6 +21,7 @@ constexpr int kThreads = 256;    // threads per workgroup everywhere
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 #define LBT_GLOBAL __attribute__((address_space(1)))
 

@@ -27,10 +27,13 @@
 #ifdef LBT_GEMV_TRACE
 // Debug build only: per-workgroup wall-clock stamps of the GEMV phases.
 __device__ unsigned long long lbt_gemv_trace[4096 * 16];
+#ifndef LBT_TRACE_IN
+#define LBT_TRACE_IN (-1)
+#endif
 #define GTR(i) \
-    if (threadIdx.x == 0 && blockIdx.y == 0 && blockIdx.x < 4096) lbt_gemv_trace[blockIdx.x * 16 + (i)] = wall_clock64();
-#define GCLK(i) \
-    if (threadIdx.x == 0 && blockIdx.y == 0 && blockIdx.x < 4096) lbt_gemv_trace[blockIdx.x * 16 + (i)] = clock64();
+    if ((LBT_TRACE_IN < 0 || LBT_TRACE_IN == IN) && threadIdx.x == 0 && blockIdx.y == 0 && blockIdx.x < 4096) \
+        lbt_gemv_trace[blockIdx.x * 16 + (i)] = wall_clock64();
+#define GCLK(i)
 extern "C" int lbt_debug_gemv_trace(unsigned long long* out) {
     return (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(lbt_gemv_trace), sizeof(lbt_gemv_trace));
 }
@@ -39,7 +42,14 @@ extern "C" int lbt_debug_gemv_clear() {
     if (hipGetSymbolAddress(&p, HIP_SYMBOL(lbt_gemv_trace)) != hipSuccess) return -1;
     return (int)hipMemset(p, 0, sizeof(lbt_gemv_trace));
 }
-#define LBT_QTR(i) GTR(i)
+#if LBT_TRACE_IN == 2
+#define LBT_CTR(i) \
+    if (threadIdx.x == 0 && blockIdx.y == 0 && blockIdx.x < 4096) lbt_gemv_trace[blockIdx.x * 16 + (i)] = wall_clock64();
+#endif
+#if LBT_TRACE_IN < 0
+#define LBT_QTR(i) \
+    if (threadIdx.x == 0 && blockIdx.y == 0 && blockIdx.x < 4096) lbt_gemv_trace[blockIdx.x * 16 + (i)] = wall_clock64();
+#endif
 #else
 #define GTR(i)
 #define GCLK(i)
@@ -167,6 +177,7 @@ __global__ __launch_bounds__(kThreads) void tgemv_kernel(GemvArgs a) {
         __shared__ AttnTab tab;
         attn.ns = attn_splits((a.pos_dev ? *a.pos_dev : a.pos0) + 1);
         attn_row_finish(attn, arow, rrow, tab);
+        GTR(5)
         quantize_row_regs(rrow, a.cols, a.kp, norm_w, a.eps, xq, [C](int i) { return perm_pos(i, C); }, &sa[0],
                           &qs[0], red);
     } else if constexpr (kRegs) {

@@ -602,7 +602,8 @@ static void rope(float* v, size_t hd, const float* c, const float* s) {
  * ks = max(64, ceil(vis/16)) keys per split; per split and head the max m_s,
  * l_s = block sum of per-thread sums of exp(s_u - m_s) (thread t: u = t, t+256,
  * ...), o_s = attn_pv of the exponentials; then in split order
- * L += l_s f_s, O += o_s f_s with f_s = exp(m_s - M), out = O / L. */
+ * f_s = exp(m_s - M), L = xor butterfly over 16 split slots of l_s f_s,
+ * O = fma(o_s, f_s, O) in split order, out = O * (1 / L). */
 #define ATTN_SPLITS 16
 #define ATTN_MIN_KEYS 64
 static void attn_split_group(const float* qg, const uint16_t* K, const uint16_t* V, size_t vis, size_t hd,
@@ -638,14 +639,17 @@ static void attn_split_group(const float* qg, const uint16_t* K, const uint16_t*
     for (size_t h = 0; h < gh; h++) {
         float M = -INFINITY;
         for (size_t s = 0; s < ns; s++) M = fmaxf(M, ms[s * gh + h]);
+        float f[ATTN_SPLITS], lf[ATTN_SPLITS];
+        for (size_t s = 0; s < ATTN_SPLITS; s++) {
+            f[s] = s < ns ? or_expf(ms[s * gh + h] - M) : 0.0f;
+            lf[s] = s < ns ? ls[s * gh + h] * f[s] : 0.0f;
+        }
+        float L = butterfly_n(lf, ATTN_SPLITS);
+        float rl = 1.0f / L;
         for (size_t d = 0; d < hd; d++) {
-            float L = 0.0f, O = 0.0f;
-            for (size_t s = 0; s < ns; s++) {
-                float f = or_expf(ms[s * gh + h] - M);
-                L = L + ls[s * gh + h] * f;
-                O = O + os[(s * gh + h) * hd + d] * f;
-            }
-            out[h * hd + d] = O / L;
+            float O = 0.0f;
+            for (size_t s = 0; s < ns; s++) O = fmaf(os[(s * gh + h) * hd + d], f[s], O);
+            out[h * hd + d] = O * rl;
         }
     }
     free(ms); free(ls); free(os); free(e);
