@@ -123,7 +123,7 @@ __global__ __launch_bounds__(kThreads) void lmhead_kernel(const uint16_t* W, int
                                                           const float* norm_w, float eps, float* logits,
                                                           unsigned long long* key) {
     extern __shared__ __align__(16) float xs[];  // cols
-    __shared__ float red[16];
+    __shared__ float red[kRedFloats];
     const int t = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
     const float* xr = x + (size_t)t * cols;
     if (cols <= 16 * kThreads) {

@@ -16,7 +16,8 @@ namespace lbt {
 
 constexpr int kBlock = 128;      // weights per LB2 block (pack.rs:18)
 constexpr int kBlockBytes = 32;  // bytes per LB2 block (pack.rs:19)
-constexpr int kThreads = 256;    // threads per workgroup everywhere
+constexpr int kThreads = 256;    // threads per workgroup of most kernels
+constexpr int kRedFloats = 48;   // LDS floats of a row prologue's reductions
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -229,6 +230,31 @@ __device__ __forceinline__ int block_sum_i_slot(int v, int* red, int slot) {
     return r[0] + r[1] + r[2] + r[3];
 }
 
+// Max / integer sum over the first NT threads (NT/64 wavefronts, values at
+// w[0 .. NT/64)); one barrier, no trailing barrier (order independent).
+template <int NT>
+__device__ __forceinline__ float block_max_n(float v, float* w) {
+    v = wave_max(v);
+    const int wi = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0 && wi < NT / 64) w[wi] = v;
+    __syncthreads();
+    float r = w[0];
+#pragma unroll
+    for (int i = 1; i < NT / 64; i++) r = fmaxf(r, w[i]);
+    return r;
+}
+template <int NT>
+__device__ __forceinline__ int block_sum_i_n(int v, int* w) {
+    v = wave_sum_i(v);
+    const int wi = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0 && wi < NT / 64) w[wi] = v;
+    __syncthreads();
+    int r = 0;
+#pragma unroll
+    for (int i = 0; i < NT / 64; i++) r += w[i];
+    return r;
+}
+
 // The same reductions followed by a barrier, so `red` is free on return.
 __device__ __forceinline__ float block_sum(float v, float* red) {
     const float r = block_sum_slot(v, red, 0);
@@ -302,10 +328,14 @@ struct SrcBf16 {
     __device__ __forceinline__ SrcBf16 fresh() const { return SrcBf16{launder(p)}; }
 };
 
-// Element layout of the row prologues: thread t (< 256) holds EPT/4 groups of
-// four consecutive elements, v[4g + k] = x[1024 g + 4 t + k].  Rows of up to
-// 256 * EPT elements are held in registers (one global pass).
-__device__ __forceinline__ int row_elem(int tid, int e) { return 1024 * (e >> 2) + 4 * tid + (e & 3); }
+// Element layout of the row prologues with NT participating threads (256,
+// 512 or 1024; threads past NT take no part): thread t holds EPT/4 groups of
+// four consecutive elements, v[4g + k] = x[4*NT*g + 4t + k].  Rows of up to
+// NT * EPT elements are held in registers (one global pass).
+template <int NT = kThreads>
+__device__ __forceinline__ int row_elem(int tid, int e) {
+    return 4 * NT * (e >> 2) + 4 * tid + (e & 3);
+}
 
 template <int EPT>
 struct RowRegs {
@@ -315,15 +345,15 @@ struct RowRegs {
 };
 
 // Issues the loads of row x[0..cols) (0 past cols) and, if norm_w is set, of
-// the norm weights, into r.  Only the first 256 threads load.
-template <int EPT, typename Src>
+// the norm weights, into r.
+template <int EPT, int NT = kThreads, typename Src>
 __device__ __forceinline__ void row_load(Src x, int cols, const float* norm_w, RowRegs<EPT>& r) {
     const int tid = (int)threadIdx.x;
-    const bool act = tid < kThreads;
+    const bool act = tid < NT;
     const bool vec = x.vec_ok(cols) && (!norm_w || ((uintptr_t)norm_w & 15) == 0);
 #pragma unroll
     for (int g = 0; g < EPT / 4; g++) {
-        const int i0 = 1024 * g + 4 * tid;
+        const int i0 = 4 * NT * g + 4 * tid;
         if (vec && act && i0 < cols) {
             x.load4(i0, &r.v[4 * g]);
             if (norm_w) {
@@ -348,21 +378,50 @@ __device__ __forceinline__ void row_load(Src x, int cols, const float* norm_w, R
     }
 }
 
+// Sum of the 16 per-wavefront partial sums w[0..15] as a full binary tree.
+__device__ __forceinline__ float tree16(const float* w) {
+    const float a = ((w[0] + w[1]) + (w[2] + w[3])) + ((w[4] + w[5]) + (w[6] + w[7]));
+    const float b = ((w[8] + w[9]) + (w[10] + w[11])) + ((w[12] + w[13]) + (w[14] + w[15]));
+    return a + b;
+}
+
+// Canonical sum of squares of a row (the same bits for any thread count):
+// element groups gi (elements 4gi .. 4gi+3) belong to virtual thread
+// vt = gi mod 1024, which accumulates x^2 by fused multiply-adds over its
+// elements in ascending order; the 16 virtual wavefronts (vt / 64) reduce
+// by xor butterflies, then tree16.  A kernel with NT threads holds
+// A = 1024 / NT virtual threads per thread (vt = t + NT*j).  Uses red[0..15]
+// (reduction slots 0..3); one barrier.
+template <int EPT, int NT = kThreads>
+__device__ __forceinline__ float row_sumsq(const RowRegs<EPT>& r, int cols, float* red) {
+    static_assert(NT == 256 || NT == 512 || NT == 1024, "threads of a row prologue");
+    constexpr int A = 1024 / NT;
+    const int tid = (int)threadIdx.x, lane = tid & 63;
+    const bool act = tid < NT;
+    float acc[A];
+#pragma unroll
+    for (int j = 0; j < A; j++) acc[j] = 0.0f;
+#pragma unroll
+    for (int g = 0; g < EPT / 4; g++)
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+            if (act && row_elem<NT>(tid, 4 * g + k) < cols)
+                acc[g % A] = __builtin_fmaf(r.v[4 * g + k], r.v[4 * g + k], acc[g % A]);
+#pragma unroll
+    for (int j = 0; j < A; j++) {
+        const float s = wave_sum(acc[j]);
+        if (lane == 0 && act) red[(tid >> 6) + j * (NT / 64)] = s;
+    }
+    __syncthreads();
+    return tree16(red);
+}
+
 // rms_norm (crates/lb-model/src/model.rs:267-272) of the loaded row, in place,
-// when norm_w is set: r = 1 / sqrt(sum(x^2)/cols + eps), with each thread's
-// sum of squares accumulated by fused multiply-adds over its elements in the
-// order v[0], v[1], ... (ascending i) and combined by block_sum; then
-// v = (x * r) * w.  Uses reduction slot 0 of `red` (see block_sum_slot).
-template <int EPT>
+// when norm_w is set: f = 1 / sqrt(row_sumsq/cols + eps); v = (x * f) * w.
+template <int EPT, int NT = kThreads>
 __device__ __forceinline__ void row_norm(RowRegs<EPT>& r, int cols, const float* norm_w, float eps, float* red) {
     if (!norm_w) return;
-    const int tid = (int)threadIdx.x;
-    const bool act = tid < kThreads;
-    float p = 0.0f;
-#pragma unroll
-    for (int e = 0; e < EPT; e++)
-        if (act && row_elem(tid, e) < cols) p = __builtin_fmaf(r.v[e], r.v[e], p);
-    const float ss = block_sum_slot(p, red, 0);
+    const float ss = row_sumsq<EPT, NT>(r, cols, red);
     const float f = 1.0f / __builtin_sqrtf(ss / (float)cols + eps);
 #pragma unroll
     for (int e = 0; e < EPT; e++) r.v[e] = (r.v[e] * f) * r.nw[e];
@@ -382,17 +441,25 @@ __device__ __forceinline__ void load_norm_row(Src x, int cols, const float* norm
     for (int e = 0; e < EPT; e++) v[e] = r.v[e];
 }
 
-// Same result for rows longer than 256 * EPT, re-reading x from memory (same
-// per-thread element order).
+// The same norm factor for rows longer than the register path, re-reading x
+// from memory (first 256 threads, four virtual threads each).
 template <typename Src>
 __device__ __forceinline__ float norm_factor_global(Src x, int cols, const float* norm_w, float eps, float* red) {
     if (!norm_w) return 1.0f;
-    float p = 0.0f;
-    const int tid = (int)threadIdx.x;
-    if (tid < kThreads)
-        for (int i0 = 4 * tid; i0 < cols; i0 += 1024)
-            for (int i = i0; i < i0 + 4 && i < cols; i++) p = __builtin_fmaf(x(i), x(i), p);
-    const float ss = block_sum(p, red);
+    const int tid = (int)threadIdx.x, lane = tid & 63;
+    const bool act = tid < kThreads;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        float p = 0.0f;
+        if (act)
+            for (int gi = tid + kThreads * j; 4 * gi < cols; gi += 1024)
+                for (int i = 4 * gi; i < 4 * gi + 4 && i < cols; i++) p = __builtin_fmaf(x(i), x(i), p);
+        const float s = wave_sum(p);
+        if (lane == 0 && act) red[(tid >> 6) + 4 * j] = s;
+    }
+    __syncthreads();
+    const float ss = tree16(red);
+    __syncthreads();
     return 1.0f / __builtin_sqrtf(ss / (float)cols + eps);
 }
 

@@ -177,34 +177,34 @@ __device__ __forceinline__ float act_scale(Src x, int cols, const float* norm_w,
 // row_norm applied here when norm_w is set) into `dst` at positions pos(i),
 // four bytes per store (pos keeps each 4-aligned group contiguous); zeros
 // fill [cols, kp).  s_a and sum(q) go to *sa / *qs (written by thread 0).
-// Requires kp <= 256 * EPT.  Work is done by the first 256 threads; every
-// thread must call it (shared barriers).  Reduction slots 0..2 of `red` are
-// in use until two more barriers have passed (successive calls are safe; see
-// block_sum_slot).
-template <int EPT, typename Pos>
+// Requires kp <= NT * EPT.  Work is done by the first NT threads; every
+// thread must call it (shared barriers).  `red` holds kRedFloats floats:
+// [0, 16) sum of squares, [16, 32) max, [32, 48) integer sum, each in use
+// until two more barriers have passed (successive calls are safe).
+template <int EPT, int NT = kThreads, typename Pos>
 __device__ __forceinline__ void quantize_row_regs(RowRegs<EPT>& r, int cols, int kp, const float* norm_w, float eps,
                                                   int8_t* dst, Pos pos, float* sa, int* qs, float* red) {
     const int tid = (int)threadIdx.x;
-    const bool act = tid < kThreads;
-    row_norm<EPT>(r, cols, norm_w, eps, red);
+    const bool act = tid < NT;
+    row_norm<EPT, NT>(r, cols, norm_w, eps, red);
     float am = 0.0f;
 #pragma unroll
     for (int e = 0; e < EPT; e++) am = fmaxf(am, fabsf(r.v[e]));
     LBT_QTR(5)
-    am = block_max_slot(am, red, 1);
+    am = block_max_n<NT>(am, red + 16);
     const float scale = 127.0f / fmaxf(am, 1e-5f);
     LBT_QTR(6)
     int s = 0;
 #pragma unroll
     for (int g = 0; g < EPT / 4; g++) {
-        const int i0 = 1024 * g + 4 * tid;
+        const int i0 = 4 * NT * g + 4 * tid;
         if (act && i0 < kp) {
             // elements past cols hold 0 and quantize to 0
             *(uint32_t*)(dst + pos(i0)) = quant4(&r.v[4 * g], scale, s);
         }
     }
     LBT_QTR(7)
-    s = block_sum_i_slot(s, (int*)red, 2);
+    s = block_sum_i_n<NT>(s, (int*)(red + 32));
     LBT_QTR(8)
     if (tid == 0) {
         *sa = scale;
@@ -237,7 +237,7 @@ __device__ __forceinline__ void quantize_row_block(Src x0, int cols, int kp, con
             dst[pos(i)] = (int8_t)qv;
             s += qv;
         }
-    s = block_sum_i_slot(s, (int*)red, 2);
+    s = block_sum_i_n<kThreads>(s, (int*)(red + 32));
     if (threadIdx.x == 0) {
         *sa = scale;
         *qs = s;

@@ -267,23 +267,33 @@ float or_block_sum256(const float* partials) {
     return (w[0] + w[1]) + (w[2] + w[3]);
 }
 
-/* Thread t of 256 holds the groups of four consecutive elements
- * i = 1024 g + 4 t + k (k = 0..3) and accumulates x[i]^2 (fma) over them in
- * ascending i, then the block sum above. */
-float or_sumsq256(const float* x, size_t n) {
-    float p[256];
-    for (int t = 0; t < 256; t++) {
-        float a = 0.0f;
-        for (size_t i0 = 4 * (size_t)t; i0 < n; i0 += 1024)
-            for (size_t i = i0; i < i0 + 4 && i < n; i++) a = fmaf(x[i], x[i], a);
-        p[t] = a;
+/* Canonical sum of squares of a row, the device order for any workgroup size
+ * (lemonade-burn_amd/csrc/lbt_device.h row_sumsq): element group gi (elements
+ * 4gi..4gi+3) belongs to virtual thread vt = gi mod 1024, which accumulates
+ * x^2 by fused multiply-adds over its elements in ascending order; each of the
+ * 16 virtual wavefronts (vt / 64) reduces with the xor butterfly, and the 16
+ * wavefront sums are added as a full binary tree. */
+float or_sumsq(const float* x, size_t n) {
+    float w[16];
+    for (int wv = 0; wv < 16; wv++) {
+        float v[64];
+        for (int l = 0; l < 64; l++) {
+            size_t vt = (size_t)(64 * wv + l);
+            float a = 0.0f;
+            for (size_t gi = vt; 4 * gi < n; gi += 1024)
+                for (size_t i = 4 * gi; i < 4 * gi + 4 && i < n; i++) a = fmaf(x[i], x[i], a);
+            v[l] = a;
+        }
+        w[wv] = butterfly64(v);
     }
-    return or_block_sum256(p);
+    float a = ((w[0] + w[1]) + (w[2] + w[3])) + ((w[4] + w[5]) + (w[6] + w[7]));
+    float b = ((w[8] + w[9]) + (w[10] + w[11])) + ((w[12] + w[13]) + (w[14] + w[15]));
+    return a + b;
 }
 
 /* rms_norm (model.rs:267-272): x * (mean(x^2) + eps).sqrt().recip() * w */
 void or_rmsnorm(const float* x, const float* w, size_t n, float eps, float* out) {
-    float mean = or_sumsq256(x, n) / (float)n;
+    float mean = or_sumsq(x, n) / (float)n;
     float r = 1.0f / sqrtf(mean + eps);
     for (size_t i = 0; i < n; i++) out[i] = (x[i] * r) * w[i];
 }

@@ -62,7 +62,7 @@ void or_bf16_gemv_lanes(const uint16_t* w, size_t rows, size_t cols, const float
 
 /* ---- float building blocks in the device order ------------------------- */
 float or_block_sum256(const float* partials);                 /* wave butterflies, then (w0+w1)+(w2+w3) */
-float or_sumsq256(const float* x, size_t n);                  /* per-thread fma partials (groups of 4) + block sum */
+float or_sumsq(const float* x, size_t n);                     /* canonical order (1024 virtual threads) */
 /* rms_norm (crates/lb-model/src/model.rs:267-272): x * (mean(x^2)+eps).sqrt().recip() * w */
 void or_rmsnorm(const float* x, const float* w, size_t n, float eps, float* out);
 float or_expf(float x);                                       /* Cody-Waite + Taylor(7) */

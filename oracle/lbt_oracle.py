@@ -46,7 +46,7 @@ _SIGS = {
     "or_bf16_dot_lanes": (f32, [vp, vp, sz]),
     "or_bf16_gemv_lanes": (None, [vp, sz, sz, vp, vp]),
     "or_block_sum256": (f32, [vp]),
-    "or_sumsq256": (f32, [vp, sz]),
+    "or_sumsq": (f32, [vp, sz]),
     "or_rmsnorm": (None, [vp, vp, sz, f32, vp]),
     "or_expf": (f32, [f32]),
     "or_argmax": (C.c_uint32, [vp, sz]),

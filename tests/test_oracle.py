@@ -215,7 +215,7 @@ def test_bf16_rounding_closed_form():
 def test_tree_and_sumsq_exact_on_integers():
     # small integers: every partial sum is exact, so any order gives the true sum
     x = (np.arange(2000) % 101 - 50).astype(np.float32)  # squares <= 2500, total < 2^24
-    got = orc.lib().or_sumsq256(orc._p(x), x.size)
+    got = orc.lib().or_sumsq(orc._p(x), x.size)
     assert got == float(np.sum(x.astype(np.float64) ** 2))
 
 
