@@ -218,8 +218,8 @@ __device__ __forceinline__ void attention_split(const float* q, int h, int nh, i
 
 // ---------------------------------------------------------------------------
 // Combine of one row's splits, as a row source for the activation prologues.
-// Thread t (< 256) produces the row elements of RowRegs (groups of four,
-// v[4g + k] = att[1024 g + 4 t + k]).  attn_row_issue starts the loads (the
+// Thread t (< NT) produces the row elements of RowRegs (groups of four,
+// v[4g + k] = att[4 NT g + 4 t + k]).  attn_row_issue starts the loads (the
 // first NSB splits of the outputs, the (m, l) pairs and the norm weights);
 // attn_row_finish builds the per-(head, split) factors in LDS and combines.
 // The issue does not depend on the split count (a.ns is read by the finish
@@ -232,12 +232,16 @@ struct AttnRow {
     int nh, hd, H;
 };
 
-constexpr int kAttnPairSlots = (kAttnMaxHeads * kAttnSplits + kThreads - 1) / kThreads;
+// (head, split) pairs per thread
+template <int NT>
+constexpr int attn_pair_slots() {
+    return (kAttnMaxHeads * kAttnSplits + NT - 1) / NT;
+}
 
-template <int EPT, int NSB>
+template <int EPT, int NSB, int NT = kThreads>
 struct AttnRegs {
     f32x4 ov[EPT / 4][NSB];
-    f32x2 mlv[kAttnPairSlots];
+    f32x2 mlv[attn_pair_slots<NT>()];
 };
 
 // LDS of the combine: f per (head, split) and 1 / L per head.
@@ -246,14 +250,14 @@ struct AttnTab {
     float L[kAttnMaxHeads];
 };
 
-template <int EPT, int NSB>
-__device__ __forceinline__ void attn_row_issue(const AttnRow& a, const float* norm_w, AttnRegs<EPT, NSB>& ar,
+template <int EPT, int NSB, int NT = kThreads>
+__device__ __forceinline__ void attn_row_issue(const AttnRow& a, const float* norm_w, AttnRegs<EPT, NSB, NT>& ar,
                                                RowRegs<EPT>& r) {
     const int tid = (int)threadIdx.x;
-    const bool act = tid < kThreads;
+    const bool act = tid < NT;
 #pragma unroll
     for (int g = 0; g < EPT / 4; g++) {
-        const int i0 = 1024 * g + 4 * tid;
+        const int i0 = 4 * NT * g + 4 * tid;
 #pragma unroll
         for (int s = 0; s < NSB; s++)
             ar.ov[g][s] = (act && i0 < a.H) ? gload((const f32x4*)(a.o + (size_t)s * a.H + i0))
@@ -270,27 +274,27 @@ __device__ __forceinline__ void attn_row_issue(const AttnRow& a, const float* no
         }
     }
 #pragma unroll
-    for (int j = 0; j < kAttnPairSlots; j++) {
-        const int pi = tid + j * kThreads, h = pi / kAttnSplits, s = pi % kAttnSplits;
+    for (int j = 0; j < attn_pair_slots<NT>(); j++) {
+        const int pi = tid + j * NT, h = pi / kAttnSplits, s = pi % kAttnSplits;
         ar.mlv[j] = (act && h < a.nh) ? gload((const f32x2*)(a.ml + ((size_t)s * a.nh + h) * 2))
                                       : f32x2{0.0f, 0.0f};
     }
 }
 
-template <int EPT, int NSB>
-__device__ __forceinline__ void attn_row_finish(const AttnRow& a, AttnRegs<EPT, NSB>& ar, RowRegs<EPT>& r,
+template <int EPT, int NSB, int NT = kThreads>
+__device__ __forceinline__ void attn_row_finish(const AttnRow& a, AttnRegs<EPT, NSB, NT>& ar, RowRegs<EPT>& r,
                                                 AttnTab& tab) {
     const int tid = (int)threadIdx.x;
-    const bool act = tid < kThreads;
+    const bool act = tid < NT;
     const int hs = __builtin_ctz((unsigned)a.hd);  // head_dim is a power of two
     LBT_CTR(6)
     // (head, split) pairs sit in 16 consecutive lanes per head: M, the split
     // factors f_s and L come from lane butterflies, no LDS round trip
-    static_assert(kAttnSplits == 16 && kThreads % kAttnSplits == 0, "16-lane head segments");
+    static_assert(kAttnSplits == 16 && NT % kAttnSplits == 0, "16-lane head segments");
 #pragma unroll
-    for (int j = 0; j < kAttnPairSlots; j++) {
-        const int pi = tid + j * kThreads, h = pi / kAttnSplits, s = pi % kAttnSplits;
-        if (j * kThreads >= a.nh * kAttnSplits) break;  // uniform
+    for (int j = 0; j < attn_pair_slots<NT>(); j++) {
+        const int pi = tid + j * NT, h = pi / kAttnSplits, s = pi % kAttnSplits;
+        if (j * NT >= a.nh * kAttnSplits) break;  // uniform
         const bool live = act && h < a.nh && s < a.ns;
         const float m = live ? ar.mlv[j].x : -__builtin_inff();
         float M = xor_max<8>(m);
@@ -313,7 +317,7 @@ __device__ __forceinline__ void attn_row_finish(const AttnRow& a, AttnRegs<EPT, 
     auto accumulate = [&](const f32x4 (&ov)[EPT / 4][NSB], int s0) {
 #pragma unroll
         for (int g = 0; g < EPT / 4; g++) {
-            const int i0 = 1024 * g + 4 * tid;
+            const int i0 = 4 * NT * g + 4 * tid;
             if (!act || i0 >= a.H) continue;
             const float* fh = tab.f[i0 >> hs];
 #pragma unroll
@@ -333,7 +337,7 @@ __device__ __forceinline__ void attn_row_finish(const AttnRow& a, AttnRegs<EPT, 
         f32x4 ov[EPT / 4][NSB];
 #pragma unroll
         for (int g = 0; g < EPT / 4; g++) {
-            const int i0 = 1024 * g + 4 * tid;
+            const int i0 = 4 * NT * g + 4 * tid;
 #pragma unroll
             for (int s = 0; s < NSB; s++)
                 ov[g][s] = (act && i0 < a.H && s0 + s < a.ns) ? gload((const f32x4*)(a.o + (size_t)(s0 + s) * a.H + i0))
@@ -343,7 +347,7 @@ __device__ __forceinline__ void attn_row_finish(const AttnRow& a, AttnRegs<EPT, 
     }
 #pragma unroll
     for (int g = 0; g < EPT / 4; g++) {
-        const int i0 = 1024 * g + 4 * tid;
+        const int i0 = 4 * NT * g + 4 * tid;
         const bool in = act && i0 < a.H;
         const float rl = in ? tab.L[i0 >> hs] : 0.0f;
 #pragma unroll

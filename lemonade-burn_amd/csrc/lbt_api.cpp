@@ -127,6 +127,8 @@ int lbt_ctx_create(int device, lbt_ctx** out) {
     if (hipSetDevice(device) != hipSuccess) return LBT_E_DEVICE;
     lbt_ctx* c = new lbt_ctx();
     c->device = device;
+    if (hipDeviceGetAttribute(&c->cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || c->cus <= 0)
+        c->cus = 256;
     if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
         delete c;
         return LBT_E_DEVICE;

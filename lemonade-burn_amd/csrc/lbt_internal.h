@@ -12,6 +12,7 @@
 
 struct lbt_ctx {
     int device = 0;
+    int cus = 256;  // compute units of the device
     hipStream_t stream = nullptr;
     std::string err;
     // grow-only device workspace for the host-pointer entry points
@@ -110,6 +111,10 @@ struct TernaryOp {
 constexpr int kMfmaMinTokens = 16;
 int launch_ternary(lbt_ctx* ctx, const TernaryOp& op);
 int launch_ternary_gemv(lbt_ctx* ctx, const TernaryOp& op);
+// Single-token GEMV with one 1024-thread workgroup per compute unit (f32 or
+// attention-combine input); returns 1 (nothing launched) for shapes it does
+// not take.
+int launch_ternary_gemv_cu(lbt_ctx* ctx, const TernaryOp& op);
 int launch_ternary_mfma(lbt_ctx* ctx, const TernaryOp& op);
 
 // Standalone (rms)norm + quantize of m rows into global q [m, kp], scale, sum.

@@ -366,6 +366,10 @@ int make_gemv_args(lbt_ctx* ctx, const TernaryOp& op, GemvArgs& a) {
 }
 
 int launch_ternary_gemv(lbt_ctx* ctx, const TernaryOp& op) {
+    if (op.m == 1 && op.in_mode != kInPreQ && !getenv("LBT_GEMV_CLASSIC")) {
+        const int rc = launch_ternary_gemv_cu(ctx, op);
+        if (rc != 1) return rc;  // launched, or an error
+    }
     GemvArgs a;
     int rc = make_gemv_args(ctx, op, a);
     if (rc) return rc;

@@ -1,0 +1,183 @@
+// ternary_gemv_cu.hip -- single-token decode GEMV, one 1024-thread workgroup
+// per compute unit.
+//
+// Same arithmetic as the decode GEMV of ternary_gemv.hip (the reference's
+// quantize_acts_into + ternary_gemm_multi decode branch, quant.rs:45-75,
+// gemm.rs:137-154, with the model's fused epilogues), laid out for a
+// batch-1 decode step, where the time goes to latency rather than to HBM:
+//   * about one workgroup per CU (rows per workgroup = rows / CUs, even), so
+//     the activation prologue (RMSNorm + ActQuant, or the attention combine)
+//     runs once per CU, spread over 16 wavefronts: 4x fewer elements per
+//     thread than a 256-thread workgroup;
+//   * each row lives inside one wavefront (L = 16, 32 or 64 lanes per row,
+//     lane j takes 16-byte chunks j, j+L, ...), so a row reduces with lane
+//     butterflies only;
+//   * the activation loads go out first, then every weight load of the
+//     workgroup (CPL 16-byte chunks per lane), then the prologue runs while
+//     the weights are in flight;
+//   * epilogues are the shared ones of ternary_common.h.
+#include "lbt_device.h"
+#include "lbt_internal.h"
+#include "ternary_common.h"
+#include "attn_common.h"
+
+namespace lbt {
+
+constexpr int kCuThreads = 1024;
+constexpr int kCuEPT = 8;       // row elements per thread: rows up to 8192
+constexpr int kCuMaxRows = 64;  // rows per workgroup (16 wavefronts x 64 / L, L >= 16)
+
+template <int L, int CPL, int IN, int OUT>
+__global__ __launch_bounds__(kCuThreads) void tgemv_cu_kernel(GemvArgs a, int rpw) {
+    constexpr int RPWV = 64 / L;  // rows per wavefront
+    __shared__ __align__(16) int8_t xq[kCuEPT * kCuThreads];
+    __shared__ float red[kRedFloats];
+    __shared__ float sa_s;
+    __shared__ int qs_s;
+    __shared__ int dots[kCuMaxRows];
+    const int tid = (int)threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int rs = w * RPWV + lane / L, j = lane % L;
+    const int C = a.C;
+    const int vr0 = blockIdx.x * rpw;
+    const bool rvalid = rs < rpw && vr0 + rs < a.total_rows;
+
+    // the activation row's loads first
+    RowRegs<kCuEPT> row;
+    AttnRegs<IN == kInAttn ? kCuEPT : 4, IN == kInAttn ? 4 : 1, kCuThreads> arow;
+    AttnRow attn{a.att_o, a.att_ml, 0, a.att_nh, a.hd, a.cols};
+    const float* norm_w = a.norm_w ? launder(a.norm_w) : nullptr;
+    if constexpr (IN == kInAttn)
+        attn_row_issue<kCuEPT, 4, kCuThreads>(attn, norm_w, arow, row);
+    else
+        row_load<kCuEPT, kCuThreads>(SrcF32{launder(a.x)}, a.cols, norm_w, row);
+
+    // then every weight load of this workgroup
+    uint4 wv[CPL];
+    {
+        int mat, r;
+        resolve_row<OUT>(a, rvalid ? vr0 + rs : 0, mat, r);
+        const uint4* rowp = (const uint4*)(sel3(a.w, mat) + (size_t)r * (size_t)(a.kp >> 2));
+#pragma unroll
+        for (int i = 0; i < CPL; i++) {
+            const int c = j + L * i;
+            wv[i] = (rvalid && c < C) ? ld_stream(rowp + c) : make_uint4(0, 0, 0, 0);
+        }
+    }
+
+    // prologue: (attention combine,) RMSNorm + ActQuant into the permuted LDS image
+    if constexpr (IN == kInAttn) {
+        __shared__ AttnTab tab;
+        attn.ns = attn_splits((a.pos_dev ? *a.pos_dev : a.pos0) + 1);
+        attn_row_finish<kCuEPT, 4, kCuThreads>(attn, arow, row, tab);
+    }
+    quantize_row_regs<kCuEPT, kCuThreads>(row, a.cols, a.kp, norm_w, a.eps, xq,
+                                          [C](int i) { return perm_pos(i, C); }, &sa_s, &qs_s, red);
+    __syncthreads();
+
+    // codes . q over this lane's chunks, then the row's lanes
+    int acc = 0;
+#pragma unroll
+    for (int i = 0; i < CPL; i++) {
+        const int c = j + L * i;
+        if (c < C) {
+            const uint32_t d[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++) {
+                const int4 xv = *(const int4*)(xq + ((kk * C + c) << 4));
+                const int sh = 2 * kk;
+                acc = __builtin_amdgcn_sdot4((int)((d[0] >> sh) & 0x03030303u), xv.x, acc, false);
+                acc = __builtin_amdgcn_sdot4((int)((d[1] >> sh) & 0x03030303u), xv.y, acc, false);
+                acc = __builtin_amdgcn_sdot4((int)((d[2] >> sh) & 0x03030303u), xv.z, acc, false);
+                acc = __builtin_amdgcn_sdot4((int)((d[3] >> sh) & 0x03030303u), xv.w, acc, false);
+            }
+        }
+    }
+    acc = xor_sum_down_i<L / 2>(acc);
+    if (j == 0 && rs < rpw) dots[rs] = acc - qs_s;
+    __syncthreads();
+
+    // epilogue, one thread per output (or row pair)
+    if constexpr (OUT == kOutRelu2 || OUT == kOutQKV) {
+        if (tid < rpw / 2 && vr0 + 2 * tid < a.total_rows)
+            store_pair<OUT>(a, 0, vr0 + 2 * tid, dots[2 * tid], dots[2 * tid + 1], sa_s);
+    } else {
+        if (tid < rpw && vr0 + tid < a.total_rows) store_single<OUT>(a, 0, vr0 + tid, dots[tid], sa_s);
+    }
+}
+
+namespace {
+
+template <int L, int CPL>
+hipError_t launch_cu(const GemvArgs& a, int in_mode, int out_mode, int rpw, dim3 grid, hipStream_t s, hipEvent_t e0,
+                     hipEvent_t e1) {
+    if (in_mode == kInAttn) {
+        hipExtLaunchKernelGGL((tgemv_cu_kernel<L, CPL, kInAttn, kOutF32Add>), grid, dim3(kCuThreads), 0, s, e0, e1, 0,
+                              a, rpw);
+        return hipGetLastError();
+    }
+    switch (out_mode) {
+        case kOutI32:
+            hipExtLaunchKernelGGL((tgemv_cu_kernel<L, CPL, kInF32, kOutI32>), grid, dim3(kCuThreads), 0, s, e0, e1, 0,
+                                  a, rpw);
+            break;
+        case kOutF32:
+            hipExtLaunchKernelGGL((tgemv_cu_kernel<L, CPL, kInF32, kOutF32>), grid, dim3(kCuThreads), 0, s, e0, e1, 0,
+                                  a, rpw);
+            break;
+        case kOutF32Add:
+            hipExtLaunchKernelGGL((tgemv_cu_kernel<L, CPL, kInF32, kOutF32Add>), grid, dim3(kCuThreads), 0, s, e0, e1,
+                                  0, a, rpw);
+            break;
+        case kOutRelu2:
+            hipExtLaunchKernelGGL((tgemv_cu_kernel<L, CPL, kInF32, kOutRelu2>), grid, dim3(kCuThreads), 0, s, e0, e1,
+                                  0, a, rpw);
+            break;
+        default:
+            hipExtLaunchKernelGGL((tgemv_cu_kernel<L, CPL, kInF32, kOutQKV>), grid, dim3(kCuThreads), 0, s, e0, e1, 0,
+                                  a, rpw);
+            break;
+    }
+    return hipGetLastError();
+}
+
+template <int L>
+hipError_t launch_cu_l(const GemvArgs& a, int cpl, int in_mode, int out_mode, int rpw, dim3 grid, hipStream_t s,
+                       hipEvent_t e0, hipEvent_t e1) {
+    switch (cpl) {
+        case 1: return launch_cu<L, 1>(a, in_mode, out_mode, rpw, grid, s, e0, e1);
+        case 2: return launch_cu<L, 2>(a, in_mode, out_mode, rpw, grid, s, e0, e1);
+        case 4: return launch_cu<L, 4>(a, in_mode, out_mode, rpw, grid, s, e0, e1);
+        default: return launch_cu<L, 8>(a, in_mode, out_mode, rpw, grid, s, e0, e1);
+    }
+}
+
+}  // namespace
+
+int launch_ternary_gemv_cu(lbt_ctx* ctx, const TernaryOp& op) {
+    if (op.m != 1 || (op.in_mode != kInF32 && op.in_mode != kInAttn)) return 1;
+    GemvArgs a;
+    int rc = make_gemv_args(ctx, op, a);
+    if (rc) return rc;
+    if (a.kp > kCuEPT * kCuThreads) return 1;
+    const int total = a.total_rows;
+    int rpw = (total + ctx->cus - 1) / ctx->cus;
+    rpw = (rpw + 1) & ~1;  // row pairs never straddle workgroups
+    if (rpw > kCuMaxRows) rpw = kCuMaxRows;
+    const int L = rpw <= 16 ? 64 : (rpw <= 32 ? 32 : 16);
+    const int need = (a.C + L - 1) / L;
+    if (need > 8) return 1;
+    const int cpl = need <= 1 ? 1 : (need <= 2 ? 2 : (need <= 4 ? 4 : 8));
+    dim3 grid((unsigned)((total + rpw - 1) / rpw));
+    hipEvent_t e0, e1;
+    prof_pair(ctx, &e0, &e1);
+    hipError_t e;
+    if (L == 64) e = launch_cu_l<64>(a, cpl, op.in_mode, op.out_mode, rpw, grid, ctx->stream, e0, e1);
+    else if (L == 32) e = launch_cu_l<32>(a, cpl, op.in_mode, op.out_mode, rpw, grid, ctx->stream, e0, e1);
+    else e = launch_cu_l<16>(a, cpl, op.in_mode, op.out_mode, rpw, grid, ctx->stream, e0, e1);
+    if (e != hipSuccess) return hip_err(ctx, e, "tgemv_cu_kernel launch");
+    const double bytes = (double)total * (a.kp / 4) + (double)op.cols * 4.0;
+    prof_commit(ctx, e0, e1, kProfGemv, bytes);
+    return LBT_OK;
+}
+
+}  // namespace lbt
