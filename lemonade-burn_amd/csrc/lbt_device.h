@@ -33,6 +33,20 @@ __device__ __forceinline__ T gload(const T* p) {
     return *(const LBT_GLOBAL T*)p;
 }
 
+// Buffer resource over [base, base + bytes): raw buffer loads past the end
+// return zeros, so bounded loads need no branch (and no register merge that
+// would make the compiler wait for them early).  Word 3 is the gfx9-family
+// raw-buffer format.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ f32x4 buf_load_f4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0));
+}
+__device__ __forceinline__ f32x2 buf_load_f2(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+    return __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(r, byte_off, 0, 0));
+}
+
 // 16-byte streaming load (nontemporal: the weights are read once per token).
 __device__ __forceinline__ uint4 ld_stream(const uint4* p) {
     const u32x4 v = __builtin_nontemporal_load((const LBT_GLOBAL u32x4*)p);
@@ -378,6 +392,29 @@ __device__ __forceinline__ void row_load(Src x, int cols, const float* norm_w, R
     }
 }
 
+// row_load for a 16-byte aligned f32 row with cols % 4 == 0, through
+// bounded buffer loads (branch-free; threads past NT load nothing).
+template <int EPT, int NT>
+__device__ __forceinline__ void row_load_buf(const float* x, int cols, const float* norm_w, RowRegs<EPT>& r) {
+    const int tid = (int)threadIdx.x;
+    const auto rx = buf_rsrc(x, (uint32_t)cols * 4u);
+    const auto rw = buf_rsrc(norm_w ? norm_w : x, norm_w ? (uint32_t)cols * 4u : 0u);
+#pragma unroll
+    for (int g = 0; g < EPT / 4; g++) {
+        const uint32_t off = tid < NT ? (uint32_t)(4 * NT * g + 4 * tid) * 4u : 0xfffffff0u;
+        const f32x4 v = buf_load_f4(rx, off);
+        const f32x4 w = buf_load_f4(rw, off);
+        r.v[4 * g] = v.x;
+        r.v[4 * g + 1] = v.y;
+        r.v[4 * g + 2] = v.z;
+        r.v[4 * g + 3] = v.w;
+        r.nw[4 * g] = w.x;
+        r.nw[4 * g + 1] = w.y;
+        r.nw[4 * g + 2] = w.z;
+        r.nw[4 * g + 3] = w.w;
+    }
+}
+
 // Sum of the 16 per-wavefront partial sums w[0..15] as a full binary tree.
 __device__ __forceinline__ float tree16(const float* w) {
     const float a = ((w[0] + w[1]) + (w[2] + w[3])) + ((w[4] + w[5]) + (w[6] + w[7]));
@@ -418,9 +455,12 @@ __device__ __forceinline__ float row_sumsq(const RowRegs<EPT>& r, int cols, floa
 
 // rms_norm (crates/lb-model/src/model.rs:267-272) of the loaded row, in place,
 // when norm_w is set: f = 1 / sqrt(row_sumsq/cols + eps); v = (x * f) * w.
-template <int EPT, int NT = kThreads>
+// NORM: 1 norm present, 0 absent, -1 decided at run time by norm_w (a
+// compile-time choice keeps the caller's code free of a merge point).
+template <int EPT, int NT = kThreads, int NORM = -1>
 __device__ __forceinline__ void row_norm(RowRegs<EPT>& r, int cols, const float* norm_w, float eps, float* red) {
-    if (!norm_w) return;
+    if constexpr (NORM == 0) return;
+    if (NORM < 0 && !norm_w) return;
     const float ss = row_sumsq<EPT, NT>(r, cols, red);
     const float f = 1.0f / __builtin_sqrtf(ss / (float)cols + eps);
 #pragma unroll

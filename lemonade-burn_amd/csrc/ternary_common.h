@@ -181,12 +181,13 @@ __device__ __forceinline__ float act_scale(Src x, int cols, const float* norm_w,
 // thread must call it (shared barriers).  `red` holds kRedFloats floats:
 // [0, 16) sum of squares, [16, 32) max, [32, 48) integer sum, each in use
 // until two more barriers have passed (successive calls are safe).
-template <int EPT, int NT = kThreads, typename Pos>
+template <int EPT, int NT = kThreads, int NORM = -1, typename Pos>
 __device__ __forceinline__ void quantize_row_regs(RowRegs<EPT>& r, int cols, int kp, const float* norm_w, float eps,
                                                   int8_t* dst, Pos pos, float* sa, int* qs, float* red) {
     const int tid = (int)threadIdx.x;
     const bool act = tid < NT;
-    row_norm<EPT, NT>(r, cols, norm_w, eps, red);
+    row_norm<EPT, NT, NORM>(r, cols, norm_w, eps, red);
+    LBT_QTR(4)
     float am = 0.0f;
 #pragma unroll
     for (int e = 0; e < EPT; e++) am = fmaxf(am, fabsf(r.v[e]));

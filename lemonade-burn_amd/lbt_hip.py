@@ -104,7 +104,7 @@ def load_library(path: str | os.PathLike | None = None) -> C.CDLL:
     global _lib
     if _lib is not None and path is None:
         return _lib
-    p = Path(path) if path else LIB_PATH
+    p = Path(path) if path else Path(os.environ.get("LBT_LIB", LIB_PATH))
     if not p.exists():
         raise FileNotFoundError(f"{p} is missing: build it with __graft_entry__.build() (no CPU fallback exists)")
     lib = C.CDLL(str(p))
