@@ -26,6 +26,54 @@ sys.path.insert(0, str(REPO / "lemonade-burn_amd"))
 HBM_PEAK_GBS = 8000.0
 SEED = 2026
 PROMPT_LEN = 64
+CALIB_BYTES = 256 << 20  # the copy kernel of known size that calibrates the HBM counters
+TRAFFIC_SUMMARY = REPO / "profiles" / "decode_gemv_hbm_traffic.md"
+
+
+def gemv_traffic() -> float | None:
+    """HBM bytes per decode-GEMV launch from the committed rocprofv3 counter
+    summary (FETCH_SIZE + WRITE_SIZE per dispatch, each scaled by the same
+    counter's reading on the copy kernel of known size), or None."""
+    try:
+        for ln in TRAFFIC_SUMMARY.read_text().splitlines():
+            if ln.startswith("traffic_bytes_per_launch:"):
+                return float(ln.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
+def pmc_pass() -> int:
+    """The command profiled for the HBM counters (under rocprofv3 --pmc):
+    one copy of CALIB_BYTES with the library's copy kernel (the calibration
+    dispatch), then the 2B model's 64-token prefill and 8 decode steps with
+    per-kernel launches (no graph), so every GEMV is its own dispatch."""
+    import ctypes as C
+
+    import lbt_hip
+
+    os.environ["LBT_NO_GRAPH"] = "1"
+    ctx = lbt_hip.Ctx(0)
+    lib = ctx.lib
+    a, b = C.c_void_p(), C.c_void_p()
+    ctx.check(lib.lbt_dev_alloc(ctx.h, CALIB_BYTES, C.byref(a)))
+    ctx.check(lib.lbt_dev_alloc(ctx.h, CALIB_BYTES, C.byref(b)))
+    ctx.check(lib.lbt_memcpy_d2d(ctx.h, b, a, CALIB_BYTES))
+    ctx.sync()
+    lib.lbt_dev_free(ctx.h, a)
+    lib.lbt_dev_free(ctx.h, b)
+    cfg = lbt_hip.make_config()
+    model = lbt_hip.Model.synthetic(ctx, cfg, SEED)
+    prompt = np.random.default_rng(64).integers(0, cfg.vocab_size, PROMPT_LEN).astype(np.uint32)
+    cache = model.new_cache()
+    first = model.forward_argmax(prompt, cache)
+    model.decode_greedy(cache, first, 8)
+    ctx.sync()
+    cache.free()
+    model.free()
+    ctx.close()
+    print("pmc pass done", flush=True)
+    return 0
 
 
 def cpu_baseline(budget_s: float = 15.0) -> dict:
@@ -69,7 +117,10 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--prof-steps", type=int, default=32)
+    ap.add_argument("--pmc-pass", action="store_true", help="the workload profiled for the HBM counters")
     args = ap.parse_args()
+    if args.pmc_pass:
+        return pmc_pass()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU; a multi-GPU figure is not part of it "
               "(rows of the ternary GEMVs would shard across GPUs with no exchange).", file=sys.stderr)
@@ -139,8 +190,8 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
-            "kernel": "tgemv_kernel (ternary decode GEMV, all 4 per-layer groups)",
+            "traffic": gemv_traffic(),
+            "kernel": "tgemv_cu_kernel (ternary decode GEMV, all 4 per-layer groups)",
             "bytes_per_launch": round(g["bytes"] / max(g["launches"], 1)),
             "avg_launch_us": round(g["ms"] * 1e3 / max(g["launches"], 1), 3),
             "launches": g["launches"],

@@ -54,6 +54,11 @@ int lbt_dev_alloc(lbt_ctx* ctx, size_t bytes, void** out);
 int lbt_dev_free(lbt_ctx* ctx, void* p);
 int lbt_memcpy_h2d(lbt_ctx* ctx, void* dst, const void* src, size_t bytes);
 int lbt_memcpy_d2h(lbt_ctx* ctx, void* dst, const void* src, size_t bytes);
+/* Device-to-device copy on the context's stream by the library's own
+ * streaming kernel (16-byte loads/stores; asynchronous).  Also the known-size
+ * reference kernel when HBM counters are calibrated.  No counterpart in the
+ * reference (its tensors live in host memory). */
+int lbt_memcpy_d2d(lbt_ctx* ctx, void* dst, const void* src, size_t bytes);
 /* Library build id (kernel set + arch). */
 const char* lbt_version(void);
 

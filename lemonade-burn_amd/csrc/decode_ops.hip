@@ -199,6 +199,26 @@ __global__ void set_state_kernel(int* state, int pos, int slot) {
     }
 }
 
+// Streaming copy: 16-byte granules (grid-stride, nontemporal), then the tail
+// bytes.
+__global__ __launch_bounds__(kThreads) void copy_kernel(uint4* __restrict__ dst, const uint4* __restrict__ src,
+                                                        size_t n16, uint8_t* dtail, const uint8_t* stail,
+                                                        int ntail) {
+    const size_t stride = (size_t)gridDim.x * kThreads;
+    for (size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x; i < n16; i += stride) {
+        const u32x4 v = __builtin_nontemporal_load((const u32x4*)(src + i));
+        __builtin_nontemporal_store(v, (u32x4*)(dst + i));
+    }
+    if (blockIdx.x == 0 && (int)threadIdx.x < ntail) dtail[threadIdx.x] = stail[threadIdx.x];
+}
+
+// Byte copy for unaligned buffers (grid-stride).
+__global__ __launch_bounds__(kThreads) void copy_bytes_kernel(uint8_t* __restrict__ dst,
+                                                              const uint8_t* __restrict__ src, size_t n) {
+    const size_t stride = (size_t)gridDim.x * kThreads;
+    for (size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += stride) dst[i] = src[i];
+}
+
 __global__ void fill_u64_kernel(unsigned long long* p, int n, unsigned long long v) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) p[i] = v;
@@ -325,6 +345,28 @@ int launch_bf16_linear(lbt_ctx* ctx, const uint16_t* w, int rows, int cols, cons
                        eps, logits, key);
     LBT_HIP(ctx, hipGetLastError());
     prof_commit(ctx, e0, e1, kProfHead, (double)rows * cols * 2.0 * m);
+    return LBT_OK;
+}
+
+int launch_copy(lbt_ctx* ctx, void* dst, const void* src, size_t bytes) {
+    const bool aligned = (((uintptr_t)dst | (uintptr_t)src) & 15) == 0;
+    const size_t cap = (size_t)ctx->cus * 8;
+    if (!aligned) {
+        size_t blocks = (bytes + kThreads - 1) / kThreads;
+        if (blocks > cap) blocks = cap;
+        hipLaunchKernelGGL(copy_bytes_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, ctx->stream, (uint8_t*)dst,
+                           (const uint8_t*)src, bytes);
+        LBT_HIP(ctx, hipGetLastError());
+        return LBT_OK;
+    }
+    const size_t n16 = bytes / 16;
+    const size_t done = n16 * 16;
+    size_t blocks = (n16 + kThreads - 1) / kThreads;
+    if (blocks > cap) blocks = cap;
+    if (blocks == 0) blocks = 1;
+    hipLaunchKernelGGL(copy_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, ctx->stream, (uint4*)dst,
+                       (const uint4*)src, n16, (uint8_t*)dst + done, (const uint8_t*)src + done, (int)(bytes - done));
+    LBT_HIP(ctx, hipGetLastError());
     return LBT_OK;
 }
 

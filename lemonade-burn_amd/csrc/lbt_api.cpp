@@ -191,6 +191,12 @@ int lbt_memcpy_d2h(lbt_ctx* ctx, void* dst, const void* src, size_t bytes) {
     return LBT_OK;
 }
 
+int lbt_memcpy_d2d(lbt_ctx* ctx, void* dst, const void* src, size_t bytes) {
+    if (!ctx || (bytes && (!dst || !src))) return set_err(ctx, LBT_E_INVALID, "memcpy_d2d: bad arguments");
+    if (!bytes) return LBT_OK;
+    return lbt::launch_copy(ctx, dst, src, bytes);
+}
+
 // ---- weights ---------------------------------------------------------------
 static int weight_new(lbt_ctx* ctx, const uint8_t* src, bool src_dev, size_t rows, size_t cols, float scale,
                       lbt_weight** out) {

@@ -150,6 +150,8 @@ int launch_attention(lbt_ctx* ctx, const float* q, int m, int nh, int kvh, int h
 int launch_attn_combine(lbt_ctx* ctx, const float* o, const float* ml, int m, int nh, int hd, int pos0, float* out,
                         const int* pos_dev = nullptr);
 int launch_fill_u64(lbt_ctx* ctx, unsigned long long* p, int n, unsigned long long v);
+// Streaming device copy (16-byte granules, byte tail).
+int launch_copy(lbt_ctx* ctx, void* dst, const void* src, size_t bytes);
 int launch_set_state(lbt_ctx* ctx, int* state, int pos, int slot);
 
 // ---- persistent decode step (one dispatch for all layers of one token) -----

@@ -58,6 +58,7 @@ SIGNATURES = {
     "lbt_dev_free": (i32, [vp, vp]),
     "lbt_memcpy_h2d": (i32, [vp, vp, vp, sz]),
     "lbt_memcpy_d2h": (i32, [vp, vp, vp, sz]),
+    "lbt_memcpy_d2d": (i32, [vp, vp, vp, sz]),
     "lbt_version": (C.c_char_p, []),
     "lbt_weight_upload": (i32, [vp, vp, sz, sz, f32, C.POINTER(vp)]),
     "lbt_weight_upload_dev": (i32, [vp, vp, sz, sz, f32, C.POINTER(vp)]),

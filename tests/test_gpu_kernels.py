@@ -217,3 +217,27 @@ def test_fused_prologue_edge_cases_match_oracle(ctx):
         exp = orc.gemm_f32(p, rows, cols, 0.75, q, sa, su)
         assert np.array_equal(y, exp, equal_nan=True)
         w.free()
+
+
+@pytest.mark.gpu
+def test_memcpy_d2d_sizes(ctx):
+    lib = ctx.lib
+    rng = np.random.default_rng(5)
+    for n, off in [(0, 0), (1, 0), (15, 0), (16, 0), (4096 + 7, 0), (1 << 20, 0), (1000, 3), (100000, 1)]:
+        announce(f"memcpy_d2d n={n} off={off}")
+        src_h = rng.integers(0, 256, n + 64, dtype=np.uint8)
+        a, b = C.c_void_p(), C.c_void_p()
+        ctx.check(lib.lbt_dev_alloc(ctx.h, n + 64, C.byref(a)))
+        ctx.check(lib.lbt_dev_alloc(ctx.h, n + 64, C.byref(b)))
+        ctx.check(lib.lbt_memcpy_h2d(ctx.h, a, src_h.ctypes.data, n + 64))
+        zeros = np.zeros(n + 64, np.uint8)  # kept alive across the call
+        ctx.check(lib.lbt_memcpy_h2d(ctx.h, b, zeros.ctypes.data, n + 64))
+        ctx.check(lib.lbt_memcpy_d2d(ctx.h, C.c_void_p(b.value + off), C.c_void_p(a.value + off), n))
+        ctx.sync()
+        got = np.zeros(n + 64, np.uint8)
+        ctx.check(lib.lbt_memcpy_d2h(ctx.h, got.ctypes.data, b, n + 64))
+        exp = np.zeros(n + 64, np.uint8)
+        exp[off:off + n] = src_h[off:off + n]
+        assert np.array_equal(got, exp)
+        lib.lbt_dev_free(ctx.h, a)
+        lib.lbt_dev_free(ctx.h, b)
