@@ -43,6 +43,30 @@ def gemv_traffic() -> float | None:
     return None
 
 
+def batched_decode(model, cfg, batch: int, cap: int = 4096, steps: int = 8) -> dict:
+    """`batch` sequences, each with a `cap`-position bf16
+    KV cache (the model's max_position_embeddings) pre-filled with synthetic
+    values (approximately N(0,1)) up to cap - steps - 1, decoded together;
+    greedy steps timed on the device after one untimed step.  Bytes per step:
+    every sequence's K and V over all layers plus one pass over the weights."""
+    ctx_len = cap - steps - 1
+    b = model.new_batch(batch, cap)
+    try:
+        b.fill_synthetic(ctx_len, 5)
+        first = np.random.default_rng(batch).integers(0, cfg.vocab_size, batch).astype(np.uint32)
+        toks, _ = b.decode_greedy(first, 1)
+        out, ms = b.decode_greedy(toks[-1], steps)
+    finally:
+        b.free()
+    hd = cfg.hidden_size // cfg.num_attention_heads
+    kv = batch * cfg.num_hidden_layers * 2 * cfg.num_key_value_heads * (ctx_len + 1 + steps / 2) * hd * 2
+    weights = 521_011_200 + cfg.vocab_size * cfg.hidden_size * 2
+    ms_step = ms / steps
+    gbs = (kv + weights) / (ms_step / 1e3) / 1e9
+    return {"batch": batch, "ctx": ctx_len, "steps": steps, "tok_s": round(batch * steps / (ms / 1e3), 1),
+            "ms_per_step": round(ms_step, 3), "hbm_GBs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+
 def pmc_pass() -> int:
     """The command profiled for the HBM counters (under rocprofv3 --pmc):
     one copy of CALIB_BYTES with the library's copy kernel (the calibration
@@ -118,6 +142,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--prof-steps", type=int, default=32)
     ap.add_argument("--pmc-pass", action="store_true", help="the workload profiled for the HBM counters")
+    ap.add_argument("--no-batched", action="store_true", help="skip the batched-decode (config 5) figures")
     args = ap.parse_args()
     if args.pmc_pass:
         return pmc_pass()
@@ -202,6 +227,8 @@ def main() -> int:
         "wall_tok_s": round(args.steps / wall, 2),
         "tokens_head": [int(t) for t in out[:8]],
     }
+    if not args.no_batched:
+        line["batched_decode"] = [batched_decode(model, cfg, bsz) for bsz in (16, 64)]
     model.free()
     ctx.close()
     if not args.no_cpu_baseline:

@@ -182,6 +182,32 @@ int lbt_model_decode_greedy(lbt_model* m, lbt_cache* c, uint32_t first, size_t s
 /* Residual stream of the last forward ([n, hidden] f32) for layer-level tests. */
 int lbt_model_read_hidden(lbt_model* m, float* out, size_t n);
 
+/* ---- batched decode ------------------------------------
+ * No counterpart in the reference, which decodes one sequence at a time
+ * (lb-server main.rs:92-100).  `nseq` independent sequences, each with its own
+ * bf16 KV cache of fixed capacity `cap` positions; a step appends one token to
+ * every sequence with one pass over the weights (rows of the ternary GEMMs are
+ * the sequences) and attention over each sequence's own cache.  Per-sequence
+ * results equal those of the single-sequence API on the same tokens. */
+typedef struct lbt_batch lbt_batch;
+int lbt_batch_new(lbt_model* m, int nseq, int cap, lbt_batch** out);
+void lbt_batch_free(lbt_batch* b);
+int lbt_batch_len(const lbt_batch* b, int seq);
+/* Prompt of sequence `seq` (n tokens after its current length); its greedy
+ * next token in *next (nullable). */
+int lbt_batch_prefill(lbt_batch* b, int seq, const uint32_t* tokens, size_t n, uint32_t* next);
+/* Every sequence's cache holds `len` positions of seeded synthetic K/V
+ * (approximately N(0,1), bf16) and its length becomes `len`. */
+int lbt_batch_fill_synthetic(lbt_batch* b, int len, uint64_t seed);
+/* One step: tokens[s] is appended to sequence s; logits [nseq][vocab]
+ * (nullable) and greedy next[s] (nullable). */
+int lbt_batch_forward(lbt_batch* b, const uint32_t* tokens, float* logits, uint32_t* next);
+/* `steps` greedy steps of every sequence starting from first[s]:
+ * out_tokens[i * nseq + s] is sequence s's token produced by step i;
+ * *ms_decode (nullable) the device time of the steps. */
+int lbt_batch_decode_greedy(lbt_batch* b, const uint32_t* first, size_t steps, uint32_t* out_tokens,
+                            float* ms_decode);
+
 /* ---- profiling (replaces the PROF_* counters, ops.rs:79-97) ----------------
  * When enabled, every ternary GEMV/GEMM launch of the model loop is bracketed
  * by HIP events on the context stream; totals are per kernel class

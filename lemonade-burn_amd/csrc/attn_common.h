@@ -217,6 +217,181 @@ __device__ __forceinline__ void attention_split(const float* q, int h, int nh, i
 }
 
 // ---------------------------------------------------------------------------
+// The same split for the GH query heads h = g*GH .. g*GH + GH-1 that read KV
+// head g, in one workgroup: every K/V row is loaded once for all of them.
+// Per head the arithmetic and its order are those of attention_split_ku, so
+// both produce the same partials.
+template <int LK, int GH>
+struct AttnGroupShared {
+    __align__(16) float qs[GH][LK * 8];
+    float rmax[GH][4];
+    float rsum[GH][4];
+    __align__(16) float pv[4][GH][LK * 8];
+};
+
+template <int LK, int GH, int KU>
+__device__ __forceinline__ void attention_split_group(const float* q, int g, int nh, int s, int p, const uint16_t* K0,
+                                                      const uint16_t* V0, float scaling, float* o, float* ml,
+                                                      float* sc, AttnGroupShared<LK, GH>& sh) {
+    constexpr int HD = LK * 8, GW = 64 / LK, NK = kThreads / LK;
+    const int vis = p + 1;
+    const int ks = attn_split_keys(vis);
+    const int ns = (vis + ks - 1) / ks;
+    if (s >= ns) return;
+    const int j0 = s * ks, cnt = vis - j0 < ks ? vis - j0 : ks;
+    const int tid = (int)threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const bool act = tid < kThreads;
+    const uint16_t* K = K0 + (size_t)j0 * HD;
+    const uint16_t* V = V0 + (size_t)j0 * HD;
+    const int kslot = lane / LK, cc = lane % LK;
+    const int grp = tid / LK, c = tid % LK;
+    constexpr int QPT = (GH * HD + kThreads - 1) / kThreads;
+    float qv[QPT];
+#pragma unroll
+    for (int i = 0; i < QPT; i++) {
+        const int idx = tid + i * kThreads;
+        qv[i] = (act && idx < GH * HD) ? q[(size_t)g * GH * HD + idx] : 0.0f;
+    }
+    uint4 kb[KU], vb[KU];
+#pragma unroll
+    for (int u = 0; u < KU; u++) {
+        const int k = u * NK + w * GW + kslot;
+        kb[u] = (act && k < cnt) ? *(const uint4*)(K + (size_t)k * HD + 8 * cc) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < KU; u++) {
+        const int k = grp + u * NK;
+        vb[u] = (act && k < cnt) ? *(const uint4*)(V + (size_t)k * HD + 8 * c) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < QPT; i++) {
+        const int idx = tid + i * kThreads;
+        if (act && idx < GH * HD) (&sh.qs[0][0])[idx] = qv[i];
+    }
+    __syncthreads();
+    float q8[GH][8];
+#pragma unroll
+    for (int h = 0; h < GH; h++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) q8[h][e] = sh.qs[h][8 * cc + e];
+
+    float mx[GH];
+#pragma unroll
+    for (int h = 0; h < GH; h++) mx[h] = -__builtin_inff();
+    if (act) {
+        for (int b0 = 0;; b0 += KU * NK) {
+            if (b0 > 0) {
+#pragma unroll
+                for (int u = 0; u < KU; u++) {
+                    const int k = b0 + u * NK + w * GW + kslot;
+                    kb[u] = k < cnt ? *(const uint4*)(K + (size_t)k * HD + 8 * cc) : make_uint4(0, 0, 0, 0);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < KU; u++) {
+                const int k = b0 + u * NK + w * GW + kslot;
+                const uint32_t wv[4] = {kb[u].x, kb[u].y, kb[u].z, kb[u].w};
+#pragma unroll
+                for (int h = 0; h < GH; h++) {
+                    float a = 0.0f;
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        a = __builtin_fmaf(q8[h][2 * e], bf16_to_f32((uint16_t)(wv[e] & 0xffffu)), a);
+                        a = __builtin_fmaf(q8[h][2 * e + 1], bf16_to_f32((uint16_t)(wv[e] >> 16)), a);
+                    }
+                    a = xor_sum_down<LK / 2>(a);
+                    if (k < cnt) {
+                        const float sv = a * scaling;
+                        if (cc == 0) sc[h * ks + k] = sv;
+                        mx[h] = fmaxf(mx[h], sv);
+                    }
+                }
+            }
+            if (b0 + KU * NK >= cnt) break;
+        }
+    }
+#pragma unroll
+    for (int h = 0; h < GH; h++) {
+        const float v = wave_max(mx[h]);
+        if (lane == 0 && w < 4) sh.rmax[h][w] = v;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int h = 0; h < GH; h++) {
+        const float m = fmaxf(fmaxf(sh.rmax[h][0], sh.rmax[h][1]), fmaxf(sh.rmax[h][2], sh.rmax[h][3]));
+        float ps = 0.0f;
+        if (act)
+            for (int u = tid; u < cnt; u += kThreads) {
+                const float e = lbt_expf(sc[h * ks + u] - m);
+                sc[h * ks + u] = e;
+                ps = ps + e;
+            }
+        ps = wave_sum(ps);
+        if (lane == 0 && w < 4) sh.rsum[h][w] = ps;
+    }
+    __syncthreads();
+
+    float acc[GH][8];
+#pragma unroll
+    for (int h = 0; h < GH; h++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) acc[h][e] = 0.0f;
+    if (act) {
+        for (int b0 = 0;; b0 += KU * NK) {
+            if (b0 > 0) {
+#pragma unroll
+                for (int u = 0; u < KU; u++) {
+                    const int k = b0 + grp + u * NK;
+                    vb[u] = k < cnt ? *(const uint4*)(V + (size_t)k * HD + 8 * c) : make_uint4(0, 0, 0, 0);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < KU; u++) {
+                const int k = b0 + grp + u * NK;
+                if (k < cnt) {
+                    const uint32_t wv[4] = {vb[u].x, vb[u].y, vb[u].z, vb[u].w};
+#pragma unroll
+                    for (int h = 0; h < GH; h++) {
+                        const float pj = sc[h * ks + k];
+#pragma unroll
+                        for (int e = 0; e < 4; e++) {
+                            acc[h][2 * e] = __builtin_fmaf(pj, bf16_to_f32((uint16_t)(wv[e] & 0xffffu)), acc[h][2 * e]);
+                            acc[h][2 * e + 1] =
+                                __builtin_fmaf(pj, bf16_to_f32((uint16_t)(wv[e] >> 16)), acc[h][2 * e + 1]);
+                        }
+                    }
+                }
+            }
+            if (b0 + KU * NK >= cnt) break;
+        }
+    }
+    if constexpr (GW > 1) {
+#pragma unroll
+        for (int h = 0; h < GH; h++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) acc[h][e] = xor_sum_up<LK>(acc[h][e]);
+    }
+    if (act && lane < LK) {
+#pragma unroll
+        for (int h = 0; h < GH; h++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) sh.pv[w][h][8 * c + e] = acc[h][e];
+    }
+    __syncthreads();
+    for (int idx = tid; idx < GH * HD && act; idx += kThreads) {
+        const int h = idx / HD, d = idx % HD;
+        o[(size_t)s * nh * HD + (size_t)(g * GH + h) * HD + d] =
+            (sh.pv[0][h][d] + sh.pv[1][h][d]) + (sh.pv[2][h][d] + sh.pv[3][h][d]);
+    }
+    if (tid < GH) {
+        const int h = tid;
+        ml[((size_t)s * nh + g * GH + h) * 2] =
+            fmaxf(fmaxf(sh.rmax[h][0], sh.rmax[h][1]), fmaxf(sh.rmax[h][2], sh.rmax[h][3]));
+        ml[((size_t)s * nh + g * GH + h) * 2 + 1] = (sh.rsum[h][0] + sh.rsum[h][1]) + (sh.rsum[h][2] + sh.rsum[h][3]);
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Combine of one row's splits, as a row source for the activation prologues.
 // Thread t (< NT) produces the row elements of RowRegs (groups of four,
 // v[4g + k] = att[4 NT g + 4 t + k]).  attn_row_issue starts the loads (the

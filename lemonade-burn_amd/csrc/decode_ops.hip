@@ -58,32 +58,53 @@ __global__ __launch_bounds__(kThreads) void embed_kernel(const uint16_t* embed, 
 // row); see attn_common.h.  Grid (nh * kAttnSplits, m); splits past a row's
 // last one exit at once.
 template <int LK>
-__global__ __launch_bounds__(kThreads) void attention_kernel(const float* q, int nh, int kvh, int pos0,
+__global__ __launch_bounds__(kThreads) void attention_kernel(const float* q, int nh, int kvh, RowPos rp,
                                                              const uint16_t* kc, const uint16_t* vc, int cap,
-                                                             float scaling, float* o, float* ml, const int* pos_dev) {
+                                                             float scaling, float* o, float* ml) {
     extern __shared__ float sc[];  // [attn_split_keys(visible keys)]
     __shared__ AttnShared<LK> sh;
     LBT_ATR(0)
-    if (pos_dev) pos0 = *pos_dev;
     const int h = blockIdx.x / kAttnSplits, s = blockIdx.x % kAttnSplits, t = blockIdx.y;
     const int H = nh * LK * 8, g = h / (nh / kvh);
-    const size_t kvoff = (size_t)g * cap * LK * 8;
-    attention_split<LK>(q + (size_t)t * H, h, nh, s, pos0 + t, kc + kvoff, vc + kvoff, scaling,
+    const size_t kvoff = row_cache_offset(rp, t) + (size_t)g * cap * LK * 8;
+    attention_split<LK>(q + (size_t)t * H, h, nh, s, row_position(rp, t), kc + kvoff, vc + kvoff, scaling,
                         o + (size_t)t * kAttnSplits * H, ml + (size_t)t * kAttnSplits * nh * 2, sc, sh);
     LBT_ATR(7)
+}
+
+// The same splits with one workgroup per (KV head, key split, query row)
+// taking all GH query heads of the KV head.  Grid (kvh * kAttnSplits, m).
+template <int LK, int GH>
+__global__ __launch_bounds__(kThreads) void attention_group_kernel(const float* q, int nh, int kvh, RowPos rp,
+                                                                   const uint16_t* kc, const uint16_t* vc, int cap,
+                                                                   float scaling, float* o, float* ml) {
+    extern __shared__ float sc[];  // [GH][attn_split_keys(visible keys)]
+    __shared__ AttnGroupShared<LK, GH> sh;
+    const int g = blockIdx.x / kAttnSplits, s = blockIdx.x % kAttnSplits, t = blockIdx.y;
+    const int H = nh * LK * 8;
+    const size_t kvoff = row_cache_offset(rp, t) + (size_t)g * cap * LK * 8;
+    const int p = row_position(rp, t);
+    if (attn_split_keys(p + 1) <= 2 * (kThreads / LK))
+        attention_split_group<LK, GH, 2>(q + (size_t)t * H, g, nh, s, p, kc + kvoff, vc + kvoff, scaling,
+                                         o + (size_t)t * kAttnSplits * H, ml + (size_t)t * kAttnSplits * nh * 2, sc,
+                                         sh);
+    else
+        attention_split_group<LK, GH, 4>(q + (size_t)t * H, g, nh, s, p, kc + kvoff, vc + kvoff, scaling,
+                                         o + (size_t)t * kAttnSplits * H, ml + (size_t)t * kAttnSplits * nh * 2, sc,
+                                         sh);
 }
 
 // Combine of the attention splits of row blockIdx.x into out (attn_common.h).
 template <int EPT>
 __global__ __launch_bounds__(kThreads) void attn_combine_kernel(const float* o, const float* ml, int nh, int hd,
-                                                                int pos0, float* out, const int* pos_dev) {
+                                                                RowPos rp, float* out) {
     __shared__ AttnTab tab;
     const int t = blockIdx.x, H = nh * hd;
     AttnRow a{o + (size_t)t * kAttnSplits * H, ml + (size_t)t * kAttnSplits * nh * 2, 0, nh, hd, H};
     RowRegs<EPT> r;
     AttnRegs<EPT, 4> ar;
     attn_row_issue(a, nullptr, ar, r);
-    a.ns = attn_splits((pos_dev ? *pos_dev : pos0) + t + 1);
+    a.ns = attn_splits(row_position(rp, t) + 1);
     attn_row_finish(a, ar, r, tab);
     float* dst = out + (size_t)t * H;
 #pragma unroll
@@ -270,6 +291,29 @@ __global__ void synth_bf16_kernel(uint64_t seed, uint64_t tensor, size_t n, uint
     }
 }
 
+// Synthetic KV rows: positions [0, len) of every (layer, sequence, KV head)
+// of a cache laid out [layers * nseq * kvh][cap][hd], bf16 of an
+// approximately N(0,1) value: (u1 + u2 + u3 + u4 - 2) * sqrt(3) of four
+// uniforms on [0, 1) from one splitmix64 draw per element.
+__global__ void synth_kv_kernel(uint64_t seed, size_t rows, int cap, int len, int hd, uint16_t* out) {
+    const uint64_t base = splitmix64(seed);
+    const size_t per_row = (size_t)len * hd, n = rows * per_row;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        const size_t r = i / per_row, rem = i % per_row;
+        const uint64_t z = splitmix64(base + i);
+        float acc = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 4; k++) acc += (float)((z >> (16 * k)) & 0xffffu) * (1.0f / 65536.0f);
+        out[r * (size_t)cap * hd + rem] = f32_to_bf16((acc - 2.0f) * 1.7320508075688772f);
+    }
+}
+
+// p[i] += 1 for i < n (positions of a batch after a step).
+__global__ void advance_pos_kernel(int* p, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] += 1;
+}
+
 // ---------------------------------------------------------------------------
 // launchers
 int launch_embed(lbt_ctx* ctx, const uint16_t* embed, int hidden, int vocab, const uint32_t* tokens,
@@ -280,40 +324,72 @@ int launch_embed(lbt_ctx* ctx, const uint16_t* embed, int hidden, int vocab, con
     return LBT_OK;
 }
 
-int launch_attention(lbt_ctx* ctx, const float* q, int m, int nh, int kvh, int hd, int pos0, const uint16_t* kc,
-                     const uint16_t* vc, int cap, float scaling, float* o, float* ml, const int* pos_dev) {
+namespace {
+
+template <int LK>
+hipError_t launch_attn_lk(int gh, bool grouped, dim3 grid, size_t lds, hipStream_t st, hipEvent_t e0, hipEvent_t e1,
+                          const float* q, int nh, int kvh, const RowPos& rp, const uint16_t* kc, const uint16_t* vc,
+                          int cap, float scaling, float* o, float* ml) {
+    if (!grouped) {
+        hipExtLaunchKernelGGL(attention_kernel<LK>, grid, dim3(kThreads), lds, st, e0, e1, 0, q, nh, kvh, rp, kc, vc,
+                              cap, scaling, o, ml);
+        return hipGetLastError();
+    }
+    switch (gh) {
+        case 1:
+            hipExtLaunchKernelGGL((attention_group_kernel<LK, 1>), grid, dim3(kThreads), lds, st, e0, e1, 0, q, nh,
+                                  kvh, rp, kc, vc, cap, scaling, o, ml);
+            break;
+        case 2:
+            hipExtLaunchKernelGGL((attention_group_kernel<LK, 2>), grid, dim3(kThreads), lds, st, e0, e1, 0, q, nh,
+                                  kvh, rp, kc, vc, cap, scaling, o, ml);
+            break;
+        default:
+            hipExtLaunchKernelGGL((attention_group_kernel<LK, 4>), grid, dim3(kThreads), lds, st, e0, e1, 0, q, nh,
+                                  kvh, rp, kc, vc, cap, scaling, o, ml);
+            break;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace
+
+int launch_attention(lbt_ctx* ctx, const float* q, int m, int nh, int kvh, int hd, const RowPos& rp,
+                     const uint16_t* kc, const uint16_t* vc, int cap, float scaling, float* o, float* ml,
+                     bool grouped) {
     if (kvh <= 0 || nh % kvh) return set_err(ctx, LBT_E_INVALID, "attention: heads must be a multiple of kv heads");
-    // a graph-replayed step reads its position on the device: size for the cache
-    const int vis_max = pos_dev ? cap : pos0 + m;
-    const size_t lds = (size_t)attn_split_keys(vis_max) * sizeof(float);
+    const int gh = nh / kvh;
+    if (gh != 1 && gh != 2 && gh != 4) grouped = false;
+    const size_t lds = (size_t)(grouped ? gh : 1) * attn_split_keys(rp.vis_max) * sizeof(float);
     if (lds > 64 * 1024) return set_err(ctx, LBT_E_RANGE, "attention: context too long for the LDS score buffer");
     hipEvent_t e0, e1;
     prof_pair(ctx, &e0, &e1);
-    dim3 grid(nh * kAttnSplits, m);
+    dim3 grid((grouped ? kvh : nh) * kAttnSplits, m);
+    hipError_t e;
     switch (hd) {
         case 64:
-            hipExtLaunchKernelGGL(attention_kernel<8>, grid, dim3(kThreads), lds, ctx->stream, e0, e1, 0, q, nh, kvh,
-                                  pos0, kc, vc, cap, scaling, o, ml, pos_dev);
+            e = launch_attn_lk<8>(gh, grouped, grid, lds, ctx->stream, e0, e1, q, nh, kvh, rp, kc, vc, cap, scaling, o,
+                                  ml);
             break;
         case 128:
-            hipExtLaunchKernelGGL(attention_kernel<16>, grid, dim3(kThreads), lds, ctx->stream, e0, e1, 0, q, nh, kvh,
-                                  pos0, kc, vc, cap, scaling, o, ml, pos_dev);
+            e = launch_attn_lk<16>(gh, grouped, grid, lds, ctx->stream, e0, e1, q, nh, kvh, rp, kc, vc, cap, scaling,
+                                   o, ml);
             break;
         case 256:
-            hipExtLaunchKernelGGL(attention_kernel<32>, grid, dim3(kThreads), lds, ctx->stream, e0, e1, 0, q, nh, kvh,
-                                  pos0, kc, vc, cap, scaling, o, ml, pos_dev);
+            e = launch_attn_lk<32>(gh, grouped, grid, lds, ctx->stream, e0, e1, q, nh, kvh, rp, kc, vc, cap, scaling,
+                                   o, ml);
             break;
         default:
             return set_err(ctx, LBT_E_INVALID, "attention: head_dim must be 64, 128 or 256");
     }
-    LBT_HIP(ctx, hipGetLastError());
-    const double kv_bytes = 2.0 * kvh * (double)(pos0 + m) * hd * 2.0;
+    if (e != hipSuccess) return hip_err(ctx, e, "attention_kernel launch");
+    const double kv_bytes = 2.0 * kvh * (double)rp.vis_max * hd * 2.0 * m;
     prof_commit(ctx, e0, e1, kProfAttn, kv_bytes);
     return LBT_OK;
 }
 
-int launch_attn_combine(lbt_ctx* ctx, const float* o, const float* ml, int m, int nh, int hd, int pos0, float* out,
-                        const int* pos_dev) {
+int launch_attn_combine(lbt_ctx* ctx, const float* o, const float* ml, int m, int nh, int hd, const RowPos& rp,
+                        float* out) {
     const int H = nh * hd;
     if (nh <= 0 || nh > kAttnMaxHeads || hd % 4 || H > 8192)
         return set_err(ctx, LBT_E_INVALID, "attention combine: at most 64 heads and 8192 columns");
@@ -321,10 +397,10 @@ int launch_attn_combine(lbt_ctx* ctx, const float* o, const float* ml, int m, in
     prof_pair(ctx, &e0, &e1);
     if (H <= 16 * kThreads)
         hipExtLaunchKernelGGL(attn_combine_kernel<16>, dim3(m), dim3(kThreads), 0, ctx->stream, e0, e1, 0, o, ml, nh,
-                              hd, pos0, out, pos_dev);
+                              hd, rp, out);
     else
         hipExtLaunchKernelGGL(attn_combine_kernel<32>, dim3(m), dim3(kThreads), 0, ctx->stream, e0, e1, 0, o, ml, nh,
-                              hd, pos0, out, pos_dev);
+                              hd, rp, out);
     LBT_HIP(ctx, hipGetLastError());
     prof_commit(ctx, e0, e1, kProfAttn, 0.0);
     return LBT_OK;
@@ -398,6 +474,20 @@ int launch_synth_packed(lbt_ctx* ctx, uint64_t seed, uint64_t tensor, int rows, 
 
 int launch_synth_f32(lbt_ctx* ctx, uint64_t seed, uint64_t tensor, size_t n, float lo, float span, float* out) {
     hipLaunchKernelGGL(synth_f32_kernel, dim3(grid_for(n)), dim3(256), 0, ctx->stream, seed, tensor, n, lo, span, out);
+    LBT_HIP(ctx, hipGetLastError());
+    return LBT_OK;
+}
+
+int launch_synth_kv(lbt_ctx* ctx, uint64_t seed, size_t rows, int cap, int len, int hd, uint16_t* out) {
+    if (len <= 0) return LBT_OK;
+    hipLaunchKernelGGL(synth_kv_kernel, dim3(grid_for(rows * (size_t)len * hd)), dim3(256), 0, ctx->stream, seed, rows,
+                       cap, len, hd, out);
+    LBT_HIP(ctx, hipGetLastError());
+    return LBT_OK;
+}
+
+int launch_advance_pos(lbt_ctx* ctx, int* p, int n) {
+    hipLaunchKernelGGL(advance_pos_kernel, dim3((n + 255) / 256), dim3(256), 0, ctx->stream, p, n);
     LBT_HIP(ctx, hipGetLastError());
     return LBT_OK;
 }

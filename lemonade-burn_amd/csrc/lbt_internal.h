@@ -102,6 +102,10 @@ struct TernaryOp {
     // cache at positions pos0 + token ([kv_heads][cap][hd] of this layer)
     int hd = 0, pos0 = 0, cap = 0;
     const int* pos_dev = nullptr;  // device position (graph replay) instead of pos0
+    // batch of sequences: token t is sequence t at position tok_pos[t], its
+    // cache rows seq_stride elements after sequence t-1's (replaces pos0/pos_dev)
+    const int* tok_pos = nullptr;
+    size_t seq_stride = 0;
     const float* cos_t = nullptr;
     const float* sin_t = nullptr;
     uint16_t* kc = nullptr;
@@ -142,13 +146,34 @@ __host__ __device__ __forceinline__ int attn_split_keys(int vis) {
     return ks < kAttnMinKeys ? kAttnMinKeys : ks;
 }
 
-// Attention splits of m query rows at positions pos0 + t (or *pos_dev + t):
-// partials o [m][kAttnSplits][nh*hd], ml [m][kAttnSplits][nh][2].
-int launch_attention(lbt_ctx* ctx, const float* q, int m, int nh, int kvh, int hd, int pos0, const uint16_t* kc,
-                     const uint16_t* vc, int cap, float scaling, float* o, float* ml, const int* pos_dev = nullptr);
+// Positions of the rows of a forward pass: one sequence (row t at pos0 + t,
+// or *pos_dev + t in a graph-replayed step) or a batch of sequences (row t is
+// sequence t at position tok_pos[t]; its cache rows start seq_stride
+// elements after sequence t-1's).  vis_max bounds every row's visible keys.
+struct RowPos {
+    int pos0 = 0;
+    const int* pos_dev = nullptr;
+    const int* tok_pos = nullptr;
+    size_t seq_stride = 0;
+    int vis_max = 0;
+};
+__host__ __device__ __forceinline__ int row_position(const RowPos& r, int t) {
+    return r.tok_pos ? r.tok_pos[t] : (r.pos_dev ? *r.pos_dev : r.pos0) + t;
+}
+__host__ __device__ __forceinline__ size_t row_cache_offset(const RowPos& r, int t) {
+    return r.tok_pos ? (size_t)t * r.seq_stride : 0;
+}
+
+// Attention splits of m query rows: partials o [m][kAttnSplits][nh*hd],
+// ml [m][kAttnSplits][nh][2].  grouped: one workgroup per KV head and split
+// takes all its query heads (K/V read once; long contexts), else one per query
+// head and split (more workgroups; short contexts).  Both give the same bits.
+int launch_attention(lbt_ctx* ctx, const float* q, int m, int nh, int kvh, int hd, const RowPos& rp,
+                     const uint16_t* kc, const uint16_t* vc, int cap, float scaling, float* o, float* ml,
+                     bool grouped = false);
 // Combine of the splits into out [m][nh*hd].
-int launch_attn_combine(lbt_ctx* ctx, const float* o, const float* ml, int m, int nh, int hd, int pos0, float* out,
-                        const int* pos_dev = nullptr);
+int launch_attn_combine(lbt_ctx* ctx, const float* o, const float* ml, int m, int nh, int hd, const RowPos& rp,
+                        float* out);
 int launch_fill_u64(lbt_ctx* ctx, unsigned long long* p, int n, unsigned long long v);
 // Streaming device copy (16-byte granules, byte tail).
 int launch_copy(lbt_ctx* ctx, void* dst, const void* src, size_t bytes);
@@ -193,6 +218,11 @@ int launch_synth_packed(lbt_ctx* ctx, uint64_t seed, uint64_t tensor, int rows, 
 int launch_synth_f32(lbt_ctx* ctx, uint64_t seed, uint64_t tensor, size_t n, float lo, float span,
                      float* out);
 int launch_synth_bf16(lbt_ctx* ctx, uint64_t seed, uint64_t tensor, size_t n, uint16_t* out);
+// Synthetic KV rows (approximately N(0,1), bf16) at positions [0, len) of
+// `rows` (layer, sequence, KV head) rows of `cap` positions each.
+int launch_synth_kv(lbt_ctx* ctx, uint64_t seed, size_t rows, int cap, int len, int hd, uint16_t* out);
+// p[i] += 1 for i < n.
+int launch_advance_pos(lbt_ctx* ctx, int* p, int n);
 
 inline size_t padded_cols(size_t cols) { return (cols + 127) / 128 * 128; }
 

@@ -256,6 +256,21 @@ struct lbt_cache {
     int cap = 0;
 };
 
+// nseq sequences with fixed-capacity caches [layers][nseq][kvh][cap][hd].
+struct lbt_batch {
+    lbt_model* m = nullptr;
+    int nseq = 0;
+    int cap = 0;
+    uint16_t* k = nullptr;
+    uint16_t* v = nullptr;
+    std::vector<int> len;
+    int* pos = nullptr;        // device positions of the current step [nseq]
+    uint32_t* tok_out = nullptr;
+    size_t tok_out_cap = 0;
+    size_t seq_stride() const;
+    size_t layer_stride() const { return (size_t)nseq * seq_stride(); }
+};
+
 namespace {
 
 void lin_shape(const lbt_config& c, int which, int& rows, int& cols) {
@@ -405,21 +420,33 @@ int ensure_cap(lbt_cache* cc, int need) {
     return LBT_OK;
 }
 
-// One forward over n tokens at positions cache.len.. (tokens from `toks_dev`,
-// or from the previous step's argmax key when null).  Leaves the argmax key of
-// the last row in m->key[0] and logits (if `logits_all` or `want_logits`).
-int forward_dev(lbt_model* m, lbt_cache* cc, const uint32_t* toks_dev, int n, bool all_logits, bool want_logits,
-                uint32_t* tok_out_dev, int* state = nullptr) {
+// KV cache rows of a forward pass: layer l of sequence 0 starts at
+// k + l * layer_stride; cap positions per (sequence, KV head).
+struct KvView {
+    uint16_t* k;
+    uint16_t* v;
+    size_t layer_stride;
+    int cap;
+};
+
+// One forward over n rows placed by `rp` (tokens from `toks_dev`, or from the
+// previous step's argmax keys when null).  Leaves the argmax key of each
+// returned row in m->key and logits (if `all_logits` or `want_logits`);
+// without all_logits only the last row goes through the LM head, unless
+// every row is its own sequence (rp.tok_pos), when all rows do.  `grouped`
+// picks the KV-head-grouped attention (long contexts).
+int forward_rows(lbt_model* m, const KvView& kv, const RowPos& rp, const uint32_t* toks_dev, int n, bool all_logits,
+                 bool want_logits, uint32_t* tok_out_dev, int* state, bool grouped) {
     lbt_ctx* ctx = m->ctx;
     const lbt_config& c = m->cfg;
     const int H = c.hidden_size, I = c.intermediate_size, nh = c.num_attention_heads, kvh = c.num_key_value_heads;
-    const int hd = m->hd, pos0 = cc->len;
+    const int hd = m->hd;
     const float eps = (float)c.rms_norm_eps;
     // with `state`, positions come from the device (state[0]) so that the step
     // can be captured once and replayed
     int rc = launch_embed(ctx, m->embed, H, c.vocab_size, toks_dev, m->key, tok_out_dev, n, m->x, state);
     if (rc) return rc;
-    const size_t layer_kv = (size_t)kvh * cc->cap * hd;
+    const size_t layer_kv = kv.layer_stride;
     for (int l = 0; l < c.num_hidden_layers; l++) {
         const lbt_weight* W = &m->lin[l * 7];
         TernaryOp op;
@@ -438,23 +465,25 @@ int forward_dev(lbt_model* m, lbt_cache* cc, const uint32_t* toks_dev, int n, bo
         op.norm_w = m->norm[l * 4 + 0];
         op.out_mode = kOutQKV;
         op.out[0] = m->q;
-        uint16_t* Kl = cc->k + (size_t)l * layer_kv;
-        uint16_t* Vl = cc->v + (size_t)l * layer_kv;
+        uint16_t* Kl = kv.k + (size_t)l * layer_kv;
+        uint16_t* Vl = kv.v + (size_t)l * layer_kv;
         op.hd = hd;
-        op.pos0 = pos0;
-        op.pos_dev = state;
-        op.cap = cc->cap;
+        op.pos0 = rp.pos0;
+        op.pos_dev = rp.pos_dev;
+        op.tok_pos = rp.tok_pos;
+        op.seq_stride = rp.seq_stride;
+        op.cap = kv.cap;
         op.cos_t = m->cos_t;
         op.sin_t = m->sin_t;
         op.kc = Kl;
         op.vc = Vl;
         if ((rc = launch_ternary(ctx, op))) return rc;
-        if ((rc = launch_attention(ctx, m->q, n, nh, kvh, hd, pos0, Kl, Vl, cc->cap, m->scaling, m->ao, m->aml,
-                                   state)))
+        if ((rc = launch_attention(ctx, m->q, n, nh, kvh, hd, rp, Kl, Vl, kv.cap, m->scaling, m->ao, m->aml,
+                                   grouped)))
             return rc;
-        // one token: the o-projection prologue combines the splits itself
-        const bool fused = n == 1 && nh <= kAttnMaxHeads && H <= 4096;
-        if (!fused && (rc = launch_attn_combine(ctx, m->ao, m->aml, n, nh, hd, pos0, m->att, state))) return rc;
+        // one token of one sequence: the o-projection prologue combines the splits itself
+        const bool fused = n == 1 && !rp.tok_pos && nh <= kAttnMaxHeads && H <= 4096;
+        if (!fused && (rc = launch_attn_combine(ctx, m->ao, m->aml, n, nh, hd, rp, m->att))) return rc;
         // o_proj on attn_sub_norm(attn), residual (model.rs:358-359)
         TernaryOp o;
         o.nmat = 1;
@@ -469,8 +498,8 @@ int forward_dev(lbt_model* m, lbt_cache* cc, const uint32_t* toks_dev, int n, bo
         o.att_ml = m->aml;
         o.att_nh = nh;
         o.hd = hd;
-        o.pos0 = pos0;
-        o.pos_dev = state;
+        o.pos0 = rp.pos0;
+        o.pos_dev = rp.pos_dev;
         o.norm_w = m->norm[l * 4 + 2];
         o.eps = eps;
         o.out_mode = kOutF32Add;
@@ -509,13 +538,28 @@ int forward_dev(lbt_model* m, lbt_cache* cc, const uint32_t* toks_dev, int n, bo
         dn.out[0] = m->x;
         if ((rc = launch_ternary(ctx, dn))) return rc;
     }
-    cc->len = pos0 + n;
     m->last_n = n;
     // final norm + tied LM head (model.rs:368-373) + argmax
-    const int first = all_logits ? 0 : n - 1;
+    const int first = (all_logits || rp.tok_pos) ? 0 : n - 1;
     const int rows_out = n - first;
     return launch_bf16_linear(ctx, m->embed, c.vocab_size, H, m->x + (size_t)first * H, rows_out, m->final_norm, eps,
-                              (all_logits || want_logits) ? m->logits : nullptr, all_logits ? nullptr : m->key);
+                              (all_logits || want_logits) ? m->logits : nullptr,
+                              (all_logits && !rp.tok_pos) ? nullptr : m->key);
+}
+
+// One forward of n tokens of one sequence at positions cache.len.. (or, with
+// `state`, at the device position of a graph-replayed step).
+int forward_dev(lbt_model* m, lbt_cache* cc, const uint32_t* toks_dev, int n, bool all_logits, bool want_logits,
+                uint32_t* tok_out_dev, int* state = nullptr) {
+    const lbt_config& c = m->cfg;
+    KvView kv{cc->k, cc->v, (size_t)c.num_key_value_heads * cc->cap * m->hd, cc->cap};
+    RowPos rp;
+    rp.pos0 = cc->len;
+    rp.pos_dev = state;
+    rp.vis_max = state ? cc->cap : cc->len + n;
+    const int rc = forward_rows(m, kv, rp, toks_dev, n, all_logits, want_logits, tok_out_dev, state, false);
+    if (!rc) cc->len += n;
+    return rc;
 }
 
 int ensure_state(lbt_model* m) {
@@ -1084,6 +1128,183 @@ int lbt_model_read_hidden(lbt_model* m, float* out, size_t n) {
     LBT_HIP(ctx, hipMemcpyAsync(out, m->x, n * (size_t)m->cfg.hidden_size * 4, hipMemcpyDeviceToHost, ctx->stream));
     LBT_HIP(ctx, hipStreamSynchronize(ctx->stream));
     return LBT_OK;
+}
+
+// ---- batched decode --------------------------------------------------------
+size_t lbt_batch::seq_stride() const { return (size_t)m->cfg.num_key_value_heads * cap * m->hd; }
+
+namespace {
+
+// KV view and row positions of one step of every sequence of the batch,
+// with b->pos holding the positions.
+int batch_step(lbt_batch* b, const uint32_t* toks_dev, bool want_logits, uint32_t* tok_out_dev) {
+    lbt_model* m = b->m;
+    KvView kv{b->k, b->v, b->layer_stride(), b->cap};
+    RowPos rp;
+    rp.tok_pos = b->pos;
+    rp.seq_stride = b->seq_stride();
+    int vmax = 0;
+    for (int l : b->len) vmax = l + 1 > vmax ? l + 1 : vmax;
+    rp.vis_max = vmax;
+    return forward_rows(m, kv, rp, toks_dev, b->nseq, want_logits, want_logits, tok_out_dev, nullptr, true);
+}
+
+int batch_upload_pos(lbt_batch* b) {
+    lbt_ctx* ctx = b->m->ctx;
+    LBT_HIP(ctx, hipMemcpyAsync(b->pos, b->len.data(), (size_t)b->nseq * 4, hipMemcpyHostToDevice, ctx->stream));
+    return LBT_OK;
+}
+
+}  // namespace
+
+int lbt_batch_new(lbt_model* m, int nseq, int cap, lbt_batch** out) {
+    if (!m || !out || nseq <= 0 || cap <= 0) return set_err(m ? m->ctx : nullptr, LBT_E_INVALID, "bad arguments");
+    lbt_ctx* ctx = m->ctx;
+    *out = nullptr;
+    if (cap > m->cfg.max_position_embeddings)
+        return set_err(ctx, LBT_E_RANGE, "batch: capacity above max_position_embeddings");
+    lbt_batch* b = new lbt_batch();
+    b->m = m;
+    b->nseq = nseq;
+    b->cap = cap;
+    b->len.assign(nseq, 0);
+    const size_t bytes = (size_t)m->cfg.num_hidden_layers * b->layer_stride() * 2;
+    hipError_t e = hipMalloc(&b->k, bytes);
+    if (e == hipSuccess) e = hipMalloc(&b->v, bytes);
+    if (e == hipSuccess) e = hipMalloc(&b->pos, (size_t)nseq * 4);
+    if (e != hipSuccess) {
+        lbt_batch_free(b);
+        return set_err(ctx, LBT_E_NOMEM, "batch: cache allocation failed");
+    }
+    *out = b;
+    return LBT_OK;
+}
+
+void lbt_batch_free(lbt_batch* b) {
+    if (!b) return;
+    hipStreamSynchronize(b->m->ctx->stream);
+    void* bufs[] = {b->k, b->v, b->pos, b->tok_out};
+    for (void* p : bufs)
+        if (p) hipFree(p);
+    delete b;
+}
+
+int lbt_batch_len(const lbt_batch* b, int seq) {
+    if (!b || seq < 0 || seq >= b->nseq) return -1;
+    return b->len[seq];
+}
+
+int lbt_batch_prefill(lbt_batch* b, int seq, const uint32_t* tokens, size_t n, uint32_t* next) {
+    if (!b || !tokens || n == 0 || seq < 0 || seq >= b->nseq)
+        return set_err(b ? b->m->ctx : nullptr, LBT_E_INVALID, "bad arguments");
+    lbt_model* m = b->m;
+    lbt_ctx* ctx = m->ctx;
+    if (b->len[seq] + (int)n > b->cap) return set_err(ctx, LBT_E_RANGE, "batch: sequence capacity exceeded");
+    int rc;
+    if ((rc = ensure_ws(m, (int)n))) return rc;
+    if ((rc = upload_tokens(m, tokens, n))) return rc;
+    const size_t off = (size_t)seq * b->seq_stride();
+    KvView kv{b->k + off, b->v + off, b->layer_stride(), b->cap};
+    RowPos rp;
+    rp.pos0 = b->len[seq];
+    rp.vis_max = b->len[seq] + (int)n;
+    if ((rc = forward_rows(m, kv, rp, m->toks, (int)n, false, false, nullptr, nullptr, (int)n > 1))) return rc;
+    b->len[seq] += (int)n;
+    unsigned long long key = 0;
+    LBT_HIP(ctx, hipMemcpyAsync(&key, m->key, 8, hipMemcpyDeviceToHost, ctx->stream));
+    LBT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    if (next) *next = 0xffffffffu - (uint32_t)(key & 0xffffffffull);
+    return LBT_OK;
+}
+
+int lbt_batch_fill_synthetic(lbt_batch* b, int len, uint64_t seed) {
+    if (!b || len < 0) return set_err(b ? b->m->ctx : nullptr, LBT_E_INVALID, "bad arguments");
+    lbt_model* m = b->m;
+    lbt_ctx* ctx = m->ctx;
+    if (len > b->cap) return set_err(ctx, LBT_E_RANGE, "batch: fill beyond capacity");
+    const size_t rows = (size_t)m->cfg.num_hidden_layers * b->nseq * m->cfg.num_key_value_heads;
+    int rc;
+    if ((rc = launch_synth_kv(ctx, seed * 2 + 1, rows, b->cap, len, m->hd, b->k))) return rc;
+    if ((rc = launch_synth_kv(ctx, seed * 2 + 2, rows, b->cap, len, m->hd, b->v))) return rc;
+    LBT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    b->len.assign(b->nseq, len);
+    return LBT_OK;
+}
+
+int lbt_batch_forward(lbt_batch* b, const uint32_t* tokens, float* logits, uint32_t* next) {
+    if (!b || !tokens) return set_err(b ? b->m->ctx : nullptr, LBT_E_INVALID, "bad arguments");
+    lbt_model* m = b->m;
+    lbt_ctx* ctx = m->ctx;
+    for (int s = 0; s < b->nseq; s++) {
+        if (b->len[s] + 1 > b->cap) return set_err(ctx, LBT_E_RANGE, "batch: sequence capacity exceeded");
+        if (tokens[s] >= (uint32_t)m->cfg.vocab_size) return set_err(ctx, LBT_E_INVALID, "token id out of range");
+    }
+    int rc;
+    if ((rc = ensure_ws(m, b->nseq))) return rc;
+    if ((rc = upload_tokens(m, tokens, (size_t)b->nseq))) return rc;
+    if ((rc = batch_upload_pos(b))) return rc;
+    if ((rc = batch_step(b, m->toks, logits != nullptr, nullptr))) return rc;
+    for (int s = 0; s < b->nseq; s++) b->len[s] += 1;
+    std::vector<unsigned long long> keys((size_t)b->nseq);
+    LBT_HIP(ctx, hipMemcpyAsync(keys.data(), m->key, keys.size() * 8, hipMemcpyDeviceToHost, ctx->stream));
+    if (logits)
+        LBT_HIP(ctx, hipMemcpyAsync(logits, m->logits, (size_t)b->nseq * m->cfg.vocab_size * 4, hipMemcpyDeviceToHost,
+                                    ctx->stream));
+    LBT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    if (next)
+        for (int s = 0; s < b->nseq; s++) next[s] = 0xffffffffu - (uint32_t)(keys[s] & 0xffffffffull);
+    return LBT_OK;
+}
+
+int lbt_batch_decode_greedy(lbt_batch* b, const uint32_t* first, size_t steps, uint32_t* out_tokens,
+                            float* ms_decode) {
+    if (!b || !first || !out_tokens || steps == 0)
+        return set_err(b ? b->m->ctx : nullptr, LBT_E_INVALID, "bad arguments");
+    lbt_model* m = b->m;
+    lbt_ctx* ctx = m->ctx;
+    const int n = b->nseq;
+    for (int s = 0; s < n; s++) {
+        if (b->len[s] + (int)steps > b->cap) return set_err(ctx, LBT_E_RANGE, "batch: sequence capacity exceeded");
+        if (first[s] >= (uint32_t)m->cfg.vocab_size) return set_err(ctx, LBT_E_INVALID, "token id out of range");
+    }
+    int rc;
+    if ((rc = ensure_ws(m, n))) return rc;
+    if (steps * n > b->tok_out_cap) {
+        if (b->tok_out) hipFree(b->tok_out);
+        b->tok_out = nullptr;
+        LBT_HIP(ctx, hipMalloc(&b->tok_out, steps * n * 4));
+        b->tok_out_cap = steps * n;
+    }
+    if ((rc = upload_tokens(m, first, (size_t)n))) return rc;
+    if ((rc = batch_upload_pos(b))) return rc;
+    hipEvent_t e0, e1;
+    LBT_HIP(ctx, hipEventCreate(&e0));
+    LBT_HIP(ctx, hipEventCreate(&e1));
+    hipEventRecord(e0, ctx->stream);
+    // step i consumes the previous step's argmax keys; its embed records them
+    // as step i-1's tokens; positions advance on the device
+    const std::vector<int> len0 = b->len;
+    for (size_t i = 0; i < steps && !rc; i++) {
+        rc = batch_step(b, i == 0 ? m->toks : nullptr, false, i == 0 ? nullptr : b->tok_out + (i - 1) * n);
+        if (!rc) rc = launch_advance_pos(ctx, b->pos, n);
+        for (int s = 0; s < n; s++) b->len[s] += 1;  // vis_max of the next step
+    }
+    if (!rc) rc = launch_embed(ctx, m->embed, 0, m->cfg.vocab_size, nullptr, m->key, b->tok_out + (steps - 1) * n, n, m->x);
+    hipEventRecord(e1, ctx->stream);
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (!rc && e != hipSuccess) rc = hip_err(ctx, e, "batch decode");
+    if (rc) {
+        b->len = len0;
+    } else {
+        float a = 0;
+        hipEventElapsedTime(&a, e0, e1);
+        if (ms_decode) *ms_decode = a;
+        e = hipMemcpy(out_tokens, b->tok_out, steps * n * 4, hipMemcpyDeviceToHost);
+        if (e != hipSuccess) rc = hip_err(ctx, e, "read tokens");
+    }
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    return rc;
 }
 
 }  // extern "C"

@@ -32,6 +32,8 @@ struct GemvArgs {
     // kOutQKV: RoPE at positions pos0 + token and bf16 K/V cache append
     int hd, pos0, cap;
     const int* pos_dev;  // if set, *pos_dev replaces pos0 (graph-replayed steps)
+    const int* tok_pos;  // if set, token t is sequence t at position tok_pos[t]
+    size_t seq_stride;   // its cache rows start t * seq_stride elements in
     const float* cos_t;
     const float* sin_t;
     uint16_t* kc;
@@ -124,7 +126,7 @@ __device__ __forceinline__ void store_single(const GemvArgs& a, int tok, int v, 
 
 // Output of the virtual-row pair (v0, v0 + 1) for the paired modes:
 // kOutRelu2: relu(gate)^2 * up (model.rs:362-363);
-// kOutQKV:   q/k get apply_rope (model.rs:295-301) at position pos + tok, q is
+// kOutQKV:   q/k get apply_rope (model.rs:295-301) at the token's position, q is
 //            stored f32, k and v are rounded to bf16 into the cache.
 template <int OUT>
 __device__ __forceinline__ void store_pair(const GemvArgs& a, int tok, int v0, int d0, int d1, float sa) {
@@ -139,10 +141,11 @@ __device__ __forceinline__ void store_pair(const GemvArgs& a, int tok, int v0, i
         return;
     }
     const float y1 = (float)d1 * inv;
-    const int pos = (a.pos_dev ? *a.pos_dev : a.pos0) + tok;
+    const int pos = a.tok_pos ? a.tok_pos[tok] : (a.pos_dev ? *a.pos_dev : a.pos0) + tok;
+    const size_t coff = a.tok_pos ? (size_t)tok * a.seq_stride : 0;
     if (mat == 2) {  // v: rows r0, r0 + 1 of head r0 / hd
         const int g = r0 / a.hd, d = r0 % a.hd;
-        uint16_t* dst = a.vc + ((size_t)g * a.cap + pos) * a.hd + d;
+        uint16_t* dst = a.vc + coff + ((size_t)g * a.cap + pos) * a.hd + d;
         dst[0] = f32_to_bf16(y0);
         dst[1] = f32_to_bf16(y1);
         return;
@@ -156,7 +159,7 @@ __device__ __forceinline__ void store_pair(const GemvArgs& a, int tok, int v0, i
         q[r0] = z0;
         q[r0 + h2] = z1;
     } else {
-        uint16_t* dst = a.kc + ((size_t)g * a.cap + pos) * a.hd + d;
+        uint16_t* dst = a.kc + coff + ((size_t)g * a.cap + pos) * a.hd + d;
         dst[0] = f32_to_bf16(z0);
         dst[h2] = f32_to_bf16(z1);
     }

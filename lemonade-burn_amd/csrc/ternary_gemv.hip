@@ -328,7 +328,7 @@ int make_gemv_args(lbt_ctx* ctx, const TernaryOp& op, GemvArgs& a) {
         (nmat != 3 || op.hd <= 0 || op.hd % 2 || op.rows[0] % op.hd || op.rows[1] % op.hd || op.rows[1] != op.rows[2]))
         return set_err(ctx, LBT_E_INVALID, "ternary: q/k/v fusion needs head-aligned q, k, v");
     if (op.in_mode == kInAttn &&
-        (op.m != 1 || op.out_mode != kOutF32Add || !op.att_o || !op.att_ml || op.att_nh <= 0 ||
+        (op.m != 1 || op.tok_pos || op.out_mode != kOutF32Add || !op.att_o || !op.att_ml || op.att_nh <= 0 ||
          op.att_nh > kAttnMaxHeads || op.hd <= 0 || op.hd % 4 || op.att_nh * op.hd != op.cols || op.cols % 4 ||
          op.cols > 4096))
         return set_err(ctx, LBT_E_INVALID, "ternary: attention-combine input needs one token, nh*hd = cols <= 4096");
@@ -357,6 +357,8 @@ int make_gemv_args(lbt_ctx* ctx, const TernaryOp& op, GemvArgs& a) {
     a.hd = op.hd;
     a.pos0 = op.pos0;
     a.pos_dev = op.pos_dev;
+    a.tok_pos = op.tok_pos;
+    a.seq_stride = op.seq_stride;
     a.cap = op.cap;
     a.cos_t = op.cos_t;
     a.sin_t = op.sin_t;

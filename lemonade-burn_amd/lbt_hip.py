@@ -93,6 +93,13 @@ SIGNATURES = {
     "lbt_model_generate_greedy": (i32, [vp, vp, sz, sz, vp, vp, vp, vp]),
     "lbt_model_decode_greedy": (i32, [vp, vp, C.c_uint32, sz, vp, vp]),
     "lbt_model_read_hidden": (i32, [vp, vp, sz]),
+    "lbt_batch_new": (i32, [vp, i32, i32, C.POINTER(vp)]),
+    "lbt_batch_free": (None, [vp]),
+    "lbt_batch_len": (i32, [vp, i32]),
+    "lbt_batch_prefill": (i32, [vp, i32, vp, sz, vp]),
+    "lbt_batch_fill_synthetic": (i32, [vp, i32, C.c_uint64]),
+    "lbt_batch_forward": (i32, [vp, vp, vp, vp]),
+    "lbt_batch_decode_greedy": (i32, [vp, vp, sz, vp, vp]),
     "lbt_prof_enable": (i32, [vp, i32]),
     "lbt_prof_read": (i32, [vp, C.POINTER(LbtProf), i32]),
 }
@@ -340,6 +347,11 @@ class Model:
     def linear(self, layer: int, which: int) -> int:
         return self.ctx.lib.lbt_model_linear(self.h, layer, which)
 
+    def new_batch(self, nseq: int, cap: int) -> "Batch":
+        h = C.c_void_p()
+        self.ctx.check(self.ctx.lib.lbt_batch_new(self.h, nseq, cap, C.byref(h)))
+        return Batch(self, h, nseq)
+
 
 class Cache:
     def __init__(self, model: Model, h):
@@ -358,4 +370,48 @@ class Cache:
     def free(self):
         if self.h:
             self.model.ctx.lib.lbt_cache_free(self.h)
+            self.h = None
+
+
+class Batch:
+    """nseq sequences decoded together (lbt_batch_*)."""
+
+    def __init__(self, model: Model, h, nseq: int):
+        self.model, self.h, self.nseq = model, h, nseq
+
+    def _check(self, rc):
+        self.model.ctx.check(rc)
+
+    def len(self, seq: int) -> int:
+        return self.model.ctx.lib.lbt_batch_len(self.h, seq)
+
+    def prefill(self, seq: int, tokens) -> int:
+        t = np.ascontiguousarray(tokens, np.uint32)
+        nxt = C.c_uint32()
+        self._check(self.model.ctx.lib.lbt_batch_prefill(self.h, seq, _ptr(t), t.size, C.byref(nxt)))
+        return int(nxt.value)
+
+    def fill_synthetic(self, length: int, seed: int):
+        self._check(self.model.ctx.lib.lbt_batch_fill_synthetic(self.h, length, C.c_uint64(seed)))
+
+    def forward(self, tokens, want_logits: bool = True):
+        t = np.ascontiguousarray(tokens, np.uint32)
+        assert t.size == self.nseq
+        nxt = np.zeros(self.nseq, np.uint32)
+        logits = np.zeros((self.nseq, self.model.cfg.vocab_size), np.float32) if want_logits else None
+        self._check(self.model.ctx.lib.lbt_batch_forward(self.h, _ptr(t), _ptr(logits) if want_logits else None,
+                                                         _ptr(nxt)))
+        return logits, nxt
+
+    def decode_greedy(self, first, steps: int):
+        f = np.ascontiguousarray(first, np.uint32)
+        assert f.size == self.nseq
+        out = np.zeros((steps, self.nseq), np.uint32)
+        md = C.c_float()
+        self._check(self.model.ctx.lib.lbt_batch_decode_greedy(self.h, _ptr(f), steps, _ptr(out), C.byref(md)))
+        return out, float(md.value)
+
+    def free(self):
+        if self.h:
+            self.model.ctx.lib.lbt_batch_free(self.h)
             self.h = None
