@@ -213,6 +213,114 @@ __global__ __launch_bounds__(kThreads) void lmhead_kernel(const uint16_t* W, int
     if (key && lane == 0 && best) atomicMax(&key[t], best);
 }
 
+// Final RMSNorm of row blockIdx.x into xn (the LM head prologue's
+// arithmetic, written out once for the batched head below).
+__global__ __launch_bounds__(kThreads) void row_norm_kernel(const float* x, int cols, const float* norm_w, float eps,
+                                                            float* xn) {
+    __shared__ float red[kRedFloats];
+    const int t = blockIdx.x, tid = threadIdx.x;
+    const float* xr = x + (size_t)t * cols;
+    float* dst = xn + (size_t)t * cols;
+    if (cols <= 16 * kThreads) {
+        float v[16];
+        load_norm_row<16>(SrcF32{xr}, cols, norm_w, eps, v, red);
+#pragma unroll
+        for (int e = 0; e < 16; e++)
+            if (row_elem(tid, e) < cols) dst[row_elem(tid, e)] = v[e];
+    } else {
+        const float rr = norm_factor_global(SrcF32{xr}, cols, norm_w, eps, red);
+        for (int i = tid; i < cols; i += kThreads) dst[i] = norm_w ? (xr[i] * rr) * norm_w[i] : xr[i];
+    }
+}
+
+// LM head for several token rows at once (normalized rows xn [m][cols]):
+// each (weight row, token) dot product has lmhead_kernel's order (lane l
+// takes chunks l, l+64, ... with fused multiply-adds in element order, then
+// the butterfly), so the logits and argmax keys are the same bits; what
+// changes is reuse: a workgroup keeps TG token rows in LDS and each wavefront
+// holds R weight rows unpacked in registers for all of them.  Workgroup i
+// takes token group i % ngroups of row tile i / ngroups, so the groups of one
+// tile run together and share its weight rows through the caches.
+template <int R, int NCH>
+__global__ __launch_bounds__(kThreads) void lmhead_batch_kernel(const uint16_t* W, int rows, int cols, const float* xn,
+                                                                int m, int tg, int tile_rows, float* logits,
+                                                                unsigned long long* key) {
+    extern __shared__ __align__(16) float xs[];  // [tg][cols]
+    const int ngroups = (m + tg - 1) / tg;
+    const int grp = blockIdx.x % ngroups, tile = blockIdx.x / ngroups;
+    const int t0 = grp * tg, nt = m - t0 < tg ? m - t0 : tg;
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    for (int i = tid * 4; i < nt * cols; i += kThreads * 4)
+        *(float4*)(xs + i) = *(const float4*)(xn + (size_t)t0 * cols + i);
+    __syncthreads();
+    const int nchunks = cols >> 3;
+    const int r_begin = tile * tile_rows, r_end = r_begin + tile_rows < rows ? r_begin + tile_rows : rows;
+    unsigned long long best[16];
+#pragma unroll
+    for (int t = 0; t < 16; t++) best[t] = 0ull;
+    for (int rb = r_begin + w * R; rb < r_end; rb += 4 * R) {
+        // R weight rows of this wavefront, unpacked to f32
+        float wf[R][NCH][8];
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const int row = rb + r < r_end ? rb + r : rb;
+            const uint4* wr = (const uint4*)(W + (size_t)row * cols);
+#pragma unroll
+            for (int i = 0; i < NCH; i++) {
+                const int c = lane + 64 * i;
+                const uint4 v = c < nchunks ? ld_stream(wr + c) : make_uint4(0, 0, 0, 0);
+                wf[r][i][0] = bf_lo(v.x);
+                wf[r][i][1] = bf_hi(v.x);
+                wf[r][i][2] = bf_lo(v.y);
+                wf[r][i][3] = bf_hi(v.y);
+                wf[r][i][4] = bf_lo(v.z);
+                wf[r][i][5] = bf_hi(v.z);
+                wf[r][i][6] = bf_lo(v.w);
+                wf[r][i][7] = bf_hi(v.w);
+            }
+        }
+        for (int t = 0; t < nt; t++) {
+            const float* xt = xs + t * cols;
+            float acc[R];
+#pragma unroll
+            for (int r = 0; r < R; r++) acc[r] = 0.0f;
+#pragma unroll
+            for (int i = 0; i < NCH; i++) {
+                const int c = lane + 64 * i;
+                if (c < nchunks) {
+                    const float4 x0 = *(const float4*)(xt + 8 * c);
+                    const float4 x1 = *(const float4*)(xt + 8 * c + 4);
+                    const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+                    for (int r = 0; r < R; r++)
+#pragma unroll
+                        for (int e = 0; e < 8; e++) acc[r] = __builtin_fmaf(wf[r][i][e], xv[e], acc[r]);
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const float a = wave_sum(acc[r]);
+                const int row = rb + r;
+                if (lane == 0 && row < r_end) {
+                    if (logits) logits[(size_t)(t0 + t) * rows + row] = a;
+                    const unsigned long long k = argmax_key(a, (uint32_t)row);
+#pragma unroll
+                    for (int u = 0; u < 16; u++)
+                        if (u == t) best[u] = k > best[u] ? k : best[u];
+                }
+            }
+        }
+    }
+    if (key && lane == 0)
+        for (int t = 0; t < nt; t++) {
+            unsigned long long b = 0ull;
+#pragma unroll
+            for (int u = 0; u < 16; u++)
+                if (u == t) b = best[u];
+            if (b) atomicMax(&key[t0 + t], b);
+        }
+}
+
 __global__ void set_state_kernel(int* state, int pos, int slot) {
     if (threadIdx.x == 0) {
         state[0] = pos;
@@ -407,9 +515,38 @@ int launch_attn_combine(lbt_ctx* ctx, const float* o, const float* ml, int m, in
 }
 
 int launch_bf16_linear(lbt_ctx* ctx, const uint16_t* w, int rows, int cols, const float* x, int m,
-                       const float* norm_w, float eps, float* logits, unsigned long long* key) {
+                       const float* norm_w, float eps, float* logits, unsigned long long* key, float* xn) {
     if (cols % 8) return set_err(ctx, LBT_E_INVALID, "bf16 linear: cols must be a multiple of 8");
     if (m <= 0) return LBT_OK;
+    constexpr int kTG = 8, kR = 2;
+    if (m >= 2 && xn && cols <= 64 * kLmChunks * 8) {
+        // several rows: normalize once, then the weight-reusing head
+        hipLaunchKernelGGL(row_norm_kernel, dim3(m), dim3(kThreads), 0, ctx->stream, x, cols, norm_w, eps, xn);
+        LBT_HIP(ctx, hipGetLastError());
+        const int tg = m < kTG ? m : kTG;
+        const int ngroups = (m + tg - 1) / tg;
+        int tiles = ctx->cus * 4 / ngroups;
+        if (tiles < 1) tiles = 1;
+        int tile_rows = (rows + tiles - 1) / tiles;
+        tile_rows = (tile_rows + 4 * kR - 1) / (4 * kR) * (4 * kR);
+        tiles = (rows + tile_rows - 1) / tile_rows;
+        const size_t lds = (size_t)tg * cols * sizeof(float);
+        static bool attr = false;
+        if (!attr) {
+            (void)hipFuncSetAttribute((const void*)lmhead_batch_kernel<kR, kLmChunks>,
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024);
+            (void)hipGetLastError();
+            attr = true;
+        }
+        if (lds > 96 * 1024) return set_err(ctx, LBT_E_INVALID, "bf16 linear: token group exceeds LDS");
+        hipEvent_t e0, e1;
+        prof_pair(ctx, &e0, &e1);
+        hipExtLaunchKernelGGL((lmhead_batch_kernel<kR, kLmChunks>), dim3(tiles * ngroups), dim3(kThreads), lds,
+                              ctx->stream, e0, e1, 0, w, rows, cols, xn, m, tg, tile_rows, logits, key);
+        LBT_HIP(ctx, hipGetLastError());
+        prof_commit(ctx, e0, e1, kProfHead, (double)rows * cols * 2.0);
+        return LBT_OK;
+    }
     const size_t lds = (size_t)cols * sizeof(float);
     if (lds > 64 * 1024) return set_err(ctx, LBT_E_INVALID, "bf16 linear: cols too large");
     int blocks = (rows + 31) / 32;

@@ -129,7 +129,7 @@ int launch_quantize(lbt_ctx* ctx, const float* x, const float* norm_w, float eps
 // logits[t*rows + r] = sum_k xn[t,k] * W[r,k] with xn = rmsnorm(x) if norm_w.
 // If key != nullptr, the first-max key of row t is atomically maxed into key[t].
 int launch_bf16_linear(lbt_ctx* ctx, const uint16_t* w, int rows, int cols, const float* x, int m,
-                       const float* norm_w, float eps, float* logits, unsigned long long* key);
+                       const float* norm_w, float eps, float* logits, unsigned long long* key, float* xn = nullptr);
 
 // ---- model pieces --------------------------------------------------------
 // state (nullable, device): {position, output slot}; when set, the kernel

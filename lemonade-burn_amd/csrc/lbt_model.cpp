@@ -544,7 +544,7 @@ int forward_rows(lbt_model* m, const KvView& kv, const RowPos& rp, const uint32_
     const int rows_out = n - first;
     return launch_bf16_linear(ctx, m->embed, c.vocab_size, H, m->x + (size_t)first * H, rows_out, m->final_norm, eps,
                               (all_logits || want_logits) ? m->logits : nullptr,
-                              (all_logits && !rp.tok_pos) ? nullptr : m->key);
+                              (all_logits && !rp.tok_pos) ? nullptr : m->key, m->att);
 }
 
 // One forward of n tokens of one sequence at positions cache.len.. (or, with
