@@ -67,6 +67,56 @@ def batched_decode(model, cfg, batch: int, cap: int = 4096, steps: int = 8) -> d
             "ms_per_step": round(ms_step, 3), "hbm_GBs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
 
 
+MFMA_INT8_PEAK_TOPS = 5000.0
+
+
+def prefill_gemm(ctx, reps: int = 10) -> list:
+    """the prefill GEMM (int8 MFMA) on the FFN shapes
+    2560->6912 and 6912->2560 at M = 128, 512, 2048 tokens; seeded ternary
+    weights (P = 0.3/0.4/0.3) and int8 activations resident on the device;
+    HIP events around each launch (the library's profiling pass)."""
+    import ctypes as C
+
+    lib = ctx.lib
+    rng = np.random.default_rng(3)
+    res = []
+    for rows, cols in [(6912, 2560), (2560, 6912)]:
+        kp = (cols + 127) // 128 * 128
+        codes = rng.choice(np.array([0, 1, 2], np.uint8), size=(rows, kp), p=[0.3, 0.4, 0.3])
+        c4 = codes.reshape(rows, kp // 128, 4, 32)  # block, code group k, byte j
+        packed = (c4[:, :, 0] | (c4[:, :, 1] << 2) | (c4[:, :, 2] << 4) | (c4[:, :, 3] << 6)).reshape(rows, kp // 4)
+        w = ctx.upload(packed, rows, cols, 1.0)
+        for m in (128, 512, 2048):
+            q = rng.integers(-127, 128, (m, kp)).astype(np.int8)
+            q[:, cols:] = 0
+            qs = q.astype(np.int32).sum(1).astype(np.int32)
+            sa = np.full(m, 0.05, np.float32)
+            dq, ds, dsum, dout = C.c_void_p(), C.c_void_p(), C.c_void_p(), C.c_void_p()
+            for p_, n in ((dq, q.nbytes), (ds, sa.nbytes), (dsum, qs.nbytes), (dout, m * rows * 4)):
+                ctx.check(lib.lbt_dev_alloc(ctx.h, n, C.byref(p_)))
+            ctx.check(lib.lbt_memcpy_h2d(ctx.h, dq, q.ctypes.data, q.nbytes))
+            ctx.check(lib.lbt_memcpy_h2d(ctx.h, ds, sa.ctypes.data, sa.nbytes))
+            ctx.check(lib.lbt_memcpy_h2d(ctx.h, dsum, qs.ctypes.data, qs.nbytes))
+            wa = (C.c_void_p * 1)(w.h)
+            oa = (C.c_void_p * 1)(dout.value)
+            ctx.check(lib.lbt_gemm_multi_dev(ctx.h, wa, 1, dq, ds, dsum, m, oa))
+            ctx.sync()
+            ctx.prof_read(reset=True)
+            ctx.prof_enable(True)
+            for _ in range(reps):
+                ctx.check(lib.lbt_gemm_multi_dev(ctx.h, wa, 1, dq, ds, dsum, m, oa))
+            p = ctx.prof_read(reset=True)
+            ctx.prof_enable(False)
+            us = p["gemm"]["ms"] * 1e3 / max(p["gemm"]["launches"], 1)
+            tops = 2.0 * m * rows * kp / (us * 1e-6) / 1e12
+            res.append({"rows": rows, "cols": cols, "m": m, "us": round(us, 2), "TOPS": round(tops, 1),
+                        "frac": round(tops / MFMA_INT8_PEAK_TOPS, 4)})
+            for p_ in (dq, ds, dsum, dout):
+                lib.lbt_dev_free(ctx.h, p_)
+        w.free()
+    return res
+
+
 def pmc_pass() -> int:
     """The command profiled for the HBM counters (under rocprofv3 --pmc):
     one copy of CALIB_BYTES with the library's copy kernel (the calibration
@@ -229,6 +279,7 @@ def main() -> int:
     }
     if not args.no_batched:
         line["batched_decode"] = [batched_decode(model, cfg, bsz) for bsz in (16, 64)]
+        line["prefill_gemm"] = prefill_gemm(ctx)
     model.free()
     ctx.close()
     if not args.no_cpu_baseline:
