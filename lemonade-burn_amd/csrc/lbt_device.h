@@ -32,6 +32,12 @@ template <typename T>
 __device__ __forceinline__ T gload(const T* p) {
     return *(const LBT_GLOBAL T*)p;
 }
+// Store through the global address space (a flat store also counts on the
+// LDS counter, and waits for it then wait for every store in flight).
+template <typename T>
+__device__ __forceinline__ void gstore(T* p, T v) {
+    *(LBT_GLOBAL T*)p = v;
+}
 
 // Buffer resource over [base, base + bytes): raw buffer loads past the end
 // return zeros, so bounded loads need no branch (and no register merge that

@@ -115,12 +115,11 @@ __device__ __forceinline__ void store_single(const GemvArgs& a, int tok, int v, 
     resolve_row<OUT>(a, v, mt, ro);
     const size_t o = (size_t)tok * sel3(a.rows, mt) + ro;
     if (OUT == kOutI32) {
-        ((int32_t*)sel3(a.out, mt))[o] = dot;
+        gstore((int32_t*)sel3(a.out, mt) + o, (int32_t)dot);
     } else {
         const float y = (float)dot * (1.0f / (sa * sel3(a.sw, mt)));
-        float* dst = (float*)sel3(a.out, mt);
-        if (OUT == kOutF32Add) dst[o] = dst[o] + y;
-        else dst[o] = y;
+        float* dst = (float*)sel3(a.out, mt) + o;
+        gstore(dst, OUT == kOutF32Add ? gload(dst) + y : y);
     }
 }
 
@@ -137,31 +136,31 @@ __device__ __forceinline__ void store_pair(const GemvArgs& a, int tok, int v0, i
     if (OUT == kOutRelu2) {
         const float u = (float)d1 * (1.0f / (sa * a.sw[1]));
         const float rl = y0 > 0.0f ? y0 : 0.0f;
-        ((float*)a.out[0])[(size_t)tok * a.rows[0] + r0] = (rl * rl) * u;
+        gstore((float*)a.out[0] + (size_t)tok * a.rows[0] + r0, (rl * rl) * u);
         return;
     }
     const float y1 = (float)d1 * inv;
-    const int pos = a.tok_pos ? a.tok_pos[tok] : (a.pos_dev ? *a.pos_dev : a.pos0) + tok;
+    const int pos = a.tok_pos ? gload(a.tok_pos + tok) : (a.pos_dev ? gload(a.pos_dev) : a.pos0) + tok;
     const size_t coff = a.tok_pos ? (size_t)tok * a.seq_stride : 0;
     if (mat == 2) {  // v: rows r0, r0 + 1 of head r0 / hd
         const int g = r0 / a.hd, d = r0 % a.hd;
         uint16_t* dst = a.vc + coff + ((size_t)g * a.cap + pos) * a.hd + d;
-        dst[0] = f32_to_bf16(y0);
-        dst[1] = f32_to_bf16(y1);
+        gstore(dst, f32_to_bf16(y0));
+        gstore(dst + 1, f32_to_bf16(y1));
         return;
     }
     const int h2 = a.hd >> 1, g = r0 / a.hd, d = r0 % a.hd;
-    const float c = a.cos_t[(size_t)pos * h2 + d], sn = a.sin_t[(size_t)pos * h2 + d];
+    const float c = gload(a.cos_t + (size_t)pos * h2 + d), sn = gload(a.sin_t + (size_t)pos * h2 + d);
     const float z0 = y0 * c + (-y1) * sn;
     const float z1 = y1 * c + y0 * sn;
     if (mat == 0) {
         float* q = (float*)a.out[0] + (size_t)tok * a.rows[0];
-        q[r0] = z0;
-        q[r0 + h2] = z1;
+        gstore(q + r0, z0);
+        gstore(q + r0 + h2, z1);
     } else {
         uint16_t* dst = a.kc + coff + ((size_t)g * a.cap + pos) * a.hd + d;
-        dst[0] = f32_to_bf16(z0);
-        dst[h2] = f32_to_bf16(z1);
+        gstore(dst, f32_to_bf16(z0));
+        gstore(dst + h2, f32_to_bf16(z1));
     }
 }
 

@@ -23,11 +23,174 @@
 // the decode GEMV (ternary_common.h), so outputs are identical.
 #include <stdlib.h>
 
+#include <type_traits>
+
 #include "ternary_common.h"
+
+#ifdef LBT_GEMM_TRACE
+// Debug build only: per-workgroup wall-clock stamps of the GEMM phases.
+__device__ unsigned long long lbt_gemm_trace[4096 * 8];
+#define MTR(i)                                                       \
+    {                                                                \
+        const unsigned b = blockIdx.y * gridDim.x + blockIdx.x;      \
+        if (threadIdx.x == 0 && b < 4096) {                          \
+            lbt_gemm_trace[b * 8 + (i)] = wall_clock64();            \
+            if ((i) == 0 || (i) == 4) lbt_gemm_trace[b * 8 + 5 + (i) / 4] = clock64(); \
+        }                                                            \
+    }
+extern "C" int lbt_debug_gemm_trace(unsigned long long* out) {
+    return (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(lbt_gemm_trace), sizeof(lbt_gemm_trace));
+}
+#else
+#define MTR(i)
+#endif
 
 namespace lbt {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+// MFMA D layouts.  16 x 16 tiles (v4i): lane l holds row l & 15 and tokens
+// 4 (l >> 4) + r, r = 0..3.  32 x 32 tiles (v16i): lane l holds row l & 31
+// and tokens 8 (r >> 2) + 4 (l >> 5) + (r & 3), r = 0..15.
+template <int TM>
+struct DLayout;
+template <>
+struct DLayout<16> {
+    static constexpr int R = 4;
+    __device__ static int tok(int lane, int r) { return 4 * (lane >> 4) + r; }
+    __device__ static int row(int lane) { return lane & 15; }
+};
+template <>
+struct DLayout<32> {
+    static constexpr int R = 16;
+    __device__ static int tok(int lane, int r) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
+    __device__ static int row(int lane) { return lane & 31; }
+};
+
+// Output stage of one wave's MS x NS block of TM x TM MFMA tiles (tokens
+// from tok0, virtual rows from row0), in the D layout above.  Values are
+// those of store_single / store_pair: dot = acc - sum(q) and the same float
+// expressions.  Every load comes first, with clamped (always valid)
+// indices, so the loads are in flight together; the stores follow under the
+// bounds checks.
+template <int OUT, int TM, int MS, int NS, typename AccT>
+__device__ __forceinline__ void mfma_epilogue(const GemvArgs& a, AccT (&acc)[MS][NS], int tok0, int row0) {
+    using L = DLayout<TM>;
+    constexpr int R = L::R;
+    const int lane = (int)threadIdx.x & 63, lr = L::row(lane);
+    const int M = a.m;
+    int qs[MS][R];
+    float sa[MS][R];
+#pragma unroll
+    for (int ms = 0; ms < MS; ms++)
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const int tok = tok0 + ms * TM + L::tok(lane, r);
+            const int tc = tok < M ? tok : M - 1;
+            qs[ms][r] = gload(a.qsum + tc);
+            sa[ms][r] = a.qscale ? gload(a.qscale + tc) : 1.0f;
+        }
+    if (OUT == kOutRelu2) {
+        // store_pair's relu(gate)^2 * up with the two scale divisions once
+        // per token: even lanes hold gate row r, odd lanes up row r
+        float* out0 = (float*)a.out[0];
+        const int ld0 = a.rows[0];
+#pragma unroll
+        for (int ms = 0; ms < MS; ms++)
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const int tok = tok0 + ms * TM + L::tok(lane, r);
+                const float ig = 1.0f / (sa[ms][r] * a.sw[0]);
+                const float iu = 1.0f / (sa[ms][r] * a.sw[1]);
+#pragma unroll
+                for (int s = 0; s < NS; s++) {
+                    const int vr = row0 + s * TM + lr;
+                    const int d = acc[ms][s][r] - qs[ms][r];
+                    const int dp = __shfl_xor(d, 1);
+                    if (tok < M && vr < a.total_rows && (lr & 1) == 0) {
+                        const float y0 = (float)d * ig;
+                        const float u = (float)dp * iu;
+                        const float rl = y0 > 0.0f ? y0 : 0.0f;
+                        gstore(out0 + (size_t)tok * ld0 + (vr >> 1), (rl * rl) * u);
+                    }
+                }
+            }
+        return;
+    }
+    if (OUT == kOutQKV) {
+#pragma unroll
+        for (int ms = 0; ms < MS; ms++)
+#pragma unroll
+            for (int s = 0; s < NS; s++)
+#pragma unroll
+                for (int r = 0; r < R; r++) {
+                    const int tok = tok0 + ms * TM + L::tok(lane, r);
+                    const int vr = row0 + s * TM + lr;
+                    const int d = acc[ms][s][r] - qs[ms][r];
+                    const int dp = __shfl_xor(d, 1);
+                    if (tok < M && vr < a.total_rows && (lr & 1) == 0) store_pair<OUT>(a, tok, vr, d, dp, sa[ms][r]);
+                }
+        return;
+    }
+    // unpaired modes: row -> (matrix, row) once per row block
+    void* base[NS];
+    int ld[NS];
+    float sw[NS];
+    bool okr[NS];
+#pragma unroll
+    for (int s = 0; s < NS; s++) {
+        const int vr = row0 + s * TM + lr;
+        okr[s] = vr < a.total_rows;
+        int mt, ro;
+        resolve_row<OUT>(a, okr[s] ? vr : 0, mt, ro);
+        ld[s] = sel3(a.rows, mt);
+        sw[s] = sel3(a.sw, mt);
+        base[s] = OUT == kOutI32 ? (void*)((int32_t*)sel3(a.out, mt) + ro) : (void*)((float*)sel3(a.out, mt) + ro);
+    }
+    // residual add: the old values, at most 32 loads in flight at a time
+    constexpr int MH = (MS * NS * R > 32 && MS > 1) ? MS / 2 : MS;
+#pragma unroll
+    for (int h = 0; h < MS; h += MH) {
+        float old[MH][NS][R];
+        if (OUT == kOutF32Add) {
+#pragma unroll
+            for (int mi = 0; mi < MH; mi++)
+#pragma unroll
+                for (int s = 0; s < NS; s++)
+#pragma unroll
+                    for (int r = 0; r < R; r++) {
+                        const int tok = tok0 + (h + mi) * TM + L::tok(lane, r);
+                        const int tc = tok < M ? tok : M - 1;
+                        old[mi][s][r] = gload((const float*)base[s] + (size_t)tc * ld[s]);
+                    }
+        }
+#pragma unroll
+        for (int mi = 0; mi < MH; mi++)
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const int ms = h + mi;
+                const int tok = tok0 + ms * TM + L::tok(lane, r);
+                // 1/(s_a*s_w): one correctly rounded division per token while
+                // the row blocks share one matrix scale
+                const float inv0 = OUT == kOutI32 ? 0.0f : 1.0f / (sa[ms][r] * sw[0]);
+#pragma unroll
+                for (int s = 0; s < NS; s++) {
+                    if (tok >= M || !okr[s]) continue;
+                    const int d = acc[ms][s][r] - qs[ms][r];
+                    const size_t o = (size_t)tok * ld[s];
+                    if (OUT == kOutI32) {
+                        gstore((int32_t*)base[s] + o, (int32_t)d);
+                    } else {
+                        const float inv = sw[s] == sw[0] ? inv0 : 1.0f / (sa[ms][r] * sw[s]);
+                        const float y = (float)d * inv;
+                        gstore((float*)base[s] + o, OUT == kOutF32Add ? old[mi][s][r] + y : y);
+                    }
+                }
+            }
+    }
+}
 
 template <int MS, int NS, int OUT>
 __global__ __launch_bounds__(kThreads) void tgemm_kernel(GemvArgs a) {
@@ -116,25 +279,211 @@ __global__ __launch_bounds__(kThreads) void tgemm_kernel(GemvArgs a) {
         __syncthreads();
     }
 
-    // D layout: lane (g, i) holds tokens 4g..4g+3 of the 16-token block, row i.
+    mfma_epilogue<OUT, 16>(a, acc, m0 + wm * (BM / 2), n0 + wn * (BN / 2));
+}
+
+// ---------------------------------------------------------------------------
+// Pipelined prefill GEMM on the full-rate int8 MFMA of gfx950
+// (v_mfma_i32_32x32x32_i8: 32768 MACs in 8 passes, twice the rate of the
+// 16x16x64 form).  A workgroup of 4 wavefronts (2 x 2) computes BM = 64 MS
+// tokens x BN = 64 NS rows, each wavefront MS x NS tiles of 32 x 32.  A step
+// covers KB 128-k blocks (8 KB MFMAs per tile).
+//
+// Activations go HBM -> LDS with global_load_lds_dwordx4 (no registers) into
+// a ring of 4 stages of one step's slice each, 4 slices ahead; the MFMA A
+// operands of slice p+1 are read from LDS while the MFMAs of slice p run.
+// Packed weights go to registers 4 steps ahead and are unpacked per MFMA.
+// One barrier per step.  With KB = 1 and MS = NS = 2 the ring is 64 KB, so
+// two workgroups share a CU and one's prologue and epilogue overlap the
+// other's MFMAs.
+//
+// LDS slice layout: token T of the tile owns RB = 128 KB bytes; its 16-byte
+// chunk c sits at T*RB + ((c ^ swz(T)) * 16), swz(T) = T & 15 for 256-byte
+// rows and (T >> 1) & 7 for 128-byte rows, so the 16 lanes of an operand
+// read (16 consecutive tokens, same c) hit 16 different 16-byte bank groups.
+//
+// MFMA operands (32 x 32 x 32): lane l supplies, for A, token (l & 31) and
+// for B, row (l & 31), the 16 k values 16 (l >> 5) .. 16 (l >> 5) + 15 of the
+// 32-k chunk.  Chunk kc of a step (k = 32 kc .. 32 kc + 31) lies in 128-k
+// block kc >> 2, 2-bit field kc & 3; its bytes 16 g .. 16 g + 15 (g = l >> 5)
+// hold k = 32 (kc & 3) + 16 g + j: packed uint4 number 2 (kc >> 2) + g of the
+// step, shifted right by 2 (kc & 3).
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+constexpr int kG2Stages = 4;
+
+template <int KB>
+__device__ __forceinline__ int g2_swz(int T) {
+    return KB == 2 ? (T & 15) : ((T >> 1) & 7);
+}
+
+template <int OUT, int MS, int NS, int KB>
+__global__ __launch_bounds__(kThreads) void tgemm2_kernel(GemvArgs a) {
+    constexpr int TM = 32, BM = 2 * TM * MS, BN = 2 * TM * NS;
+    constexpr int RB = 128 * KB;                 // LDS bytes per token per stage
+    constexpr int KC = 4 * KB;                   // 32-k chunks per step
+    constexpr int kSlice = BM * RB;              // bytes of one LDS stage
+    constexpr int NA = kSlice / 16 / kThreads;   // A chunks per lane per step
+    constexpr int NB = NS * KB;                  // weight uint4 loads per lane per step
+    constexpr int TPB = 1024 / RB;               // tokens per 1 KB DMA block
+    extern __shared__ __align__(16) int8_t As[];  // [kG2Stages][kSlice]
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int wm = w & 1, wn = w >> 1;
+    const int l32 = lane & 31, g = lane >> 5;
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    const int kp = a.kp, M = a.m;
+    const int nsteps = kp / RB;
+    MTR(0)
+
+    // weights: row tile s of this wave, row l32; packed uint4 2b + g of a step
+    const uint4* brow[NS];
+#pragma unroll
+    for (int s = 0; s < NS; s++) {
+        const int vr = n0 + wn * (BN / 2) + s * TM + l32;
+        int mat, r;
+        resolve_row<OUT>(a, vr < a.total_rows ? vr : 0, mat, r);
+        brow[s] = (const uint4*)(sel3(a.w, mat) + (size_t)r * (size_t)(kp >> 2)) + g;
+    }
+    // activations: this lane's NA chunks of a slice (LDS slot fixed by the
+    // lane, global chunk chosen to realise the swizzle)
+    const int8_t* asrc[NA];
+    int adst[NA];
+#pragma unroll
+    for (int j = 0; j < NA; j++) {
+        const int blk = w * NA + j;  // 1 KB block of the slice
+        const int T = blk * TPB + lane / (RB / 16), cs = lane % (RB / 16);
+        const int c = cs ^ g2_swz<KB>(T);
+        const int tok = m0 + T < M ? m0 + T : M - 1;  // past M: any valid row, never stored
+        asrc[j] = a.q + (size_t)tok * kp + c * 16;
+        adst[j] = blk * 1024;
+    }
+    auto a_issue = [&](int p, int stage) {
+        int8_t* dst = As + stage * kSlice;
+#pragma unroll
+        for (int j = 0; j < NA; j++)
+            __builtin_amdgcn_global_load_lds((const void*)(asrc[j] + p * RB), (lds_void_t*)(dst + adst[j]), 16, 0, 0);
+    };
+    // Rows past total_rows load row 0 of matrix 0 (never stored), so every
+    // load is unconditional and the outstanding-load count is the same on
+    // every step.  The weight loads are issued as inline asm: the compiler
+    // does not track them, so it adds no waits of its own (its tracking of
+    // loop-carried loads falls back to waiting for everything); the step's
+    // explicit s_waitcnt covers them, and pin() after it keeps every use of
+    // the registers below the wait.
+    u32x4 bw[kG2Stages][NB];  // [slot][s * KB + 128-k block]
+    auto b_issue = [&](int p, u32x4 (&dst)[NB]) {
+#pragma unroll
+        for (int s = 0; s < NS; s++)
+#pragma unroll
+            for (int b = 0; b < KB; b++)
+                asm volatile("global_load_dwordx4 %0, %1, off"
+                             : "=v"(dst[s * KB + b])
+                             : "v"(brow[s] + 2 * (KB * p + b))
+                             : "memory");
+    };
+    auto pin = [](u32x4& v) { asm volatile("" : "+v"(v)); };
+    auto wait_vm = [](auto n_c) {
+        constexpr int n = decltype(n_c)::value;
+        __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
+    };
+
+    v16i acc[MS][NS];
 #pragma unroll
     for (int ms = 0; ms < MS; ms++)
 #pragma unroll
         for (int s = 0; s < NS; s++)
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int tok = m0 + wm * (BM / 2) + ms * 16 + 4 * lg + r;
-                const int vr = n0 + wn * (BN / 2) + s * 16 + li;
-                const bool ok = tok < M && vr < a.total_rows;
-                const int d = acc[ms][s][r] - (tok < M ? a.qsum[tok] : 0);
-                const float sa = (tok < M && a.qscale) ? a.qscale[tok] : 1.0f;
-                if (OUT == kOutRelu2 || OUT == kOutQKV) {
-                    const int dp = __shfl_xor(d, 1);
-                    if (ok && (li & 1) == 0) store_pair<OUT>(a, tok, vr, d, dp, sa);
-                } else if (ok) {
-                    store_single<OUT>(a, tok, vr, d, sa);
-                }
+            for (int r = 0; r < 16; r++) acc[ms][s][r] = 0;
+
+    // A operand of (kc, ms): token wm*64 + ms*32 + l32 (its swizzle depends
+    // on l32 only), chunk 2 kc + g of the slice
+    const int arow = (wm * (BM / 2) + l32) * RB;
+    int axo[KC];
+#pragma unroll
+    for (int kc = 0; kc < KC; kc++) axo[kc] = ((2 * kc + g) ^ g2_swz<KB>(l32)) << 4;
+    v4i aop[2][KC][MS];  // A operands of the current and the next step
+    auto a_read = [&](int stage, v4i (&dst)[KC][MS]) {
+        const int8_t* Ab = As + stage * kSlice + arow;
+#pragma unroll
+        for (int kc = 0; kc < KC; kc++)
+#pragma unroll
+            for (int ms = 0; ms < MS; ms++) dst[kc][ms] = *(const v4i*)(Ab + axo[kc] + ms * TM * RB);
+    };
+
+    // Prologue: slices and weights of steps 0..3 in flight (steps past the
+    // end re-load the last one: cache hits into a stage nobody reads, so the
+    // count of loads in flight is the same on every step), then the A
+    // operands of step 0.
+    const int plast = nsteps - 1;
+#pragma unroll
+    for (int p = 0; p < kG2Stages; p++) {
+        const int pi = p < plast ? p : plast;
+        a_issue(pi, p);
+        b_issue(pi, bw[p]);
+    }
+    MTR(1)
+    wait_vm(std::integral_constant<int, NB + 3 * (NA + NB)>{});
+    __builtin_amdgcn_s_barrier();
+    MTR(2)
+    a_read(0, aop[0]);
+
+    // Step p (ring slot p % 4 and operand buffer p % 2 as constants: no
+    // register rotation, which would wait for every load in flight):
+    //   wait for slice p+1 (own chunks) and weights p, barrier (all chunks of
+    //   slice p+1; every wave has read slice p into registers);
+    //   slice p+4 -> stage p % 4; LDS reads of slice p+1 into the other
+    //   operand buffer while the MFMAs of step p run; weights p+4 into the
+    //   registers of weights p once they are unpacked.
+    auto step = [&](int p, auto slot_c) {
+        constexpr int slot = decltype(slot_c)::value;
+        constexpr int cur = slot & 1;
+        wait_vm(std::integral_constant<int, NB + 2 * (NA + NB)>{});
+#pragma unroll
+        for (int i = 0; i < NB; i++) pin(bw[slot][i]);
+        __builtin_amdgcn_s_barrier();
+        const int pn = p + kG2Stages < plast ? p + kG2Stages : plast;
+        a_issue(pn, slot);
+        a_read((slot + 1) % kG2Stages, aop[cur ^ 1]);
+#pragma unroll
+        for (int kc = 0; kc < KC; kc++) {
+            const int sh = 2 * (kc & 3), b = kc >> 2;
+            v4i bop[NS];
+#pragma unroll
+            for (int s = 0; s < NS; s++) {
+                const u32x4 v = bw[slot][s * KB + b];
+                bop[s] = v4i{(int)((v.x >> sh) & 0x03030303u), (int)((v.y >> sh) & 0x03030303u),
+                             (int)((v.z >> sh) & 0x03030303u), (int)((v.w >> sh) & 0x03030303u)};
             }
+#pragma unroll
+            for (int ms = 0; ms < MS; ms++)
+#pragma unroll
+                for (int s = 0; s < NS; s++)
+                    acc[ms][s] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop[cur][kc][ms], bop[s], acc[ms][s], 0, 0, 0);
+        }
+        b_issue(pn, bw[slot]);
+    };
+    for (int p = 0; p < nsteps; p += kG2Stages) {
+        step(p, std::integral_constant<int, 0>{});
+        if (p + 1 < nsteps) step(p + 1, std::integral_constant<int, 1>{});
+        if (p + 2 < nsteps) step(p + 2, std::integral_constant<int, 2>{});
+        if (p + 3 < nsteps) step(p + 3, std::integral_constant<int, 3>{});
+    }
+    // No load in flight past this point.  The weight registers of the last
+    // steps are never read, so each is used here, after the wait: until then
+    // the compiler cannot give a register to anything else while a load
+    // untracked by it is still to write it.
+    __builtin_amdgcn_s_waitcnt(0);
+#pragma unroll
+    for (int k = 0; k < kG2Stages; k++)
+#pragma unroll
+        for (int i = 0; i < NB; i++) asm volatile("" ::"v"(bw[k][i]));
+    MTR(3)
+
+    mfma_epilogue<OUT, TM>(a, acc, m0 + wm * (BM / 2), n0 + wn * (BN / 2));
+#ifdef LBT_GEMM_TRACE
+    __builtin_amdgcn_s_waitcnt(0);
+#endif
+    MTR(4)
 }
 
 namespace {
@@ -147,6 +496,29 @@ hipError_t launch_tiles(const GemvArgs& a, int out_mode, dim3 grid, hipStream_t 
         case kOutF32Add: hipExtLaunchKernelGGL((tgemm_kernel<MS, NS, kOutF32Add>), grid, dim3(kThreads), 0, s, e0, e1, 0, a); break;
         case kOutRelu2: hipExtLaunchKernelGGL((tgemm_kernel<MS, NS, kOutRelu2>), grid, dim3(kThreads), 0, s, e0, e1, 0, a); break;
         default: hipExtLaunchKernelGGL((tgemm_kernel<MS, NS, kOutQKV>), grid, dim3(kThreads), 0, s, e0, e1, 0, a); break;
+    }
+    return hipGetLastError();
+}
+
+template <int MS, int NS, int KB>
+hipError_t launch_tiles2(const GemvArgs& a, int out_mode, dim3 grid, hipStream_t s, hipEvent_t e0, hipEvent_t e1) {
+    constexpr size_t lds = (size_t)kG2Stages * (64 * MS) * (128 * KB);
+    static bool attr = false;
+    if (!attr) {
+        const void* fns[] = {(const void*)tgemm2_kernel<kOutI32, MS, NS, KB>, (const void*)tgemm2_kernel<kOutF32, MS, NS, KB>,
+                             (const void*)tgemm2_kernel<kOutF32Add, MS, NS, KB>,
+                             (const void*)tgemm2_kernel<kOutRelu2, MS, NS, KB>,
+                             (const void*)tgemm2_kernel<kOutQKV, MS, NS, KB>};
+        for (const void* f : fns) (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        (void)hipGetLastError();
+        attr = true;
+    }
+    switch (out_mode) {
+        case kOutI32: hipExtLaunchKernelGGL((tgemm2_kernel<kOutI32, MS, NS, KB>), grid, dim3(kThreads), lds, s, e0, e1, 0, a); break;
+        case kOutF32: hipExtLaunchKernelGGL((tgemm2_kernel<kOutF32, MS, NS, KB>), grid, dim3(kThreads), lds, s, e0, e1, 0, a); break;
+        case kOutF32Add: hipExtLaunchKernelGGL((tgemm2_kernel<kOutF32Add, MS, NS, KB>), grid, dim3(kThreads), lds, s, e0, e1, 0, a); break;
+        case kOutRelu2: hipExtLaunchKernelGGL((tgemm2_kernel<kOutRelu2, MS, NS, KB>), grid, dim3(kThreads), lds, s, e0, e1, 0, a); break;
+        default: hipExtLaunchKernelGGL((tgemm2_kernel<kOutQKV, MS, NS, KB>), grid, dim3(kThreads), lds, s, e0, e1, 0, a); break;
     }
     return hipGetLastError();
 }
@@ -195,12 +567,23 @@ int launch_ternary_mfma(lbt_ctx* ctx, const TernaryOp& op_in) {
     hipEvent_t e0, e1;
     prof_pair(ctx, &e0, &e1);
     hipError_t e;
-    if (big) {
-        dim3 grid((unsigned)((total + 127) / 128), (unsigned)((op.m + 127) / 128));
-        e = launch_tiles<4, 4>(a, op.out_mode, grid, ctx->stream, e0, e1);
+    static const int gmode = getenv("LBT_GEMM_MODE") ? atoi(getenv("LBT_GEMM_MODE")) : 0;
+    const long t128 = (long)((total + 127) / 128) * ((op.m + 127) / 128);
+    const dim3 g128((unsigned)((total + 127) / 128), (unsigned)((op.m + 127) / 128));
+    const dim3 g64((unsigned)((total + 63) / 64), (unsigned)((op.m + 63) / 64));
+    if (gmode == 1) {
+        e = big ? launch_tiles<4, 4>(a, op.out_mode, g128, ctx->stream, e0, e1)
+                : launch_tiles<2, 2>(a, op.out_mode, g64, ctx->stream, e0, e1);
+    } else if (gmode == 2 && a.kp % 256 == 0) {
+        e = launch_tiles2<2, 2, 2>(a, op.out_mode, g128, ctx->stream, e0, e1);
+    } else if (gmode == 3 && a.kp % 256 == 0) {
+        e = launch_tiles2<1, 1, 2>(a, op.out_mode, g64, ctx->stream, e0, e1);
+    } else if (gmode == 4) {
+        e = launch_tiles2<1, 1, 1>(a, op.out_mode, g64, ctx->stream, e0, e1);
+    } else if (t128 >= 200 || gmode == 5) {
+        e = launch_tiles2<2, 2, 1>(a, op.out_mode, g128, ctx->stream, e0, e1);
     } else {
-        dim3 grid((unsigned)((total + 63) / 64), (unsigned)((op.m + 63) / 64));
-        e = launch_tiles<2, 2>(a, op.out_mode, grid, ctx->stream, e0, e1);
+        e = launch_tiles2<1, 1, 1>(a, op.out_mode, g64, ctx->stream, e0, e1);
     }
     if (e != hipSuccess) return hip_err(ctx, e, "tgemm_kernel launch");
     prof_commit(ctx, e0, e1, kProfGemm, 2.0 * op.m * (double)total * a.kp);

@@ -33,7 +33,8 @@ def test_config3_ffn_shapes_bitexact(ctx, rows, cols, m):
     w.free()
 
 
-@pytest.mark.parametrize("rows,cols,m", [(23, 384, 17), (37, 2560, 33), (130, 300, 65), (5, 129, 16), (100, 1000, 200)])
+@pytest.mark.parametrize("rows,cols,m", [(23, 384, 17), (37, 2560, 33), (130, 300, 65), (5, 129, 16), (100, 1000, 200),
+                                         (130, 2560, 129), (300, 512, 257), (1, 256, 128), (257, 768, 1000)])
 def test_ragged_tiles(ctx, rows, cols, m):
     announce(f"prefill ragged {rows}x{cols} m={m}")
     t, scale, x = golden_case(rows, cols, m, rows + cols + m)
@@ -60,12 +61,13 @@ def test_prefill_extreme_long_rows_mfma(ctx):
     w.free()
 
 
-def test_fused_multi_mfma_equals_separate(ctx):
+@pytest.mark.parametrize("m", [96, 200])
+def test_fused_multi_mfma_equals_separate(ctx, m):
     cols = 2560
     rng = np.random.default_rng(77)
     ws = [ctx.upload(orc.pack(ternary_iid(rng, r, cols)), r, cols, s) for r, s in [(2560, 0.9), (640, 1.1), (640, 1.3)]]
-    x = rng.standard_normal((96, cols)).astype(np.float32)
-    announce("prefill fused multi")
+    x = rng.standard_normal((m, cols)).astype(np.float32)
+    announce(f"prefill fused multi m={m}")
     fused = ctx.ternary_linear(ws, x)
     for i, w in enumerate(ws):
         (single,) = ctx.ternary_linear([w], x)
