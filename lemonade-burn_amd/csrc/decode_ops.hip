@@ -161,7 +161,76 @@ __global__ __launch_bounds__(kThreads) void lmhead_kernel(const uint16_t* W, int
     const int nchunks = cols >> 3;
     const int gw = blockIdx.x * 4 + (tid >> 6), nw = gridDim.x * 4;
     unsigned long long best = 0ull;
-    if (nchunks <= 64 * kLmChunks) {
+    if (nchunks == 64 * kLmChunks) {
+        // Row pairs (r, r + nw), r = gw + 2 nw p, with the next pair's loads in
+        // flight while a pair computes (untracked loads, explicit waits; pairs
+        // past the end load row 0 and are not used).  Same per-row order as
+        // the loop below.
+        constexpr int NL = 2 * kLmChunks;
+        const int np = gw < rows ? (rows - gw + 2 * nw - 1) / (2 * nw) : 0;
+        u32x4 A[2][kLmChunks], B[2][kLmChunks];
+        auto issue = [&](int p, u32x4 (&a)[kLmChunks], u32x4 (&b)[kLmChunks]) {
+            const int r0 = gw + 2 * nw * p, r1 = r0 + nw;
+            const uint4* w0 = (const uint4*)(W + (size_t)(r0 < rows ? r0 : 0) * cols);
+            const uint4* w1 = (const uint4*)(W + (size_t)(r1 < rows ? r1 : 0) * cols);
+#pragma unroll
+            for (int i = 0; i < kLmChunks; i++) {
+                a[i] = ld_u4_async_nt(w0 + lane + 64 * i);
+                b[i] = ld_u4_async_nt(w1 + lane + 64 * i);
+            }
+        };
+        auto land = [&](u32x4 (&a)[kLmChunks], u32x4 (&b)[kLmChunks]) {
+            vm_wait<NL>();  // all but the pair issued last
+#pragma unroll
+            for (int i = 0; i < kLmChunks; i++) {
+                pin(a[i]);
+                pin(b[i]);
+            }
+        };
+        auto consume = [&](int p, u32x4 (&a)[kLmChunks], u32x4 (&b)[kLmChunks]) {
+            const int r0 = gw + 2 * nw * p, r1 = r0 + nw;
+            float acc0 = 0.0f, acc1 = 0.0f;
+#pragma unroll
+            for (int i = 0; i < kLmChunks; i++) {
+                const int c = lane + 64 * i;
+                acc0 = dot8(make_uint4(a[i].x, a[i].y, a[i].z, a[i].w), xs + 8 * c, acc0);
+                acc1 = dot8(make_uint4(b[i].x, b[i].y, b[i].z, b[i].w), xs + 8 * c, acc1);
+            }
+            acc0 = wave_sum(acc0);
+            acc1 = wave_sum(acc1);
+            if (lane == 0) {
+                if (r0 < rows) {
+                    if (logits) logits[(size_t)t * rows + r0] = acc0;
+                    const unsigned long long k = argmax_key(acc0, (uint32_t)r0);
+                    best = k > best ? k : best;
+                }
+                if (r1 < rows) {
+                    if (logits) logits[(size_t)t * rows + r1] = acc1;
+                    const unsigned long long k = argmax_key(acc1, (uint32_t)r1);
+                    best = k > best ? k : best;
+                }
+            }
+        };
+        // loads, waits and pins are unconditional (no register copies of a
+        // result still in flight); only the use of the last odd pair is not
+        issue(0, A[0], B[0]);
+        for (int p = 0; p < np; p += 2) {
+            issue(p + 1, A[1], B[1]);
+            land(A[0], B[0]);
+            consume(p, A[0], B[0]);
+            issue(p + 2, A[0], B[0]);
+            land(A[1], B[1]);
+            if (p + 1 < np) consume(p + 1, A[1], B[1]);
+        }
+        vm_wait<0>();
+#pragma unroll
+        for (int i = 0; i < kLmChunks; i++) {
+            keep(A[0][i]);
+            keep(B[0][i]);
+            keep(A[1][i]);
+            keep(B[1][i]);
+        }
+    } else if (nchunks <= 64 * kLmChunks) {
         // two rows per iteration, all their chunk loads in flight at once
         for (int r = gw; r < rows; r += 2 * nw) {
             const int r1 = r + nw;
@@ -210,7 +279,17 @@ __global__ __launch_bounds__(kThreads) void lmhead_kernel(const uint16_t* W, int
             }
         }
     }
-    if (key && lane == 0 && best) atomicMax(&key[t], best);
+    // one atomic per workgroup: device-scope atomics on one word serialize,
+    // one per wavefront (8192 of them) costed a third of the kernel
+    __shared__ unsigned long long wbest[kThreads / 64];
+    if (lane == 0) wbest[tid >> 6] = best;
+    __syncthreads();
+    if (key && tid == 0) {
+        unsigned long long b = wbest[0];
+#pragma unroll
+        for (int i = 1; i < kThreads / 64; i++) b = wbest[i] > b ? wbest[i] : b;
+        if (b) atomicMax(&key[t], b);
+    }
 }
 
 // Final RMSNorm of row blockIdx.x into xn (the LM head prologue's
@@ -311,14 +390,18 @@ __global__ __launch_bounds__(kThreads) void lmhead_batch_kernel(const uint16_t* 
             }
         }
     }
-    if (key && lane == 0)
-        for (int t = 0; t < nt; t++) {
-            unsigned long long b = 0ull;
+    // one atomic per (workgroup, token): the wavefronts' keys meet in LDS
+    __shared__ unsigned long long wbest[kThreads / 64][16];
+    if (lane == 0)
 #pragma unroll
-            for (int u = 0; u < 16; u++)
-                if (u == t) b = best[u];
-            if (b) atomicMax(&key[t0 + t], b);
-        }
+        for (int u = 0; u < 16; u++) wbest[w][u] = best[u];
+    __syncthreads();
+    if (key && tid < nt) {
+        unsigned long long b = 0ull;
+#pragma unroll
+        for (int i = 0; i < kThreads / 64; i++) b = wbest[i][tid] > b ? wbest[i][tid] : b;
+        if (b) atomicMax(&key[t0 + tid], b);
+    }
 }
 
 __global__ void set_state_kernel(int* state, int pos, int slot) {

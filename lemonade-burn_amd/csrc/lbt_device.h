@@ -53,6 +53,34 @@ __device__ __forceinline__ f32x2 buf_load_f2(__amdgpu_buffer_rsrc_t r, uint32_t 
     return __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(r, byte_off, 0, 0));
 }
 
+// Loads the compiler does not track (inline asm), waited for with explicit
+// counts (vm_wait<N>: at most N vector-memory operations still outstanding;
+// loads complete in issue order, stores count too).  For loops that keep the
+// next iteration's loads in flight: the compiler's own tracking of
+// loop-carried loads falls back to waiting for everything.  Rules: every use
+// of a result comes after a vm_wait that covers it, followed by pin() on the
+// value (so no use is scheduled above the wait), and every result stays live
+// until such a wait (a dead result's register could be handed to another
+// value while the load is still to write it).
+__device__ __forceinline__ u32x4 ld_u4_async_nt(const void* p) {
+    u32x4 v;
+    asm volatile("global_load_dwordx4 %0, %1, off nt" : "=v"(v) : "v"(p) : "memory");
+    return v;
+}
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+template <typename T>
+__device__ __forceinline__ void pin(T& v) {
+    asm volatile("" : "+v"(v));
+}
+template <typename T>
+__device__ __forceinline__ void keep(const T& v) {
+    asm volatile("" ::"v"(v));
+}
+
 // 16-byte streaming load (nontemporal: the weights are read once per token).
 __device__ __forceinline__ uint4 ld_stream(const uint4* p) {
     const u32x4 v = __builtin_nontemporal_load((const LBT_GLOBAL u32x4*)p);
