@@ -193,9 +193,16 @@ def main() -> int:
     ap.add_argument("--prof-steps", type=int, default=32)
     ap.add_argument("--pmc-pass", action="store_true", help="the workload profiled for the HBM counters")
     ap.add_argument("--no-batched", action="store_true", help="skip the batched-decode (config 5) figures")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only the config-3 prefill GEMM sweep (the workload profiled for the MFMA counters)")
     args = ap.parse_args()
     if args.pmc_pass:
         return pmc_pass()
+    if args.prefill_only:
+        import lbt_hip
+
+        print(json.dumps({"prefill_gemm": prefill_gemm(lbt_hip.Ctx(0))}), flush=True)
+        return 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU; a multi-GPU figure is not part of it "
               "(rows of the ternary GEMVs would shard across GPUs with no exchange).", file=sys.stderr)
