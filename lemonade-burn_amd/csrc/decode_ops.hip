@@ -390,16 +390,19 @@ __global__ __launch_bounds__(kThreads) void lmhead_batch_kernel(const uint16_t* 
             }
         }
     }
-    // one atomic per (workgroup, token): the wavefronts' keys meet in LDS
-    __shared__ unsigned long long wbest[kThreads / 64][16];
+    // one atomic per (workgroup, token): the wavefronts' keys meet in the
+    // token rows' LDS once every wavefront is done with them (no static LDS:
+    // two workgroups of 80 KB share a CU only with nothing beside it)
+    __syncthreads();
+    unsigned long long* wbest = (unsigned long long*)xs;  // [4][16]
     if (lane == 0)
 #pragma unroll
-        for (int u = 0; u < 16; u++) wbest[w][u] = best[u];
+        for (int u = 0; u < 16; u++) wbest[w * 16 + u] = best[u];
     __syncthreads();
     if (key && tid < nt) {
         unsigned long long b = 0ull;
 #pragma unroll
-        for (int i = 0; i < kThreads / 64; i++) b = wbest[i][tid] > b ? wbest[i][tid] : b;
+        for (int i = 0; i < kThreads / 64; i++) b = wbest[i * 16 + tid] > b ? wbest[i * 16 + tid] : b;
         if (b) atomicMax(&key[t0 + tid], b);
     }
 }
