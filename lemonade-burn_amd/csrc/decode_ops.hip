@@ -312,31 +312,65 @@ __global__ __launch_bounds__(kThreads) void row_norm_kernel(const float* x, int 
     }
 }
 
+// Recursive halving of K per-lane partial sums over the wavefront: step M
+// pairs accumulator j with j + K/2, the lanes with bit M set keep the upper
+// one and receive the partner lanes' values of it, the others the lower one;
+// each kept sum is v[l] + v[l ^ M], the same pairwise sums (bit for bit, the
+// adds being commutative) as a full butterfly of that accumulator.  After
+// steps 32, 16, ..., 2, lane l holds accumulator (l >> 1) & 31 (K = 32).
+template <int M, int K>
+__device__ __forceinline__ void halve(const float (&v)[K], float (&o)[K / 2]) {
+    const int lane = (int)threadIdx.x & 63;
+#pragma unroll
+    for (int j = 0; j < K / 2; j++) {
+        const uint32_t lo = __float_as_uint(v[j]), hi = __float_as_uint(v[j + K / 2]);
+        if constexpr (M == 32) {
+            // lanes 0-31 get (lo[l], lo[l+32]), lanes 32-63 (hi[l-32], hi[l])
+            const auto r = __builtin_amdgcn_permlane32_swap(lo, hi, false, false);
+            o[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+        } else if constexpr (M == 16) {
+            // rows 0, 2 get (lo, lo of the next row), rows 1, 3 (hi of the previous row, hi)
+            const auto r = __builtin_amdgcn_permlane16_swap(lo, hi, false, false);
+            o[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+        } else {
+            const bool up = (lane & M) != 0;
+            const uint32_t keep = up ? hi : lo, send = up ? lo : hi;
+            uint32_t a, b;
+            xor_pair<M>(send, a, b);  // b: the partner's `send` (a is own)
+            o[j] = __uint_as_float(keep) + __uint_as_float(b);
+        }
+    }
+}
+
 // LM head for several token rows at once (normalized rows xn [m][cols]):
 // each (weight row, token) dot product has lmhead_kernel's order (lane l
 // takes chunks l, l+64, ... with fused multiply-adds in element order, then
-// the butterfly), so the logits and argmax keys are the same bits; what
-// changes is reuse: a workgroup keeps TG token rows in LDS and each wavefront
-// holds R weight rows unpacked in registers for all of them.  Workgroup i
-// takes token group i % ngroups of row tile i / ngroups, so the groups of one
-// tile run together and share its weight rows through the caches.
-template <int R, int NCH>
+// the xor tree over the 64 lanes), so the logits and argmax keys are the same
+// bits; what changes is reuse: a workgroup keeps TG = 8 token rows in LDS and
+// each wavefront holds R = 4 weight rows unpacked in registers for all of
+// them (one LDS read of x per 4 rows), and the 32 (token, row) sums of a
+// wavefront reduce together by recursive halving.  Workgroup i takes token
+// group i % ngroups of row tile i / ngroups, so the groups of one tile run
+// together and share its weight rows through the caches.
+template <int R, int NCH, int TG>
 __global__ __launch_bounds__(kThreads) void lmhead_batch_kernel(const uint16_t* W, int rows, int cols, const float* xn,
-                                                                int m, int tg, int tile_rows, float* logits,
+                                                                int m, int tile_rows, float* logits,
                                                                 unsigned long long* key) {
-    extern __shared__ __align__(16) float xs[];  // [tg][cols]
-    const int ngroups = (m + tg - 1) / tg;
+    static_assert(R * TG == 32, "32 accumulators per lane");
+    extern __shared__ __align__(16) float xs[];  // [TG][cols]
+    const int ngroups = (m + TG - 1) / TG;
     const int grp = blockIdx.x % ngroups, tile = blockIdx.x / ngroups;
-    const int t0 = grp * tg, nt = m - t0 < tg ? m - t0 : tg;
+    const int t0 = grp * TG, nt = m - t0 < TG ? m - t0 : TG;
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     for (int i = tid * 4; i < nt * cols; i += kThreads * 4)
         *(float4*)(xs + i) = *(const float4*)(xn + (size_t)t0 * cols + i);
+    for (int i = nt * cols + tid; i < TG * cols; i += kThreads) xs[i] = 0.0f;  // unused token rows
     __syncthreads();
     const int nchunks = cols >> 3;
     const int r_begin = tile * tile_rows, r_end = r_begin + tile_rows < rows ? r_begin + tile_rows : rows;
-    unsigned long long best[16];
-#pragma unroll
-    for (int t = 0; t < 16; t++) best[t] = 0ull;
+    // this lane's (token, row) after the reduction: accumulator (lane >> 1) & 31
+    const int my_t = ((lane >> 1) & 31) / R, my_r = ((lane >> 1) & 31) % R;
+    unsigned long long best = 0ull;  // of token my_t, lanes with (lane & 1) == 0
     for (int rb = r_begin + w * R; rb < r_end; rb += 4 * R) {
         // R weight rows of this wavefront, unpacked to f32
         float wf[R][NCH][8];
@@ -358,11 +392,12 @@ __global__ __launch_bounds__(kThreads) void lmhead_batch_kernel(const uint16_t* 
                 wf[r][i][7] = bf_hi(v.w);
             }
         }
-        for (int t = 0; t < nt; t++) {
-            const float* xt = xs + t * cols;
-            float acc[R];
+        float acc[TG * R];
 #pragma unroll
-            for (int r = 0; r < R; r++) acc[r] = 0.0f;
+        for (int t = 0; t < TG; t++) {
+            const float* xt = xs + t * cols;
+#pragma unroll
+            for (int r = 0; r < R; r++) acc[t * R + r] = 0.0f;
 #pragma unroll
             for (int i = 0; i < NCH; i++) {
                 const int c = lane + 64 * i;
@@ -373,36 +408,36 @@ __global__ __launch_bounds__(kThreads) void lmhead_batch_kernel(const uint16_t* 
 #pragma unroll
                     for (int r = 0; r < R; r++)
 #pragma unroll
-                        for (int e = 0; e < 8; e++) acc[r] = __builtin_fmaf(wf[r][i][e], xv[e], acc[r]);
-                }
-            }
-#pragma unroll
-            for (int r = 0; r < R; r++) {
-                const float a = wave_sum(acc[r]);
-                const int row = rb + r;
-                if (lane == 0 && row < r_end) {
-                    if (logits) logits[(size_t)(t0 + t) * rows + row] = a;
-                    const unsigned long long k = argmax_key(a, (uint32_t)row);
-#pragma unroll
-                    for (int u = 0; u < 16; u++)
-                        if (u == t) best[u] = k > best[u] ? k : best[u];
+                        for (int e = 0; e < 8; e++)
+                            acc[t * R + r] = __builtin_fmaf(wf[r][i][e], xv[e], acc[t * R + r]);
                 }
             }
         }
+        float h16[16], h8[8], h4[4], h2[2], h1[1];
+        halve<32>(acc, h16);
+        halve<16>(h16, h8);
+        halve<8>(h8, h4);
+        halve<4>(h4, h2);
+        halve<2>(h2, h1);
+        const float a = xor_add<1>(h1[0]);
+        const int row = rb + my_r;
+        if ((lane & 1) == 0 && my_t < nt && row < r_end) {
+            if (logits) logits[(size_t)(t0 + my_t) * rows + row] = a;
+            const unsigned long long k = argmax_key(a, (uint32_t)row);
+            best = k > best ? k : best;
+        }
     }
-    // one atomic per (workgroup, token): the wavefronts' keys meet in the
-    // token rows' LDS once every wavefront is done with them (no static LDS:
-    // two workgroups of 80 KB share a CU only with nothing beside it)
+    // one atomic per (workgroup, token): the lanes' keys meet in the token
+    // rows' LDS once every wavefront is done with them (no static LDS: two
+    // workgroups of 80 KB share a CU only with nothing beside it)
     __syncthreads();
-    unsigned long long* wbest = (unsigned long long*)xs;  // [4][16]
-    if (lane == 0)
-#pragma unroll
-        for (int u = 0; u < 16; u++) wbest[w * 16 + u] = best[u];
+    unsigned long long* wbest = (unsigned long long*)xs;  // [4 waves][32 lanes / 2]
+    if ((lane & 1) == 0) wbest[w * 32 + (lane >> 1)] = best;
     __syncthreads();
     if (key && tid < nt) {
         unsigned long long b = 0ull;
-#pragma unroll
-        for (int i = 0; i < kThreads / 64; i++) b = wbest[i * 16 + tid] > b ? wbest[i * 16 + tid] : b;
+        for (int i = 0; i < (kThreads / 64) * 32; i++)
+            if (i % 32 / R == tid) b = wbest[i] > b ? wbest[i] : b;
         if (b) atomicMax(&key[t0 + tid], b);
     }
 }
@@ -604,22 +639,21 @@ int launch_bf16_linear(lbt_ctx* ctx, const uint16_t* w, int rows, int cols, cons
                        const float* norm_w, float eps, float* logits, unsigned long long* key, float* xn) {
     if (cols % 8) return set_err(ctx, LBT_E_INVALID, "bf16 linear: cols must be a multiple of 8");
     if (m <= 0) return LBT_OK;
-    constexpr int kTG = 8, kR = 2;
+    constexpr int kTG = 8, kR = 4;
     if (m >= 2 && xn && cols <= 64 * kLmChunks * 8) {
         // several rows: normalize once, then the weight-reusing head
         hipLaunchKernelGGL(row_norm_kernel, dim3(m), dim3(kThreads), 0, ctx->stream, x, cols, norm_w, eps, xn);
         LBT_HIP(ctx, hipGetLastError());
-        const int tg = m < kTG ? m : kTG;
-        const int ngroups = (m + tg - 1) / tg;
+        const int ngroups = (m + kTG - 1) / kTG;
         int tiles = ctx->cus * 4 / ngroups;
         if (tiles < 1) tiles = 1;
         int tile_rows = (rows + tiles - 1) / tiles;
         tile_rows = (tile_rows + 4 * kR - 1) / (4 * kR) * (4 * kR);
         tiles = (rows + tile_rows - 1) / tile_rows;
-        const size_t lds = (size_t)tg * cols * sizeof(float);
+        const size_t lds = (size_t)kTG * cols * sizeof(float);
         static bool attr = false;
         if (!attr) {
-            (void)hipFuncSetAttribute((const void*)lmhead_batch_kernel<kR, kLmChunks>,
+            (void)hipFuncSetAttribute((const void*)lmhead_batch_kernel<kR, kLmChunks, kTG>,
                                       hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024);
             (void)hipGetLastError();
             attr = true;
@@ -627,8 +661,8 @@ int launch_bf16_linear(lbt_ctx* ctx, const uint16_t* w, int rows, int cols, cons
         if (lds > 96 * 1024) return set_err(ctx, LBT_E_INVALID, "bf16 linear: token group exceeds LDS");
         hipEvent_t e0, e1;
         prof_pair(ctx, &e0, &e1);
-        hipExtLaunchKernelGGL((lmhead_batch_kernel<kR, kLmChunks>), dim3(tiles * ngroups), dim3(kThreads), lds,
-                              ctx->stream, e0, e1, 0, w, rows, cols, xn, m, tg, tile_rows, logits, key);
+        hipExtLaunchKernelGGL((lmhead_batch_kernel<kR, kLmChunks, kTG>), dim3(tiles * ngroups), dim3(kThreads), lds,
+                              ctx->stream, e0, e1, 0, w, rows, cols, xn, m, tile_rows, logits, key);
         LBT_HIP(ctx, hipGetLastError());
         prof_commit(ctx, e0, e1, kProfHead, (double)rows * cols * 2.0);
         return LBT_OK;
