@@ -252,17 +252,27 @@ __device__ __forceinline__ void attention_split_group(const float* q, int g, int
         const int idx = tid + i * kThreads;
         qv[i] = (act && idx < GH * HD) ? q[(size_t)g * GH * HD + idx] : 0.0f;
     }
-    uint4 kb[KU], vb[KU];
+    // K and V rows go through two register buffers each: the next key pass's
+    // loads are in flight while a pass computes.  Loads are unconditional
+    // (rows past the split re-read its last row; they are masked out below),
+    // so the compiler's waits count exactly.
+    uint4 kb[2][KU], vb[2][KU];
+    auto k_load = [&](int b0, uint4 (&dst)[KU]) {
 #pragma unroll
-    for (int u = 0; u < KU; u++) {
-        const int k = u * NK + w * GW + kslot;
-        kb[u] = (act && k < cnt) ? *(const uint4*)(K + (size_t)k * HD + 8 * cc) : make_uint4(0, 0, 0, 0);
-    }
+        for (int u = 0; u < KU; u++) {
+            const int k = b0 + u * NK + w * GW + kslot;
+            dst[u] = *(const uint4*)(K + (size_t)(k < cnt ? k : cnt - 1) * HD + 8 * cc);
+        }
+    };
+    auto v_load = [&](int b0, uint4 (&dst)[KU]) {
 #pragma unroll
-    for (int u = 0; u < KU; u++) {
-        const int k = grp + u * NK;
-        vb[u] = (act && k < cnt) ? *(const uint4*)(V + (size_t)k * HD + 8 * c) : make_uint4(0, 0, 0, 0);
-    }
+        for (int u = 0; u < KU; u++) {
+            const int k = b0 + grp + u * NK;
+            dst[u] = *(const uint4*)(V + (size_t)(k < cnt ? k : cnt - 1) * HD + 8 * c);
+        }
+    };
+    k_load(0, kb[0]);
+    v_load(0, vb[0]);
 #pragma unroll
     for (int i = 0; i < QPT; i++) {
         const int idx = tid + i * kThreads;
@@ -275,44 +285,63 @@ __device__ __forceinline__ void attention_split_group(const float* q, int g, int
 #pragma unroll
         for (int e = 0; e < 8; e++) q8[h][e] = sh.qs[h][8 * cc + e];
 
-    float mx[GH];
+    // The GH scores of a key reduce over the key's LK lanes together: the
+    // first log2(GH) butterfly steps by recursive halving (lane cc ends with
+    // head cc / (LK / GH)), the rest as a butterfly; the same sums, bit for
+    // bit, as a butterfly per head.  A lane keeps the running max of its head.
+    constexpr int LPH = LK / GH;  // lanes per head after the halving
+    const int hh = cc / LPH;
+    float mxo = -__builtin_inff();
+    auto k_pass = [&](int b0, const uint4 (&kbuf)[KU]) {
 #pragma unroll
-    for (int h = 0; h < GH; h++) mx[h] = -__builtin_inff();
+        for (int u = 0; u < KU; u++) {
+            const int k = b0 + u * NK + w * GW + kslot;
+            const uint32_t wv[4] = {kbuf[u].x, kbuf[u].y, kbuf[u].z, kbuf[u].w};
+            float a[GH];
+#pragma unroll
+            for (int h = 0; h < GH; h++) {
+                a[h] = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    a[h] = __builtin_fmaf(q8[h][2 * e], bf16_to_f32((uint16_t)(wv[e] & 0xffffu)), a[h]);
+                    a[h] = __builtin_fmaf(q8[h][2 * e + 1], bf16_to_f32((uint16_t)(wv[e] >> 16)), a[h]);
+                }
+            }
+            float r;
+            if constexpr (GH == 1) {
+                r = xor_sum_down<LK / 2>(a[0]);
+            } else if constexpr (GH == 2) {
+                float h1[1];
+                halve<LK / 2>(a, h1);
+                r = xor_sum_down<LK / 4>(h1[0]);
+            } else {
+                static_assert(GH == 4, "1, 2 or 4 heads per group");
+                float h2[2], h1[1];
+                halve<LK / 2>(a, h2);
+                halve<LK / 4>(h2, h1);
+                r = xor_sum_down<LK / 8>(h1[0]);
+            }
+            if (k < cnt) {
+                const float sv = r * scaling;
+                if (cc % LPH == 0) sc[hh * ks + k] = sv;
+                mxo = fmaxf(mxo, sv);
+            }
+        }
+    };
+    constexpr int STEP = KU * NK;
     if (act) {
-        for (int b0 = 0;; b0 += KU * NK) {
-            if (b0 > 0) {
-#pragma unroll
-                for (int u = 0; u < KU; u++) {
-                    const int k = b0 + u * NK + w * GW + kslot;
-                    kb[u] = k < cnt ? *(const uint4*)(K + (size_t)k * HD + 8 * cc) : make_uint4(0, 0, 0, 0);
-                }
-            }
-#pragma unroll
-            for (int u = 0; u < KU; u++) {
-                const int k = b0 + u * NK + w * GW + kslot;
-                const uint32_t wv[4] = {kb[u].x, kb[u].y, kb[u].z, kb[u].w};
-#pragma unroll
-                for (int h = 0; h < GH; h++) {
-                    float a = 0.0f;
-#pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        a = __builtin_fmaf(q8[h][2 * e], bf16_to_f32((uint16_t)(wv[e] & 0xffffu)), a);
-                        a = __builtin_fmaf(q8[h][2 * e + 1], bf16_to_f32((uint16_t)(wv[e] >> 16)), a);
-                    }
-                    a = xor_sum_down<LK / 2>(a);
-                    if (k < cnt) {
-                        const float sv = a * scaling;
-                        if (cc == 0) sc[h * ks + k] = sv;
-                        mx[h] = fmaxf(mx[h], sv);
-                    }
-                }
-            }
-            if (b0 + KU * NK >= cnt) break;
+        for (int b0 = 0;; b0 += 2 * STEP) {
+            k_load(b0 + STEP, kb[1]);
+            k_pass(b0, kb[0]);
+            if (b0 + STEP >= cnt) break;
+            k_load(b0 + 2 * STEP, kb[0]);
+            k_pass(b0 + STEP, kb[1]);
+            if (b0 + 2 * STEP >= cnt) break;
         }
     }
 #pragma unroll
     for (int h = 0; h < GH; h++) {
-        const float v = wave_max(mx[h]);
+        const float v = wave_max(hh == h ? mxo : -__builtin_inff());
         if (lane == 0 && w < 4) sh.rmax[h][w] = v;
     }
     __syncthreads();
@@ -336,33 +365,33 @@ __device__ __forceinline__ void attention_split_group(const float* q, int g, int
     for (int h = 0; h < GH; h++)
 #pragma unroll
         for (int e = 0; e < 8; e++) acc[h][e] = 0.0f;
-    if (act) {
-        for (int b0 = 0;; b0 += KU * NK) {
-            if (b0 > 0) {
+    auto v_pass = [&](int b0, const uint4 (&vbuf)[KU]) {
 #pragma unroll
-                for (int u = 0; u < KU; u++) {
-                    const int k = b0 + grp + u * NK;
-                    vb[u] = k < cnt ? *(const uint4*)(V + (size_t)k * HD + 8 * c) : make_uint4(0, 0, 0, 0);
-                }
-            }
+        for (int u = 0; u < KU; u++) {
+            const int k = b0 + grp + u * NK;
+            if (k < cnt) {
+                const uint32_t wv[4] = {vbuf[u].x, vbuf[u].y, vbuf[u].z, vbuf[u].w};
 #pragma unroll
-            for (int u = 0; u < KU; u++) {
-                const int k = b0 + grp + u * NK;
-                if (k < cnt) {
-                    const uint32_t wv[4] = {vb[u].x, vb[u].y, vb[u].z, vb[u].w};
+                for (int h = 0; h < GH; h++) {
+                    const float pj = sc[h * ks + k];
 #pragma unroll
-                    for (int h = 0; h < GH; h++) {
-                        const float pj = sc[h * ks + k];
-#pragma unroll
-                        for (int e = 0; e < 4; e++) {
-                            acc[h][2 * e] = __builtin_fmaf(pj, bf16_to_f32((uint16_t)(wv[e] & 0xffffu)), acc[h][2 * e]);
-                            acc[h][2 * e + 1] =
-                                __builtin_fmaf(pj, bf16_to_f32((uint16_t)(wv[e] >> 16)), acc[h][2 * e + 1]);
-                        }
+                    for (int e = 0; e < 4; e++) {
+                        acc[h][2 * e] = __builtin_fmaf(pj, bf16_to_f32((uint16_t)(wv[e] & 0xffffu)), acc[h][2 * e]);
+                        acc[h][2 * e + 1] =
+                            __builtin_fmaf(pj, bf16_to_f32((uint16_t)(wv[e] >> 16)), acc[h][2 * e + 1]);
                     }
                 }
             }
-            if (b0 + KU * NK >= cnt) break;
+        }
+    };
+    if (act) {
+        for (int b0 = 0;; b0 += 2 * STEP) {
+            v_load(b0 + STEP, vb[1]);
+            v_pass(b0, vb[0]);
+            if (b0 + STEP >= cnt) break;
+            v_load(b0 + 2 * STEP, vb[0]);
+            v_pass(b0 + STEP, vb[1]);
+            if (b0 + 2 * STEP >= cnt) break;
         }
     }
     if constexpr (GW > 1) {

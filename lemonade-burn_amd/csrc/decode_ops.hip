@@ -312,36 +312,6 @@ __global__ __launch_bounds__(kThreads) void row_norm_kernel(const float* x, int 
     }
 }
 
-// Recursive halving of K per-lane partial sums over the wavefront: step M
-// pairs accumulator j with j + K/2, the lanes with bit M set keep the upper
-// one and receive the partner lanes' values of it, the others the lower one;
-// each kept sum is v[l] + v[l ^ M], the same pairwise sums (bit for bit, the
-// adds being commutative) as a full butterfly of that accumulator.  After
-// steps 32, 16, ..., 2, lane l holds accumulator (l >> 1) & 31 (K = 32).
-template <int M, int K>
-__device__ __forceinline__ void halve(const float (&v)[K], float (&o)[K / 2]) {
-    const int lane = (int)threadIdx.x & 63;
-#pragma unroll
-    for (int j = 0; j < K / 2; j++) {
-        const uint32_t lo = __float_as_uint(v[j]), hi = __float_as_uint(v[j + K / 2]);
-        if constexpr (M == 32) {
-            // lanes 0-31 get (lo[l], lo[l+32]), lanes 32-63 (hi[l-32], hi[l])
-            const auto r = __builtin_amdgcn_permlane32_swap(lo, hi, false, false);
-            o[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-        } else if constexpr (M == 16) {
-            // rows 0, 2 get (lo, lo of the next row), rows 1, 3 (hi of the previous row, hi)
-            const auto r = __builtin_amdgcn_permlane16_swap(lo, hi, false, false);
-            o[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-        } else {
-            const bool up = (lane & M) != 0;
-            const uint32_t keep = up ? hi : lo, send = up ? lo : hi;
-            uint32_t a, b;
-            xor_pair<M>(send, a, b);  // b: the partner's `send` (a is own)
-            o[j] = __uint_as_float(keep) + __uint_as_float(b);
-        }
-    }
-}
-
 // LM head for several token rows at once (normalized rows xn [m][cols]):
 // each (weight row, token) dot product has lmhead_kernel's order (lane l
 // takes chunks l, l+64, ... with fused multiply-adds in element order, then
