@@ -567,7 +567,11 @@ int launch_ternary_mfma(lbt_ctx* ctx, const TernaryOp& op_in) {
     hipEvent_t e0, e1;
     prof_pair(ctx, &e0, &e1);
     hipError_t e;
-    static const int gmode = getenv("LBT_GEMM_MODE") ? atoi(getenv("LBT_GEMM_MODE")) : 0;
+    // LBT_GEMM_MODE (tests and measurements): 1 = 16x16x64 kernel, 2 / 3 =
+    // 32x32x32 with 256-k steps (128 / 64 tiles), 4 / 5 = 128-k steps with 64 /
+    // 128 tiles; default: 128 tiles when there are >= 200 of them, else 64
+    const char* gm = getenv("LBT_GEMM_MODE");
+    const int gmode = gm ? atoi(gm) : 0;
     const long t128 = (long)((total + 127) / 128) * ((op.m + 127) / 128);
     const dim3 g128((unsigned)((total + 127) / 128), (unsigned)((op.m + 127) / 128));
     const dim3 g64((unsigned)((total + 63) / 64), (unsigned)((op.m + 63) / 64));

@@ -95,3 +95,22 @@ def test_model_prefill_mfma_matches_oracle_and_gemv(ctx, monkeypatch, n):
     c.free()
     m.free()
     om.free()
+
+
+@pytest.mark.parametrize("mode", ["1", "4", "5"])
+def test_model_prefill_every_gemm_tiling_matches_oracle(ctx, monkeypatch, mode):
+    # every epilogue (q/k/v + RoPE + KV append, residual add, relu^2*up) through
+    # each MFMA tiling: 16x16x64 kernel, 64x64 and 128x128 tiles of the 32x32x32 one
+    cfg = dict(hidden=512, intermediate=1536, heads=4, kv_heads=1, layers=2, vocab=1000, max_pos=1024)
+    n = 200
+    monkeypatch.setenv("LBT_GEMM_MODE", mode)
+    announce(f"model prefill gemm mode {mode} n={n}")
+    m = lbt_hip.Model.synthetic(ctx, lbt_hip.make_config(**cfg), 5)
+    om = orc.OracleModel(orc.config(**cfg), 5)
+    toks = (np.arange(n) * 17 % cfg["vocab"]).astype(np.uint32)
+    c = m.new_cache()
+    got = m.forward(toks, c, all_logits=True)
+    assert np.array_equal(got, om.forward(toks, all_logits=True))
+    c.free()
+    m.free()
+    om.free()
