@@ -382,9 +382,11 @@ __global__ __launch_bounds__(kThreads) void tgemm2_kernel(GemvArgs a) {
                              : "memory");
     };
     auto pin = [](u32x4& v) { asm volatile("" : "+v"(v)); };
+    // vector-memory count n, and the LDS counter 0 (this wave's operand reads
+    // of a stage are done before any wave passes the barrier and refills it)
     auto wait_vm = [](auto n_c) {
         constexpr int n = decltype(n_c)::value;
-        __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
+        __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (0 << 8));
     };
 
     v16i acc[MS][NS];
