@@ -174,6 +174,13 @@ int launch_attention(lbt_ctx* ctx, const float* q, int m, int nh, int kvh, int h
 // Combine of the splits into out [m][nh*hd].
 int launch_attn_combine(lbt_ctx* ctx, const float* o, const float* ml, int m, int nh, int hd, const RowPos& rp,
                         float* out);
+// Combine of the splits, RMSNorm (norm_w) and ActQuant per row, into q [m][kp]
+// (0 past nh*hd), s_a and sum(q): the attention-combine input of a GEMM in
+// one kernel (the values combine + quantize would give).
+int launch_attn_quantize(lbt_ctx* ctx, const float* o, const float* ml, int m, int nh, int hd, const RowPos& rp,
+                         const float* norm_w, float eps, int kp, int8_t* q, float* scale, int32_t* sum);
+// Grow-only per-context device scratch for quantized activations.
+int qws_reserve(lbt_ctx* ctx, size_t bytes, void** out);
 int launch_fill_u64(lbt_ctx* ctx, unsigned long long* p, int n, unsigned long long v);
 // Streaming device copy (16-byte granules, byte tail).
 int launch_copy(lbt_ctx* ctx, void* dst, const void* src, size_t bytes);

@@ -481,8 +481,9 @@ int forward_rows(lbt_model* m, const KvView& kv, const RowPos& rp, const uint32_
         if ((rc = launch_attention(ctx, m->q, n, nh, kvh, hd, rp, Kl, Vl, kv.cap, m->scaling, m->ao, m->aml,
                                    grouped)))
             return rc;
-        // one token of one sequence: the o-projection prologue combines the splits itself
-        const bool fused = n == 1 && !rp.tok_pos && nh <= kAttnMaxHeads && H <= 4096;
+        // the o projection takes the splits: one token of one sequence combines
+        // them in the GEMV prologue, several rows in one combine + quantize kernel
+        const bool fused = nh <= kAttnMaxHeads && H <= 4096;
         if (!fused && (rc = launch_attn_combine(ctx, m->ao, m->aml, n, nh, hd, rp, m->att))) return rc;
         // o_proj on attn_sub_norm(attn), residual (model.rs:358-359)
         TernaryOp o;
@@ -500,6 +501,7 @@ int forward_rows(lbt_model* m, const KvView& kv, const RowPos& rp, const uint32_
         o.hd = hd;
         o.pos0 = rp.pos0;
         o.pos_dev = rp.pos_dev;
+        o.tok_pos = fused ? rp.tok_pos : nullptr;
         o.norm_w = m->norm[l * 4 + 2];
         o.eps = eps;
         o.out_mode = kOutF32Add;

@@ -411,7 +411,65 @@ int launch_quantize(lbt_ctx* ctx, const float* x, const float* norm_w, float eps
 }
 
 // Decode GEMV for a few tokens, the int8-MFMA GEMM from kMfmaMinTokens up.
-int launch_ternary(lbt_ctx* ctx, const TernaryOp& op) {
+// Combine of row blockIdx.x's splits, then RMSNorm + ActQuant of the row
+// into q (the GEMM input of the o projection for several rows): the combine
+// of attn_combine_kernel and the quantizer of quantize_kernel on the same
+// element layout, so the same q, s_a and sum(q).
+template <int EPT>
+__global__ __launch_bounds__(kThreads) void attn_quantize_kernel(const float* o, const float* ml, int nh, int hd,
+                                                                 RowPos rp, const float* norm_w, float eps, int kp,
+                                                                 int8_t* q, float* scale, int32_t* sum) {
+    __shared__ AttnTab tab;
+    __shared__ float red[kRedFloats];
+    const int t = blockIdx.x, H = nh * hd;
+    AttnRow a{o + (size_t)t * kAttnSplits * H, ml + (size_t)t * kAttnSplits * nh * 2, 0, nh, hd, H};
+    RowRegs<EPT> r;
+    AttnRegs<EPT, 4> ar;
+    const float* nw = norm_w ? launder(norm_w) : nullptr;
+    attn_row_issue(a, nw, ar, r);
+    a.ns = attn_splits(row_position(rp, t) + 1);
+    attn_row_finish(a, ar, r, tab);
+    quantize_row_regs<EPT>(r, H, kp, nw, eps, q + (size_t)t * kp, [](int i) { return i; }, &scale[t], &sum[t], red);
+}
+
+int launch_attn_quantize(lbt_ctx* ctx, const float* o, const float* ml, int m, int nh, int hd, const RowPos& rp,
+                         const float* norm_w, float eps, int kp, int8_t* q, float* scale, int32_t* sum) {
+    const int H = nh * hd;
+    if (nh <= 0 || nh > kAttnMaxHeads || hd % 4 || H > 16 * kThreads || kp < H || kp > 16 * kThreads)
+        return set_err(ctx, LBT_E_INVALID, "attention quantize: at most 64 heads and 4096 columns");
+    hipLaunchKernelGGL(attn_quantize_kernel<16>, dim3(m), dim3(kThreads), 0, ctx->stream, o, ml, nh, hd, rp, norm_w,
+                       eps, kp, q, scale, sum);
+    LBT_HIP(ctx, hipGetLastError());
+    return LBT_OK;
+}
+
+int launch_ternary(lbt_ctx* ctx, const TernaryOp& op_in) {
+    TernaryOp op = op_in;
+    if (op.in_mode == kInAttn && (op.m > 1 || op.tok_pos)) {
+        // several rows: combine + norm + quantize in one kernel, then the
+        // pre-quantized GEMV / GEMM (one token keeps the combine in the GEMV
+        // prologue)
+        const size_t kp = padded_cols((size_t)op.cols);
+        const size_t qb = ((size_t)op.m * kp + 255) & ~(size_t)255;
+        void* q;
+        int rc = qws_reserve(ctx, qb + (size_t)op.m * 8, &q);
+        if (rc) return rc;
+        float* sd = (float*)((char*)q + qb);
+        int32_t* ud = (int32_t*)(sd + op.m);
+        RowPos rp;
+        rp.pos0 = op.pos0;
+        rp.pos_dev = op.pos_dev;
+        rp.tok_pos = op.tok_pos;
+        if ((rc = launch_attn_quantize(ctx, op.att_o, op.att_ml, op.m, op.att_nh, op.hd, rp, op.norm_w, op.eps,
+                                       (int)kp, (int8_t*)q, sd, ud)))
+            return rc;
+        op.in_mode = kInPreQ;
+        op.q = (const int8_t*)q;
+        op.qscale = sd;
+        op.qsum = ud;
+        op.tok_pos = nullptr;
+        op.pos_dev = nullptr;
+    }
     if (op.m >= kMfmaMinTokens && !getenv("LBT_NO_MFMA")) return launch_ternary_mfma(ctx, op);
     return launch_ternary_gemv(ctx, op);
 }

@@ -525,6 +525,10 @@ hipError_t launch_tiles2(const GemvArgs& a, int out_mode, dim3 grid, hipStream_t
     return hipGetLastError();
 }
 
+
+}  // namespace
+
+// Grow-only per-context scratch for quantized activations.
 int qws_reserve(lbt_ctx* ctx, size_t bytes, void** out) {
     if (bytes > ctx->qws_bytes) {
         if (ctx->qws) {
@@ -539,8 +543,6 @@ int qws_reserve(lbt_ctx* ctx, size_t bytes, void** out) {
     *out = ctx->qws;
     return LBT_OK;
 }
-
-}  // namespace
 
 int launch_ternary_mfma(lbt_ctx* ctx, const TernaryOp& op_in) {
     TernaryOp op = op_in;
