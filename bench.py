@@ -70,6 +70,36 @@ def batched_decode(model, cfg, batch: int, cap: int = 4096, steps: int = 8) -> d
 MFMA_INT8_PEAK_TOPS = 5000.0
 
 
+def int8_head_decode(model, ctx, prompt, steps: int = 128) -> dict:
+    """Decode tok/s with the opt-in int8 LM head (q8head.rs), the same loop as
+    `value`; its logits are not the exact bf16 head's, so it is reported
+    beside the headline figure, never as it."""
+    model.set_head(1)
+    try:
+        cache = model.new_cache()
+        first = model.forward_argmax(prompt, cache)
+        model.decode_greedy(cache, first, 8)  # builds the step graph
+        cache.free()
+        cache = model.new_cache()
+        first = model.forward_argmax(prompt, cache)
+        _, ms_dev = model.decode_greedy(cache, first, steps)
+        cache.free()
+        cache = model.new_cache()
+        first = model.forward_argmax(prompt, cache)
+        ctx.prof_read(reset=True)
+        ctx.prof_enable(True)
+        model.decode_greedy(cache, first, 16)
+        prof = ctx.prof_read(reset=True)
+        ctx.prof_enable(False)
+        cache.free()
+    finally:
+        model.set_head(0)
+    h = prof["head"]
+    return {"tok_s": round(steps / (ms_dev / 1e3), 2), "ms_per_step": round(ms_dev / steps, 4),
+            "head_us": round(h["ms"] * 1e3 / max(h["launches"], 1), 2),
+            "head_GBs": round(h["bytes"] / (h["ms"] / 1e3) / 1e9, 1) if h["ms"] > 0 else 0.0}
+
+
 def prefill_gemm(ctx, reps: int = 10) -> list:
     """the prefill GEMM (int8 MFMA) on the FFN shapes
     2560->6912 and 6912->2560 at M = 128, 512, 2048 tokens; seeded ternary
@@ -284,6 +314,7 @@ def main() -> int:
         "wall_tok_s": round(args.steps / wall, 2),
         "tokens_head": [int(t) for t in out[:8]],
     }
+    line["int8_head_decode"] = int8_head_decode(model, ctx, prompt)
     if not args.no_batched:
         line["batched_decode"] = [batched_decode(model, cfg, bsz) for bsz in (16, 64)]
         line["prefill_gemm"] = prefill_gemm(ctx)

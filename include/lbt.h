@@ -122,6 +122,23 @@ void lbt_bf16_free(lbt_bf16* w);
 int lbt_bf16_linear(lbt_ctx* ctx, const lbt_bf16* w, const float* x, size_t m, float* out);
 int lbt_bf16_linear_dev(lbt_ctx* ctx, const lbt_bf16* w, const float* x, size_t m, float* out);
 
+/* ---- opt-in int8 LM head ------------------------------------------------------
+ * Q8Head (crates/lb-ternary/src/q8head.rs:9-15): int8 [rows, cols] row-major
+ * with one f32 scale per row; halves the head's weight bytes at the cost of
+ * exact logits.  lbt_q8head_from_bf16 is Q8Head::from_bf16 (:18-32), run on the
+ * device from an uploaded bf16 matrix: scale = amax / 127 (1.0 for an all-zero
+ * row), q = round_ties_even(w / scale) clamped to [-127, 127]; bit-exact. */
+typedef struct lbt_q8head lbt_q8head;
+int lbt_q8head_from_bf16(lbt_ctx* ctx, const lbt_bf16* w, lbt_q8head** out);
+void lbt_q8head_free(lbt_q8head* h);
+/* Host copies of the quantized weights (q: rows*cols bytes, scale: rows). */
+int lbt_q8head_read(lbt_ctx* ctx, const lbt_q8head* h, int8_t* q, float* scale);
+/* Q8Head::gemv (q8head.rs:34-57) for m rows: out[t*rows + r] = scale[r] *
+ * sum_k q[r,k] * x[t,k], f32 accumulation (device order; within the
+ * reference's own 1e-4 * sum|terms| bound, q8head.rs:84-97). */
+int lbt_q8head_linear(lbt_ctx* ctx, const lbt_q8head* h, const float* x, size_t m, float* out);
+int lbt_q8head_linear_dev(lbt_ctx* ctx, const lbt_q8head* h, const float* x, size_t m, float* out);
+
 /* ---- BitNet b1.58 model ------------------------------------------------------
  * Config (crates/lb-model/src/model.rs:22-42). */
 typedef struct lbt_config {
@@ -179,6 +196,10 @@ int lbt_model_generate_greedy(lbt_model* m, const uint32_t* prompt, size_t n, si
  * gets the `steps` argmax ids.  ms_decode (nullable) gets device-timed ms. */
 int lbt_model_decode_greedy(lbt_model* m, lbt_cache* c, uint32_t first, size_t steps, uint32_t* out_tokens,
                             float* ms_decode);
+/* LM head of the model's forwards: 0 = the exact tied bf16 head (default),
+ * 1 = the opt-in int8 head (q8head.rs), quantized on the device from the
+ * tied embedding when first selected.  A cached decode-step graph is rebuilt. */
+int lbt_model_set_head(lbt_model* m, int kind);
 /* Residual stream of the last forward ([n, hidden] f32) for layer-level tests. */
 int lbt_model_read_hidden(lbt_model* m, float* out, size_t n);
 

@@ -138,6 +138,29 @@ __device__ __forceinline__ float dot8(uint4 wv, const float* x, float acc) {
     return acc;
 }
 
+// Signed byte k (0..3) of v as f32 (int8 head weights).
+__device__ __forceinline__ float i8_at(uint32_t v, int k) { return (float)((int32_t)(v << (24 - 8 * k)) >> 24); }
+
+// acc += sum over e of q[e] * x[e] for the 8 int8 of one 8-byte chunk, in order.
+__device__ __forceinline__ float dot8_i8(uint2 wv, const float* x, float acc) {
+    const float4 x0 = *(const float4*)x;
+    const float4 x1 = *(const float4*)(x + 4);
+    acc = __builtin_fmaf(i8_at(wv.x, 0), x0.x, acc);
+    acc = __builtin_fmaf(i8_at(wv.x, 1), x0.y, acc);
+    acc = __builtin_fmaf(i8_at(wv.x, 2), x0.z, acc);
+    acc = __builtin_fmaf(i8_at(wv.x, 3), x0.w, acc);
+    acc = __builtin_fmaf(i8_at(wv.y, 0), x1.x, acc);
+    acc = __builtin_fmaf(i8_at(wv.y, 1), x1.y, acc);
+    acc = __builtin_fmaf(i8_at(wv.y, 2), x1.z, acc);
+    acc = __builtin_fmaf(i8_at(wv.y, 3), x1.w, acc);
+    return acc;
+}
+
+__device__ __forceinline__ uint2 ld_stream8(const uint2* p) {
+    const u32x2 v = __builtin_nontemporal_load((const LBT_GLOBAL u32x2*)p);
+    return make_uint2(v.x, v.y);
+}
+
 constexpr int kLmChunks = 5;  // 16-byte chunks per lane per row (hidden <= 2560 on the fast path)
 
 __global__ __launch_bounds__(kThreads) void lmhead_kernel(const uint16_t* W, int rows, int cols, const float* x,
@@ -312,6 +335,193 @@ __global__ __launch_bounds__(kThreads) void row_norm_kernel(const float* x, int 
     }
 }
 
+// ---------------------------------------------------------------------------
+// Opt-in int8 LM head (crates/lb-ternary/src/q8head.rs).
+//
+// Q8Head::from_bf16 (q8head.rs:18-32), one workgroup per row (grid-strided):
+// scale = amax / 127 (1.0 for an all-zero row; NaN ignored by the max),
+// q = round_ties_even(w / scale) clamped to [-127, 127] (NaN -> 0), with the
+// IEEE f32 division of the reference.
+__global__ __launch_bounds__(kThreads) void q8_quantize_kernel(const uint16_t* w, int rows, int cols, int8_t* q,
+                                                               float* scale) {
+    __shared__ float red[kRedFloats];
+    for (int r = blockIdx.x; r < rows; r += gridDim.x) {
+        const uint16_t* wr = w + (size_t)r * cols;
+        float am = 0.0f;
+        for (int i = threadIdx.x; i < cols; i += kThreads) am = fmaxf(am, fabsf(bf16_to_f32(wr[i])));
+        am = block_max(am, red);
+        const float s = am == 0.0f ? 1.0f : am / 127.0f;
+        for (int i = threadIdx.x; i < cols; i += kThreads) {
+            const float y = __builtin_rintf(bf16_to_f32(wr[i]) / s);
+            const float c = y != y ? 0.0f : fminf(fmaxf(y, -127.0f), 127.0f);
+            q[(size_t)r * cols + i] = (int8_t)(int)c;
+        }
+        if (threadIdx.x == 0) scale[r] = s;
+        __syncthreads();  // red is reused by the next row
+    }
+}
+
+// Q8Head::gemv (q8head.rs:34-57) for token row blockIdx.y with the final
+// RMSNorm fused as a prologue (as lmhead_kernel): logit[r] = scale[r] *
+// sum_k q[r,k] * xn[k].  One wavefront per row, several rows in flight; lane l
+// takes the 8-byte chunks l, l+64, ... with fused multiply-adds in element
+// order, then the xor butterfly, then the scale.  The first-max key of the
+// row's logits is maxed into key[t] (one atomic per workgroup).
+__global__ __launch_bounds__(kThreads) void q8head_kernel(const int8_t* Q, const float* S, int rows, int cols,
+                                                          const float* x, const float* norm_w, float eps,
+                                                          float* logits, unsigned long long* key) {
+    extern __shared__ __align__(16) float xs[];  // cols
+    __shared__ float red[kRedFloats];
+    const int t = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
+    const float* xr = x + (size_t)t * cols;
+    auto prologue = [&]() {
+        if (cols <= 16 * kThreads) {
+            float v[16];
+            load_norm_row<16>(SrcF32{xr}, cols, norm_w, eps, v, red);
+#pragma unroll
+            for (int e = 0; e < 16; e++)
+                if (tid < kThreads && row_elem(tid, e) < cols) xs[row_elem(tid, e)] = v[e];
+        } else {
+            const float rr = norm_factor_global(SrcF32{xr}, cols, norm_w, eps, red);
+            for (int i = tid; i < cols; i += kThreads) xs[i] = norm_w ? (xr[i] * rr) * norm_w[i] : xr[i];
+        }
+        __syncthreads();
+    };
+    const int nchunks = cols >> 3;
+    const int gw = blockIdx.x * 4 + (tid >> 6), nw = gridDim.x * 4;
+    unsigned long long best = 0ull;
+    auto emit = [&](int r, float acc) {
+        acc = gload(S + r) * wave_sum(acc);
+        if (lane == 0) {
+            if (logits) logits[(size_t)t * rows + r] = acc;
+            const unsigned long long k = argmax_key(acc, (uint32_t)r);
+            best = k > best ? k : best;
+        }
+    };
+    if (nchunks == 64 * kLmChunks) {
+        // Groups of 2 rows r = gw + nw (2 p + j), j = 0, 1, with the next
+        // group's loads (weights and the 2 row scales) in flight while a group
+        // computes: untracked loads with explicit waits, unconditional (rows
+        // past the end load row 0 and are not used); the first group is
+        // issued before the prologue.  Same per-row order as the loop below.
+        constexpr int G = 2, NL = G * kLmChunks + G;
+        const int ng = gw < rows ? (rows - gw + G * nw - 1) / (G * nw) : 0;
+        u32x2 A[2][G][kLmChunks];
+        float SC[2][G];
+        auto issue = [&](int p, u32x2 (&a)[G][kLmChunks], float (&sc)[G]) {
+#pragma unroll
+            for (int j = 0; j < G; j++) {
+                const int r = gw + nw * (G * p + j), rr = r < rows ? r : 0;
+                const int8_t* wr = Q + (size_t)rr * cols;
+#pragma unroll
+                for (int i = 0; i < kLmChunks; i++) a[j][i] = ld_u2_async_nt(wr + 8 * (lane + 64 * i));
+                sc[j] = ld_f32_async(S + rr);
+            }
+        };
+        auto land = [&](u32x2 (&a)[G][kLmChunks], float (&sc)[G]) {
+            vm_wait<NL>();  // all but the group issued last
+#pragma unroll
+            for (int j = 0; j < G; j++) {
+#pragma unroll
+                for (int i = 0; i < kLmChunks; i++) pin(a[j][i]);
+                pin(sc[j]);
+            }
+        };
+        auto consume = [&](int p, u32x2 (&a)[G][kLmChunks], float (&sc)[G]) {
+            float4 xv[kLmChunks][2];  // this lane's x chunks, read once for the G rows
+#pragma unroll
+            for (int i = 0; i < kLmChunks; i++) {
+                xv[i][0] = *(const float4*)(xs + 8 * (lane + 64 * i));
+                xv[i][1] = *(const float4*)(xs + 8 * (lane + 64 * i) + 4);
+            }
+#pragma unroll
+            for (int j = 0; j < G; j++) {
+                const int r = gw + nw * (G * p + j);
+                float acc = 0.0f;
+#pragma unroll
+                for (int i = 0; i < kLmChunks; i++) {
+                    const float xe[8] = {xv[i][0].x, xv[i][0].y, xv[i][0].z, xv[i][0].w,
+                                         xv[i][1].x, xv[i][1].y, xv[i][1].z, xv[i][1].w};
+#pragma unroll
+                    for (int e = 0; e < 8; e++)
+                        acc = __builtin_fmaf(i8_at(e < 4 ? a[j][i].x : a[j][i].y, e & 3), xe[e], acc);
+                }
+                acc = sc[j] * wave_sum(acc);
+                if (lane == 0 && r < rows) {
+                    if (logits) gstore(logits + (size_t)t * rows + r, acc);
+                    const unsigned long long k = argmax_key(acc, (uint32_t)r);
+                    best = k > best ? k : best;
+                }
+            }
+        };
+        issue(0, A[0], SC[0]);
+        prologue();
+        for (int p = 0; p < ng; p += 2) {
+            issue(p + 1, A[1], SC[1]);
+            land(A[0], SC[0]);
+            consume(p, A[0], SC[0]);
+            issue(p + 2, A[0], SC[0]);
+            land(A[1], SC[1]);
+            if (p + 1 < ng) consume(p + 1, A[1], SC[1]);
+        }
+        vm_wait<0>();
+#pragma unroll
+        for (int j = 0; j < G; j++) {
+#pragma unroll
+            for (int i = 0; i < kLmChunks; i++) {
+                keep(A[0][j][i]);
+                keep(A[1][j][i]);
+            }
+            keep(SC[0][j]);
+            keep(SC[1][j]);
+        }
+    } else if (nchunks <= 64 * kLmChunks) {
+        prologue();
+        constexpr int RW = 4;  // rows per wavefront per iteration
+        for (int r0 = gw; r0 < rows; r0 += RW * nw) {
+            uint2 a[RW][kLmChunks];
+#pragma unroll
+            for (int j = 0; j < RW; j++) {
+                const int r = r0 + j * nw;
+                const uint2* wr = (const uint2*)(Q + (size_t)(r < rows ? r : r0) * cols);
+#pragma unroll
+                for (int i = 0; i < kLmChunks; i++) {
+                    const int c = lane + 64 * i;
+                    a[j][i] = c < nchunks ? ld_stream8(wr + c) : make_uint2(0, 0);
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < RW; j++) {
+                const int r = r0 + j * nw;
+                float acc = 0.0f;
+#pragma unroll
+                for (int i = 0; i < kLmChunks; i++) {
+                    const int c = lane + 64 * i;
+                    if (c < nchunks) acc = dot8_i8(a[j][i], xs + 8 * c, acc);
+                }
+                if (r < rows) emit(r, acc);
+            }
+        }
+    } else {
+        prologue();
+        for (int r = gw; r < rows; r += nw) {
+            const uint2* wr = (const uint2*)(Q + (size_t)r * cols);
+            float acc = 0.0f;
+            for (int c = lane; c < nchunks; c += 64) acc = dot8_i8(ld_stream8(wr + c), xs + 8 * c, acc);
+            emit(r, acc);
+        }
+    }
+    __shared__ unsigned long long wbest[kThreads / 64];
+    if (lane == 0) wbest[tid >> 6] = best;
+    __syncthreads();
+    if (key && tid == 0) {
+        unsigned long long b = wbest[0];
+#pragma unroll
+        for (int i = 1; i < kThreads / 64; i++) b = wbest[i] > b ? wbest[i] : b;
+        if (b) atomicMax(&key[t], b);
+    }
+}
+
 // LM head for several token rows at once (normalized rows xn [m][cols]):
 // each (weight row, token) dot product has lmhead_kernel's order (lane l
 // takes chunks l, l+64, ... with fused multiply-adds in element order, then
@@ -322,9 +532,13 @@ __global__ __launch_bounds__(kThreads) void row_norm_kernel(const float* x, int 
 // wavefront reduce together by recursive halving.  Workgroup i takes token
 // group i % ngroups of row tile i / ngroups, so the groups of one tile run
 // together and share its weight rows through the caches.
-template <int R, int NCH, int TG>
-__global__ __launch_bounds__(kThreads) void lmhead_batch_kernel(const uint16_t* W, int rows, int cols, const float* xn,
-                                                                int m, int tile_rows, float* logits,
+//
+// Q8: the int8 head (q8head.rs): W is int8 [rows][cols] with one f32 scale
+// per row (rscale); chunk c is the 8 bytes 8c..8c+7, and each sum is scaled
+// by its row's scale, as in q8head_kernel.
+template <int R, int NCH, int TG, bool Q8>
+__global__ __launch_bounds__(kThreads) void lmhead_batch_kernel(const void* W, const float* rscale, int rows, int cols,
+                                                                const float* xn, int m, int tile_rows, float* logits,
                                                                 unsigned long long* key) {
     static_assert(R * TG == 32, "32 accumulators per lane");
     extern __shared__ __align__(16) float xs[];  // [TG][cols]
@@ -347,7 +561,18 @@ __global__ __launch_bounds__(kThreads) void lmhead_batch_kernel(const uint16_t* 
 #pragma unroll
         for (int r = 0; r < R; r++) {
             const int row = rb + r < r_end ? rb + r : rb;
-            const uint4* wr = (const uint4*)(W + (size_t)row * cols);
+            if constexpr (Q8) {
+                const uint2* wr = (const uint2*)((const int8_t*)W + (size_t)row * cols);
+#pragma unroll
+                for (int i = 0; i < NCH; i++) {
+                    const int c = lane + 64 * i;
+                    const uint2 v = c < nchunks ? ld_stream8(wr + c) : make_uint2(0, 0);
+#pragma unroll
+                    for (int e = 0; e < 8; e++) wf[r][i][e] = i8_at(e < 4 ? v.x : v.y, e & 3);
+                }
+                continue;
+            }
+            const uint4* wr = (const uint4*)((const uint16_t*)W + (size_t)row * cols);
 #pragma unroll
             for (int i = 0; i < NCH; i++) {
                 const int c = lane + 64 * i;
@@ -389,8 +614,9 @@ __global__ __launch_bounds__(kThreads) void lmhead_batch_kernel(const uint16_t* 
         halve<8>(h8, h4);
         halve<4>(h4, h2);
         halve<2>(h2, h1);
-        const float a = xor_add<1>(h1[0]);
+        float a = xor_add<1>(h1[0]);
         const int row = rb + my_r;
+        if (Q8) a = gload(rscale + (row < r_end ? row : r_begin)) * a;
         if ((lane & 1) == 0 && my_t < nt && row < r_end) {
             if (logits) logits[(size_t)(t0 + my_t) * rows + row] = a;
             const unsigned long long k = argmax_key(a, (uint32_t)row);
@@ -605,11 +831,16 @@ int launch_attn_combine(lbt_ctx* ctx, const float* o, const float* ml, int m, in
     return LBT_OK;
 }
 
-int launch_bf16_linear(lbt_ctx* ctx, const uint16_t* w, int rows, int cols, const float* x, int m,
-                       const float* norm_w, float eps, float* logits, unsigned long long* key, float* xn) {
-    if (cols % 8) return set_err(ctx, LBT_E_INVALID, "bf16 linear: cols must be a multiple of 8");
+namespace {
+// The LM head launch shared by the bf16 head and the int8 head (rscale set).
+int launch_head(lbt_ctx* ctx, const void* w, const float* rscale, int rows, int cols, const float* x, int m,
+                const float* norm_w, float eps, float* logits, unsigned long long* key, float* xn) {
+    const bool q8 = rscale != nullptr;
+    const char* what = q8 ? "int8 head" : "bf16 linear";
+    if (cols % 8) return set_err(ctx, LBT_E_INVALID, std::string(what) + ": cols must be a multiple of 8");
     if (m <= 0) return LBT_OK;
     constexpr int kTG = 8, kR = 4;
+    const double wbytes = (double)rows * cols * (q8 ? 1.0 : 2.0);
     if (m >= 2 && xn && cols <= 64 * kLmChunks * 8) {
         // several rows: normalize once, then the weight-reusing head
         hipLaunchKernelGGL(row_norm_kernel, dim3(m), dim3(kThreads), 0, ctx->stream, x, cols, norm_w, eps, xn);
@@ -621,33 +852,64 @@ int launch_bf16_linear(lbt_ctx* ctx, const uint16_t* w, int rows, int cols, cons
         tile_rows = (tile_rows + 4 * kR - 1) / (4 * kR) * (4 * kR);
         tiles = (rows + tile_rows - 1) / tile_rows;
         const size_t lds = (size_t)kTG * cols * sizeof(float);
-        static bool attr = false;
-        if (!attr) {
-            (void)hipFuncSetAttribute((const void*)lmhead_batch_kernel<kR, kLmChunks, kTG>,
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024);
+        const void* fn = q8 ? (const void*)lmhead_batch_kernel<kR, kLmChunks, kTG, true>
+                            : (const void*)lmhead_batch_kernel<kR, kLmChunks, kTG, false>;
+        static bool attr[2] = {false, false};
+        if (!attr[q8]) {
+            (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024);
             (void)hipGetLastError();
-            attr = true;
+            attr[q8] = true;
         }
-        if (lds > 96 * 1024) return set_err(ctx, LBT_E_INVALID, "bf16 linear: token group exceeds LDS");
+        if (lds > 96 * 1024) return set_err(ctx, LBT_E_INVALID, std::string(what) + ": token group exceeds LDS");
         hipEvent_t e0, e1;
         prof_pair(ctx, &e0, &e1);
-        hipExtLaunchKernelGGL((lmhead_batch_kernel<kR, kLmChunks, kTG>), dim3(tiles * ngroups), dim3(kThreads), lds,
-                              ctx->stream, e0, e1, 0, w, rows, cols, xn, m, tile_rows, logits, key);
+        if (q8)
+            hipExtLaunchKernelGGL((lmhead_batch_kernel<kR, kLmChunks, kTG, true>), dim3(tiles * ngroups),
+                                  dim3(kThreads), lds, ctx->stream, e0, e1, 0, w, rscale, rows, cols, xn, m, tile_rows,
+                                  logits, key);
+        else
+            hipExtLaunchKernelGGL((lmhead_batch_kernel<kR, kLmChunks, kTG, false>), dim3(tiles * ngroups),
+                                  dim3(kThreads), lds, ctx->stream, e0, e1, 0, w, rscale, rows, cols, xn, m, tile_rows,
+                                  logits, key);
         LBT_HIP(ctx, hipGetLastError());
-        prof_commit(ctx, e0, e1, kProfHead, (double)rows * cols * 2.0);
+        prof_commit(ctx, e0, e1, kProfHead, wbytes);
         return LBT_OK;
     }
     const size_t lds = (size_t)cols * sizeof(float);
-    if (lds > 64 * 1024) return set_err(ctx, LBT_E_INVALID, "bf16 linear: cols too large");
+    if (lds > 64 * 1024) return set_err(ctx, LBT_E_INVALID, std::string(what) + ": cols too large");
     int blocks = (rows + 31) / 32;
-    if (blocks > 2048) blocks = 2048;
+    if (blocks > (q8 ? 512 : 2048)) blocks = q8 ? 512 : 2048;
     if (blocks < 1) blocks = 1;
     hipEvent_t e0, e1;
     prof_pair(ctx, &e0, &e1);
-    hipExtLaunchKernelGGL(lmhead_kernel, dim3(blocks, m), dim3(kThreads), lds, ctx->stream, e0, e1, 0, w, rows, cols, x, norm_w,
-                       eps, logits, key);
+    if (q8)
+        hipExtLaunchKernelGGL(q8head_kernel, dim3(blocks, m), dim3(kThreads), lds, ctx->stream, e0, e1, 0,
+                              (const int8_t*)w, rscale, rows, cols, x, norm_w, eps, logits, key);
+    else
+        hipExtLaunchKernelGGL(lmhead_kernel, dim3(blocks, m), dim3(kThreads), lds, ctx->stream, e0, e1, 0,
+                              (const uint16_t*)w, rows, cols, x, norm_w, eps, logits, key);
     LBT_HIP(ctx, hipGetLastError());
-    prof_commit(ctx, e0, e1, kProfHead, (double)rows * cols * 2.0 * m);
+    prof_commit(ctx, e0, e1, kProfHead, wbytes * m);
+    return LBT_OK;
+}
+}  // namespace
+
+int launch_bf16_linear(lbt_ctx* ctx, const uint16_t* w, int rows, int cols, const float* x, int m,
+                       const float* norm_w, float eps, float* logits, unsigned long long* key, float* xn) {
+    return launch_head(ctx, w, nullptr, rows, cols, x, m, norm_w, eps, logits, key, xn);
+}
+
+int launch_q8_linear(lbt_ctx* ctx, const int8_t* q, const float* scale, int rows, int cols, const float* x, int m,
+                     const float* norm_w, float eps, float* logits, unsigned long long* key, float* xn) {
+    if (!scale) return set_err(ctx, LBT_E_INVALID, "int8 head: missing row scales");
+    return launch_head(ctx, q, scale, rows, cols, x, m, norm_w, eps, logits, key, xn);
+}
+
+int launch_q8_quantize(lbt_ctx* ctx, const uint16_t* w, int rows, int cols, int8_t* q, float* scale) {
+    if (rows <= 0 || cols <= 0) return set_err(ctx, LBT_E_INVALID, "int8 head: empty matrix");
+    const int blocks = rows < ctx->cus * 8 ? rows : ctx->cus * 8;
+    hipLaunchKernelGGL(q8_quantize_kernel, dim3(blocks), dim3(kThreads), 0, ctx->stream, w, rows, cols, q, scale);
+    LBT_HIP(ctx, hipGetLastError());
     return LBT_OK;
 }
 

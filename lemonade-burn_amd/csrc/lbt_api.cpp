@@ -442,6 +442,70 @@ int lbt_bf16_linear(lbt_ctx* ctx, const lbt_bf16* w, const float* x, size_t m, f
     return LBT_OK;
 }
 
+// ---- int8 LM head ----------------------------------------------------------------
+int lbt_q8head_from_bf16(lbt_ctx* ctx, const lbt_bf16* w, lbt_q8head** out) {
+    if (!ctx || !w || !out) return set_err(ctx, LBT_E_INVALID, "q8head_from_bf16: bad arguments");
+    *out = nullptr;
+    if (w->rows > (size_t)INT32_MAX || w->cols > (size_t)INT32_MAX)
+        return set_err(ctx, LBT_E_INVALID, "q8head_from_bf16: matrix too large");
+    lbt_q8head* h = new lbt_q8head();
+    h->ctx = ctx;
+    h->rows = w->rows;
+    h->cols = w->cols;
+    hipError_t e = hipMalloc(&h->q, w->rows * w->cols);
+    if (e == hipSuccess) e = hipMalloc(&h->scale, w->rows * 4);
+    if (e != hipSuccess) {
+        lbt_q8head_free(h);
+        return hip_err(ctx, e, "q8head alloc");
+    }
+    int rc = launch_q8_quantize(ctx, w->d, (int)w->rows, (int)w->cols, h->q, h->scale);
+    if (!rc && (e = hipStreamSynchronize(ctx->stream)) != hipSuccess) rc = hip_err(ctx, e, "q8head quantize");
+    if (rc) {
+        lbt_q8head_free(h);
+        return rc;
+    }
+    *out = h;
+    return LBT_OK;
+}
+
+void lbt_q8head_free(lbt_q8head* h) {
+    if (!h) return;
+    hipStreamSynchronize(h->ctx->stream);
+    if (h->q) hipFree(h->q);
+    if (h->scale) hipFree(h->scale);
+    delete h;
+}
+
+int lbt_q8head_read(lbt_ctx* ctx, const lbt_q8head* h, int8_t* q, float* scale) {
+    if (!ctx || !h) return set_err(ctx, LBT_E_INVALID, "q8head_read: bad arguments");
+    if (q) LBT_HIP(ctx, hipMemcpyAsync(q, h->q, h->rows * h->cols, hipMemcpyDeviceToHost, ctx->stream));
+    if (scale) LBT_HIP(ctx, hipMemcpyAsync(scale, h->scale, h->rows * 4, hipMemcpyDeviceToHost, ctx->stream));
+    LBT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return LBT_OK;
+}
+
+int lbt_q8head_linear_dev(lbt_ctx* ctx, const lbt_q8head* h, const float* x, size_t m, float* out) {
+    if (!ctx || !h) return set_err(ctx, LBT_E_INVALID, "q8head_linear: bad arguments");
+    return launch_q8_linear(ctx, h->q, h->scale, (int)h->rows, (int)h->cols, x, (int)m, nullptr, 0.0f, out, nullptr);
+}
+
+int lbt_q8head_linear(lbt_ctx* ctx, const lbt_q8head* h, const float* x, size_t m, float* out) {
+    if (!ctx || !h) return set_err(ctx, LBT_E_INVALID, "q8head_linear: bad arguments");
+    if (m == 0) return LBT_OK;
+    Carve cv;
+    size_t ox = cv.add(m * h->cols * 4), oo = cv.add(m * h->rows * 4);
+    void* wsp;
+    int rc = ws_reserve(ctx, cv.total(), &wsp);
+    if (rc) return rc;
+    char* b = (char*)wsp;
+    LBT_HIP(ctx, hipMemcpyAsync(b + ox, x, m * h->cols * 4, hipMemcpyHostToDevice, ctx->stream));
+    rc = lbt_q8head_linear_dev(ctx, h, (const float*)(b + ox), m, (float*)(b + oo));
+    if (rc) return rc;
+    LBT_HIP(ctx, hipMemcpyAsync(out, b + oo, m * h->rows * 4, hipMemcpyDeviceToHost, ctx->stream));
+    LBT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return LBT_OK;
+}
+
 // ---- profiling -------------------------------------------------------------------
 int lbt_prof_enable(lbt_ctx* ctx, int on) {
     if (!ctx) return LBT_E_INVALID;

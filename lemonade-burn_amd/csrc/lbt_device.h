@@ -67,6 +67,17 @@ __device__ __forceinline__ u32x4 ld_u4_async_nt(const void* p) {
     asm volatile("global_load_dwordx4 %0, %1, off nt" : "=v"(v) : "v"(p) : "memory");
     return v;
 }
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ u32x2 ld_u2_async_nt(const void* p) {
+    u32x2 v;
+    asm volatile("global_load_dwordx2 %0, %1, off nt" : "=v"(v) : "v"(p) : "memory");
+    return v;
+}
+__device__ __forceinline__ float ld_f32_async(const float* p) {
+    float v;
+    asm volatile("global_load_dword %0, %1, off" : "=v"(v) : "v"(p) : "memory");
+    return v;
+}
 template <int N>
 __device__ __forceinline__ void vm_wait() {
     static_assert(N >= 0 && N < 64, "vmcnt range");

@@ -48,6 +48,13 @@ struct lbt_bf16 {
     bool owns = true;
 };
 
+struct lbt_q8head {
+    lbt_ctx* ctx = nullptr;
+    int8_t* q = nullptr;
+    float* scale = nullptr;
+    size_t rows = 0, cols = 0;
+};
+
 namespace lbt {
 
 // Error helpers: every entry point converts failures into a status code.
@@ -130,6 +137,12 @@ int launch_quantize(lbt_ctx* ctx, const float* x, const float* norm_w, float eps
 // If key != nullptr, the first-max key of row t is atomically maxed into key[t].
 int launch_bf16_linear(lbt_ctx* ctx, const uint16_t* w, int rows, int cols, const float* x, int m,
                        const float* norm_w, float eps, float* logits, unsigned long long* key, float* xn = nullptr);
+// The opt-in int8 head (q8head.rs): logits[t*rows + r] = scale[r] *
+// sum_k xn[t,k] * q[r,k]; same norm, key and xn contract as above.
+int launch_q8_linear(lbt_ctx* ctx, const int8_t* q, const float* scale, int rows, int cols, const float* x, int m,
+                     const float* norm_w, float eps, float* logits, unsigned long long* key, float* xn = nullptr);
+// Q8Head::from_bf16 (q8head.rs:18-32) of a device bf16 [rows][cols] matrix.
+int launch_q8_quantize(lbt_ctx* ctx, const uint16_t* w, int rows, int cols, int8_t* q, float* scale);
 
 // ---- model pieces --------------------------------------------------------
 // state (nullable, device): {position, output slot}; when set, the kernel

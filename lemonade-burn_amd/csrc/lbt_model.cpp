@@ -223,6 +223,10 @@ struct lbt_model {
     std::vector<const float*> norm;
     const float* final_norm = nullptr;
     uint16_t* embed = nullptr;
+    // opt-in int8 head (q8head.rs), quantized from embed when selected
+    int head_kind = 0;
+    int8_t* q8 = nullptr;
+    float* q8s = nullptr;
     float* cos_t = nullptr;
     float* sin_t = nullptr;
     float scaling = 0.0f;
@@ -247,6 +251,20 @@ struct lbt_model {
     unsigned* bar = nullptr;  // flags [G*16], go, err
     int bar_g = 0;
 };
+
+namespace {
+// Final RMSNorm + the model's LM head (model.rs:368-373): the tied bf16 head,
+// or the int8 head when selected.
+int model_head(lbt_model* m, const float* x, int rows, float eps, float* logits, unsigned long long* key,
+               float* xn) {
+    const lbt_config& c = m->cfg;
+    if (m->head_kind == 1)
+        return launch_q8_linear(m->ctx, m->q8, m->q8s, c.vocab_size, c.hidden_size, x, rows, m->final_norm, eps,
+                                logits, key, xn);
+    return launch_bf16_linear(m->ctx, m->embed, c.vocab_size, c.hidden_size, x, rows, m->final_norm, eps, logits,
+                              key, xn);
+}
+}  // namespace
 
 struct lbt_cache {
     lbt_model* m = nullptr;
@@ -544,9 +562,8 @@ int forward_rows(lbt_model* m, const KvView& kv, const RowPos& rp, const uint32_
     // final norm + tied LM head (model.rs:368-373) + argmax
     const int first = (all_logits || rp.tok_pos) ? 0 : n - 1;
     const int rows_out = n - first;
-    return launch_bf16_linear(ctx, m->embed, c.vocab_size, H, m->x + (size_t)first * H, rows_out, m->final_norm, eps,
-                              (all_logits || want_logits) ? m->logits : nullptr,
-                              (all_logits && !rp.tok_pos) ? nullptr : m->key, m->att);
+    return model_head(m, m->x + (size_t)first * H, rows_out, eps, (all_logits || want_logits) ? m->logits : nullptr,
+                      (all_logits && !rp.tok_pos) ? nullptr : m->key, m->att);
 }
 
 // One forward of n tokens of one sequence at positions cache.len.. (or, with
@@ -706,8 +723,7 @@ int decode_steps(lbt_model* m, lbt_cache* c, int n, int slot0) {
         const lbt_config& cf = m->cfg;
         for (int s = 0; s < n; s++) {
             if ((rc = launch_decode_persistent(ctx, h, G, ctx->stream))) return rc;
-            if ((rc = launch_bf16_linear(ctx, m->embed, cf.vocab_size, cf.hidden_size, m->x, 1, m->final_norm,
-                                         (float)cf.rms_norm_eps, nullptr, m->key)))
+            if ((rc = model_head(m, m->x, 1, (float)cf.rms_norm_eps, nullptr, m->key, nullptr)))
                 return rc;
         }
         c->len += n;
@@ -952,7 +968,7 @@ void lbt_model_free(lbt_model* m) {
     if (m->bar) hipFree(m->bar);
     void* bufs[] = {m->wbuf, m->fbuf, m->embed, m->cos_t, m->sin_t, m->x,   m->q,       m->k,
                     m->v,    m->att,  m->h,     m->logits, m->toks, m->key, m->tok_out, m->state,
-                    m->ao,   m->aml};
+                    m->ao,   m->aml,  m->q8,    m->q8s};
     for (void* b : bufs)
         if (b) hipFree(b);
     delete m;
@@ -1121,6 +1137,28 @@ int lbt_model_decode_greedy(lbt_model* m, lbt_cache* c, uint32_t first, size_t s
     hipEventDestroy(e0);
     hipEventDestroy(e1);
     return rc;
+}
+
+int lbt_model_set_head(lbt_model* m, int kind) {
+    if (!m) return LBT_E_INVALID;
+    lbt_ctx* ctx = m->ctx;
+    if (kind != 0 && kind != 1) return set_err(ctx, LBT_E_INVALID, "set_head: kind must be 0 (bf16) or 1 (int8)");
+    const lbt_config& c = m->cfg;
+    if (kind == 1 && !m->q8) {
+        const size_t n = (size_t)c.vocab_size * c.hidden_size;
+        LBT_HIP(ctx, hipMalloc(&m->q8, n));
+        LBT_HIP(ctx, hipMalloc(&m->q8s, (size_t)c.vocab_size * 4));
+        int rc = launch_q8_quantize(ctx, m->embed, c.vocab_size, c.hidden_size, m->q8, m->q8s);
+        if (rc) return rc;
+        LBT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    }
+    if (kind != m->head_kind && m->step_exec) {
+        LBT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        hipGraphExecDestroy(m->step_exec);
+        m->step_exec = nullptr;
+    }
+    m->head_kind = kind;
+    return LBT_OK;
 }
 
 int lbt_model_read_hidden(lbt_model* m, float* out, size_t n) {

@@ -79,6 +79,11 @@ SIGNATURES = {
     "lbt_bf16_free": (None, [vp]),
     "lbt_bf16_linear": (i32, [vp, vp, vp, sz, vp]),
     "lbt_bf16_linear_dev": (i32, [vp, vp, vp, sz, vp]),
+    "lbt_q8head_from_bf16": (i32, [vp, vp, C.POINTER(vp)]),
+    "lbt_q8head_free": (None, [vp]),
+    "lbt_q8head_read": (i32, [vp, vp, vp, vp]),
+    "lbt_q8head_linear": (i32, [vp, vp, vp, sz, vp]),
+    "lbt_q8head_linear_dev": (i32, [vp, vp, vp, sz, vp]),
     "lbt_model_load": (i32, [vp, C.c_char_p, C.POINTER(vp)]),
     "lbt_model_create_synthetic": (i32, [vp, C.POINTER(LbtConfig), u64, C.POINTER(vp)]),
     "lbt_model_free": (None, [vp]),
@@ -93,6 +98,7 @@ SIGNATURES = {
     "lbt_model_generate_greedy": (i32, [vp, vp, sz, sz, vp, vp, vp, vp]),
     "lbt_model_decode_greedy": (i32, [vp, vp, C.c_uint32, sz, vp, vp]),
     "lbt_model_read_hidden": (i32, [vp, vp, sz]),
+    "lbt_model_set_head": (i32, [vp, i32]),
     "lbt_batch_new": (i32, [vp, i32, i32, C.POINTER(vp)]),
     "lbt_batch_free": (None, [vp]),
     "lbt_batch_len": (i32, [vp, i32]),
@@ -229,6 +235,18 @@ class Ctx:
         self.check(self.lib.lbt_bf16_linear(self.h, w.h, _ptr(x), m, _ptr(out)))
         return out
 
+    def q8head_from_bf16(self, w: "Bf16Weight") -> "Q8Head":
+        h = C.c_void_p()
+        self.check(self.lib.lbt_q8head_from_bf16(self.h, w.h, C.byref(h)))
+        return Q8Head(self, h, w.rows, w.cols)
+
+    def q8head_linear(self, h: "Q8Head", x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        m = x.shape[0]
+        out = np.zeros((m, h.rows), np.float32)
+        self.check(self.lib.lbt_q8head_linear(self.h, h.h, _ptr(x), m, _ptr(out)))
+        return out
+
     # ---- profiling ---------------------------------------------------------------
     def prof_enable(self, on: bool):
         self.check(self.lib.lbt_prof_enable(self.h, 1 if on else 0))
@@ -274,6 +292,31 @@ class Bf16Weight:
             pass
 
 
+class Q8Head:
+    """Q8Head (q8head.rs:9-15) on the device."""
+
+    def __init__(self, ctx: Ctx, h, rows, cols):
+        self.ctx, self.h, self.rows, self.cols = ctx, h, rows, cols
+
+    def read(self):
+        q = np.zeros((self.rows, self.cols), np.int8)
+        s = np.zeros(self.rows, np.float32)
+        self.ctx.check(self.ctx.lib.lbt_q8head_read(self.ctx.h, self.h, _ptr(q), _ptr(s)))
+        return q, s
+
+    def free(self):
+        if self.h:
+            self.ctx.lib.lbt_q8head_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            if self.ctx.h:
+                self.free()
+        except Exception:
+            pass
+
+
 def make_config(hidden=2560, intermediate=6912, heads=20, kv_heads=5, layers=30, vocab=128256, max_pos=4096,
                 eps=1e-5, theta=500000.0, bos=128000) -> LbtConfig:
     """BitNet b1.58 2B4T shape by default."""
@@ -309,6 +352,10 @@ class Model:
         h = C.c_void_p()
         self.ctx.check(self.ctx.lib.lbt_cache_new(self.h, C.byref(h)))
         return Cache(self, h)
+
+    def set_head(self, kind: int):
+        """0 = the exact tied bf16 head, 1 = the opt-in int8 head (q8head.rs)."""
+        self.ctx.check(self.ctx.lib.lbt_model_set_head(self.h, kind))
 
     def forward(self, tokens, cache: "Cache", all_logits: bool = False) -> np.ndarray:
         t = np.ascontiguousarray(tokens, dtype=np.uint32)

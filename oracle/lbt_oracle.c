@@ -251,6 +251,75 @@ void or_bf16_gemv_lanes(const uint16_t* w, size_t rows, size_t cols, const float
 }
 
 /* ------------------------------------------------------------------------ */
+/* q8head.rs: opt-in int8 LM head                                            */
+/* ------------------------------------------------------------------------ */
+
+/* Q8Head::from_bf16 (q8head.rs:18-32): per row amax (f32::max ignores NaN),
+ * scale = amax / 127 (1.0 when amax == 0), q = round_ties_even(w / scale)
+ * clamped to [-127, 127]; a NaN quotient casts to 0 (Rust `as i8`). */
+void or_q8head_from_bf16(const uint16_t* w, size_t rows, size_t cols, int8_t* q, float* scale) {
+    for (size_t r = 0; r < rows; r++) {
+        const uint16_t* wr = w + r * cols;
+        float amax = 0.0f;
+        for (size_t i = 0; i < cols; i++) {
+            float a = fabsf(or_bf16_to_f32(wr[i]));
+            if (a > amax) amax = a; /* a NaN never compares greater */
+        }
+        float s = amax == 0.0f ? 1.0f : amax / 127.0f;
+        scale[r] = s;
+        for (size_t i = 0; i < cols; i++) {
+            float y = rintf(or_bf16_to_f32(wr[i]) / s); /* default rounding: ties to even */
+            if (y != y) y = 0.0f;
+            if (y < -127.0f) y = -127.0f;
+            if (y > 127.0f) y = 127.0f;
+            q[r * cols + i] = (int8_t)y;
+        }
+    }
+}
+
+/* Q8Head::gemv (q8head.rs:35-57), the reference's order: 8 lane accumulators
+ * over k in steps of 8 (unfused multiply, add), their sequential sum, the
+ * scalar tail, then scale[r] * sum. */
+void or_q8head_gemv_ref(const int8_t* q, const float* scale, size_t rows, size_t cols, const float* x, float* out) {
+    size_t n8 = cols / 8 * 8;
+    for (size_t r = 0; r < rows; r++) {
+        const int8_t* row = q + r * cols;
+        float acc[8] = {0};
+        for (size_t k = 0; k < n8; k += 8)
+            for (int j = 0; j < 8; j++) {
+                float p = (float)row[k + j] * x[k + j];
+                acc[j] = acc[j] + p;
+            }
+        float sum = 0.0f;
+        for (int j = 0; j < 8; j++) sum = sum + acc[j];
+        for (size_t k = n8; k < cols; k++) {
+            float p = (float)row[k] * x[k];
+            sum = sum + p;
+        }
+        out[r] = scale[r] * sum;
+    }
+}
+
+/* The device int8 head: cols % 8 == 0; lane l accumulates the 8-byte chunks
+ * c = l + 64 i with fused multiply-adds in element order, the xor butterfly,
+ * then scale[r] * sum. */
+void or_q8head_gemv_lanes(const int8_t* q, const float* scale, size_t rows, size_t cols, const float* x, float* out) {
+    size_t chunks = cols / 8;
+#pragma omp parallel for schedule(static) if (rows * cols > (1u << 22))
+    for (long r = 0; r < (long)rows; r++) {
+        const int8_t* row = q + (size_t)r * cols;
+        float lane[64];
+        for (int l = 0; l < 64; l++) {
+            float acc = 0.0f;
+            for (size_t c = (size_t)l; c < chunks; c += 64)
+                for (int e = 0; e < 8; e++) acc = fmaf((float)row[c * 8 + e], x[c * 8 + e], acc);
+            lane[l] = acc;
+        }
+        out[r] = scale[r] * butterfly64(lane);
+    }
+}
+
+/* ------------------------------------------------------------------------ */
 /* device-order float building blocks                                        */
 /* ------------------------------------------------------------------------ */
 
@@ -424,6 +493,9 @@ struct or_model {
     int cap, len;
     float* hidden; /* residual stream of the last forward, [n, hidden] */
     size_t hidden_rows;
+    int head_kind; /* 0 = bf16 head, 1 = int8 head (q8, q8s from embed) */
+    int8_t* q8;
+    float* q8s;
 };
 
 static int g_fast = 0;
@@ -504,7 +576,20 @@ void or_model_free(or_model* m) {
         free((void*)m->embed);
     }
     free(m->cos_t); free(m->sin_t); free(m->kc); free(m->vc); free(m->hidden);
+    free(m->q8); free(m->q8s);
     free(m);
+}
+
+int or_model_set_head(or_model* m, int kind) {
+    if (kind != 0 && kind != 1) return -1;
+    if (kind == 1 && !m->q8) {
+        size_t V = (size_t)m->c.vocab, H = (size_t)m->c.hidden;
+        m->q8 = (int8_t*)malloc(V * H);
+        m->q8s = (float*)malloc(V * sizeof(float));
+        or_q8head_from_bf16(m->embed, V, H, m->q8, m->q8s);
+    }
+    m->head_kind = kind;
+    return 0;
 }
 
 const uint8_t* or_model_packed(const or_model* m, int layer, int which) { return m->packed[layer * 7 + which]; }
@@ -743,7 +828,8 @@ int or_model_forward(or_model* m, const uint32_t* tokens, size_t n, int all_logi
     for (size_t t = first; t < n; t++) {
         or_rmsnorm(x + t * H, m->final_norm, H, eps, nrm);
         float* lt = logits + (t - first) * (size_t)c->vocab;
-        if (g_fast >= 2) port_bf16_gemv(m->embed, (size_t)c->vocab, H, nrm, lt, 0); /* reference order */
+        if (m->head_kind == 1) or_q8head_gemv_lanes(m->q8, m->q8s, (size_t)c->vocab, H, nrm, lt);
+        else if (g_fast >= 2) port_bf16_gemv(m->embed, (size_t)c->vocab, H, nrm, lt, 0); /* reference order */
         else or_bf16_gemv_lanes(m->embed, (size_t)c->vocab, H, nrm, lt);
     }
     free(x); free(nrm); free(q); free(kk); free(vv); free(att); free(y); free(g); free(u);

@@ -60,6 +60,13 @@ float or_bf16_dot_ref(const uint16_t* w, const float* x, size_t n);
 float or_bf16_dot_lanes(const uint16_t* w, const float* x, size_t n);
 void or_bf16_gemv_lanes(const uint16_t* w, size_t rows, size_t cols, const float* x, float* out);
 
+/* ---- opt-in int8 LM head (crates/lb-ternary/src/q8head.rs) ----------------- */
+void or_q8head_from_bf16(const uint16_t* w, size_t rows, size_t cols, int8_t* q, float* scale); /* :18-32 */
+void or_q8head_gemv_ref(const int8_t* q, const float* scale, size_t rows, size_t cols, const float* x,
+                        float* out); /* :35-57, the reference's order */
+void or_q8head_gemv_lanes(const int8_t* q, const float* scale, size_t rows, size_t cols, const float* x,
+                          float* out); /* the device order */
+
 /* ---- float building blocks in the device order ------------------------- */
 float or_block_sum256(const float* partials);                 /* wave butterflies, then (w0+w1)+(w2+w3) */
 float or_sumsq(const float* x, size_t n);                     /* canonical order (1024 virtual threads) */
@@ -101,6 +108,8 @@ or_model* or_model_wrap(const or_config* cfg, const uint8_t* const* packed /*[la
                         const float* wscales /*[layers*7]*/, const float* const* norms /*[layers*4]*/,
                         const float* final_norm, const uint16_t* embed);
 void or_model_free(or_model* m);
+/* LM head of the forwards: 0 = bf16 (default), 1 = int8 head from the embedding. */
+int or_model_set_head(or_model* m, int kind);
 const uint8_t* or_model_packed(const or_model* m, int layer, int which);
 float or_model_wscale(const or_model* m, int layer, int which);
 const uint16_t* or_model_embed(const or_model* m);

@@ -45,6 +45,10 @@ _SIGS = {
     "or_bf16_dot_ref": (f32, [vp, vp, sz]),
     "or_bf16_dot_lanes": (f32, [vp, vp, sz]),
     "or_bf16_gemv_lanes": (None, [vp, sz, sz, vp, vp]),
+    "or_q8head_from_bf16": (None, [vp, sz, sz, vp, vp]),
+    "or_q8head_gemv_ref": (None, [vp, vp, sz, sz, vp, vp]),
+    "or_q8head_gemv_lanes": (None, [vp, vp, sz, sz, vp, vp]),
+    "or_model_set_head": (C.c_int, [vp, C.c_int]),
     "or_block_sum256": (f32, [vp]),
     "or_sumsq": (f32, [vp, sz]),
     "or_rmsnorm": (None, [vp, vp, sz, f32, vp]),
@@ -241,6 +245,37 @@ def port_bf16_gemv(w: np.ndarray, x: np.ndarray, threads=0) -> np.ndarray:
     return out
 
 
+# ---- int8 head (q8head.rs) ----------------------------------------------------------
+def q8head_from_bf16(w: np.ndarray):
+    """Q8Head::from_bf16 (q8head.rs:18-32) -> (q int8 [rows, cols], scale f32 [rows])."""
+    w = np.ascontiguousarray(w, np.uint16)
+    rows, cols = w.shape
+    q = np.zeros((rows, cols), np.int8)
+    s = np.zeros(rows, np.float32)
+    lib().or_q8head_from_bf16(_p(w), rows, cols, _p(q), _p(s))
+    return q, s
+
+
+def _q8_gemv(fn, q, s, x):
+    q = np.ascontiguousarray(q, np.int8)
+    s = np.ascontiguousarray(s, np.float32)
+    x = np.ascontiguousarray(x, np.float32)
+    rows, cols = q.shape
+    out = np.zeros(rows, np.float32)
+    fn(_p(q), _p(s), rows, cols, _p(x), _p(out))
+    return out
+
+
+def q8head_gemv_ref(q, s, x) -> np.ndarray:
+    """Q8Head::gemv (q8head.rs:35-57) in the reference's order."""
+    return _q8_gemv(lib().or_q8head_gemv_ref, q, s, x)
+
+
+def q8head_gemv_lanes(q, s, x) -> np.ndarray:
+    """The device int8 head's order (lane chunks, fused multiply-adds, butterfly)."""
+    return _q8_gemv(lib().or_q8head_gemv_lanes, q, s, x)
+
+
 def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
     x = np.ascontiguousarray(x, np.float32)
     w = np.ascontiguousarray(w, np.float32)
@@ -318,6 +353,10 @@ class OracleModel:
 
     def reset(self):
         lib().or_model_reset(self.h)
+
+    def set_head(self, kind: int):
+        if lib().or_model_set_head(self.h, kind) != 0:
+            raise ValueError("head kind must be 0 (bf16) or 1 (int8)")
 
     def __len__(self):
         return lib().or_model_len(self.h)

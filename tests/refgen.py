@@ -32,6 +32,25 @@ class XorShift:
         return np.float32(np.float32(v * np.float32(2.0)) - np.float32(1.0))
 
 
+def xorshift_f32(rng: XorShift, n: int) -> np.ndarray:
+    """n successive XorShift.f() values (vectorized float conversion)."""
+    s, out = rng.s, np.empty(n, np.uint64)
+    for i in range(n):
+        s ^= (s << 13) & M64
+        s ^= s >> 7
+        s ^= (s << 17) & M64
+        out[i] = s >> 11
+    rng.s = s
+    v = out.astype(np.float64).astype(np.float32) / F2_53
+    return (v * np.float32(2.0)).astype(np.float32) - np.float32(1.0)
+
+
+def q8_bf16_matrix(rng: XorShift, n: int, amp: float) -> np.ndarray:
+    """bf16_matrix of q8head.rs:76-78: the bf16 bits of rnd() * amp by truncation."""
+    v = (xorshift_f32(rng, n) * np.float32(amp)).astype(np.float32)
+    return (v.view(np.uint32) >> 16).astype(np.uint16)
+
+
 class XorShiftStar:
     """gpu_matches_scalar.rs:6-20."""
 
