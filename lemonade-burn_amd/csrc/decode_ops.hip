@@ -167,7 +167,7 @@ __global__ __launch_bounds__(kThreads) void lmhead_kernel(const uint16_t* W, int
                                                           const float* norm_w, float eps, float* logits,
                                                           unsigned long long* key) {
     extern __shared__ __align__(16) float xs[];  // cols
-    __shared__ float red[kRedFloats];
+    __shared__ __align__(16) float red[kRedFloats];
     const int t = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
     const float* xr = x + (size_t)t * cols;
     if (cols <= 16 * kThreads) {
@@ -319,7 +319,7 @@ __global__ __launch_bounds__(kThreads) void lmhead_kernel(const uint16_t* W, int
 // arithmetic, written out once for the batched head below).
 __global__ __launch_bounds__(kThreads) void row_norm_kernel(const float* x, int cols, const float* norm_w, float eps,
                                                             float* xn) {
-    __shared__ float red[kRedFloats];
+    __shared__ __align__(16) float red[kRedFloats];
     const int t = blockIdx.x, tid = threadIdx.x;
     const float* xr = x + (size_t)t * cols;
     float* dst = xn + (size_t)t * cols;
@@ -344,7 +344,7 @@ __global__ __launch_bounds__(kThreads) void row_norm_kernel(const float* x, int 
 // IEEE f32 division of the reference.
 __global__ __launch_bounds__(kThreads) void q8_quantize_kernel(const uint16_t* w, int rows, int cols, int8_t* q,
                                                                float* scale) {
-    __shared__ float red[kRedFloats];
+    __shared__ __align__(16) float red[kRedFloats];
     for (int r = blockIdx.x; r < rows; r += gridDim.x) {
         const uint16_t* wr = w + (size_t)r * cols;
         float am = 0.0f;
@@ -371,7 +371,7 @@ __global__ __launch_bounds__(kThreads) void q8head_kernel(const int8_t* Q, const
                                                           const float* x, const float* norm_w, float eps,
                                                           float* logits, unsigned long long* key) {
     extern __shared__ __align__(16) float xs[];  // cols
-    __shared__ float red[kRedFloats];
+    __shared__ __align__(16) float red[kRedFloats];
     const int t = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
     const float* xr = x + (size_t)t * cols;
     auto prologue = [&]() {

@@ -235,7 +235,7 @@ __device__ __forceinline__ GemvArgs make_args(const PersistArgs& a, int layer, i
 template <int LK>
 __global__ __launch_bounds__(kPT) void decode_persistent_kernel(PersistArgs a) {
     extern __shared__ __align__(16) int8_t dyn[];  // [weight tiles: wbytes][activation image / scores]
-    __shared__ float red[kRedFloats];
+    __shared__ __align__(16) float red[kRedFloats];
     __shared__ float sa_s;
     __shared__ int qs_s;
     __shared__ AttnShared<LK> ash;

@@ -17,7 +17,7 @@ namespace lbt {
 constexpr int kBlock = 128;      // weights per LB2 block (pack.rs:18)
 constexpr int kBlockBytes = 32;  // bytes per LB2 block (pack.rs:19)
 constexpr int kThreads = 256;    // threads per workgroup of most kernels
-constexpr int kRedFloats = 48;   // LDS floats of a row prologue's reductions
+constexpr int kRedFloats = 48;   // LDS floats of a row prologue's reductions (16-byte aligned)
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));

@@ -180,10 +180,13 @@ __device__ __forceinline__ float act_scale(Src x, int cols, const float* norm_w,
 // four bytes per store (pos keeps each 4-aligned group contiguous); zeros
 // fill [cols, kp).  s_a and sum(q) go to *sa / *qs (written by thread 0).
 // Requires kp <= NT * EPT.  Work is done by the first NT threads; every
-// thread must call it (shared barriers).  `red` holds kRedFloats floats:
-// [0, 16) sum of squares, [16, 32) max, [32, 48) integer sum, each in use
-// until two more barriers have passed (successive calls are safe).
-template <int EPT, int NT = kThreads, int NORM = -1, typename Pos>
+// thread must call it (shared barriers).  `red` holds kRedFloats floats
+// (16-byte aligned): [0, 16) sum of squares, [16, 32) max, [32, 48) integer
+// sum, each in use until two more barriers have passed (successive calls are
+// safe).  DEFER_QS: sum(q) is not reduced;
+// wavefront w's partial is left at ((int*)(red + 32))[w] for the caller to
+// add up after its next barrier (integer sum: any order), and *qs is unused.
+template <int EPT, int NT = kThreads, int NORM = -1, bool DEFER_QS = false, typename Pos>
 __device__ __forceinline__ void quantize_row_regs(RowRegs<EPT>& r, int cols, int kp, const float* norm_w, float eps,
                                                   int8_t* dst, Pos pos, float* sa, int* qs, float* red) {
     const int tid = (int)threadIdx.x;
@@ -207,6 +210,12 @@ __device__ __forceinline__ void quantize_row_regs(RowRegs<EPT>& r, int cols, int
         }
     }
     LBT_QTR(7)
+    if constexpr (DEFER_QS) {
+        s = wave_sum_i(s);
+        if ((tid & 63) == 0 && act) ((int*)(red + 32))[tid >> 6] = s;
+        if (tid == 0) *sa = scale;
+        return;
+    }
     s = block_sum_i_n<NT>(s, (int*)(red + 32));
     LBT_QTR(8)
     if (tid == 0) {

@@ -125,7 +125,7 @@ template <int L, int T, int NCH, int TILES, int IN, int OUT>
 __global__ __launch_bounds__(kThreads) void tgemv_kernel(GemvArgs a) {
     constexpr int R = 64 / L;
     extern __shared__ __align__(16) int8_t xq[];  // T * kp, permuted
-    __shared__ float red[kRedFloats];
+    __shared__ __align__(16) float red[kRedFloats];
     __shared__ float sa[T];
     __shared__ int qs[T];
     __shared__ int part[TILES][4][R][T];
@@ -254,7 +254,7 @@ __global__ __launch_bounds__(kThreads) void tgemv_kernel(GemvArgs a) {
 __global__ __launch_bounds__(kThreads) void quantize_kernel(const float* x, const float* norm_w, float eps,
                                                             int k, int kp, int8_t* q, float* scale,
                                                             int32_t* sum) {
-    __shared__ float red[kRedFloats];
+    __shared__ __align__(16) float red[kRedFloats];
     const int row = blockIdx.x;
     quantize_row_block<32>(SrcF32{x + (size_t)row * k}, k, kp, norm_w, eps, q + (size_t)row * kp, [](int i) { return i; },
                            &scale[row], &sum[row], red);
@@ -420,7 +420,7 @@ __global__ __launch_bounds__(kThreads) void attn_quantize_kernel(const float* o,
                                                                  RowPos rp, const float* norm_w, float eps, int kp,
                                                                  int8_t* q, float* scale, int32_t* sum) {
     __shared__ AttnTab tab;
-    __shared__ float red[kRedFloats];
+    __shared__ __align__(16) float red[kRedFloats];
     const int t = blockIdx.x, H = nh * hd;
     AttnRow a{o + (size_t)t * kAttnSplits * H, ml + (size_t)t * kAttnSplits * nh * 2, 0, nh, hd, H};
     RowRegs<EPT> r;

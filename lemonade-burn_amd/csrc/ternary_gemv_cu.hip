@@ -24,16 +24,15 @@
 namespace lbt {
 
 constexpr int kCuThreads = 1024;
-constexpr int kCuEPT = 8;       // row elements per thread: rows up to 8192
+constexpr int kCuEPT = 8;       // row elements per thread: rows up to 8192 (4: rows up to 4096)
 constexpr int kCuMaxRows = 64;  // rows per workgroup (16 wavefronts x 64 / L, L >= 16)
 
-template <int L, int CPL, int IN, int OUT>
+template <int L, int CPL, int IN, int OUT, int EPT>
 __global__ __launch_bounds__(kCuThreads) void tgemv_cu_kernel(GemvArgs a, int rpw) {
     constexpr int RPWV = 64 / L;  // rows per wavefront
-    __shared__ __align__(16) int8_t xq[kCuEPT * kCuThreads];
-    __shared__ float red[kRedFloats];
+    __shared__ __align__(16) int8_t xq[EPT * kCuThreads];
+    __shared__ __align__(16) float red[kRedFloats];
     __shared__ float sa_s;
-    __shared__ int qs_s;
     __shared__ int dots[kCuMaxRows];
     const int tid = (int)threadIdx.x, w = tid >> 6, lane = tid & 63;
     const int rs = w * RPWV + lane / L, j = lane % L;
@@ -42,14 +41,14 @@ __global__ __launch_bounds__(kCuThreads) void tgemv_cu_kernel(GemvArgs a, int rp
     const bool rvalid = rs < rpw && vr0 + rs < a.total_rows;
 
     // the activation row's loads first
-    RowRegs<kCuEPT> row;
-    AttnRegs<IN == kInAttn ? kCuEPT : 4, IN == kInAttn ? 4 : 1, kCuThreads> arow;
+    RowRegs<EPT> row;
+    AttnRegs<IN == kInAttn ? EPT : 4, IN == kInAttn ? 4 : 1, kCuThreads> arow;
     AttnRow attn{a.att_o, a.att_ml, 0, a.att_nh, a.hd, a.cols};
     const float* norm_w = a.norm_w ? launder(a.norm_w) : nullptr;
     if constexpr (IN == kInAttn)
-        attn_row_issue<kCuEPT, 4, kCuThreads>(attn, norm_w, arow, row);
+        attn_row_issue<EPT, 4, kCuThreads>(attn, norm_w, arow, row);
     else
-        row_load<kCuEPT, kCuThreads>(SrcF32{launder(a.x)}, a.cols, norm_w, row);
+        row_load<EPT, kCuThreads>(SrcF32{launder(a.x)}, a.cols, norm_w, row);
 
     // then every weight load of this workgroup
     uint4 wv[CPL];
@@ -68,11 +67,21 @@ __global__ __launch_bounds__(kCuThreads) void tgemv_cu_kernel(GemvArgs a, int rp
     if constexpr (IN == kInAttn) {
         __shared__ AttnTab tab;
         attn.ns = attn_splits((a.pos_dev ? *a.pos_dev : a.pos0) + 1);
-        attn_row_finish<kCuEPT, 4, kCuThreads>(attn, arow, row, tab);
+        attn_row_finish<EPT, 4, kCuThreads>(attn, arow, row, tab);
     }
-    quantize_row_regs<kCuEPT, kCuThreads>(row, a.cols, a.kp, norm_w, a.eps, xq,
-                                          [C](int i) { return perm_pos(i, C); }, &sa_s, &qs_s, red);
+    quantize_row_regs<EPT, kCuThreads, -1, true>(row, a.cols, a.kp, norm_w, a.eps, xq,
+                                                    [C](int i) { return perm_pos(i, C); }, &sa_s, nullptr, red);
     __syncthreads();
+    // sum(q): the wavefronts' partials left by the quantizer
+    int qsum = 0;
+    {
+        const int4* qp = (const int4*)(red + 32);
+#pragma unroll
+        for (int i = 0; i < kCuThreads / 256; i++) {
+            const int4 v = qp[i];
+            qsum += (v.x + v.y) + (v.z + v.w);
+        }
+    }
 
     // codes . q over this lane's chunks, then the row's lanes
     int acc = 0;
@@ -93,7 +102,7 @@ __global__ __launch_bounds__(kCuThreads) void tgemv_cu_kernel(GemvArgs a, int rp
         }
     }
     acc = xor_sum_down_i<L / 2>(acc);
-    if (j == 0 && rs < rpw) dots[rs] = acc - qs_s;
+    if (j == 0 && rs < rpw) dots[rs] = acc - qsum;
     __syncthreads();
 
     // epilogue, one thread per output (or row pair)
@@ -107,47 +116,45 @@ __global__ __launch_bounds__(kCuThreads) void tgemv_cu_kernel(GemvArgs a, int rp
 
 namespace {
 
-template <int L, int CPL>
+template <int L, int CPL, int EPT>
 hipError_t launch_cu(const GemvArgs& a, int in_mode, int out_mode, int rpw, dim3 grid, hipStream_t s, hipEvent_t e0,
                      hipEvent_t e1) {
+#define LBT_CU_LAUNCH(IN, OUT)                                                                                   \
+    hipExtLaunchKernelGGL((tgemv_cu_kernel<L, CPL, IN, OUT, EPT>), grid, dim3(kCuThreads), 0, s, e0, e1, 0, a, \
+                          rpw)
     if (in_mode == kInAttn) {
-        hipExtLaunchKernelGGL((tgemv_cu_kernel<L, CPL, kInAttn, kOutF32Add>), grid, dim3(kCuThreads), 0, s, e0, e1, 0,
-                              a, rpw);
+        LBT_CU_LAUNCH(kInAttn, kOutF32Add);
         return hipGetLastError();
     }
     switch (out_mode) {
-        case kOutI32:
-            hipExtLaunchKernelGGL((tgemv_cu_kernel<L, CPL, kInF32, kOutI32>), grid, dim3(kCuThreads), 0, s, e0, e1, 0,
-                                  a, rpw);
-            break;
-        case kOutF32:
-            hipExtLaunchKernelGGL((tgemv_cu_kernel<L, CPL, kInF32, kOutF32>), grid, dim3(kCuThreads), 0, s, e0, e1, 0,
-                                  a, rpw);
-            break;
-        case kOutF32Add:
-            hipExtLaunchKernelGGL((tgemv_cu_kernel<L, CPL, kInF32, kOutF32Add>), grid, dim3(kCuThreads), 0, s, e0, e1,
-                                  0, a, rpw);
-            break;
-        case kOutRelu2:
-            hipExtLaunchKernelGGL((tgemv_cu_kernel<L, CPL, kInF32, kOutRelu2>), grid, dim3(kCuThreads), 0, s, e0, e1,
-                                  0, a, rpw);
-            break;
-        default:
-            hipExtLaunchKernelGGL((tgemv_cu_kernel<L, CPL, kInF32, kOutQKV>), grid, dim3(kCuThreads), 0, s, e0, e1, 0,
-                                  a, rpw);
-            break;
+        case kOutI32: LBT_CU_LAUNCH(kInF32, kOutI32); break;
+        case kOutF32: LBT_CU_LAUNCH(kInF32, kOutF32); break;
+        case kOutF32Add: LBT_CU_LAUNCH(kInF32, kOutF32Add); break;
+        case kOutRelu2: LBT_CU_LAUNCH(kInF32, kOutRelu2); break;
+        default: LBT_CU_LAUNCH(kInF32, kOutQKV); break;
     }
+#undef LBT_CU_LAUNCH
     return hipGetLastError();
+}
+
+// Rows of up to 4096 elements take 4 per thread (half the prologue's
+// instructions of the 8-per-thread build; the same float order: element
+// groups beyond the row are skipped either way).
+template <int L, int CPL>
+hipError_t launch_cu_e(const GemvArgs& a, int in_mode, int out_mode, int rpw, dim3 grid, hipStream_t s,
+                       hipEvent_t e0, hipEvent_t e1) {
+    if (a.kp <= 4 * kCuThreads) return launch_cu<L, CPL, 4>(a, in_mode, out_mode, rpw, grid, s, e0, e1);
+    return launch_cu<L, CPL, 8>(a, in_mode, out_mode, rpw, grid, s, e0, e1);
 }
 
 template <int L>
 hipError_t launch_cu_l(const GemvArgs& a, int cpl, int in_mode, int out_mode, int rpw, dim3 grid, hipStream_t s,
                        hipEvent_t e0, hipEvent_t e1) {
     switch (cpl) {
-        case 1: return launch_cu<L, 1>(a, in_mode, out_mode, rpw, grid, s, e0, e1);
-        case 2: return launch_cu<L, 2>(a, in_mode, out_mode, rpw, grid, s, e0, e1);
-        case 4: return launch_cu<L, 4>(a, in_mode, out_mode, rpw, grid, s, e0, e1);
-        default: return launch_cu<L, 8>(a, in_mode, out_mode, rpw, grid, s, e0, e1);
+        case 1: return launch_cu_e<L, 1>(a, in_mode, out_mode, rpw, grid, s, e0, e1);
+        case 2: return launch_cu_e<L, 2>(a, in_mode, out_mode, rpw, grid, s, e0, e1);
+        case 4: return launch_cu_e<L, 4>(a, in_mode, out_mode, rpw, grid, s, e0, e1);
+        default: return launch_cu_e<L, 8>(a, in_mode, out_mode, rpw, grid, s, e0, e1);
     }
 }
 

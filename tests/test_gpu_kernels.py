@@ -191,6 +191,70 @@ def test_rmsnorm_quantize_fused(ctx):
             ctx.check(lib.lbt_dev_free(ctx.h, p))
 
 
+def _rmsnorm_quantize_dev(ctx, x, nw, eps=1e-5):
+    lib = ctx.lib
+    m, k = x.shape
+    kp = orc.padded_cols(k)
+    ptrs = []
+    for nbytes in (x.nbytes, nw.nbytes, m * kp, m * 4, m * 4):
+        p = C.c_void_p()
+        ctx.check(lib.lbt_dev_alloc(ctx.h, nbytes, C.byref(p)))
+        ptrs.append(p)
+    ctx.check(lib.lbt_memcpy_h2d(ctx.h, ptrs[0], x.ctypes.data, x.nbytes))
+    ctx.check(lib.lbt_memcpy_h2d(ctx.h, ptrs[1], nw.ctypes.data, nw.nbytes))
+    ctx.check(lib.lbt_rmsnorm_quantize_dev(ctx.h, ptrs[0], ptrs[1], C.c_float(eps), m, k, ptrs[2], ptrs[3], ptrs[4]))
+    q = np.zeros((m, kp), np.int8)
+    s = np.zeros(m, np.float32)
+    su = np.zeros(m, np.int32)
+    for host, dev in ((q, ptrs[2]), (s, ptrs[3]), (su, ptrs[4])):
+        ctx.check(lib.lbt_memcpy_d2h(ctx.h, host.ctypes.data, dev, host.nbytes))
+    for p in ptrs:
+        ctx.check(lib.lbt_dev_free(ctx.h, p))
+    return q, s, su
+
+
+def absmax_cases():
+    """Rows at the edges of the normed absmax: one clear maximum; equal
+    maxima far apart; near-ties (one ulp) far apart and close together;
+    huge and zero norm weights; tiny, huge, zero and NaN rows."""
+    rng = np.random.default_rng(17)
+    k = 2560
+    base = rng.standard_normal(k).astype(np.float32)
+    nw = rng.uniform(0.5, 1.5, k).astype(np.float32)
+    one = np.ones(k, np.float32)
+    cases = [("random", base, nw), ("ones", np.ones(k, np.float32), one)]
+    x = base.copy(); x[0] = 10.0; x[2000] = 10.0
+    cases.append(("equal maxima, two waves", x, one))
+    x = base.copy(); x[5] = 10.0; x[700] = np.nextafter(np.float32(10.0), np.float32(0.0))
+    cases.append(("near tie, two waves", x, one))
+    x = base.copy(); x[5] = 10.0; x[9] = np.nextafter(np.float32(10.0), np.float32(0.0))
+    cases.append(("near tie, one wave", x, one))
+    x = base.copy(); x[3] = -50.0
+    cases.append(("negative max", x, nw))
+    w = nw.copy(); w[17] = 2.0**21
+    cases.append(("huge norm weight", base, w))
+    cases.append(("tiny 1e-15", (base * np.float32(1e-15)).astype(np.float32), nw))
+    cases.append(("tiny 1e-30", (base * np.float32(1e-30)).astype(np.float32), nw))
+    cases.append(("huge 1e20", (base * np.float32(1e20)).astype(np.float32), nw))
+    cases.append(("zeros", np.zeros(k, np.float32), nw))
+    x = base.copy(); x[100] = np.nan
+    cases.append(("nan", x, nw))
+    w = nw.copy(); w[::7] = 0.0
+    cases.append(("zero norm weights", base, w))
+    return cases
+
+
+@pytest.mark.parametrize("case", range(13))
+def test_rmsnorm_quantize_absmax_edges(ctx, case):
+    name, x, nw = absmax_cases()[case]
+    announce(f"rmsnorm+quant absmax case {name}")
+    x = x[None, :]
+    q, s, su = _rmsnorm_quantize_dev(ctx, x, nw)
+    normed = orc.rmsnorm(x[0], nw, 1e-5)[None, :]
+    eq, es, esu = orc.quantize_acts(normed)
+    assert np.array_equal(q, eq) and s.tobytes() == es.tobytes() and np.array_equal(su, esu)
+
+
 def test_invalid_arguments_return_errors(ctx):
     import lbt_hip
 
