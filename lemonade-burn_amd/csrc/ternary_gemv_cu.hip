@@ -12,9 +12,10 @@
 //   * each row lives inside one wavefront (L = 16, 32 or 64 lanes per row,
 //     lane j takes 16-byte chunks j, j+L, ...), so a row reduces with lane
 //     butterflies only;
-//   * the activation loads go out first, then every weight load of the
-//     workgroup (CPL 16-byte chunks per lane), then the prologue runs while
-//     the weights are in flight;
+//   * the activation loads go out first (unconditional buffer loads), then
+//     every weight load of the workgroup (CPL 16-byte chunks per lane)
+//     without waiting for the row, then the prologue runs while the weights
+//     are in flight;
 //   * epilogues are the shared ones of ternary_common.h.
 #include "lbt_device.h"
 #include "lbt_internal.h"
@@ -33,7 +34,6 @@ __global__ __launch_bounds__(kCuThreads) void tgemv_cu_kernel(GemvArgs a, int rp
     __shared__ __align__(16) int8_t xq[EPT * kCuThreads];
     __shared__ __align__(16) float red[kRedFloats];
     __shared__ float sa_s;
-    __shared__ int dots[kCuMaxRows];
     const int tid = (int)threadIdx.x, w = tid >> 6, lane = tid & 63;
     const int rs = w * RPWV + lane / L, j = lane % L;
     const int C = a.C;
@@ -45,28 +45,41 @@ __global__ __launch_bounds__(kCuThreads) void tgemv_cu_kernel(GemvArgs a, int rp
     AttnRegs<IN == kInAttn ? EPT : 4, IN == kInAttn ? 4 : 1, kCuThreads> arow;
     AttnRow attn{a.att_o, a.att_ml, 0, a.att_nh, a.hd, a.cols};
     const float* norm_w = a.norm_w ? launder(a.norm_w) : nullptr;
+    // the decode position (attention splits): an untracked load issued first,
+    // waited for with the row (below), so no wait on it covers the weights
+    float posf = 0.0f;
+    // (without a device position, a harmless word of the partials is read)
+    if constexpr (IN == kInAttn) posf = ld_f32_async(a.pos_dev ? (const float*)a.pos_dev : a.att_ml);
     if constexpr (IN == kInAttn)
         attn_row_issue<EPT, 4, kCuThreads>(attn, norm_w, arow, row);
     else
-        row_load<EPT, kCuThreads>(SrcF32{launder(a.x)}, a.cols, norm_w, row);
+        row_load_buf<EPT, kCuThreads>(launder(a.x), a.cols, norm_w, row);
 
-    // then every weight load of this workgroup
+    // then every weight load of this workgroup, once every wavefront's row
+    // loads are queued ahead of them (a bare barrier: no wait for the data)
+    __builtin_amdgcn_s_barrier();
     uint4 wv[CPL];
     {
         int mat, r;
         resolve_row<OUT>(a, rvalid ? vr0 + rs : 0, mat, r);
         const uint4* rowp = (const uint4*)(sel3(a.w, mat) + (size_t)r * (size_t)(a.kp >> 2));
+        // unconditional (chunks past the row re-read its last one; rows past
+        // the matrix read row 0), so the compiler's wait for the activation
+        // row counts every weight load as issued; unused chunks are skipped
+        // in the dot loop and unused rows are not stored
 #pragma unroll
         for (int i = 0; i < CPL; i++) {
             const int c = j + L * i;
-            wv[i] = (rvalid && c < C) ? ld_stream(rowp + c) : make_uint4(0, 0, 0, 0);
+            wv[i] = ld_stream(rowp + (c < C ? c : C - 1));
         }
     }
 
     // prologue: (attention combine,) RMSNorm + ActQuant into the permuted LDS image
     if constexpr (IN == kInAttn) {
         __shared__ AttnTab tab;
-        attn.ns = attn_splits((a.pos_dev ? *a.pos_dev : a.pos0) + 1);
+        vm_wait<CPL>();  // all but the weight loads: the position and the row
+        pin(posf);
+        attn.ns = attn_splits((a.pos_dev ? __float_as_int(posf) : a.pos0) + 1);
         attn_row_finish<EPT, 4, kCuThreads>(attn, arow, row, tab);
     }
     quantize_row_regs<EPT, kCuThreads, -1, true>(row, a.cols, a.kp, norm_w, a.eps, xq,
@@ -83,8 +96,12 @@ __global__ __launch_bounds__(kCuThreads) void tgemv_cu_kernel(GemvArgs a, int rp
         }
     }
 
-    // codes . q over this lane's chunks, then the row's lanes
-    int acc = 0;
+    // codes . q over this lane's chunks, one accumulator per 2-bit plane kk.
+    // Planes 0..2 are masked in place, without the shift: their bytes hold
+    // code << 2kk (at most 32, a valid signed byte), so accs[kk] is exactly
+    // 4^kk times the plane's dot and is divided back exactly at the end;
+    // plane 3 would reach 128 and is shifted down first.
+    int accs[4] = {0, 0, 0, 0};
 #pragma unroll
     for (int i = 0; i < CPL; i++) {
         const int c = j + L * i;
@@ -93,24 +110,36 @@ __global__ __launch_bounds__(kCuThreads) void tgemv_cu_kernel(GemvArgs a, int rp
 #pragma unroll
             for (int kk = 0; kk < 4; kk++) {
                 const int4 xv = *(const int4*)(xq + ((kk * C + c) << 4));
-                const int sh = 2 * kk;
-                acc = __builtin_amdgcn_sdot4((int)((d[0] >> sh) & 0x03030303u), xv.x, acc, false);
-                acc = __builtin_amdgcn_sdot4((int)((d[1] >> sh) & 0x03030303u), xv.y, acc, false);
-                acc = __builtin_amdgcn_sdot4((int)((d[2] >> sh) & 0x03030303u), xv.z, acc, false);
-                acc = __builtin_amdgcn_sdot4((int)((d[3] >> sh) & 0x03030303u), xv.w, acc, false);
+                const uint32_t m = 0x03030303u << (2 * kk);
+                int& acc = accs[kk];
+                if (kk < 3) {
+                    acc = __builtin_amdgcn_sdot4((int)(d[0] & m), xv.x, acc, false);
+                    acc = __builtin_amdgcn_sdot4((int)(d[1] & m), xv.y, acc, false);
+                    acc = __builtin_amdgcn_sdot4((int)(d[2] & m), xv.z, acc, false);
+                    acc = __builtin_amdgcn_sdot4((int)(d[3] & m), xv.w, acc, false);
+                } else {
+                    acc = __builtin_amdgcn_sdot4((int)((d[0] >> 6) & 0x03030303u), xv.x, acc, false);
+                    acc = __builtin_amdgcn_sdot4((int)((d[1] >> 6) & 0x03030303u), xv.y, acc, false);
+                    acc = __builtin_amdgcn_sdot4((int)((d[2] >> 6) & 0x03030303u), xv.z, acc, false);
+                    acc = __builtin_amdgcn_sdot4((int)((d[3] >> 6) & 0x03030303u), xv.w, acc, false);
+                }
             }
         }
     }
-    acc = xor_sum_down_i<L / 2>(acc);
-    if (j == 0 && rs < rpw) dots[rs] = acc - qsum;
-    __syncthreads();
+    int acc = (accs[0] + (accs[1] >> 2)) + ((accs[2] >> 4) + accs[3]);
+    acc = xor_sum_down_i<L / 2>(acc);  // every lane of the row holds its sum
+    const int dot = acc - qsum;
 
-    // epilogue, one thread per output (or row pair)
+    // epilogue by the row's first lane, no LDS pass: a row pair (2p, 2p + 1)
+    // lies in one wavefront (L <= 32 for the paired outputs), the odd row's
+    // dot L lanes up
+    const bool out_row = j == 0 && rs < rpw && vr0 + rs < a.total_rows;
     if constexpr (OUT == kOutRelu2 || OUT == kOutQKV) {
-        if (tid < rpw / 2 && vr0 + 2 * tid < a.total_rows)
-            store_pair<OUT>(a, 0, vr0 + 2 * tid, dots[2 * tid], dots[2 * tid + 1], sa_s);
+        static_assert(L <= 32, "row pairs within a wavefront");
+        const int d1 = __shfl_down(dot, L);
+        if (out_row && (rs & 1) == 0) store_pair<OUT>(a, 0, vr0 + rs, dot, d1, sa_s);
     } else {
-        if (tid < rpw && vr0 + tid < a.total_rows) store_single<OUT>(a, 0, vr0 + tid, dots[tid], sa_s);
+        if (out_row) store_single<OUT>(a, 0, vr0 + rs, dot, sa_s);
     }
 }
 
@@ -130,8 +159,14 @@ hipError_t launch_cu(const GemvArgs& a, int in_mode, int out_mode, int rpw, dim3
         case kOutI32: LBT_CU_LAUNCH(kInF32, kOutI32); break;
         case kOutF32: LBT_CU_LAUNCH(kInF32, kOutF32); break;
         case kOutF32Add: LBT_CU_LAUNCH(kInF32, kOutF32Add); break;
-        case kOutRelu2: LBT_CU_LAUNCH(kInF32, kOutRelu2); break;
-        default: LBT_CU_LAUNCH(kInF32, kOutQKV); break;
+        default:
+            if constexpr (L <= 32) {  // the host picks L <= 32 for the paired outputs
+                if (out_mode == kOutRelu2) LBT_CU_LAUNCH(kInF32, kOutRelu2);
+                else LBT_CU_LAUNCH(kInF32, kOutQKV);
+            } else {
+                return hipErrorInvalidValue;
+            }
+            break;
     }
 #undef LBT_CU_LAUNCH
     return hipGetLastError();
@@ -166,11 +201,17 @@ int launch_ternary_gemv_cu(lbt_ctx* ctx, const TernaryOp& op) {
     int rc = make_gemv_args(ctx, op, a);
     if (rc) return rc;
     if (a.kp > kCuEPT * kCuThreads) return 1;
+    // the f32 row is read with bounded 16-byte buffer loads (branch-free, so
+    // the weight loads behind them are issued before the row has arrived)
+    if (op.in_mode == kInF32 &&
+        (op.cols % 4 || ((uintptr_t)op.x & 15) || ((uintptr_t)op.norm_w & 15)))
+        return 1;
     const int total = a.total_rows;
     int rpw = (total + ctx->cus - 1) / ctx->cus;
     rpw = (rpw + 1) & ~1;  // row pairs never straddle workgroups
     if (rpw > kCuMaxRows) rpw = kCuMaxRows;
-    const int L = rpw <= 16 ? 64 : (rpw <= 32 ? 32 : 16);
+    const bool paired = op.in_mode != kInAttn && (op.out_mode == kOutRelu2 || op.out_mode == kOutQKV);
+    const int L = rpw <= 16 && !paired ? 64 : (rpw <= 32 ? 32 : 16);
     const int need = (a.C + L - 1) / L;
     if (need > 8) return 1;
     const int cpl = need <= 1 ? 1 : (need <= 2 ? 2 : (need <= 4 ? 4 : 8));
