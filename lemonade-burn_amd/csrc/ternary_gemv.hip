@@ -260,6 +260,22 @@ __global__ __launch_bounds__(kThreads) void quantize_kernel(const float* x, cons
                            &scale[row], &sum[row], red);
 }
 
+// The same quantizer for 16-byte aligned rows with k % 4 == 0, on 1024
+// threads with EPT (4 or 8) elements each: short dependent chains per thread
+// (the same float order: the norm's virtual-thread layout does not depend on
+// the thread count) and branch-free buffer loads of the row.
+template <int EPT>
+__global__ __launch_bounds__(1024) void quantize_wide_kernel(const float* x, const float* norm_w, float eps, int k,
+                                                            int kp, int8_t* q, float* scale, int32_t* sum) {
+    __shared__ __align__(16) float red[kRedFloats];
+    const int row = blockIdx.x;
+    RowRegs<EPT> r;
+    const float* nw = norm_w ? launder(norm_w) : nullptr;
+    row_load_buf<EPT, 1024>(x + (size_t)row * k, k, nw, r);
+    quantize_row_regs<EPT, 1024>(r, k, kp, nw, eps, q + (size_t)row * kp, [](int i) { return i; }, &scale[row],
+                                 &sum[row], red);
+}
+
 namespace {
 
 constexpr int kL = 8;
@@ -404,8 +420,16 @@ int launch_quantize(lbt_ctx* ctx, const float* x, const float* norm_w, float eps
                     float* scale, int32_t* sum) {
     if (m <= 0) return LBT_OK;
     const int kp = (int)padded_cols((size_t)k);
-    hipLaunchKernelGGL(quantize_kernel, dim3(m), dim3(kThreads), 0, ctx->stream, x, norm_w, eps, k, kp, q, scale,
-                       sum);
+    const bool wide = k % 4 == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)norm_w & 15) == 0 && kp <= 8 * 1024;
+    if (wide && kp <= 4 * 1024)
+        hipLaunchKernelGGL(quantize_wide_kernel<4>, dim3(m), dim3(1024), 0, ctx->stream, x, norm_w, eps, k, kp, q,
+                           scale, sum);
+    else if (wide)
+        hipLaunchKernelGGL(quantize_wide_kernel<8>, dim3(m), dim3(1024), 0, ctx->stream, x, norm_w, eps, k, kp, q,
+                           scale, sum);
+    else
+        hipLaunchKernelGGL(quantize_kernel, dim3(m), dim3(kThreads), 0, ctx->stream, x, norm_w, eps, k, kp, q, scale,
+                           sum);
     LBT_HIP(ctx, hipGetLastError());
     return LBT_OK;
 }
@@ -416,7 +440,7 @@ int launch_quantize(lbt_ctx* ctx, const float* x, const float* norm_w, float eps
 // of attn_combine_kernel and the quantizer of quantize_kernel on the same
 // element layout, so the same q, s_a and sum(q).
 template <int EPT>
-__global__ __launch_bounds__(kThreads) void attn_quantize_kernel(const float* o, const float* ml, int nh, int hd,
+__global__ __launch_bounds__(1024) void attn_quantize_kernel(const float* o, const float* ml, int nh, int hd,
                                                                  RowPos rp, const float* norm_w, float eps, int kp,
                                                                  int8_t* q, float* scale, int32_t* sum) {
     __shared__ AttnTab tab;
@@ -424,21 +448,22 @@ __global__ __launch_bounds__(kThreads) void attn_quantize_kernel(const float* o,
     const int t = blockIdx.x, H = nh * hd;
     AttnRow a{o + (size_t)t * kAttnSplits * H, ml + (size_t)t * kAttnSplits * nh * 2, 0, nh, hd, H};
     RowRegs<EPT> r;
-    AttnRegs<EPT, 4> ar;
+    AttnRegs<EPT, 4, 1024> ar;
     const float* nw = norm_w ? launder(norm_w) : nullptr;
-    attn_row_issue(a, nw, ar, r);
+    attn_row_issue<EPT, 4, 1024>(a, nw, ar, r);
     a.ns = attn_splits(row_position(rp, t) + 1);
-    attn_row_finish(a, ar, r, tab);
-    quantize_row_regs<EPT>(r, H, kp, nw, eps, q + (size_t)t * kp, [](int i) { return i; }, &scale[t], &sum[t], red);
+    attn_row_finish<EPT, 4, 1024>(a, ar, r, tab);
+    quantize_row_regs<EPT, 1024>(r, H, kp, nw, eps, q + (size_t)t * kp, [](int i) { return i; }, &scale[t], &sum[t],
+                                 red);
 }
 
 int launch_attn_quantize(lbt_ctx* ctx, const float* o, const float* ml, int m, int nh, int hd, const RowPos& rp,
                          const float* norm_w, float eps, int kp, int8_t* q, float* scale, int32_t* sum) {
     const int H = nh * hd;
-    if (nh <= 0 || nh > kAttnMaxHeads || hd % 4 || H > 16 * kThreads || kp < H || kp > 16 * kThreads)
+    if (nh <= 0 || nh > kAttnMaxHeads || hd % 4 || H > 4 * 1024 || kp < H || kp > 4 * 1024)
         return set_err(ctx, LBT_E_INVALID, "attention quantize: at most 64 heads and 4096 columns");
-    hipLaunchKernelGGL(attn_quantize_kernel<16>, dim3(m), dim3(kThreads), 0, ctx->stream, o, ml, nh, hd, rp, norm_w,
-                       eps, kp, q, scale, sum);
+    hipLaunchKernelGGL(attn_quantize_kernel<4>, dim3(m), dim3(1024), 0, ctx->stream, o, ml, nh, hd, rp, norm_w, eps,
+                       kp, q, scale, sum);
     LBT_HIP(ctx, hipGetLastError());
     return LBT_OK;
 }
