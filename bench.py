@@ -223,6 +223,7 @@ def main() -> int:
     ap.add_argument("--prof-steps", type=int, default=32)
     ap.add_argument("--pmc-pass", action="store_true", help="the workload profiled for the HBM counters")
     ap.add_argument("--no-batched", action="store_true", help="skip the batched-decode (config 5) figures")
+    ap.add_argument("--no-int8-head", action="store_true", help="skip the opt-in int8 LM head figure")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the config-3 prefill GEMM sweep (the workload profiled for the MFMA counters)")
     args = ap.parse_args()
@@ -314,7 +315,8 @@ def main() -> int:
         "wall_tok_s": round(args.steps / wall, 2),
         "tokens_head": [int(t) for t in out[:8]],
     }
-    line["int8_head_decode"] = int8_head_decode(model, ctx, prompt)
+    if not args.no_int8_head:
+        line["int8_head_decode"] = int8_head_decode(model, ctx, prompt)
     if not args.no_batched:
         line["batched_decode"] = [batched_decode(model, cfg, bsz) for bsz in (16, 64)]
         line["prefill_gemm"] = prefill_gemm(ctx)
