@@ -68,42 +68,81 @@ __host__ __device__ __forceinline__ int attn_splits(int vis) {
 // together.  The first 256 threads do the work; every thread of the
 // workgroup must call it (shared barriers).  Splits past the last return at
 // once.
-template <int LK, int KU>
+//
+// PDEV: the position is *pdev + p, read on the device.  The first K/V rows
+// are then issued before it arrives, on the guess that the split holds
+// kAttnMinKeys keys (every context up to kAttnSplits * kAttnMinKeys keys):
+// rows s * kAttnMinKeys + k, clamped to the cache; if the position says
+// otherwise the split is redone with the loads it needs (attention_split).
+template <int LK>
+__device__ __forceinline__ void attention_split(const float* q, int h, int nh, int s, int p, const uint16_t* K0,
+                                                const uint16_t* V0, float scaling, float* o, float* ml, float* sc,
+                                                AttnShared<LK>& sh);
+
+template <int LK, int KU, bool PDEV = false>
 __device__ __forceinline__ void attention_split_ku(const float* q, int h, int nh, int s, int p, const uint16_t* K0,
                                                    const uint16_t* V0, float scaling, float* o, float* ml, float* sc,
-                                                   AttnShared<LK>& sh) {
+                                                   AttnShared<LK>& sh, const int* pdev = nullptr, int cap = 0) {
     constexpr int HD = LK * 8, GW = 64 / LK, NK = kThreads / LK;
-    const int vis = p + 1;
-    const int ks = attn_split_keys(vis);
-    const int ns = (vis + ks - 1) / ks;
-    if (s >= ns) return;
-    const int j0 = s * ks, cnt = vis - j0 < ks ? vis - j0 : ks;
+    static_assert(!PDEV || KU * NK >= kAttnMinKeys, "one key pass covers a guessed split");
     const int tid = (int)threadIdx.x, w = tid >> 6, lane = tid & 63;
     const bool act = tid < kThreads;
-    const uint16_t* K = K0 + (size_t)j0 * HD;
-    const uint16_t* V = V0 + (size_t)j0 * HD;
     const int kslot = lane / LK, cc = lane % LK;  // score loop: key of this lane group, chunk
     const int grp = tid / LK, c = tid % LK;       // PV loop: key group, chunk
-    // q, then the first batches of K and V rows, all in flight together
-    const float qv = (act && tid < HD) ? q[(size_t)h * HD + tid] : 0.0f;
+    // this lane's 8 q values (read directly: the 16 lane groups share the
+    // row through the cache, no LDS pass), then the first batches of K and V
+    // rows, all in flight together; the K/V loads are unconditional (rows
+    // past the split re-read its last row and are masked out below), so the
+    // compiler's waits count exactly
+    const f32x4 qa = gload((const f32x4*)(q + (size_t)h * HD + 8 * cc));
+    const f32x4 qb = gload((const f32x4*)(q + (size_t)h * HD + 8 * cc + 4));
     uint4 kb[KU], vb[KU];
+    int vis, ks, ns, j0, cnt;
+    auto split_of = [&]() {
+        vis = p + 1;
+        ks = attn_split_keys(vis);
+        ns = (vis + ks - 1) / ks;
+        j0 = s * ks;
+        cnt = vis - j0 < ks ? vis - j0 : ks;
+    };
+    if constexpr (PDEV) {
+        const int g0 = s * kAttnMinKeys;
 #pragma unroll
-    for (int u = 0; u < KU; u++) {
-        const int k = u * NK + w * GW + kslot;
-        kb[u] = (act && k < cnt) ? *(const uint4*)(K + (size_t)k * HD + 8 * cc) : make_uint4(0, 0, 0, 0);
-    }
+        for (int u = 0; u < KU; u++) {
+            const int k = g0 + u * NK + w * GW + kslot;
+            kb[u] = *(const uint4*)(K0 + (size_t)(k < cap ? k : cap - 1) * HD + 8 * cc);
+        }
 #pragma unroll
-    for (int u = 0; u < KU; u++) {
-        const int k = grp + u * NK;
-        vb[u] = (act && k < cnt) ? *(const uint4*)(V + (size_t)k * HD + 8 * c) : make_uint4(0, 0, 0, 0);
+        for (int u = 0; u < KU; u++) {
+            const int k = g0 + grp + u * NK;
+            vb[u] = *(const uint4*)(V0 + (size_t)(k < cap ? k : cap - 1) * HD + 8 * c);
+        }
+        p += gload(pdev);
+        split_of();
+        if (s >= ns) return;
+        if (ks != kAttnMinKeys) {
+            attention_split<LK>(q, h, nh, s, p, K0, V0, scaling, o, ml, sc, sh);
+            return;
+        }
+    } else {
+        split_of();
+        if (s >= ns) return;
+#pragma unroll
+        for (int u = 0; u < KU; u++) {
+            const int k = u * NK + w * GW + kslot;
+            kb[u] = *(const uint4*)(K0 + ((size_t)j0 + (k < cnt ? k : cnt - 1)) * HD + 8 * cc);
+        }
+#pragma unroll
+        for (int u = 0; u < KU; u++) {
+            const int k = grp + u * NK;
+            vb[u] = *(const uint4*)(V0 + ((size_t)j0 + (k < cnt ? k : cnt - 1)) * HD + 8 * c);
+        }
     }
+    const uint16_t* K = K0 + (size_t)j0 * HD;
+    const uint16_t* V = V0 + (size_t)j0 * HD;
     LBT_ATR(1)
-    if (act && tid < HD) sh.qs[tid] = qv;
-    __syncthreads();
     LBT_ATR(2)
-    float q8[8];
-#pragma unroll
-    for (int e = 0; e < 8; e++) q8[e] = sh.qs[8 * cc + e];
+    const float q8[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
 
     // ---- scores and the split max
     float mx = -__builtin_inff();

@@ -67,8 +67,15 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(const float* q, int
     const int h = blockIdx.x / kAttnSplits, s = blockIdx.x % kAttnSplits, t = blockIdx.y;
     const int H = nh * LK * 8, g = h / (nh / kvh);
     const size_t kvoff = row_cache_offset(rp, t) + (size_t)g * cap * LK * 8;
-    attention_split<LK>(q + (size_t)t * H, h, nh, s, row_position(rp, t), kc + kvoff, vc + kvoff, scaling,
-                        o + (size_t)t * kAttnSplits * H, ml + (size_t)t * kAttnSplits * nh * 2, sc, sh);
+    float* ot = o + (size_t)t * kAttnSplits * H;
+    float* mlt = ml + (size_t)t * kAttnSplits * nh * 2;
+    constexpr bool kGuess = 4 * (kThreads / LK) >= kAttnMinKeys;  // one key pass covers a guessed split
+    if (kGuess && (rp.tok_pos || rp.pos_dev))  // the position is read after the first K/V loads
+        attention_split_ku<LK, 4, kGuess>(q + (size_t)t * H, h, nh, s, rp.tok_pos ? 0 : t, kc + kvoff, vc + kvoff,
+                                        scaling, ot, mlt, sc, sh, rp.tok_pos ? rp.tok_pos + t : rp.pos_dev, cap);
+    else
+        attention_split<LK>(q + (size_t)t * H, h, nh, s, rp.pos0 + t, kc + kvoff, vc + kvoff, scaling, ot, mlt, sc,
+                            sh);
     LBT_ATR(7)
 }
 

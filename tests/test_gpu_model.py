@@ -76,6 +76,32 @@ def test_generate_greedy_matches_oracle(ctx):
     om.free()
 
 
+def test_decode_across_split_size_change(ctx):
+    """Graph decode steps read the position on the device and issue the first
+    K/V rows on the guess of 64-key splits (contexts up to 1024 keys); steps
+    at 1021..1030 visible keys cross to 65-key splits (the guess is dropped and
+    the split reloaded).  Logits bit-exact to the oracle on both sides."""
+    hip_cfg, or_cfg = cfgs(max_pos=2048, layers=1)
+    announce("decode across 1024 visible keys")
+    m = lbt_hip.Model.synthetic(ctx, hip_cfg, 13)
+    om = orc.OracleModel(or_cfg, 13)
+    prompt = (np.arange(1020, dtype=np.uint32) * 7919) % or_cfg.vocab
+    cache = m.new_cache()
+    first = m.forward_argmax(prompt, cache)
+    e = om.forward(prompt)
+    assert first == int(e[0].argmax())
+    toks, _ = m.decode_greedy(cache, first, 10)
+    t = first
+    for i in range(10):
+        t = int(om.forward([t])[0].argmax())
+        assert toks[i] == t, f"step {i}"
+    # the residual stream of the last step (attention output included)
+    assert np.array_equal(m.read_hidden(1), om.hidden(1))
+    cache.free()
+    m.free()
+    om.free()
+
+
 def test_cache_growth_keeps_contents(ctx):
     # ensure_cap doubling (model.rs:238-265): 300 positions cross the 256 boundary
     hip_cfg, or_cfg = cfgs(layers=1)
