@@ -576,7 +576,9 @@ int forward_dev(lbt_model* m, lbt_cache* cc, const uint32_t* toks_dev, int n, bo
     rp.pos0 = cc->len;
     rp.pos_dev = state;
     rp.vis_max = state ? cc->cap : cc->len + n;
-    const int rc = forward_rows(m, kv, rp, toks_dev, n, all_logits, want_logits, tok_out_dev, state, false);
+    // several rows (prefill): the KV-head-grouped attention, every K/V row
+    // loaded once for the query heads that share it
+    const int rc = forward_rows(m, kv, rp, toks_dev, n, all_logits, want_logits, tok_out_dev, state, n > 1);
     if (!rc) cc->len += n;
     return rc;
 }
