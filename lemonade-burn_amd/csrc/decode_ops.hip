@@ -23,6 +23,8 @@ extern "C" int lbt_debug_attn_trace(unsigned long long* out) {
 #include "lbt_internal.h"
 #include "attn_common.h"
 
+#include <stdlib.h>
+
 namespace lbt {
 
 // ---------------------------------------------------------------------------
@@ -81,10 +83,12 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(const float* q, int
 
 // The same splits with one workgroup per (KV head, key split, query row)
 // taking all GH query heads of the KV head.  Grid (kvh * kAttnSplits, m).
+// wide: eight key passes in flight per split of more than 64 keys (grids of
+// many workgroups, where occupancy is not the limit); same partials.
 template <int LK, int GH>
 __global__ __launch_bounds__(kThreads) void attention_group_kernel(const float* q, int nh, int kvh, RowPos rp,
                                                                    const uint16_t* kc, const uint16_t* vc, int cap,
-                                                                   float scaling, float* o, float* ml) {
+                                                                   float scaling, float* o, float* ml, int wide) {
     extern __shared__ float sc[];  // [GH][attn_split_keys(visible keys)]
     __shared__ AttnGroupShared<LK, GH> sh;
     const int g = blockIdx.x / kAttnSplits, s = blockIdx.x % kAttnSplits, t = blockIdx.y;
@@ -95,8 +99,12 @@ __global__ __launch_bounds__(kThreads) void attention_group_kernel(const float* 
         attention_split_group<LK, GH, 2>(q + (size_t)t * H, g, nh, s, p, kc + kvoff, vc + kvoff, scaling,
                                          o + (size_t)t * kAttnSplits * H, ml + (size_t)t * kAttnSplits * nh * 2, sc,
                                          sh);
-    else
+    else if (!wide || attn_split_keys(p + 1) <= 4 * (kThreads / LK))
         attention_split_group<LK, GH, 4>(q + (size_t)t * H, g, nh, s, p, kc + kvoff, vc + kvoff, scaling,
+                                         o + (size_t)t * kAttnSplits * H, ml + (size_t)t * kAttnSplits * nh * 2, sc,
+                                         sh);
+    else
+        attention_split_group<LK, GH, 8>(q + (size_t)t * H, g, nh, s, p, kc + kvoff, vc + kvoff, scaling,
                                          o + (size_t)t * kAttnSplits * H, ml + (size_t)t * kAttnSplits * nh * 2, sc,
                                          sh);
 }
@@ -767,18 +775,19 @@ hipError_t launch_attn_lk(int gh, bool grouped, dim3 grid, size_t lds, hipStream
                               cap, scaling, o, ml);
         return hipGetLastError();
     }
+    const int wide = (long)grid.x * grid.y >= 4096 || getenv("LBT_ATTN_WIDE") ? 1 : 0;
     switch (gh) {
         case 1:
             hipExtLaunchKernelGGL((attention_group_kernel<LK, 1>), grid, dim3(kThreads), lds, st, e0, e1, 0, q, nh,
-                                  kvh, rp, kc, vc, cap, scaling, o, ml);
+                                  kvh, rp, kc, vc, cap, scaling, o, ml, wide);
             break;
         case 2:
             hipExtLaunchKernelGGL((attention_group_kernel<LK, 2>), grid, dim3(kThreads), lds, st, e0, e1, 0, q, nh,
-                                  kvh, rp, kc, vc, cap, scaling, o, ml);
+                                  kvh, rp, kc, vc, cap, scaling, o, ml, wide);
             break;
         default:
             hipExtLaunchKernelGGL((attention_group_kernel<LK, 4>), grid, dim3(kThreads), lds, st, e0, e1, 0, q, nh,
-                                  kvh, rp, kc, vc, cap, scaling, o, ml);
+                                  kvh, rp, kc, vc, cap, scaling, o, ml, wide);
             break;
     }
     return hipGetLastError();

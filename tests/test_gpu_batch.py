@@ -63,6 +63,35 @@ def test_batch_matches_single_sequence_oracle(ctx, shape, nseq):
     m.free()
 
 
+@pytest.mark.parametrize("wide", [False, True])
+def test_batch_long_context_matches_oracle(ctx, monkeypatch, wide):
+    """Prompts of 1100+ tokens (65-key and longer splits: the four- and, with
+    LBT_ATTN_WIDE, eight-pass K/V pipelines of the grouped attention); the
+    batched step's logits bit-exact to single-sequence oracles."""
+    if wide:
+        monkeypatch.setenv("LBT_ATTN_WIDE", "1")
+    hip_cfg, or_cfg = cfgs(max_pos=2048, layers=1)
+    announce(f"batch long context wide={wide}")
+    seed = 41
+    m = lbt_hip.Model.synthetic(ctx, hip_cfg, seed)
+    b = m.new_batch(3, 2048)
+    oms, nxt = [], []
+    for s in range(3):
+        prompt = (np.arange(1100 + 97 * s, dtype=np.uint32) * (31 + s)) % or_cfg.vocab
+        om = orc.OracleModel(or_cfg, seed)
+        exp = int(om.forward(prompt)[0].argmax())
+        assert b.prefill(s, prompt) == exp, f"prefill seq {s}"
+        oms.append(om)
+        nxt.append(exp)
+    logits, _ = b.forward(np.array(nxt, np.uint32))
+    for s in range(3):
+        assert np.array_equal(logits[s], oms[s].forward([nxt[s]])[0]), f"seq {s}"
+    for om in oms:
+        om.free()
+    b.free()
+    m.free()
+
+
 def test_batch_capacity_and_synthetic_fill(ctx):
     hip_cfg, _ = cfgs()
     announce("batch capacity / synthetic fill")
