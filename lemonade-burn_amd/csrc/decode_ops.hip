@@ -551,26 +551,30 @@ __global__ __launch_bounds__(kThreads) void q8head_kernel(const int8_t* Q, const
 // Q8: the int8 head (q8head.rs): W is int8 [rows][cols] with one f32 scale
 // per row (rscale); chunk c is the 8 bytes 8c..8c+7, and each sum is scaled
 // by its row's scale, as in q8head_kernel.
-template <int R, int NCH, int TG, bool Q8>
-__global__ __launch_bounds__(kThreads) void lmhead_batch_kernel(const void* W, const float* rscale, int rows, int cols,
-                                                                const float* xn, int m, int tile_rows, float* logits,
-                                                                unsigned long long* key) {
-    static_assert(R * TG == 32, "32 accumulators per lane");
+template <int R, int NCH, int TG, bool Q8, int NT = kThreads>
+__global__ __launch_bounds__(NT) void lmhead_batch_kernel(const void* W, const float* rscale, int rows, int cols,
+                                                          const float* xn, int m, int tile_rows, float* logits,
+                                                          unsigned long long* key) {
+    constexpr int A = R * TG, NW = NT / 64;
+    static_assert(A == 32 || A == 64, "32 or 64 accumulators per lane");
     extern __shared__ __align__(16) float xs[];  // [TG][cols]
     const int ngroups = (m + TG - 1) / TG;
     const int grp = blockIdx.x % ngroups, tile = blockIdx.x / ngroups;
     const int t0 = grp * TG, nt = m - t0 < TG ? m - t0 : TG;
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
-    for (int i = tid * 4; i < nt * cols; i += kThreads * 4)
+    for (int i = tid * 4; i < nt * cols; i += NT * 4)
         *(float4*)(xs + i) = *(const float4*)(xn + (size_t)t0 * cols + i);
-    for (int i = nt * cols + tid; i < TG * cols; i += kThreads) xs[i] = 0.0f;  // unused token rows
+    for (int i = nt * cols + tid; i < TG * cols; i += NT) xs[i] = 0.0f;  // unused token rows
     __syncthreads();
     const int nchunks = cols >> 3;
     const int r_begin = tile * tile_rows, r_end = r_begin + tile_rows < rows ? r_begin + tile_rows : rows;
     // this lane's (token, row) after the reduction: accumulator (lane >> 1) & 31
-    const int my_t = ((lane >> 1) & 31) / R, my_r = ((lane >> 1) & 31) % R;
-    unsigned long long best = 0ull;  // of token my_t, lanes with (lane & 1) == 0
-    for (int rb = r_begin + w * R; rb < r_end; rb += 4 * R) {
+    // (A = 32, lane pairs hold the same sum) or lane (A = 64)
+    const int my_a = A == 32 ? ((lane >> 1) & 31) : lane;
+    const int my_t = my_a / R, my_r = my_a % R;
+    const bool writer = A == 64 || (lane & 1) == 0;
+    unsigned long long best = 0ull;  // of token my_t
+    for (int rb = r_begin + w * R; rb < r_end; rb += NW * R) {
         // R weight rows of this wavefront, unpacked to f32
         float wf[R][NCH][8];
 #pragma unroll
@@ -602,7 +606,7 @@ __global__ __launch_bounds__(kThreads) void lmhead_batch_kernel(const void* W, c
                 wf[r][i][7] = bf_hi(v.w);
             }
         }
-        float acc[TG * R];
+        float acc[A];
 #pragma unroll
         for (int t = 0; t < TG; t++) {
             const float* xt = xs + t * cols;
@@ -623,32 +627,42 @@ __global__ __launch_bounds__(kThreads) void lmhead_batch_kernel(const void* W, c
                 }
             }
         }
-        float h16[16], h8[8], h4[4], h2[2], h1[1];
-        halve<32>(acc, h16);
-        halve<16>(h16, h8);
-        halve<8>(h8, h4);
-        halve<4>(h4, h2);
-        halve<2>(h2, h1);
-        float a = xor_add<1>(h1[0]);
+        float a;
+        {
+            float h16[16], h8[8], h4[4], h2[2], h1[1];
+            if constexpr (A == 64) {
+                float h32[32];
+                halve<32>(acc, h32);
+                halve<16>(h32, h16);
+            } else {
+                halve<32>(acc, h16);
+            }
+            halve<A == 64 ? 8 : 16>(h16, h8);
+            halve<A == 64 ? 4 : 8>(h8, h4);
+            halve<A == 64 ? 2 : 4>(h4, h2);
+            halve<A == 64 ? 1 : 2>(h2, h1);
+            a = A == 64 ? h1[0] : xor_add<1>(h1[0]);
+        }
         const int row = rb + my_r;
         if (Q8) a = gload(rscale + (row < r_end ? row : r_begin)) * a;
-        if ((lane & 1) == 0 && my_t < nt && row < r_end) {
+        if (writer && my_t < nt && row < r_end) {
             if (logits) logits[(size_t)(t0 + my_t) * rows + row] = a;
             const unsigned long long k = argmax_key(a, (uint32_t)row);
             best = k > best ? k : best;
         }
     }
     // one atomic per (workgroup, token): the lanes' keys meet in the token
-    // rows' LDS once every wavefront is done with them (no static LDS: two
-    // workgroups of 80 KB share a CU only with nothing beside it)
+    // rows' LDS once every wavefront is done with them (no static LDS: the
+    // token rows fill the workgroup's share of the CU's LDS)
+    constexpr int KW = A == 64 ? 64 : 32;  // keys per wavefront
     __syncthreads();
-    unsigned long long* wbest = (unsigned long long*)xs;  // [4 waves][32 lanes / 2]
-    if ((lane & 1) == 0) wbest[w * 32 + (lane >> 1)] = best;
+    unsigned long long* wbest = (unsigned long long*)xs;  // [NW][KW]
+    if (writer) wbest[w * KW + (A == 64 ? lane : (lane >> 1))] = best;
     __syncthreads();
     if (key && tid < nt) {
         unsigned long long b = 0ull;
-        for (int i = 0; i < (kThreads / 64) * 32; i++)
-            if (i % 32 / R == tid) b = wbest[i] > b ? wbest[i] : b;
+        for (int i = 0; i < NW * KW; i++)
+            if (i % KW / R == tid) b = wbest[i] > b ? wbest[i] : b;
         if (b) atomicMax(&key[t0 + tid], b);
     }
 }
@@ -861,32 +875,43 @@ int launch_head(lbt_ctx* ctx, const void* w, const float* rscale, int rows, int 
         // several rows: normalize once, then the weight-reusing head
         hipLaunchKernelGGL(row_norm_kernel, dim3(m), dim3(kThreads), 0, ctx->stream, x, cols, norm_w, eps, xn);
         LBT_HIP(ctx, hipGetLastError());
-        const int ngroups = (m + kTG - 1) / kTG;
-        int tiles = ctx->cus * 4 / ngroups;
+        // more than 8 rows: 16-token groups on 512 threads (the whole LDS of a
+        // CU; each weight row is then read from L2 half as often), else
+        // 8-token groups on 256 threads (two workgroups per CU)
+        const bool big = m > 8 && (size_t)16 * cols * sizeof(float) <= 160 * 1024 && !getenv("LBT_HEAD_TG8");
+        const int tg = big ? 16 : kTG, nt = big ? 512 : kThreads, nw = nt / 64;
+        const int ngroups = (m + tg - 1) / tg;
+        int tiles = ctx->cus * (big ? 2 : 4) / ngroups;
         if (tiles < 1) tiles = 1;
         int tile_rows = (rows + tiles - 1) / tiles;
-        tile_rows = (tile_rows + 4 * kR - 1) / (4 * kR) * (4 * kR);
+        tile_rows = (tile_rows + nw * kR - 1) / (nw * kR) * (nw * kR);
         tiles = (rows + tile_rows - 1) / tile_rows;
-        const size_t lds = (size_t)kTG * cols * sizeof(float);
-        const void* fn = q8 ? (const void*)lmhead_batch_kernel<kR, kLmChunks, kTG, true>
-                            : (const void*)lmhead_batch_kernel<kR, kLmChunks, kTG, false>;
-        static bool attr[2] = {false, false};
-        if (!attr[q8]) {
-            (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024);
+        const size_t lds = (size_t)tg * cols * sizeof(float);
+        const void* fn = big ? (q8 ? (const void*)lmhead_batch_kernel<kR, kLmChunks, 16, true, 512>
+                                   : (const void*)lmhead_batch_kernel<kR, kLmChunks, 16, false, 512>)
+                             : (q8 ? (const void*)lmhead_batch_kernel<kR, kLmChunks, kTG, true>
+                                   : (const void*)lmhead_batch_kernel<kR, kLmChunks, kTG, false>);
+        static bool attr[4] = {false, false, false, false};
+        if (!attr[q8 + 2 * big]) {
+            (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, big ? 160 * 1024 : 96 * 1024);
             (void)hipGetLastError();
-            attr[q8] = true;
+            attr[q8 + 2 * big] = true;
         }
-        if (lds > 96 * 1024) return set_err(ctx, LBT_E_INVALID, std::string(what) + ": token group exceeds LDS");
+        if (lds > (big ? 160 : 96) * 1024)
+            return set_err(ctx, LBT_E_INVALID, std::string(what) + ": token group exceeds LDS");
         hipEvent_t e0, e1;
         prof_pair(ctx, &e0, &e1);
-        if (q8)
-            hipExtLaunchKernelGGL((lmhead_batch_kernel<kR, kLmChunks, kTG, true>), dim3(tiles * ngroups),
-                                  dim3(kThreads), lds, ctx->stream, e0, e1, 0, w, rscale, rows, cols, xn, m, tile_rows,
-                                  logits, key);
-        else
-            hipExtLaunchKernelGGL((lmhead_batch_kernel<kR, kLmChunks, kTG, false>), dim3(tiles * ngroups),
-                                  dim3(kThreads), lds, ctx->stream, e0, e1, 0, w, rscale, rows, cols, xn, m, tile_rows,
-                                  logits, key);
+#define LBT_HEAD_LAUNCH(TGv, Q8v, NTv)                                                                               \
+    hipExtLaunchKernelGGL((lmhead_batch_kernel<kR, kLmChunks, TGv, Q8v, NTv>), dim3(tiles * ngroups), dim3(NTv), lds, \
+                          ctx->stream, e0, e1, 0, w, rscale, rows, cols, xn, m, tile_rows, logits, key)
+        if (big) {
+            if (q8) LBT_HEAD_LAUNCH(16, true, 512);
+            else LBT_HEAD_LAUNCH(16, false, 512);
+        } else {
+            if (q8) LBT_HEAD_LAUNCH(kTG, true, kThreads);
+            else LBT_HEAD_LAUNCH(kTG, false, kThreads);
+        }
+#undef LBT_HEAD_LAUNCH
         LBT_HIP(ctx, hipGetLastError());
         prof_commit(ctx, e0, e1, kProfHead, wbytes);
         return LBT_OK;

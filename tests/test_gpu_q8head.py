@@ -124,14 +124,14 @@ def test_model_int8_head_matches_oracle(ctx):
     om2.free()
 
 
-def test_batch_int8_head_equals_single(ctx):
+@pytest.mark.parametrize("nseq", [5, 17])
+def test_batch_int8_head_equals_single(ctx, nseq):
     d = SMALL
     hip_cfg = lbt_hip.make_config(d["hidden"], d["intermediate"], d["heads"], d["kv_heads"], d["layers"], d["vocab"],
                                   d["max_pos"])
-    announce("batch int8 head")
+    announce(f"batch int8 head nseq={nseq}")
     m = lbt_hip.Model.synthetic(ctx, hip_cfg, 9)
     m.set_head(1)
-    nseq = 5
     b = m.new_batch(nseq, 64)
     prompts = [np.array([1 + s, 20 + s, 300 + s], np.uint32) for s in range(nseq)]
     nxt = [b.prefill(s, prompts[s]) for s in range(nseq)]
