@@ -919,7 +919,7 @@ int launch_head(lbt_ctx* ctx, const void* w, const float* rscale, int rows, int 
     const size_t lds = (size_t)cols * sizeof(float);
     if (lds > 64 * 1024) return set_err(ctx, LBT_E_INVALID, std::string(what) + ": cols too large");
     int blocks = (rows + 31) / 32;
-    if (blocks > (q8 ? 512 : 2048)) blocks = q8 ? 512 : 2048;
+    if (blocks > (q8 ? 512 : 768)) blocks = q8 ? 512 : 768;
     if (blocks < 1) blocks = 1;
     hipEvent_t e0, e1;
     prof_pair(ctx, &e0, &e1);
