@@ -1148,11 +1148,20 @@ int lbt_model_set_head(lbt_model* m, int kind) {
     const lbt_config& c = m->cfg;
     if (kind == 1 && !m->q8) {
         const size_t n = (size_t)c.vocab_size * c.hidden_size;
-        LBT_HIP(ctx, hipMalloc(&m->q8, n));
-        LBT_HIP(ctx, hipMalloc(&m->q8s, (size_t)c.vocab_size * 4));
-        int rc = launch_q8_quantize(ctx, m->embed, c.vocab_size, c.hidden_size, m->q8, m->q8s);
-        if (rc) return rc;
-        LBT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        int8_t* q = nullptr;
+        float* qs = nullptr;
+        hipError_t e = hipMalloc(&q, n);
+        if (e == hipSuccess) e = hipMalloc(&qs, (size_t)c.vocab_size * 4);
+        int rc = e == hipSuccess ? launch_q8_quantize(ctx, m->embed, c.vocab_size, c.hidden_size, q, qs)
+                                 : hip_err(ctx, e, "int8 head allocation");
+        if (!rc && (e = hipStreamSynchronize(ctx->stream)) != hipSuccess) rc = hip_err(ctx, e, "int8 head quantize");
+        if (rc) {  // the model keeps its bf16 head
+            if (q) hipFree(q);
+            if (qs) hipFree(qs);
+            return rc;
+        }
+        m->q8 = q;
+        m->q8s = qs;
     }
     if (kind != m->head_kind && m->step_exec) {
         LBT_HIP(ctx, hipStreamSynchronize(ctx->stream));

@@ -40,6 +40,22 @@ def test_no_gpu_returns_status():
     assert lib.lbt_version().decode().startswith("lbt-hip")
 
 
+def test_null_arguments_are_errors_not_crashes():
+    """Entry points reject null handles with a status (the reference asserts;
+    the C ABI never aborts).  Runs without a GPU."""
+    lib = lbt_hip.load_library()
+    out = C.c_void_p()
+    assert lib.lbt_q8head_from_bf16(None, None, C.byref(out)) != 0
+    assert lib.lbt_q8head_linear(None, None, None, 1, None) != 0
+    assert lib.lbt_q8head_linear_dev(None, None, None, 1, None) != 0
+    assert lib.lbt_q8head_read(None, None, None, None) != 0
+    assert lib.lbt_model_set_head(None, 1) != 0
+    assert lib.lbt_bf16_linear(None, None, None, 1, None) != 0
+    assert lib.lbt_gemm_i32(None, None, None, None, 1, None) != 0
+    lib.lbt_q8head_free(None)
+    lib.lbt_bf16_free(None)
+
+
 def test_header_compiles_as_c():
     import subprocess
 
