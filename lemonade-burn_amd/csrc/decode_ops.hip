@@ -57,7 +57,7 @@ __global__ __launch_bounds__(kThreads) void embed_kernel(const uint16_t* embed, 
 
 // ---------------------------------------------------------------------------
 // GQA attention splits, one workgroup per (query head, key split, query
-// row); see attn_common.h.  Grid (nh * kAttnSplits, m); splits past a row's
+// row); see attn_common.h.  Grid (nh * splits, m); splits past a row's
 // last one exit at once.
 template <int LK>
 __global__ __launch_bounds__(kThreads) void attention_kernel(const float* q, int nh, int kvh, RowPos rp,
@@ -66,7 +66,8 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(const float* q, int
     extern __shared__ float sc[];  // [attn_split_keys(visible keys)]
     __shared__ AttnShared<LK> sh;
     LBT_ATR(0)
-    const int h = blockIdx.x / kAttnSplits, s = blockIdx.x % kAttnSplits, t = blockIdx.y;
+    const int nsg = (int)gridDim.x / nh;  // splits in the grid (the most any row has)
+    const int h = blockIdx.x / nsg, s = blockIdx.x % nsg, t = blockIdx.y;
     const int H = nh * LK * 8, g = h / (nh / kvh);
     const size_t kvoff = row_cache_offset(rp, t) + (size_t)g * cap * LK * 8;
     float* ot = o + (size_t)t * kAttnSplits * H;
@@ -82,7 +83,7 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(const float* q, int
 }
 
 // The same splits with one workgroup per (KV head, key split, query row)
-// taking all GH query heads of the KV head.  Grid (kvh * kAttnSplits, m).
+// taking all GH query heads of the KV head.  Grid (kvh * splits, m).
 // wide: eight key passes in flight per split of more than 64 keys (grids of
 // many workgroups, where occupancy is not the limit); same partials.
 template <int LK, int GH>
@@ -91,7 +92,8 @@ __global__ __launch_bounds__(kThreads) void attention_group_kernel(const float* 
                                                                    float scaling, float* o, float* ml, int wide) {
     extern __shared__ float sc[];  // [GH][attn_split_keys(visible keys)]
     __shared__ AttnGroupShared<LK, GH> sh;
-    const int g = blockIdx.x / kAttnSplits, s = blockIdx.x % kAttnSplits, t = blockIdx.y;
+    const int nsg = (int)gridDim.x / kvh;  // splits in the grid (the most any row has)
+    const int g = blockIdx.x / nsg, s = blockIdx.x % nsg, t = blockIdx.y;
     const int H = nh * LK * 8;
     const size_t kvoff = row_cache_offset(rp, t) + (size_t)g * cap * LK * 8;
     const int p = row_position(rp, t);
@@ -819,7 +821,9 @@ int launch_attention(lbt_ctx* ctx, const float* q, int m, int nh, int kvh, int h
     if (lds > 64 * 1024) return set_err(ctx, LBT_E_RANGE, "attention: context too long for the LDS score buffer");
     hipEvent_t e0, e1;
     prof_pair(ctx, &e0, &e1);
-    dim3 grid((grouped ? kvh : nh) * kAttnSplits, m);
+    // as many splits as the longest visible row has (rows with fewer exit
+    // at once; a graph-replayed step is sized for the whole capacity)
+    dim3 grid((grouped ? kvh : nh) * attn_splits(rp.vis_max), m);
     hipError_t e;
     switch (hd) {
         case 64:
