@@ -224,6 +224,8 @@ def main() -> int:
     ap.add_argument("--pmc-pass", action="store_true", help="the workload profiled for the HBM counters")
     ap.add_argument("--no-batched", action="store_true", help="skip the batched-decode (config 5) figures")
     ap.add_argument("--no-int8-head", action="store_true", help="skip the opt-in int8 LM head figure")
+    ap.add_argument("--int8-head-only", action="store_true",
+                    help="only the opt-in int8 LM head decode figure (the workload profiled for its kernel)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the config-3 prefill GEMM sweep (the workload profiled for the MFMA counters)")
     args = ap.parse_args()
@@ -233,6 +235,15 @@ def main() -> int:
         import lbt_hip
 
         print(json.dumps({"prefill_gemm": prefill_gemm(lbt_hip.Ctx(0))}), flush=True)
+        return 0
+    if args.int8_head_only:
+        import lbt_hip
+
+        ctx = lbt_hip.Ctx(0)
+        cfg = lbt_hip.make_config()
+        model = lbt_hip.Model.synthetic(ctx, cfg, SEED)
+        prompt = np.random.default_rng(64).integers(0, cfg.vocab_size, PROMPT_LEN).astype(np.uint32)
+        print(json.dumps({"int8_head_decode": int8_head_decode(model, ctx, prompt)}), flush=True)
         return 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU; a multi-GPU figure is not part of it "
