@@ -229,6 +229,32 @@ int lbt_batch_forward(lbt_batch* b, const uint32_t* tokens, float* logits, uint3
 int lbt_batch_decode_greedy(lbt_batch* b, const uint32_t* first, size_t steps, uint32_t* out_tokens,
                             float* ms_decode);
 
+/* Sequence `seq` starts over (length 0); its cache rows are overwritten by
+ * the next prefill.  No counterpart in the reference (one cache per request). */
+int lbt_batch_reset(lbt_batch* b, int seq);
+
+/* ---- continuous batching (SURVEY next row; no counterpart in the reference,
+ * whose server runs one request at a time, lb-server main.rs:92-100) ---------
+ * Greedy requests share one lbt_batch of `slots` sequences: a queued request
+ * takes a free slot (its prompt prefilled there), every step advances all
+ * active slots by one token in one batched forward, and a finished request
+ * (max_new tokens, or its stop token) frees its slot for the queue.  Each
+ * request's tokens equal those of running it alone (greedy, same model). */
+typedef struct lbt_sched lbt_sched;
+int lbt_sched_new(lbt_model* m, int slots, int cap, lbt_sched** out);
+void lbt_sched_free(lbt_sched* s);
+/* Queue a request; stop = 0xFFFFFFFF for none; prompt length + max_new must
+ * fit the slot capacity.  *id receives the request's id. */
+int lbt_sched_submit(lbt_sched* s, const uint32_t* prompt, size_t n, size_t max_new, uint32_t stop,
+                     uint64_t* id);
+/* One step: admit queued requests into free slots (prefill, first token),
+ * then one batched decode step of the active slots.  *pending (nullable):
+ * requests still queued or active afterwards. */
+int lbt_sched_step(lbt_sched* s, int* pending);
+/* The tokens of request id so far (up to cap of them into tokens, nullable),
+ * their count in *n and whether it is finished in *done. */
+int lbt_sched_result(lbt_sched* s, uint64_t id, uint32_t* tokens, size_t cap, size_t* n, int* done);
+
 /* ---- profiling (replaces the PROF_* counters, ops.rs:79-97) ----------------
  * When enabled, every ternary GEMV/GEMM launch of the model loop is bracketed
  * by HIP events on the context stream; totals are per kernel class

@@ -192,6 +192,8 @@ int launch_attn_combine(lbt_ctx* ctx, const float* o, const float* ml, int m, in
 // one kernel (the values combine + quantize would give).
 int launch_attn_quantize(lbt_ctx* ctx, const float* o, const float* ml, int m, int nh, int hd, const RowPos& rp,
                          const float* norm_w, float eps, int kp, int8_t* q, float* scale, int32_t* sum);
+// The context a model was created on.
+lbt_ctx* model_ctx(const lbt_model* m);
 // Grow-only per-context device scratch for quantized activations.
 int qws_reserve(lbt_ctx* ctx, size_t bytes, void** out);
 int launch_fill_u64(lbt_ctx* ctx, unsigned long long* p, int n, unsigned long long v);

@@ -252,6 +252,10 @@ struct lbt_model {
     int bar_g = 0;
 };
 
+namespace lbt {
+lbt_ctx* model_ctx(const lbt_model* m) { return m ? m->ctx : nullptr; }
+}  // namespace lbt
+
 namespace {
 // Final RMSNorm + the model's LM head (model.rs:368-373): the tied bf16 head,
 // or the int8 head when selected.
@@ -1238,6 +1242,12 @@ void lbt_batch_free(lbt_batch* b) {
     for (void* p : bufs)
         if (p) hipFree(p);
     delete b;
+}
+
+int lbt_batch_reset(lbt_batch* b, int seq) {
+    if (!b || seq < 0 || seq >= b->nseq) return set_err(b ? b->m->ctx : nullptr, LBT_E_INVALID, "bad arguments");
+    b->len[seq] = 0;
+    return LBT_OK;
 }
 
 int lbt_batch_len(const lbt_batch* b, int seq) {

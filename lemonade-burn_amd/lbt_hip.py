@@ -106,6 +106,12 @@ SIGNATURES = {
     "lbt_batch_fill_synthetic": (i32, [vp, i32, C.c_uint64]),
     "lbt_batch_forward": (i32, [vp, vp, vp, vp]),
     "lbt_batch_decode_greedy": (i32, [vp, vp, sz, vp, vp]),
+    "lbt_batch_reset": (i32, [vp, i32]),
+    "lbt_sched_new": (i32, [vp, i32, i32, C.POINTER(vp)]),
+    "lbt_sched_free": (None, [vp]),
+    "lbt_sched_submit": (i32, [vp, vp, sz, sz, C.c_uint32, C.POINTER(C.c_uint64)]),
+    "lbt_sched_step": (i32, [vp, C.POINTER(i32)]),
+    "lbt_sched_result": (i32, [vp, C.c_uint64, vp, sz, C.POINTER(sz), C.POINTER(i32)]),
     "lbt_prof_enable": (i32, [vp, i32]),
     "lbt_prof_read": (i32, [vp, C.POINTER(LbtProf), i32]),
 }
@@ -394,6 +400,11 @@ class Model:
     def linear(self, layer: int, which: int) -> int:
         return self.ctx.lib.lbt_model_linear(self.h, layer, which)
 
+    def new_sched(self, slots: int, cap: int) -> "Sched":
+        h = C.c_void_p()
+        self.ctx.check(self.ctx.lib.lbt_sched_new(self.h, slots, cap, C.byref(h)))
+        return Sched(self, h)
+
     def new_batch(self, nseq: int, cap: int) -> "Batch":
         h = C.c_void_p()
         self.ctx.check(self.ctx.lib.lbt_batch_new(self.h, nseq, cap, C.byref(h)))
@@ -461,4 +472,42 @@ class Batch:
     def free(self):
         if self.h:
             self.model.ctx.lib.lbt_batch_free(self.h)
+            self.h = None
+
+
+class Sched:
+    """Continuous batching of greedy requests (lbt_sched_*)."""
+
+    NO_STOP = 0xFFFFFFFF
+
+    def __init__(self, model: "Model", h):
+        self.model, self.h = model, h
+
+    def _check(self, rc):
+        self.model.ctx.check(rc)
+
+    def submit(self, prompt, max_new: int, stop: int = NO_STOP) -> int:
+        t = np.ascontiguousarray(prompt, np.uint32)
+        rid = C.c_uint64()
+        self._check(self.model.ctx.lib.lbt_sched_submit(self.h, _ptr(t), t.size, max_new, C.c_uint32(stop),
+                                                        C.byref(rid)))
+        return int(rid.value)
+
+    def step(self) -> int:
+        p = C.c_int32()
+        self._check(self.model.ctx.lib.lbt_sched_step(self.h, C.byref(p)))
+        return int(p.value)
+
+    def result(self, rid: int):
+        n, done = C.c_size_t(), C.c_int32()
+        self._check(self.model.ctx.lib.lbt_sched_result(self.h, C.c_uint64(rid), None, 0, C.byref(n), C.byref(done)))
+        out = np.zeros(n.value, np.uint32)
+        if n.value:
+            self._check(self.model.ctx.lib.lbt_sched_result(self.h, C.c_uint64(rid), _ptr(out), out.size, C.byref(n),
+                                                            C.byref(done)))
+        return out, bool(done.value)
+
+    def free(self):
+        if self.h:
+            self.model.ctx.lib.lbt_sched_free(self.h)
             self.h = None

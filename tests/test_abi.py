@@ -54,6 +54,11 @@ def test_null_arguments_are_errors_not_crashes():
     assert lib.lbt_gemm_i32(None, None, None, None, 1, None) != 0
     lib.lbt_q8head_free(None)
     lib.lbt_bf16_free(None)
+    assert lib.lbt_sched_new(None, 2, 16, C.byref(out)) != 0
+    assert lib.lbt_sched_step(None, None) != 0
+    assert lib.lbt_sched_result(None, 1, None, 0, None, None) != 0
+    assert lib.lbt_batch_reset(None, 0) != 0
+    lib.lbt_sched_free(None)
 
 
 def test_header_compiles_as_c():
