@@ -100,6 +100,24 @@ def int8_head_decode(model, ctx, prompt, steps: int = 128) -> dict:
             "head_GBs": round(h["bytes"] / (h["ms"] / 1e3) / 1e9, 1) if h["ms"] > 0 else 0.0}
 
 
+def sched_throughput(model, cfg, slots: int = 16, requests: int = 32, prompt_len: int = 64, new: int = 64) -> dict:
+    """Continuous batching (lbt_sched_*): `requests` greedy requests of a
+    `prompt_len`-token prompt and `new` tokens each through `slots` slots;
+    generated tokens per second of host wall time (prefills included)."""
+    rng = np.random.default_rng(7)
+    s = model.new_sched(slots, prompt_len + new)
+    ids = [s.submit(rng.integers(0, cfg.vocab_size, prompt_len).astype(np.uint32), new) for _ in range(requests)]
+    t0 = time.perf_counter()
+    steps = 0
+    while s.step():
+        steps += 1
+    wall = time.perf_counter() - t0
+    total = sum(len(s.result(i)[0]) for i in ids)
+    s.free()
+    return {"slots": slots, "requests": requests, "prompt": prompt_len, "new_tokens": new, "steps": steps + 1,
+            "tok_s": round(total / wall, 1), "wall_s": round(wall, 3)}
+
+
 def prefill_gemm(ctx, reps: int = 10) -> list:
     """the prefill GEMM (int8 MFMA) on the FFN shapes
     2560->6912 and 6912->2560 at M = 128, 512, 2048 tokens; seeded ternary
@@ -334,6 +352,7 @@ def main() -> int:
         line["int8_head_decode"] = int8_head_decode(model, ctx, prompt)
     if not args.no_batched:
         line["batched_decode"] = [batched_decode(model, cfg, bsz) for bsz in (16, 64)]
+        line["continuous_batching"] = sched_throughput(model, cfg)
         line["prefill_gemm"] = prefill_gemm(ctx)
     model.free()
     ctx.close()
