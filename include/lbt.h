@@ -254,6 +254,8 @@ int lbt_sched_step(lbt_sched* s, int* pending);
 /* The tokens of request id so far (up to cap of them into tokens, nullable),
  * their count in *n and whether it is finished in *done. */
 int lbt_sched_result(lbt_sched* s, uint64_t id, uint32_t* tokens, size_t cap, size_t* n, int* done);
+/* Drop a finished request's record (its id becomes unknown). */
+int lbt_sched_release(lbt_sched* s, uint64_t id);
 
 /* ---- profiling (replaces the PROF_* counters, ops.rs:79-97) ----------------
  * When enabled, every ternary GEMV/GEMM launch of the model loop is bracketed

@@ -145,3 +145,12 @@ int lbt_sched_result(lbt_sched* s, uint64_t id, uint32_t* tokens, size_t cap, si
     if (done) *done = r.done ? 1 : 0;
     return LBT_OK;
 }
+
+int lbt_sched_release(lbt_sched* s, uint64_t id) {
+    if (!s) return LBT_E_INVALID;
+    auto it = s->reqs.find(id);
+    if (it == s->reqs.end()) return lbt::set_err(ctx_of(s), LBT_E_INVALID, "sched: unknown request id");
+    if (!it->second.done) return lbt::set_err(ctx_of(s), LBT_E_INVALID, "sched: request not finished");
+    s->reqs.erase(it);
+    return LBT_OK;
+}

@@ -112,6 +112,7 @@ SIGNATURES = {
     "lbt_sched_submit": (i32, [vp, vp, sz, sz, C.c_uint32, C.POINTER(C.c_uint64)]),
     "lbt_sched_step": (i32, [vp, C.POINTER(i32)]),
     "lbt_sched_result": (i32, [vp, C.c_uint64, vp, sz, C.POINTER(sz), C.POINTER(i32)]),
+    "lbt_sched_release": (i32, [vp, C.c_uint64]),
     "lbt_prof_enable": (i32, [vp, i32]),
     "lbt_prof_read": (i32, [vp, C.POINTER(LbtProf), i32]),
 }
@@ -506,6 +507,9 @@ class Sched:
             self._check(self.model.ctx.lib.lbt_sched_result(self.h, C.c_uint64(rid), _ptr(out), out.size, C.byref(n),
                                                             C.byref(done)))
         return out, bool(done.value)
+
+    def release(self, rid: int):
+        self._check(self.model.ctx.lib.lbt_sched_release(self.h, C.c_uint64(rid)))
 
     def free(self):
         if self.h:

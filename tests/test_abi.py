@@ -58,6 +58,7 @@ def test_null_arguments_are_errors_not_crashes():
     assert lib.lbt_sched_step(None, None) != 0
     assert lib.lbt_sched_result(None, 1, None, 0, None, None) != 0
     assert lib.lbt_batch_reset(None, 0) != 0
+    assert lib.lbt_sched_release(None, 1) != 0
     lib.lbt_sched_free(None)
 
 

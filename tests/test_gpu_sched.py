@@ -75,5 +75,8 @@ def test_sched_rejects_requests_beyond_capacity(ctx):
         pass
     got, done = s.result(rid)
     assert done and len(got) == 7
+    s.release(rid)
+    with pytest.raises(lbt_hip.LbtError, match="unknown"):
+        s.result(rid)
     s.free()
     m.free()
