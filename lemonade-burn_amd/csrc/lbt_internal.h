@@ -118,8 +118,12 @@ struct TernaryOp {
     uint16_t* kc = nullptr;
     uint16_t* vc = nullptr;
 };
-// Dispatches decode GEMV (small m) or the int8-MFMA prefill GEMM (large m).
-constexpr int kMfmaMinTokens = 16;
+// Dispatches the single-token decode GEMV (m = 1) or the int8-MFMA GEMMs
+// (m >= kMfmaMinTokens; the VALU few-token GEMV tgemv_kernel stays behind
+// LBT_NO_MFMA / LBT_MFMA_MIN, measured 1.2-2x slower at 2..12 tokens).
+constexpr int kMfmaMinTokens = 2;
+// the few-token MFMA GEMM (16-row tiles) serves up to this many tokens
+constexpr int kSmallMaxTokens = 32;
 int launch_ternary(lbt_ctx* ctx, const TernaryOp& op);
 int launch_ternary_gemv(lbt_ctx* ctx, const TernaryOp& op);
 // Single-token GEMV with one 1024-thread workgroup per compute unit (f32 or

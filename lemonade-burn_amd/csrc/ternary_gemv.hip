@@ -434,7 +434,8 @@ int launch_quantize(lbt_ctx* ctx, const float* x, const float* norm_w, float eps
     return LBT_OK;
 }
 
-// Decode GEMV for a few tokens, the int8-MFMA GEMM from kMfmaMinTokens up.
+// Decode GEMV for one token (the VALU few-token GEMV on request), the int8-MFMA
+// GEMM from kMfmaMinTokens up.
 // Combine of row blockIdx.x's splits, then RMSNorm + ActQuant of the row
 // into q (the GEMM input of the o projection for several rows): the combine
 // of attn_combine_kernel and the quantizer of quantize_kernel on the same
@@ -495,7 +496,8 @@ int launch_ternary(lbt_ctx* ctx, const TernaryOp& op_in) {
         op.tok_pos = nullptr;
         op.pos_dev = nullptr;
     }
-    if (op.m >= kMfmaMinTokens && !getenv("LBT_NO_MFMA")) return launch_ternary_mfma(ctx, op);
+    static const int mfma_min = getenv("LBT_MFMA_MIN") ? atoi(getenv("LBT_MFMA_MIN")) : kMfmaMinTokens;
+    if (op.m >= (mfma_min > 1 ? mfma_min : 2) && !getenv("LBT_NO_MFMA")) return launch_ternary_mfma(ctx, op);
     return launch_ternary_gemv(ctx, op);
 }
 

@@ -283,6 +283,91 @@ __global__ __launch_bounds__(kThreads) void tgemm_kernel(GemvArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Few-token GEMM (batched decode, 16..32 tokens): the weight stream is the
+// whole cost, so the grid is cut as finely as the 16 x 16 x 64 MFMA allows --
+// one workgroup per 16 rows (o/down of the 2B model: 160 workgroups instead of
+// 40 tiles of 64 rows) -- and its 4 wavefronts split K into contiguous step
+// ranges.  Each wavefront issues every weight load of its range at once (at
+// most kSmallMaxSteps uint4 per lane), reads the activations (L2-resident,
+// 16 MS tokens) straight from global memory one step ahead, and the three
+// partial int32 tiles are added to wavefront 0's through LDS (exact, any
+// order) before the shared epilogue.  Operand layout as tgemm_kernel: lane
+// (li, lg) takes chunk 4p + lg of row li and, for MFMA kk of step p, the 16
+// activations of token li at k = 256 p + 128 (lg >> 1) + 32 kk + 16 (lg & 1).
+constexpr int kSmallMaxSteps = 8;  // 256-k steps per wavefront: K <= 8192
+
+template <int OUT, int MS>
+__global__ __launch_bounds__(kThreads) void tgemm_small_kernel(GemvArgs a) {
+    __shared__ __align__(16) v4i part[3][MS][64];
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int li = lane & 15, lg = lane >> 4;
+    const int m0 = blockIdx.y * (16 * MS), n0 = blockIdx.x * 16;
+    const int C = a.C, kp = a.kp, M = a.m;
+    const int nsteps = (C + 3) / 4;
+    const int p0 = (nsteps * w) >> 2, p1 = (nsteps * (w + 1)) >> 2;
+
+    const int vr = n0 + li;
+    const bool bval = vr < a.total_rows;
+    int mat, r;
+    resolve_row<OUT>(a, bval ? vr : 0, mat, r);
+    const uint4* brow = (const uint4*)(sel3(a.w, mat) + (size_t)r * (size_t)(kp >> 2));
+    uint4 bw[kSmallMaxSteps];
+#pragma unroll
+    for (int i = 0; i < kSmallMaxSteps; i++) {
+        const int c = 4 * (p0 + i) + lg;
+        bw[i] = (bval && p0 + i < p1 && c < C) ? ld_stream(brow + c) : make_uint4(0, 0, 0, 0);
+    }
+
+    const int8_t* arow[MS];
+#pragma unroll
+    for (int ms = 0; ms < MS; ms++) {
+        const int tok = m0 + ms * 16 + li;
+        arow[ms] = a.q + (size_t)(tok < M ? tok : M - 1) * kp + (lg >> 1) * 128 + (lg & 1) * 16;
+    }
+    // activation operands of one step; k beyond kp only meets zero weights,
+    // so its address is clamped to the row's last step
+    auto a_load = [&](int p, v4i (&dst)[MS][4]) {
+        const int pc = 256 * p < kp ? p : (kp - 1) / 256;
+#pragma unroll
+        for (int ms = 0; ms < MS; ms++)
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++) {
+                const int off = 256 * pc + 32 * kk + (lg >> 1) * 128 + (lg & 1) * 16;
+                dst[ms][kk] = off + 16 <= kp ? *(const v4i*)(arow[ms] + 256 * pc + 32 * kk) : v4i{0, 0, 0, 0};
+            }
+    };
+
+    v4i acc[MS][1];
+#pragma unroll
+    for (int ms = 0; ms < MS; ms++) acc[ms][0] = v4i{0, 0, 0, 0};
+    v4i aop[2][MS][4];
+    if (p0 < p1) a_load(p0, aop[0]);
+#pragma unroll
+    for (int i = 0; i < kSmallMaxSteps; i++) {
+        if (p0 + i >= p1) break;
+        if (p0 + i + 1 < p1) a_load(p0 + i + 1, aop[(i + 1) & 1]);
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++) {
+            const int sh = 2 * kk;
+            const v4i bop = v4i{(int)((bw[i].x >> sh) & 0x03030303u), (int)((bw[i].y >> sh) & 0x03030303u),
+                                (int)((bw[i].z >> sh) & 0x03030303u), (int)((bw[i].w >> sh) & 0x03030303u)};
+#pragma unroll
+            for (int ms = 0; ms < MS; ms++)
+                acc[ms][0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aop[i & 1][ms][kk], bop, acc[ms][0], 0, 0, 0);
+        }
+    }
+    if (w > 0) {
+#pragma unroll
+        for (int ms = 0; ms < MS; ms++) part[w - 1][ms][lane] = acc[ms][0];
+    }
+    __syncthreads();
+    if (w > 0) return;
+#pragma unroll
+    for (int ms = 0; ms < MS; ms++) acc[ms][0] += (part[0][ms][lane] + part[1][ms][lane]) + part[2][ms][lane];
+    mfma_epilogue<OUT, 16>(a, acc, m0, n0);
+}
+
+// ---------------------------------------------------------------------------
 // Pipelined prefill GEMM on the full-rate int8 MFMA of gfx950
 // (v_mfma_i32_32x32x32_i8: 32768 MACs in 8 passes, twice the rate of the
 // 16x16x64 form).  A workgroup of 4 wavefronts (2 x 2) computes BM = 64 MS
@@ -526,6 +611,18 @@ hipError_t launch_tiles2(const GemvArgs& a, int out_mode, dim3 grid, hipStream_t
 }
 
 
+template <int MS>
+hipError_t launch_small(const GemvArgs& a, int out_mode, dim3 grid, hipStream_t s, hipEvent_t e0, hipEvent_t e1) {
+    switch (out_mode) {
+        case kOutI32: hipExtLaunchKernelGGL((tgemm_small_kernel<kOutI32, MS>), grid, dim3(kThreads), 0, s, e0, e1, 0, a); break;
+        case kOutF32: hipExtLaunchKernelGGL((tgemm_small_kernel<kOutF32, MS>), grid, dim3(kThreads), 0, s, e0, e1, 0, a); break;
+        case kOutF32Add: hipExtLaunchKernelGGL((tgemm_small_kernel<kOutF32Add, MS>), grid, dim3(kThreads), 0, s, e0, e1, 0, a); break;
+        case kOutRelu2: hipExtLaunchKernelGGL((tgemm_small_kernel<kOutRelu2, MS>), grid, dim3(kThreads), 0, s, e0, e1, 0, a); break;
+        default: hipExtLaunchKernelGGL((tgemm_small_kernel<kOutQKV, MS>), grid, dim3(kThreads), 0, s, e0, e1, 0, a); break;
+    }
+    return hipGetLastError();
+}
+
 }  // namespace
 
 // Grow-only per-context scratch for quantized activations.
@@ -573,13 +670,32 @@ int launch_ternary_mfma(lbt_ctx* ctx, const TernaryOp& op_in) {
     hipError_t e;
     // LBT_GEMM_MODE (tests and measurements): 1 = 16x16x64 kernel, 2 / 3 =
     // 32x32x32 with 256-k steps (128 / 64 tiles), 4 / 5 = 128-k steps with 64 /
-    // 128 tiles; default: 128 tiles when there are >= 200 of them, else 64
+    // 128 tiles, 6 = few-token kernel (16-row tiles, K split over the
+    // wavefronts); default: the few-token kernel up to kSmallMaxTokens tokens
+    // (LBT_GEMM_SMALL_MAX overrides), then 128 tiles when there are >= 200 of
+    // them, else 64
     const char* gm = getenv("LBT_GEMM_MODE");
     const int gmode = gm ? atoi(gm) : 0;
     const long t128 = (long)((total + 127) / 128) * ((op.m + 127) / 128);
     const dim3 g128((unsigned)((total + 127) / 128), (unsigned)((op.m + 127) / 128));
     const dim3 g64((unsigned)((total + 63) / 64), (unsigned)((op.m + 63) / 64));
-    if (gmode == 1) {
+    const char* sm = getenv("LBT_GEMM_SMALL_MAX");
+    const int small_max = sm ? atoi(sm) : kSmallMaxTokens;
+    const bool small_ok = a.kp <= 256 * 4 * kSmallMaxSteps;
+    if (small_ok && (gmode == 6 || (gmode == 0 && op.m <= small_max))) {
+        // 16-token tiles (more workgroups) measured faster than 32..64-token
+        // ones at every batch served here; LBT_GEMM_SMALL_MS = 2..4 selects
+        // the wider tiles
+        const char* mc = getenv("LBT_GEMM_SMALL_MS");
+        const int mcap = mc ? atoi(mc) : 1;
+        int ms = op.m <= 16 ? 1 : op.m <= 32 ? 2 : op.m <= 48 ? 3 : 4;
+        if (ms > mcap) ms = mcap < 1 ? 1 : mcap;
+        const dim3 g((unsigned)((total + 15) / 16), (unsigned)((op.m + 16 * ms - 1) / (16 * ms)));
+        e = ms == 1   ? launch_small<1>(a, op.out_mode, g, ctx->stream, e0, e1)
+            : ms == 2 ? launch_small<2>(a, op.out_mode, g, ctx->stream, e0, e1)
+            : ms == 3 ? launch_small<3>(a, op.out_mode, g, ctx->stream, e0, e1)
+                      : launch_small<4>(a, op.out_mode, g, ctx->stream, e0, e1);
+    } else if (gmode == 1) {
         e = big ? launch_tiles<4, 4>(a, op.out_mode, g128, ctx->stream, e0, e1)
                 : launch_tiles<2, 2>(a, op.out_mode, g64, ctx->stream, e0, e1);
     } else if (gmode == 2 && a.kp % 256 == 0) {

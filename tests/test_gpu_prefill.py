@@ -47,6 +47,45 @@ def test_ragged_tiles(ctx, rows, cols, m):
     w.free()
 
 
+@pytest.mark.parametrize("rows,cols", [(6912, 2560), (2560, 6912), (640, 2560)])
+@pytest.mark.parametrize("m", [16, 17, 32, 48, 64])
+def test_few_token_gemm_bitexact(ctx, rows, cols, m):
+    # batched-decode sizes through the few-token kernel (16-row tiles, K split
+    # over four wavefronts)
+    announce(f"few-token gemm {rows}x{cols} m={m}")
+    rng = np.random.default_rng(rows + 3 * cols + m)
+    t = ternary_iid(rng, rows, cols)
+    p = orc.pack(t)
+    x = rng.standard_normal((m, cols)).astype(np.float32)
+    q, sa, su = orc.quantize_acts(x)
+    sw = float(np.float32(0.8))
+    w = ctx.upload(p, rows, cols, sw)
+    d = q[:, :cols].astype(np.int64) @ t.T.astype(np.int64)
+    assert np.array_equal(ctx.gemm_i32(w, q, su), d)
+    (y,) = ctx.ternary_linear([w], x)
+    assert np.array_equal(y, orc.gemm_f32(p, rows, cols, sw, q, sa, su))
+    w.free()
+
+
+@pytest.mark.parametrize("rows,cols,m", [(23, 384, 17), (37, 2560, 33), (130, 300, 65), (5, 129, 16), (100, 1000, 200),
+                                         (1, 256, 20), (257, 768, 130), (31, 8192, 64)])
+@pytest.mark.parametrize("ms", ["1", "2", "3", "4"])
+def test_few_token_kernel_ragged(ctx, monkeypatch, rows, cols, m, ms):
+    # LBT_GEMM_MODE=6 forces the few-token kernel at any token count;
+    # LBT_GEMM_SMALL_MS its tile width (16 * ms tokens)
+    monkeypatch.setenv("LBT_GEMM_MODE", "6")
+    monkeypatch.setenv("LBT_GEMM_SMALL_MS", ms)
+    announce(f"few-token ragged {rows}x{cols} m={m} ms={ms}")
+    t, scale, x = golden_case(rows, cols, m, 7 * rows + cols + m)
+    p = orc.pack(t)
+    q, sa, su = orc.quantize_acts(x)
+    w = ctx.upload(p, rows, cols, float(scale))
+    assert np.array_equal(ctx.gemm_i32(w, q, su), q[:, :cols].astype(np.int64) @ t.T.astype(np.int64))
+    (y,) = ctx.ternary_linear([w], x)
+    assert np.array_equal(y, orc.gemm_f32(p, rows, cols, scale, q, sa, su))
+    w.free()
+
+
 def test_prefill_extreme_long_rows_mfma(ctx):
     # golden.rs:181-194 at an MFMA-sized token count
     rows, cols, m = 3, 6912 * 2, 32
@@ -97,10 +136,11 @@ def test_model_prefill_mfma_matches_oracle_and_gemv(ctx, monkeypatch, n):
     om.free()
 
 
-@pytest.mark.parametrize("mode", ["1", "4", "5"])
+@pytest.mark.parametrize("mode", ["1", "4", "5", "6"])
 def test_model_prefill_every_gemm_tiling_matches_oracle(ctx, monkeypatch, mode):
     # every epilogue (q/k/v + RoPE + KV append, residual add, relu^2*up) through
-    # each MFMA tiling: 16x16x64 kernel, 64x64 and 128x128 tiles of the 32x32x32 one
+    # each MFMA tiling: 16x16x64 kernel, 64x64 and 128x128 tiles of the 32x32x32 one,
+    # the few-token kernel
     cfg = dict(hidden=512, intermediate=1536, heads=4, kv_heads=1, layers=2, vocab=1000, max_pos=1024)
     n = 200
     monkeypatch.setenv("LBT_GEMM_MODE", mode)
