@@ -286,7 +286,9 @@ __global__ __launch_bounds__(kThreads) void tgemm_kernel(GemvArgs a) {
 // Few-token GEMM (batched decode, 16..32 tokens): the weight stream is the
 // whole cost, so the grid is cut as finely as the 16 x 16 x 64 MFMA allows --
 // one workgroup per 16 rows (o/down of the 2B model: 160 workgroups instead of
-// 40 tiles of 64 rows) -- and its 4 wavefronts split K into contiguous step
+// 40 tiles of 64 rows; 32 rows, NS = 2, where that still leaves >= 384
+// workgroups, halving the activation re-reads) -- and its 4 wavefronts split K
+// into contiguous step
 // ranges.  Each wavefront issues every weight load of its range at once (at
 // most kSmallMaxSteps uint4 per lane), reads the activations (L2-resident,
 // 16 MS tokens) straight from global memory one step ahead, and the three
@@ -295,27 +297,31 @@ __global__ __launch_bounds__(kThreads) void tgemm_kernel(GemvArgs a) {
 // (li, lg) takes chunk 4p + lg of row li and, for MFMA kk of step p, the 16
 // activations of token li at k = 256 p + 128 (lg >> 1) + 32 kk + 16 (lg & 1).
 constexpr int kSmallMaxSteps = 8;  // 256-k steps per wavefront: K <= 8192
+constexpr int kSmallWideRowTiles = 384;  // 32-row tiles from 384 * 32 rows
 
-template <int OUT, int MS>
+template <int OUT, int MS, int NS>
 __global__ __launch_bounds__(kThreads) void tgemm_small_kernel(GemvArgs a) {
-    __shared__ __align__(16) v4i part[3][MS][64];
+    __shared__ __align__(16) v4i part[3][MS][NS][64];
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const int li = lane & 15, lg = lane >> 4;
-    const int m0 = blockIdx.y * (16 * MS), n0 = blockIdx.x * 16;
+    const int m0 = blockIdx.y * (16 * MS), n0 = blockIdx.x * (16 * NS);
     const int C = a.C, kp = a.kp, M = a.m;
     const int nsteps = (C + 3) / 4;
     const int p0 = (nsteps * w) >> 2, p1 = (nsteps * (w + 1)) >> 2;
 
-    const int vr = n0 + li;
-    const bool bval = vr < a.total_rows;
-    int mat, r;
-    resolve_row<OUT>(a, bval ? vr : 0, mat, r);
-    const uint4* brow = (const uint4*)(sel3(a.w, mat) + (size_t)r * (size_t)(kp >> 2));
-    uint4 bw[kSmallMaxSteps];
+    uint4 bw[NS][kSmallMaxSteps];
 #pragma unroll
-    for (int i = 0; i < kSmallMaxSteps; i++) {
-        const int c = 4 * (p0 + i) + lg;
-        bw[i] = (bval && p0 + i < p1 && c < C) ? ld_stream(brow + c) : make_uint4(0, 0, 0, 0);
+    for (int ns = 0; ns < NS; ns++) {
+        const int vr = n0 + ns * 16 + li;
+        const bool bval = vr < a.total_rows;
+        int mat, r;
+        resolve_row<OUT>(a, bval ? vr : 0, mat, r);
+        const uint4* brow = (const uint4*)(sel3(a.w, mat) + (size_t)r * (size_t)(kp >> 2));
+#pragma unroll
+        for (int i = 0; i < kSmallMaxSteps; i++) {
+            const int c = 4 * (p0 + i) + lg;
+            bw[ns][i] = (bval && p0 + i < p1 && c < C) ? ld_stream(brow + c) : make_uint4(0, 0, 0, 0);
+        }
     }
 
     const int8_t* arow[MS];
@@ -337,9 +343,11 @@ __global__ __launch_bounds__(kThreads) void tgemm_small_kernel(GemvArgs a) {
             }
     };
 
-    v4i acc[MS][1];
+    v4i acc[MS][NS];
 #pragma unroll
-    for (int ms = 0; ms < MS; ms++) acc[ms][0] = v4i{0, 0, 0, 0};
+    for (int ms = 0; ms < MS; ms++)
+#pragma unroll
+        for (int ns = 0; ns < NS; ns++) acc[ms][ns] = v4i{0, 0, 0, 0};
     v4i aop[2][MS][4];
     if (p0 < p1) a_load(p0, aop[0]);
 #pragma unroll
@@ -349,21 +357,30 @@ __global__ __launch_bounds__(kThreads) void tgemm_small_kernel(GemvArgs a) {
 #pragma unroll
         for (int kk = 0; kk < 4; kk++) {
             const int sh = 2 * kk;
-            const v4i bop = v4i{(int)((bw[i].x >> sh) & 0x03030303u), (int)((bw[i].y >> sh) & 0x03030303u),
-                                (int)((bw[i].z >> sh) & 0x03030303u), (int)((bw[i].w >> sh) & 0x03030303u)};
 #pragma unroll
-            for (int ms = 0; ms < MS; ms++)
-                acc[ms][0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aop[i & 1][ms][kk], bop, acc[ms][0], 0, 0, 0);
+            for (int ns = 0; ns < NS; ns++) {
+                const uint4 b = bw[ns][i];
+                const v4i bop = v4i{(int)((b.x >> sh) & 0x03030303u), (int)((b.y >> sh) & 0x03030303u),
+                                    (int)((b.z >> sh) & 0x03030303u), (int)((b.w >> sh) & 0x03030303u)};
+#pragma unroll
+                for (int ms = 0; ms < MS; ms++)
+                    acc[ms][ns] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aop[i & 1][ms][kk], bop, acc[ms][ns], 0, 0, 0);
+            }
         }
     }
     if (w > 0) {
 #pragma unroll
-        for (int ms = 0; ms < MS; ms++) part[w - 1][ms][lane] = acc[ms][0];
+        for (int ms = 0; ms < MS; ms++)
+#pragma unroll
+            for (int ns = 0; ns < NS; ns++) part[w - 1][ms][ns][lane] = acc[ms][ns];
     }
     __syncthreads();
     if (w > 0) return;
 #pragma unroll
-    for (int ms = 0; ms < MS; ms++) acc[ms][0] += (part[0][ms][lane] + part[1][ms][lane]) + part[2][ms][lane];
+    for (int ms = 0; ms < MS; ms++)
+#pragma unroll
+        for (int ns = 0; ns < NS; ns++)
+            acc[ms][ns] += (part[0][ms][ns][lane] + part[1][ms][ns][lane]) + part[2][ms][ns][lane];
     mfma_epilogue<OUT, 16>(a, acc, m0, n0);
 }
 
@@ -611,14 +628,14 @@ hipError_t launch_tiles2(const GemvArgs& a, int out_mode, dim3 grid, hipStream_t
 }
 
 
-template <int MS>
+template <int MS, int NS>
 hipError_t launch_small(const GemvArgs& a, int out_mode, dim3 grid, hipStream_t s, hipEvent_t e0, hipEvent_t e1) {
     switch (out_mode) {
-        case kOutI32: hipExtLaunchKernelGGL((tgemm_small_kernel<kOutI32, MS>), grid, dim3(kThreads), 0, s, e0, e1, 0, a); break;
-        case kOutF32: hipExtLaunchKernelGGL((tgemm_small_kernel<kOutF32, MS>), grid, dim3(kThreads), 0, s, e0, e1, 0, a); break;
-        case kOutF32Add: hipExtLaunchKernelGGL((tgemm_small_kernel<kOutF32Add, MS>), grid, dim3(kThreads), 0, s, e0, e1, 0, a); break;
-        case kOutRelu2: hipExtLaunchKernelGGL((tgemm_small_kernel<kOutRelu2, MS>), grid, dim3(kThreads), 0, s, e0, e1, 0, a); break;
-        default: hipExtLaunchKernelGGL((tgemm_small_kernel<kOutQKV, MS>), grid, dim3(kThreads), 0, s, e0, e1, 0, a); break;
+        case kOutI32: hipExtLaunchKernelGGL((tgemm_small_kernel<kOutI32, MS, NS>), grid, dim3(kThreads), 0, s, e0, e1, 0, a); break;
+        case kOutF32: hipExtLaunchKernelGGL((tgemm_small_kernel<kOutF32, MS, NS>), grid, dim3(kThreads), 0, s, e0, e1, 0, a); break;
+        case kOutF32Add: hipExtLaunchKernelGGL((tgemm_small_kernel<kOutF32Add, MS, NS>), grid, dim3(kThreads), 0, s, e0, e1, 0, a); break;
+        case kOutRelu2: hipExtLaunchKernelGGL((tgemm_small_kernel<kOutRelu2, MS, NS>), grid, dim3(kThreads), 0, s, e0, e1, 0, a); break;
+        default: hipExtLaunchKernelGGL((tgemm_small_kernel<kOutQKV, MS, NS>), grid, dim3(kThreads), 0, s, e0, e1, 0, a); break;
     }
     return hipGetLastError();
 }
@@ -690,11 +707,21 @@ int launch_ternary_mfma(lbt_ctx* ctx, const TernaryOp& op_in) {
         const int mcap = mc ? atoi(mc) : 1;
         int ms = op.m <= 16 ? 1 : op.m <= 32 ? 2 : op.m <= 48 ? 3 : 4;
         if (ms > mcap) ms = mcap < 1 ? 1 : mcap;
-        const dim3 g((unsigned)((total + 15) / 16), (unsigned)((op.m + 16 * ms - 1) / (16 * ms)));
-        e = ms == 1   ? launch_small<1>(a, op.out_mode, g, ctx->stream, e0, e1)
-            : ms == 2 ? launch_small<2>(a, op.out_mode, g, ctx->stream, e0, e1)
-            : ms == 3 ? launch_small<3>(a, op.out_mode, g, ctx->stream, e0, e1)
-                      : launch_small<4>(a, op.out_mode, g, ctx->stream, e0, e1);
+        // 32-row tiles (half the activation re-reads) where they still give
+        // >= 256 workgroups per token tile; LBT_GEMM_SMALL_NS = 1 / 2 forces
+        const char* nc = getenv("LBT_GEMM_SMALL_NS");
+        const int ns = nc ? (atoi(nc) == 2 ? 2 : 1) : (total >= 32 * kSmallWideRowTiles ? 2 : 1);
+        const dim3 g((unsigned)((total + 16 * ns - 1) / (16 * ns)), (unsigned)((op.m + 16 * ms - 1) / (16 * ms)));
+        if (ns == 2)
+            e = ms == 1   ? launch_small<1, 2>(a, op.out_mode, g, ctx->stream, e0, e1)
+                : ms == 2 ? launch_small<2, 2>(a, op.out_mode, g, ctx->stream, e0, e1)
+                : ms == 3 ? launch_small<3, 2>(a, op.out_mode, g, ctx->stream, e0, e1)
+                          : launch_small<4, 2>(a, op.out_mode, g, ctx->stream, e0, e1);
+        else
+            e = ms == 1   ? launch_small<1, 1>(a, op.out_mode, g, ctx->stream, e0, e1)
+                : ms == 2 ? launch_small<2, 1>(a, op.out_mode, g, ctx->stream, e0, e1)
+                : ms == 3 ? launch_small<3, 1>(a, op.out_mode, g, ctx->stream, e0, e1)
+                          : launch_small<4, 1>(a, op.out_mode, g, ctx->stream, e0, e1);
     } else if (gmode == 1) {
         e = big ? launch_tiles<4, 4>(a, op.out_mode, g128, ctx->stream, e0, e1)
                 : launch_tiles<2, 2>(a, op.out_mode, g64, ctx->stream, e0, e1);

@@ -47,8 +47,8 @@ def test_ragged_tiles(ctx, rows, cols, m):
     w.free()
 
 
-@pytest.mark.parametrize("rows,cols", [(6912, 2560), (2560, 6912), (640, 2560)])
-@pytest.mark.parametrize("m", [16, 17, 32, 48, 64])
+@pytest.mark.parametrize("rows,cols", [(6912, 2560), (2560, 6912), (640, 2560), (13824, 2560)])
+@pytest.mark.parametrize("m", [2, 7, 16, 17, 32, 48, 64])
 def test_few_token_gemm_bitexact(ctx, rows, cols, m):
     # batched-decode sizes through the few-token kernel (16-row tiles, K split
     # over four wavefronts)
@@ -69,13 +69,14 @@ def test_few_token_gemm_bitexact(ctx, rows, cols, m):
 
 @pytest.mark.parametrize("rows,cols,m", [(23, 384, 17), (37, 2560, 33), (130, 300, 65), (5, 129, 16), (100, 1000, 200),
                                          (1, 256, 20), (257, 768, 130), (31, 8192, 64)])
-@pytest.mark.parametrize("ms", ["1", "2", "3", "4"])
-def test_few_token_kernel_ragged(ctx, monkeypatch, rows, cols, m, ms):
+@pytest.mark.parametrize("ms,ns", [("1", "1"), ("2", "1"), ("3", "2"), ("4", "1"), ("1", "2"), ("4", "2")])
+def test_few_token_kernel_ragged(ctx, monkeypatch, rows, cols, m, ms, ns):
     # LBT_GEMM_MODE=6 forces the few-token kernel at any token count;
-    # LBT_GEMM_SMALL_MS its tile width (16 * ms tokens)
+    # LBT_GEMM_SMALL_MS / _NS its tile (16 * ms tokens x 16 * ns rows)
     monkeypatch.setenv("LBT_GEMM_MODE", "6")
     monkeypatch.setenv("LBT_GEMM_SMALL_MS", ms)
-    announce(f"few-token ragged {rows}x{cols} m={m} ms={ms}")
+    monkeypatch.setenv("LBT_GEMM_SMALL_NS", ns)
+    announce(f"few-token ragged {rows}x{cols} m={m} ms={ms} ns={ns}")
     t, scale, x = golden_case(rows, cols, m, 7 * rows + cols + m)
     p = orc.pack(t)
     q, sa, su = orc.quantize_acts(x)
