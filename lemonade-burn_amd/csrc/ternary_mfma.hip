@@ -283,19 +283,19 @@ __global__ __launch_bounds__(kThreads) void tgemm_kernel(GemvArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Few-token GEMM (batched decode, 16..32 tokens): the weight stream is the
-// whole cost, so the grid is cut as finely as the 16 x 16 x 64 MFMA allows --
-// one workgroup per 16 rows (o/down of the 2B model: 160 workgroups instead of
-// 40 tiles of 64 rows; 32 rows, NS = 2, where that still leaves >= 384
-// workgroups, halving the activation re-reads) -- and its 4 wavefronts split K
-// into contiguous step
-// ranges.  Each wavefront issues every weight load of its range at once (at
-// most kSmallMaxSteps uint4 per lane), reads the activations (L2-resident,
-// 16 MS tokens) straight from global memory one step ahead, and the three
-// partial int32 tiles are added to wavefront 0's through LDS (exact, any
-// order) before the shared epilogue.  Operand layout as tgemm_kernel: lane
-// (li, lg) takes chunk 4p + lg of row li and, for MFMA kk of step p, the 16
-// activations of token li at k = 256 p + 128 (lg >> 1) + 32 kk + 16 (lg & 1).
+// Few-token GEMM (batched decode and short prefills, 2..32 tokens): the
+// weight stream is the whole cost, so the grid is cut as finely as the
+// 16 x 16 x 64 MFMA allows -- one workgroup per 16 rows (o/down of the 2B
+// model: 160 workgroups instead of 40 tiles of 64 rows; 32 rows, NS = 2, where
+// that still leaves >= 384 workgroups, halving the activation re-reads) --
+// and its 4 wavefronts split K into contiguous step ranges.  Each wavefront
+// issues every weight load of its range at once (at most kSmallMaxSteps uint4
+// per lane and row tile), reads the activations (L2-resident, 16 MS tokens)
+// straight from global memory one step ahead, and the three partial int32
+// tiles are added to wavefront 0's through LDS (exact, any order) before the
+// shared epilogue.  Operand layout as tgemm_kernel: lane (li, lg) takes chunk
+// 4p + lg of row li and, for MFMA kk of step p, the 16 activations of token
+// li at k = 256 p + 128 (lg >> 1) + 32 kk + 16 (lg & 1).
 constexpr int kSmallMaxSteps = 8;  // 256-k steps per wavefront: K <= 8192
 constexpr int kSmallWideRowTiles = 384;  // 32-row tiles from 384 * 32 rows
 
