@@ -101,7 +101,7 @@ def test_prefill_extreme_long_rows_mfma(ctx):
     w.free()
 
 
-@pytest.mark.parametrize("m", [96, 200])
+@pytest.mark.parametrize("m", [3, 8, 24, 96, 200])
 def test_fused_multi_mfma_equals_separate(ctx, m):
     cols = 2560
     rng = np.random.default_rng(77)
@@ -116,7 +116,7 @@ def test_fused_multi_mfma_equals_separate(ctx, m):
         w.free()
 
 
-@pytest.mark.parametrize("n", [16, 40, 130])
+@pytest.mark.parametrize("n", [2, 5, 16, 40, 130])
 def test_model_prefill_mfma_matches_oracle_and_gemv(ctx, monkeypatch, n):
     cfg = dict(hidden=512, intermediate=1536, heads=4, kv_heads=1, layers=2, vocab=1000, max_pos=1024)
     hip_cfg = lbt_hip.make_config(**cfg)
