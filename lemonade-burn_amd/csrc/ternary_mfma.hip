@@ -283,7 +283,8 @@ __global__ __launch_bounds__(kThreads) void tgemm_kernel(GemvArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Few-token GEMM (batched decode and short prefills, 2..32 tokens): the
+// Few-token GEMM (batched decode and short prefills, 2..32 tokens, and up to
+// 64 for the shapes with few 64 x 64 tiles): the
 // weight stream is the whole cost, so the grid is cut as finely as the
 // 16 x 16 x 64 MFMA allows -- one workgroup per 16 rows (o/down of the 2B
 // model: 160 workgroups instead of 40 tiles of 64 rows; 32 rows, NS = 2, where
@@ -298,6 +299,7 @@ __global__ __launch_bounds__(kThreads) void tgemm_kernel(GemvArgs a) {
 // li at k = 256 p + 128 (lg >> 1) + 32 kk + 16 (lg & 1).
 constexpr int kSmallMaxSteps = 8;  // 256-k steps per wavefront: K <= 8192
 constexpr int kSmallWideRowTiles = 384;  // 32-row tiles from 384 * 32 rows
+constexpr long kSmallFewTiles = 100;
 
 template <int OUT, int MS, int NS>
 __global__ __launch_bounds__(kThreads) void tgemm_small_kernel(GemvArgs a) {
@@ -699,7 +701,13 @@ int launch_ternary_mfma(lbt_ctx* ctx, const TernaryOp& op_in) {
     const char* sm = getenv("LBT_GEMM_SMALL_MAX");
     const int small_max = sm ? atoi(sm) : kSmallMaxTokens;
     const bool small_ok = a.kp <= 256 * 4 * kSmallMaxSteps;
-    if (small_ok && (gmode == 6 || (gmode == 0 && op.m <= small_max))) {
+    // up to 64 tokens the few-token kernel also serves the shapes the 64 x 64
+    // tiling would give fewer than kSmallFewTiles tiles (q/k/v, o, down of
+    // the 2B model at B = 33..64; LBT_GEMM_SMALL_TILES overrides)
+    const char* st = getenv("LBT_GEMM_SMALL_TILES");
+    const long t64 = (long)((total + 63) / 64) * ((op.m + 63) / 64);
+    const bool few_tiles = op.m <= 64 && t64 < (st ? atol(st) : kSmallFewTiles);
+    if (small_ok && (gmode == 6 || (gmode == 0 && (op.m <= small_max || few_tiles)))) {
         // 16-token tiles (more workgroups) measured faster than 32..64-token
         // ones at every batch served here; LBT_GEMM_SMALL_MS = 2..4 selects
         // the wider tiles
