@@ -75,8 +75,18 @@ struct DLayout<32> {
 // expressions.  Every load comes first, with clamped (always valid)
 // indices, so the loads are in flight together; the stores follow under the
 // bounds checks.
+// Per-token values of the 16 x 16 epilogue loaded ahead of the main loop
+// (epi_prefetch): sum(q), s_a and, for the residual add, the old outputs.
+template <int MS, int NS>
+struct EpiPre {
+    int qs[MS][4];
+    float sa[MS][4];
+    float old[MS][NS][4];
+};
+
 template <int OUT, int TM, int MS, int NS, typename AccT>
-__device__ __forceinline__ void mfma_epilogue(const GemvArgs& a, AccT (&acc)[MS][NS], int tok0, int row0) {
+__device__ __forceinline__ void mfma_epilogue(const GemvArgs& a, AccT (&acc)[MS][NS], int tok0, int row0,
+                                              const EpiPre<MS, NS>* pre = nullptr) {
     using L = DLayout<TM>;
     constexpr int R = L::R;
     const int lane = (int)threadIdx.x & 63, lr = L::row(lane);
@@ -89,6 +99,13 @@ __device__ __forceinline__ void mfma_epilogue(const GemvArgs& a, AccT (&acc)[MS]
         for (int r = 0; r < R; r++) {
             const int tok = tok0 + ms * TM + L::tok(lane, r);
             const int tc = tok < M ? tok : M - 1;
+            if constexpr (TM == 16) {
+                if (pre) {
+                    qs[ms][r] = pre->qs[ms][r];
+                    sa[ms][r] = pre->sa[ms][r];
+                    continue;
+                }
+            }
             qs[ms][r] = gload(a.qsum + tc);
             sa[ms][r] = a.qscale ? gload(a.qscale + tc) : 1.0f;
         }
@@ -163,6 +180,12 @@ __device__ __forceinline__ void mfma_epilogue(const GemvArgs& a, AccT (&acc)[MS]
                     for (int r = 0; r < R; r++) {
                         const int tok = tok0 + (h + mi) * TM + L::tok(lane, r);
                         const int tc = tok < M ? tok : M - 1;
+                        if constexpr (TM == 16) {
+                            if (pre) {
+                                old[mi][s][r] = pre->old[h + mi][s][r];
+                                continue;
+                            }
+                        }
                         old[mi][s][r] = gload((const float*)base[s] + (size_t)tc * ld[s]);
                     }
         }
@@ -297,11 +320,46 @@ __global__ __launch_bounds__(kThreads) void tgemm_kernel(GemvArgs a) {
 // shared epilogue.  Operand layout as tgemm_kernel: lane (li, lg) takes chunk
 // 4p + lg of row li and, for MFMA kk of step p, the 16 activations of token
 // li at k = 256 p + 128 (lg >> 1) + 32 kk + 16 (lg & 1).
+// Loads of mfma_epilogue's per-token values (16 x 16 tiles), the same
+// addresses it would use.
+template <int OUT, int MS, int NS>
+__device__ __forceinline__ void epi_prefetch(const GemvArgs& a, int tok0, int row0, EpiPre<MS, NS>& p) {
+    using L = DLayout<16>;
+    const int lane = (int)threadIdx.x & 63, lr = L::row(lane);
+    const int M = a.m;
+#pragma unroll
+    for (int ms = 0; ms < MS; ms++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int tok = tok0 + ms * 16 + L::tok(lane, r);
+            const int tc = tok < M ? tok : M - 1;
+            p.qs[ms][r] = gload(a.qsum + tc);
+            p.sa[ms][r] = a.qscale ? gload(a.qscale + tc) : 1.0f;
+        }
+    if (OUT != kOutF32Add) return;
+#pragma unroll
+    for (int s = 0; s < NS; s++) {
+        const int vr = row0 + s * 16 + lr;
+        int mt, ro;
+        resolve_row<OUT>(a, vr < a.total_rows ? vr : 0, mt, ro);
+        const float* base = (const float*)sel3(a.out, mt) + ro;
+        const int ld = sel3(a.rows, mt);
+#pragma unroll
+        for (int ms = 0; ms < MS; ms++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int tok = tok0 + ms * 16 + L::tok(lane, r);
+                const int tc = tok < M ? tok : M - 1;
+                p.old[ms][s][r] = gload(base + (size_t)tc * ld);
+            }
+    }
+}
+
 constexpr int kSmallMaxSteps = 8;  // 256-k steps per wavefront: K <= 8192
 constexpr int kSmallWideRowTiles = 384;  // 32-row tiles from 384 * 32 rows
 constexpr long kSmallFewTiles = 100;
 
-template <int OUT, int MS, int NS>
+template <int OUT, int MS, int NS, bool PF = false>
 __global__ __launch_bounds__(kThreads) void tgemm_small_kernel(GemvArgs a) {
     __shared__ __align__(16) v4i part[3][MS][NS][64];
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
@@ -345,6 +403,8 @@ __global__ __launch_bounds__(kThreads) void tgemm_small_kernel(GemvArgs a) {
             }
     };
 
+    EpiPre<MS, NS> pre;
+    if (PF && w == 0) epi_prefetch<OUT, MS, NS>(a, m0, n0, pre);
     v4i acc[MS][NS];
 #pragma unroll
     for (int ms = 0; ms < MS; ms++)
@@ -383,7 +443,7 @@ __global__ __launch_bounds__(kThreads) void tgemm_small_kernel(GemvArgs a) {
 #pragma unroll
         for (int ns = 0; ns < NS; ns++)
             acc[ms][ns] += (part[0][ms][ns][lane] + part[1][ms][ns][lane]) + part[2][ms][ns][lane];
-    mfma_epilogue<OUT, 16>(a, acc, m0, n0);
+    mfma_epilogue<OUT, 16>(a, acc, m0, n0, PF ? &pre : nullptr);
 }
 
 // ---------------------------------------------------------------------------
@@ -630,16 +690,27 @@ hipError_t launch_tiles2(const GemvArgs& a, int out_mode, dim3 grid, hipStream_t
 }
 
 
-template <int MS, int NS>
-hipError_t launch_small(const GemvArgs& a, int out_mode, dim3 grid, hipStream_t s, hipEvent_t e0, hipEvent_t e1) {
+template <int MS, int NS, bool PF>
+hipError_t launch_small_pf(const GemvArgs& a, int out_mode, dim3 grid, hipStream_t s, hipEvent_t e0, hipEvent_t e1) {
     switch (out_mode) {
-        case kOutI32: hipExtLaunchKernelGGL((tgemm_small_kernel<kOutI32, MS, NS>), grid, dim3(kThreads), 0, s, e0, e1, 0, a); break;
-        case kOutF32: hipExtLaunchKernelGGL((tgemm_small_kernel<kOutF32, MS, NS>), grid, dim3(kThreads), 0, s, e0, e1, 0, a); break;
-        case kOutF32Add: hipExtLaunchKernelGGL((tgemm_small_kernel<kOutF32Add, MS, NS>), grid, dim3(kThreads), 0, s, e0, e1, 0, a); break;
-        case kOutRelu2: hipExtLaunchKernelGGL((tgemm_small_kernel<kOutRelu2, MS, NS>), grid, dim3(kThreads), 0, s, e0, e1, 0, a); break;
-        default: hipExtLaunchKernelGGL((tgemm_small_kernel<kOutQKV, MS, NS>), grid, dim3(kThreads), 0, s, e0, e1, 0, a); break;
+        case kOutI32: hipExtLaunchKernelGGL((tgemm_small_kernel<kOutI32, MS, NS, PF>), grid, dim3(kThreads), 0, s, e0, e1, 0, a); break;
+        case kOutF32: hipExtLaunchKernelGGL((tgemm_small_kernel<kOutF32, MS, NS, PF>), grid, dim3(kThreads), 0, s, e0, e1, 0, a); break;
+        case kOutF32Add: hipExtLaunchKernelGGL((tgemm_small_kernel<kOutF32Add, MS, NS, PF>), grid, dim3(kThreads), 0, s, e0, e1, 0, a); break;
+        case kOutRelu2: hipExtLaunchKernelGGL((tgemm_small_kernel<kOutRelu2, MS, NS, PF>), grid, dim3(kThreads), 0, s, e0, e1, 0, a); break;
+        default: hipExtLaunchKernelGGL((tgemm_small_kernel<kOutQKV, MS, NS, PF>), grid, dim3(kThreads), 0, s, e0, e1, 0, a); break;
     }
     return hipGetLastError();
+}
+
+template <int MS, int NS>
+hipError_t launch_small(const GemvArgs& a, int out_mode, dim3 grid, hipStream_t s, hipEvent_t e0, hipEvent_t e1) {
+    // 16-token tiles: the epilogue's per-token loads go out with the weight
+    // stream (measured +1.5-2% at B = 8..64); LBT_GEMM_SMALL_PF=0 turns it off
+    if constexpr (MS == 1) {
+        static const bool pf = !getenv("LBT_GEMM_SMALL_PF") || atoi(getenv("LBT_GEMM_SMALL_PF")) != 0;
+        if (pf) return launch_small_pf<MS, NS, true>(a, out_mode, grid, s, e0, e1);
+    }
+    return launch_small_pf<MS, NS, false>(a, out_mode, grid, s, e0, e1);
 }
 
 }  // namespace
