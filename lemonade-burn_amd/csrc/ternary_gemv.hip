@@ -496,7 +496,8 @@ int launch_ternary(lbt_ctx* ctx, const TernaryOp& op_in) {
         op.tok_pos = nullptr;
         op.pos_dev = nullptr;
     }
-    static const int mfma_min = getenv("LBT_MFMA_MIN") ? atoi(getenv("LBT_MFMA_MIN")) : kMfmaMinTokens;
+    const char* mm = getenv("LBT_MFMA_MIN");
+    const int mfma_min = mm ? atoi(mm) : kMfmaMinTokens;
     if (op.m >= (mfma_min > 1 ? mfma_min : 2) && !getenv("LBT_NO_MFMA")) return launch_ternary_mfma(ctx, op);
     return launch_ternary_gemv(ctx, op);
 }
