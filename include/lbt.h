@@ -200,6 +200,13 @@ int lbt_model_decode_greedy(lbt_model* m, lbt_cache* c, uint32_t first, size_t s
  * 1 = the opt-in int8 head (q8head.rs), quantized on the device from the
  * tied embedding when first selected.  A cached decode-step graph is rebuilt. */
 int lbt_model_set_head(lbt_model* m, int kind);
+/* How batch-1 decode steps (generate_greedy / decode_greedy) run; no
+ * reference counterpart (the reference's step is BitNet::forward on one token,
+ * crates/lb-model/src/model.rs:305-374, on the CPU): 0 = all decoder layers of
+ * a token in one dispatch, 1 = one dispatch per kernel, replayed as a
+ * captured graph (default).  Both give the same bits; shapes the one-dispatch step
+ * does not take use the multi-kernel step. */
+int lbt_model_set_decode(lbt_model* m, int kind);
 /* Residual stream of the last forward ([n, hidden] f32) for layer-level tests. */
 int lbt_model_read_hidden(lbt_model* m, float* out, size_t n);
 
@@ -261,11 +268,11 @@ int lbt_sched_release(lbt_sched* s, uint64_t id);
  * When enabled, every ternary GEMV/GEMM launch of the model loop is bracketed
  * by HIP events on the context stream; totals are per kernel class
  * (0 = ternary decode GEMV, 1 = ternary prefill GEMM, 2 = bf16 LM head,
- * 3 = attention, 4 = other). */
+ * 3 = attention, 4 = other, 5 = one-dispatch decode step of all layers). */
 typedef struct lbt_prof {
-    double ms[5];
-    double bytes[5];
-    uint64_t launches[5];
+    double ms[6];
+    double bytes[6];
+    uint64_t launches[6];
 } lbt_prof;
 int lbt_prof_enable(lbt_ctx* ctx, int on);
 int lbt_prof_read(lbt_ctx* ctx, lbt_prof* out, int reset);

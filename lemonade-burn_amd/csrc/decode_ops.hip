@@ -76,9 +76,9 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(const float* q, int
     if (kGuess && (rp.tok_pos || rp.pos_dev))  // the position is read after the first K/V loads
         attention_split_ku<LK, 4, kGuess>(q + (size_t)t * H, h, nh, s, rp.tok_pos ? 0 : t, kc + kvoff, vc + kvoff,
                                         scaling, ot, mlt, sc, sh, rp.tok_pos ? rp.tok_pos + t : rp.pos_dev, cap);
-    else
-        attention_split<LK>(q + (size_t)t * H, h, nh, s, rp.pos0 + t, kc + kvoff, vc + kvoff, scaling, ot, mlt, sc,
-                            sh);
+    else  // the row's position (a graph-replayed step reads it from the device)
+        attention_split<LK>(q + (size_t)t * H, h, nh, s, row_position(rp, t), kc + kvoff, vc + kvoff, scaling, ot,
+                            mlt, sc, sh);
     LBT_ATR(7)
 }
 

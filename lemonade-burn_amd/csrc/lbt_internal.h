@@ -70,7 +70,7 @@ int hip_err(lbt_ctx* ctx, hipError_t e, const char* what);
 int ws_reserve(lbt_ctx* ctx, size_t bytes, void** out);
 
 // Profiling brackets around one launch (no-ops unless ctx->prof).
-enum ProfClass { kProfGemv = 0, kProfGemm = 1, kProfHead = 2, kProfAttn = 3, kProfOther = 4 };
+enum ProfClass { kProfGemv = 0, kProfGemm = 1, kProfHead = 2, kProfAttn = 3, kProfOther = 4, kProfStep = 5 };
 // prof_pair hands out a start/stop event pair (null when profiling is off)
 // for hipExtLaunchKernelGGL, which timestamps the dispatch itself, so the
 // measured time is the kernel's execution (as rocprofv3 reports it).
@@ -204,40 +204,6 @@ int launch_fill_u64(lbt_ctx* ctx, unsigned long long* p, int n, unsigned long lo
 // Streaming device copy (16-byte granules, byte tail).
 int launch_copy(lbt_ctx* ctx, void* dst, const void* src, size_t bytes);
 int launch_set_state(lbt_ctx* ctx, int* state, int pos, int slot);
-
-// ---- persistent decode step (one dispatch for all layers of one token) -----
-struct PersistHost {
-    lbt_config cfg;
-    const uint8_t* const* w;   // device array [layers * 7]
-    const float* wscale;       // device array [layers * 7]
-    const float* const* norm;  // device array [layers * 4]
-    const uint16_t* embed;
-    const float* cos_t;
-    const float* sin_t;
-    uint16_t* kc;
-    uint16_t* vc;
-    int cap;
-    size_t layer_kv;
-    float scaling;
-    int* state;  // [0] position - 1, [1] output slot, [2] barrier epoch
-    unsigned long long* key;
-    uint32_t* tok_out;
-    float* x;
-    float* q;
-    float* att;
-    float* ao;   // attention split outputs of one row [kAttnSplits][hidden]
-    float* aml;  // attention split (max, sum) of one row [kAttnSplits][heads][2]
-    float* h;
-    unsigned* flags;
-    unsigned* go;
-    unsigned* err;
-    int rpw[4];
-    unsigned long long* trace;  // optional per-phase timestamps (LBT_PERSIST_TRACE)
-};
-// 1 if the persistent kernel handles this shape with G workgroups (fills the
-// rows per workgroup), else 0 with a reason.
-int persistent_supported(const lbt_config& c, int cap, int G, int* rpw, const char** why);
-int launch_decode_persistent(lbt_ctx* ctx, const PersistHost& h, int G, hipStream_t s);
 
 // Synthetic weights (same generator as oracle/lbt_oracle.c or_synth_*).
 int launch_synth_packed(lbt_ctx* ctx, uint64_t seed, uint64_t tensor, int rows, int cols, uint8_t* out);

@@ -26,6 +26,7 @@
 #include <string>
 #include <vector>
 
+#include "decode_step.h"
 #include "lbt_internal.h"
 
 using namespace lbt;
@@ -245,11 +246,18 @@ struct lbt_model {
     int* state = nullptr;  // device {position - 1, output slot, barrier epoch, spare}
     hipGraphExec_t step_exec = nullptr;
     const void* step_key[6] = {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
-    // persistent decode step: device tables of the layers and the barrier words
+    // one-dispatch decode step (decode_step.hip): device tables of the layers,
+    // the epoch-tagged activation words, the error word, the plan
+    int decode_kind = 1;   // 0: one-dispatch step, 1: multi-kernel graph step
     void* ptab = nullptr;  // [layers*7] weight ptrs, [layers*7] scales, [layers*4] norm ptrs
-    unsigned long long* trace = nullptr;
-    unsigned* bar = nullptr;  // flags [G*16], go, err
-    int bar_g = 0;
+    unsigned long long* ll = nullptr;  // x, q/k/v, partials, h words, then the error word
+    size_t ll_bytes = 0;
+    double epochs = 0.0;  // epochs used since the words were last cleared
+    lbt::StepPlan plan;
+    int plan_cap = 0;
+    StepArgs* dargs = nullptr;  // the step's arguments in device memory
+    unsigned long long* trace = nullptr;  // phase timestamps (LBT_STEP_TRACE, read at model creation)
+    bool want_trace = false;
 };
 
 namespace lbt {
@@ -317,6 +325,7 @@ int validate_config(lbt_ctx* ctx, const lbt_config& c) {
 // Device buffers and RoPE tables shared by load and synthetic creation.
 int model_alloc(lbt_model* m) {
     lbt_ctx* ctx = m->ctx;
+    m->want_trace = getenv("LBT_STEP_TRACE") != nullptr;
     const lbt_config& c = m->cfg;
     m->hd = c.hidden_size / c.num_attention_heads;
     size_t wbytes = 0;
@@ -595,21 +604,39 @@ int ensure_state(lbt_model* m) {
     return LBT_OK;
 }
 
-// Persistent-grid workgroups (LBT_PERSIST_G overrides) or 0 when the
-// persistent step is off or the shape does not fit.  The persistent step is
-// opt-in (LBT_DECODE=persistent): on the 2B shape it is still slower than the
-// graph-replayed per-kernel step.
-int persist_grid(lbt_model* m, lbt_cache* c, int* rpw) {
-    const char* mode = getenv("LBT_DECODE");
-    if (!mode || strcmp(mode, "persistent") != 0) return 0;
-    int G = 64;
-    if (const char* g = getenv("LBT_PERSIST_G")) G = atoi(g);
-    if (G < 1 || G > 256) return 0;
-    const char* why = nullptr;
-    return persistent_supported(m->cfg, c->cap, G, rpw, &why) ? G : 0;
+// Words of the epoch-tagged activation buffers of the one-dispatch step.
+struct StepWords {
+    size_t x, qkv, part, h, total;
+};
+StepWords step_words(const lbt_config& c, int hd) {
+    StepWords w;
+    const size_t H = (size_t)c.hidden_size, KV = (size_t)c.num_key_value_heads * hd;
+    w.x = (H + 1) & ~(size_t)1;
+    w.qkv = (H + 2 * KV + 1) & ~(size_t)1;
+    w.part = ((size_t)kAttnSplits * H + (size_t)kAttnSplits * c.num_attention_heads * 2 + 1) & ~(size_t)1;
+    w.h = ((size_t)c.intermediate_size + 1) & ~(size_t)1;
+    w.total = w.x + w.qkv + w.part + w.h + 2;  // + the error word
+    return w;
 }
 
-int persist_prepare(lbt_model* m, lbt_cache* c, int G, const int* rpw, PersistHost& h) {
+// Plan of the one-dispatch step for this cache capacity, or 0 when the model
+// uses the multi-kernel step (selected, or a shape the step does not take).
+int step_ready(lbt_model* m, lbt_cache* c) {
+    if (m->decode_kind != 0) return 0;
+    if (m->plan.fn && m->plan_cap == c->cap) return 1;
+    const char* why = nullptr;
+    lbt::StepPlan pl;
+    pl.G = m->ctx->cus;
+    if (!step_plan(m->cfg, c->cap, pl.G, pl, &why)) return 0;
+    double bytes = 0.0;
+    for (int i = 0; i < 7 * m->cfg.num_hidden_layers; i++) bytes += (double)m->lin[i].rows * (double)(m->lin[i].kp / 4);
+    pl.bytes = bytes;
+    m->plan = pl;
+    m->plan_cap = c->cap;
+    return 1;
+}
+
+int step_prepare(lbt_model* m, lbt_cache* c, StepArgs& a) {
     lbt_ctx* ctx = m->ctx;
     const lbt_config& cf = m->cfg;
     const int L = cf.num_hidden_layers;
@@ -630,82 +657,90 @@ int persist_prepare(lbt_model* m, lbt_cache* c, int G, const int* rpw, PersistHo
         LBT_HIP(ctx, hipMemcpy(t + b0, ws.data(), b1, hipMemcpyHostToDevice));
         LBT_HIP(ctx, hipMemcpy(t + ((b0 + b1 + 7) & ~(size_t)7), np.data(), b2, hipMemcpyHostToDevice));
     }
-    if (m->bar_g < G) {
-        // flags are monotonic epochs; fresh buffers start at 0 with the epoch
-        if (m->bar) hipFree(m->bar);
-        m->bar = nullptr;
-        LBT_HIP(ctx, hipMalloc(&m->bar, ((size_t)G * 16 + 32) * 4));
-        LBT_HIP(ctx, hipMemset(m->bar, 0, ((size_t)G * 16 + 32) * 4));
-        LBT_HIP(ctx, hipMemset(m->state + 2, 0, sizeof(int)));
-        m->bar_g = G;
+    const StepWords sw = step_words(cf, m->hd);
+    const double per_step = 5.0 * L;
+    if (!m->ll || m->epochs + per_step * 4096.0 > 2147483648.0) {
+        // fresh words (epoch 0) and epoch base 0; also before the 32-bit epochs
+        // could wrap (a word must never show a future epoch)
+        if (!m->ll) {
+            m->ll_bytes = sw.total * 8;
+            LBT_HIP(ctx, hipMalloc(&m->ll, m->ll_bytes));
+        }
+        LBT_HIP(ctx, hipMemsetAsync(m->ll, 0, m->ll_bytes, ctx->stream));
+        LBT_HIP(ctx, hipMemsetAsync(m->state + 2, 0, sizeof(int), ctx->stream));
+        m->epochs = 0.0;
     }
     const size_t b0 = (size_t)L * 7 * 8, b1 = (size_t)L * 7 * 4;
-    h.cfg = cf;
-    h.w = (const uint8_t* const*)m->ptab;
-    h.wscale = (const float*)((char*)m->ptab + b0);
-    h.norm = (const float* const*)((char*)m->ptab + ((b0 + b1 + 7) & ~(size_t)7));
-    h.embed = m->embed;
-    h.cos_t = m->cos_t;
-    h.sin_t = m->sin_t;
-    h.kc = c->k;
-    h.vc = c->v;
-    h.cap = c->cap;
-    h.layer_kv = (size_t)cf.num_key_value_heads * c->cap * m->hd;
-    h.scaling = m->scaling;
-    h.state = m->state;
-    h.key = m->key;
-    h.tok_out = m->tok_out;
-    h.x = m->x;
-    h.q = m->q;
-    h.att = m->att;
-    h.ao = m->ao;
-    h.aml = m->aml;
-    h.h = m->h;
-    h.flags = m->bar;
-    h.go = m->bar + (size_t)G * 16;
-    h.err = m->bar + (size_t)G * 16 + 16;
-    for (int i = 0; i < 4; i++) h.rpw[i] = rpw[i];
-    h.trace = nullptr;
-    if (getenv("LBT_PERSIST_TRACE")) {
-        if (!m->trace) LBT_HIP(ctx, hipMalloc(&m->trace, 8192 * 8));
-        h.trace = m->trace;
-    }
+    a = StepArgs{};
+    a.w = (const uint8_t* const*)m->ptab;
+    a.wscale = (const float*)((char*)m->ptab + b0);
+    a.norm = (const float* const*)((char*)m->ptab + ((b0 + b1 + 7) & ~(size_t)7));
+    a.embed = m->embed;
+    a.cos_t = m->cos_t;
+    a.sin_t = m->sin_t;
+    a.kc = c->k;
+    a.vc = c->v;
+    a.cap = c->cap;
+    a.layer_kv = (size_t)cf.num_key_value_heads * c->cap * m->hd;
+    a.layers = L;
+    a.H = cf.hidden_size;
+    a.I = cf.intermediate_size;
+    a.nh = cf.num_attention_heads;
+    a.kvh = cf.num_key_value_heads;
+    a.hd = m->hd;
+    a.KV = cf.num_key_value_heads * m->hd;
+    a.vocab = cf.vocab_size;
+    a.eps = (float)cf.rms_norm_eps;
+    a.scaling = m->scaling;
+    a.state = m->state;
+    a.key = m->key;
+    a.tok_out = m->tok_out;
+    a.xout = m->x;
+    a.llx = m->ll;
+    a.llqkv = a.llx + sw.x;
+    a.llpart = a.llqkv + sw.qkv;
+    a.llh = a.llpart + sw.part;
+    a.err = (unsigned*)(a.llh + sw.h);
+    if (m->want_trace && !m->trace) LBT_HIP(ctx, hipMalloc(&m->trace, (size_t)L * 64 * 8));
+    a.trace = m->trace;
+    step_fill(m->plan, cf, a);
+    if (!m->dargs) LBT_HIP(ctx, hipMalloc(&m->dargs, sizeof(StepArgs)));
+    // stream-ordered: earlier steps have read the previous arguments
+    LBT_HIP(ctx, hipMemcpyAsync(m->dargs, &a, sizeof(StepArgs), hipMemcpyHostToDevice, ctx->stream));
     return LBT_OK;
 }
 
-// After a synchronize: a barrier timeout inside the persistent step is an error.
-int persist_check(lbt_model* m) {
-    if (!m->bar) return LBT_OK;
+// After a synchronize: a wait that timed out inside the step is an error.
+int step_check(lbt_model* m) {
+    if (!m->ll) return LBT_OK;
     lbt_ctx* ctx = m->ctx;
+    const StepWords sw = step_words(m->cfg, m->hd);
+    unsigned* e = (unsigned*)(m->ll + sw.total - 2);
     unsigned err = 0;
-    unsigned* e = m->bar + (size_t)m->bar_g * 16 + 16;
     LBT_HIP(ctx, hipMemcpy(&err, e, 4, hipMemcpyDeviceToHost));
     if (err) {
+        // the words may hold any epoch now: start over from fresh words
+        m->epochs = 1e300;
         hipMemset(e, 0, 4);
-        return set_err(ctx, LBT_E_DEVICE, "persistent decode: grid barrier timed out");
+        return set_err(ctx, LBT_E_DEVICE, "decode step: a wait for another workgroup timed out");
     }
-    if (m->trace && getenv("LBT_PERSIST_TRACE")) {
-        // debugging aid: mean duration of each traced segment of the last step
-        std::vector<unsigned long long> t(8192);
-        LBT_HIP(ctx, hipMemcpy(t.data(), m->trace, 8192 * 8, hipMemcpyDeviceToHost));
+    if (m->trace) {
+        // measurement aid: mean time of each traced segment of the last step
         const int L = m->cfg.num_hidden_layers;
+        std::vector<unsigned long long> t((size_t)L * 64);
+        LBT_HIP(ctx, hipMemcpy(t.data(), m->trace, t.size() * 8, hipMemcpyDeviceToHost));
         for (int half = 0; half < 2; half++) {
-            double seg[16] = {0};
-            for (int l = 0; l < L; l++)
-                for (int k = 1; k < 16; k++) {
-                    const unsigned long long* r = &t[half * 4096 + l * 16];
-                    seg[k] += (double)(r[k] - r[k - 1]) / L;
-                }
-            fprintf(stderr, "persistent trace wg%s (us, 100 MHz ticks/100):", half ? "-last" : "0");
-            for (int k = 1; k < 16; k++) fprintf(stderr, " %d:%.2f", k, seg[k] / 100.0);
-            double wg = 0, wd = 0;
-            for (int l = 0; l < L; l++) {
-                const unsigned long long* r = &t[half * 4096 + l * 16];
-                const unsigned long long* x = &t[half * 4096 + 2048 + l * 4];
-                wg += (double)(x[0] - r[10]) / L;
-                wd += (double)(x[1] - r[13]) / L;
+            double seg[32] = {0};
+            for (int l = 1; l < L; l++) {
+                const unsigned long long* r = &t[(size_t)half * L * 32 + (size_t)l * 32];
+                for (int k = 1; k <= 21; k++) seg[k] += (double)(long long)(r[k] - r[k - 1]) / (L - 1);
+                seg[22] += (double)(long long)(r[22] - r[9]) / (L - 1);
+                seg[23] += (double)(long long)(r[23] - r[22]) / (L - 1);
+                seg[24] += (double)r[24] / (L - 1) * 100.0;
             }
-            fprintf(stderr, " | weights-wait gu %.2f down %.2f\n", wg / 100.0, wd / 100.0);
+            fprintf(stderr, "step trace wg%s (us):", half ? "-last" : "0");
+            for (int k = 1; k <= 24; k++) fprintf(stderr, " %d:%.2f", k, seg[k] / 100.0);
+            fprintf(stderr, "\n");
         }
     }
     return LBT_OK;
@@ -720,17 +755,15 @@ int decode_steps(lbt_model* m, lbt_cache* c, int n, int slot0) {
     lbt_ctx* ctx = m->ctx;
     if (n <= 0) return LBT_OK;
     int rc;
-    int rpw[4];
-    const int G = persist_grid(m, c, rpw);
-    if (G > 0) {
-        PersistHost h;
-        if ((rc = persist_prepare(m, c, G, rpw, h))) return rc;
+    if (step_ready(m, c)) {
+        StepArgs a;
+        if ((rc = step_prepare(m, c, a))) return rc;
         if ((rc = launch_set_state(ctx, m->state, c->len - 1, slot0))) return rc;
         const lbt_config& cf = m->cfg;
         for (int s = 0; s < n; s++) {
-            if ((rc = launch_decode_persistent(ctx, h, G, ctx->stream))) return rc;
-            if ((rc = model_head(m, m->x, 1, (float)cf.rms_norm_eps, nullptr, m->key, nullptr)))
-                return rc;
+            if ((rc = launch_decode_step(ctx, m->plan, m->dargs, ctx->stream))) return rc;
+            m->epochs += 5.0 * cf.num_hidden_layers;
+            if ((rc = model_head(m, m->x, 1, (float)cf.rms_norm_eps, nullptr, m->key, nullptr))) return rc;
         }
         c->len += n;
         m->last_n = 1;
@@ -971,7 +1004,9 @@ void lbt_model_free(lbt_model* m) {
     hipStreamSynchronize(m->ctx->stream);
     if (m->step_exec) hipGraphExecDestroy(m->step_exec);
     if (m->ptab) hipFree(m->ptab);
-    if (m->bar) hipFree(m->bar);
+    if (m->ll) hipFree(m->ll);
+    if (m->trace) hipFree(m->trace);
+    if (m->dargs) hipFree(m->dargs);
     void* bufs[] = {m->wbuf, m->fbuf, m->embed, m->cos_t, m->sin_t, m->x,   m->q,       m->k,
                     m->v,    m->att,  m->h,     m->logits, m->toks, m->key, m->tok_out, m->state,
                     m->ao,   m->aml,  m->q8,    m->q8s};
@@ -1091,7 +1126,7 @@ int lbt_model_generate_greedy(lbt_model* m, const uint32_t* prompt, size_t n, si
     }
     hipError_t e = hipStreamSynchronize(ctx->stream);
     if (!rc && e != hipSuccess) rc = hip_err(ctx, e, "generate");
-    if (!rc) rc = persist_check(m);
+    if (!rc) rc = step_check(m);
     if (!rc) {
         float a = 0, b = 0;
         hipEventElapsedTime(&a, e0, e1);
@@ -1132,7 +1167,7 @@ int lbt_model_decode_greedy(lbt_model* m, lbt_cache* c, uint32_t first, size_t s
     hipEventRecord(e1, ctx->stream);
     hipError_t e = hipStreamSynchronize(ctx->stream);
     if (!rc && e != hipSuccess) rc = hip_err(ctx, e, "decode");
-    if (!rc) rc = persist_check(m);
+    if (!rc) rc = step_check(m);
     if (!rc) {
         float a = 0;
         hipEventElapsedTime(&a, e0, e1);
@@ -1173,6 +1208,14 @@ int lbt_model_set_head(lbt_model* m, int kind) {
         m->step_exec = nullptr;
     }
     m->head_kind = kind;
+    return LBT_OK;
+}
+
+int lbt_model_set_decode(lbt_model* m, int kind) {
+    if (!m) return LBT_E_INVALID;
+    if (kind != 0 && kind != 1)
+        return set_err(m->ctx, LBT_E_INVALID, "set_decode: kind must be 0 (one dispatch) or 1 (multi-kernel)");
+    m->decode_kind = kind;
     return LBT_OK;
 }
 

@@ -45,7 +45,7 @@ class LbtConfig(C.Structure):
 
 
 class LbtProf(C.Structure):
-    _fields_ = [("ms", C.c_double * 5), ("bytes", C.c_double * 5), ("launches", C.c_uint64 * 5)]
+    _fields_ = [("ms", C.c_double * 6), ("bytes", C.c_double * 6), ("launches", C.c_uint64 * 6)]
 
 
 SIGNATURES = {
@@ -99,6 +99,7 @@ SIGNATURES = {
     "lbt_model_decode_greedy": (i32, [vp, vp, C.c_uint32, sz, vp, vp]),
     "lbt_model_read_hidden": (i32, [vp, vp, sz]),
     "lbt_model_set_head": (i32, [vp, i32]),
+    "lbt_model_set_decode": (i32, [vp, i32]),
     "lbt_batch_new": (i32, [vp, i32, i32, C.POINTER(vp)]),
     "lbt_batch_free": (None, [vp]),
     "lbt_batch_len": (i32, [vp, i32]),
@@ -261,7 +262,7 @@ class Ctx:
     def prof_read(self, reset: bool = True) -> dict:
         p = LbtProf()
         self.check(self.lib.lbt_prof_read(self.h, C.byref(p), 1 if reset else 0))
-        names = ["gemv", "gemm", "head", "attn", "other"]
+        names = ["gemv", "gemm", "head", "attn", "other", "step"]
         return {n: {"ms": p.ms[i], "bytes": p.bytes[i], "launches": int(p.launches[i])} for i, n in enumerate(names)}
 
 
@@ -359,6 +360,10 @@ class Model:
         h = C.c_void_p()
         self.ctx.check(self.ctx.lib.lbt_cache_new(self.h, C.byref(h)))
         return Cache(self, h)
+
+    def set_decode(self, kind: int):
+        """0: all layers of a decode token in one dispatch (default); 1: one dispatch per kernel (graph)."""
+        self.ctx.check(self.ctx.lib.lbt_model_set_decode(self.h, kind))
 
     def set_head(self, kind: int):
         """0 = the exact tied bf16 head, 1 = the opt-in int8 head (q8head.rs)."""
