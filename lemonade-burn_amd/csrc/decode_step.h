@@ -7,7 +7,8 @@
 namespace lbt {
 
 constexpr int kStepMaxRows = 64;  // o / down rows per workgroup (kept in LDS for the residual)
-constexpr int kStepMaxCpl = 8;    // 16-byte row chunks per lane (activations held in registers)
+constexpr int kStepMaxCpl = 8;
+
 
 // Row slice of one linear per workgroup: rpw virtual rows, L lanes per row,
 // cpl 16-byte chunks per lane, the slice's LDS bytes start at `off`.
@@ -16,9 +17,11 @@ struct StepTile {
 };
 
 struct StepArgs {
-    const uint8_t* const* w;   // device [layers * 7] packed matrices
-    const float* wscale;       // device [layers * 7]
-    const float* const* norm;  // device [layers * 4]: input, post_attention, attn_sub, ffn_sub
+    const uint8_t* w0[7];      // layer 0's packed matrices (q, k, v, o, gate, up, down)
+    size_t wstride;            // bytes from one layer's matrices to the next's
+    const float* n0[4];        // layer 0's norm gains: input, post_attention, attn_sub, ffn_sub
+    size_t nstride;            // floats from one layer's norm gains to the next's
+    const float* wscale;       // device [layers * 7] per-tensor weight scales
     const uint16_t* embed;
     const float* cos_t;
     const float* sin_t;
@@ -36,14 +39,15 @@ struct StepArgs {
     unsigned long long* llx;    // [H]
     unsigned long long* llqkv;  // [H + 2 KV]: rotated q, k (bf16 values), v (bf16 values)
     unsigned long long* llpart; // [kAttnSplits][H] split outputs, then [kAttnSplits][nh][2] (max, sum)
+    unsigned long long* llatt;  // [H] attention output (the splits combined)
     unsigned long long* llh;    // [I]
     unsigned* err;
     StepTile t[4];  // q/k/v, o, gate/up, down
     int rt_off[4];  // LDS bytes of each phase's row table
-    int xq_off, sc_off;
+    int xq_off, sc_off, ws_off;
     int CH, CI;     // 16-byte chunks of a packed row of K = H, K = I
-    // optional phase timestamps of workgroups 0 and G-1 ([2][layers][16]
-    // ticks of the 100 MHz clock), for measurements only
+    // optional phase timestamps of every workgroup ([G][layers][32] ticks of
+    // the 100 MHz clock), for measurements only
     unsigned long long* trace;
 };
 
@@ -51,7 +55,7 @@ struct StepPlan {
     int G = 0;
     StepTile t[4];
     int rt_off[4] = {0, 0, 0, 0};
-    int xq_off = 0, sc_off = 0;
+    int xq_off = 0, sc_off = 0, ws_off = 0;
     size_t lds = 0;
     const void* fn = nullptr;
     double bytes = 0.0;  // algorithmic bytes per dispatch (packed weights)

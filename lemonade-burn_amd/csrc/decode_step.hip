@@ -184,12 +184,13 @@ __device__ __forceinline__ void build_rowtab(const GemvArgs& g, const StepTile& 
 // t % 4), chunk round i < cpl: 64 lanes x 16 bytes at off + (t*cpl + i)*1024,
 // lane l holding chunk l%L + L*i of its row.  Every lane loads (chunks past
 // the row re-read its last one), so every lane counts the same loads.
-__device__ __forceinline__ void tile_load(const StepTile T, const uint8_t* w0, const uint8_t* w1, const uint8_t* w2,
-                                          int C, const uint32_t* rowtab, int8_t* lds) {
+__device__ __forceinline__ int tile_load(const StepTile T, const uint8_t* w0, const uint8_t* w1, const uint8_t* w2,
+                                         int C, const uint32_t* rowtab, int8_t* lds) {
     const int lane = (int)threadIdx.x & 63, w = (int)threadIdx.x >> 6;
     const int L = T.L, R = 64 / L, cpl = T.cpl, j = lane % L;
     const int ntiles = (T.rpw + R - 1) / R;
     const size_t rb = (size_t)C * 16;  // bytes per packed row
+    int n = 0;
     for (int t = w; t < ntiles; t += 4) {
         const uint32_t e = rowtab[t * 64 + lane];
         const uint32_t mat = e >> 30;
@@ -200,6 +201,45 @@ __device__ __forceinline__ void tile_load(const StepTile T, const uint8_t* w0, c
             __builtin_amdgcn_global_load_lds((const void*)(rowp + (c < C ? c : C - 1)),
                                              (lds_void*)(lds + T.off + (t * cpl + i) * 1024), 16, 0, 0);
         }
+        n += cpl;
+    }
+    return n;  // loads this wavefront issued
+}
+
+// One tile of this wavefront's share of a slice (tile w + 4*lt); returns the
+// loads issued (0 past the wavefront's tiles).
+__device__ __forceinline__ int tile_load_slot(const StepTile T, const uint8_t* w0, const uint8_t* w1,
+                                              const uint8_t* w2, int C, const uint32_t* rowtab, int8_t* lds,
+                                              int lt) {
+    const int lane = (int)threadIdx.x & 63, w = (int)threadIdx.x >> 6;
+    const int L = T.L, R = 64 / L, cpl = T.cpl, j = lane % L;
+    const int ntiles = (T.rpw + R - 1) / R, t = w + 4 * lt;
+    if (t >= ntiles) return 0;
+    const uint32_t e = rowtab[t * 64 + lane];
+    const uint32_t mat = e >> 30;
+    const uint8_t* base = mat == 0 ? w0 : (mat == 1 ? w1 : w2);
+    const uint4* rowp = (const uint4*)(base + (size_t)(e & 0x3fffffffu) * (size_t)C * 16);
+    for (int i = 0; i < cpl; i++) {
+        const int c = j + L * i;
+        __builtin_amdgcn_global_load_lds((const void*)(rowp + (c < C ? c : C - 1)),
+                                         (lds_void*)(lds + T.off + (t * cpl + i) * 1024), 16, 0, 0);
+    }
+    return cpl;
+}
+__device__ __forceinline__ int tile_slots(const StepTile T) {
+    const int w = (int)threadIdx.x >> 6, R = 64 / T.L, ntiles = (T.rpw + R - 1) / R;
+    return w < ntiles ? (ntiles - w + 3) / 4 : 0;
+}
+
+// Waits until at most n vector-memory operations of this wavefront are
+// outstanding (they complete in issue order): everything but the last n.
+__device__ __forceinline__ void vm_wait_n(int n) {
+    switch (n < 0 ? 0 : (n > 24 ? 24 : n)) {
+#define VW(k) case k: vm_wait<k>(); break;
+        VW(0) VW(1) VW(2) VW(3) VW(4) VW(5) VW(6) VW(7) VW(8) VW(9) VW(10) VW(11) VW(12)
+        VW(13) VW(14) VW(15) VW(16) VW(17) VW(18) VW(19) VW(20) VW(21) VW(22) VW(23)
+        default: vm_wait<24>(); break;
+#undef VW
     }
 }
 
@@ -317,13 +357,24 @@ __device__ __forceinline__ Quant prologue(RowRegs<EPT>& r, int cols, const float
 }
 
 // ---- attention: one (query head, key split) item ------------------------
+template <int LK>
+struct StepAttnShared : AttnShared<LK> {
+    float fs[kAttnSplits];  // split factors of the combine
+    float linv;
+};
+
 // attention_split_ku (attn_common.h) with key p, the row appended by this
 // step, taken from the q/k/v words instead of the cache (the cache row is
 // written by another workgroup in this dispatch and is not coherent here);
 // the same arithmetic in the same order.
 template <int LK>
-__device__ __forceinline__ void attn_item(const StepArgs& a, int l, int h, int s, int p, unsigned want,
-                                          unsigned ep, float* sc, AttnShared<LK>& sh, Waiter& wt) {
+__device__ __forceinline__ void attn_item(const StepArgs& a, int l, int h, int s, int ns, int p, unsigned want,
+                                          unsigned ep, float* sc, StepAttnShared<LK>& sh, Waiter& wt) {
+    const unsigned want2 = ep;  // the partials of the head's other splits
+#define ATR(k)                                                                                      \
+    if (a.trace && threadIdx.x == 0)                                                                \
+        gstore(a.trace + ((size_t)blockIdx.x * a.layers + l) * 32 + (k), (unsigned long long)wall_clock64());
+    ATR(22)
     constexpr int HD = LK * 8, GW = 64 / LK, NK = kST / LK, KU = 4;
     const int tid = (int)threadIdx.x, w = tid >> 6, lane = tid & 63;
     const int kslot = lane / LK, cc = lane % LK;
@@ -372,6 +423,7 @@ __device__ __forceinline__ void attn_item(const StepArgs& a, int l, int h, int s
         }
         if (__all(ok) || wt.give_up()) break;
     }
+    ATR(23)
     float q8[8], kf[8], vf[8];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -468,152 +520,96 @@ __device__ __forceinline__ void attn_item(const StepArgs& a, int l, int h, int s
         for (int e = 0; e < 8; e++) sh.pv[w][8 * c + e] = acc[e];
     }
     __syncthreads();
-    if (tid < HD)
-        ll_put(a.llpart + (size_t)s * a.H + (size_t)h * HD + tid, ep,
-               (sh.pv[0][tid] + sh.pv[1][tid]) + (sh.pv[2][tid] + sh.pv[3][tid]));
-    if (tid == 0) {
-        u64* ml = a.llpart + (size_t)kAttnSplits * a.H + ((size_t)s * a.nh + h) * 2;
-        ll_put(ml, ep, m);
-        ll_put(ml + 1, ep, (sh.rsum[0] + sh.rsum[1]) + (sh.rsum[2] + sh.rsum[3]));
-    }
-    // sc / sh are reused by the next item only after its own barriers
-    __syncthreads();
-}
-
-// ---- the o-projection input: combine of the splits ----------------------
-// attn_row_finish (attn_common.h) on the partial words: the same factors,
-// the same accumulation order.
-template <int EPT>
-__device__ __forceinline__ void combine_row(const StepArgs& a, int ns, unsigned want, const float* nw,
-                                            RowRegs<EPT>& r, AttnTab& tab, Waiter& wt) {
-    constexpr int NG = EPT / 4, NP = attn_pair_slots<kST>();
-    const int tid = (int)threadIdx.x;
-    const int hs = __builtin_ctz((unsigned)a.hd);
-    const u64* ml = a.llpart + (size_t)kAttnSplits * a.H;
-#pragma unroll
-    for (int g = 0; g < NG; g++) {
-        const int i0 = 4 * (kST * g + tid);
-        if (i0 < a.H) {
-            const f32x4 w4 = gload((const f32x4*)(nw + i0));
-            r.nw[4 * g] = w4.x;
-            r.nw[4 * g + 1] = w4.y;
-            r.nw[4 * g + 2] = w4.z;
-            r.nw[4 * g + 3] = w4.w;
-        } else {
-#pragma unroll
-            for (int k = 0; k < 4; k++) r.nw[4 * g + k] = 0.0f;
+    ATR(24)
+    const float o_own = tid < HD ? (sh.pv[0][tid] + sh.pv[1][tid]) + (sh.pv[2][tid] + sh.pv[3][tid]) : 0.0f;
+    const float l_own = (sh.rsum[0] + sh.rsum[1]) + (sh.rsum[2] + sh.rsum[3]);
+    u64* ml = a.llpart + (size_t)kAttnSplits * a.H;
+    if (s + 1 < ns) {
+        // a split other than the last: its partial goes to the head's last split
+        if (tid < HD) ll_put(a.llpart + (size_t)s * a.H + (size_t)h * HD + tid, ep, o_own);
+        if (tid == 0) {
+            ll_put(ml + ((size_t)s * a.nh + h) * 2, ep, m);
+            ll_put(ml + ((size_t)s * a.nh + h) * 2 + 1, ep, l_own);
         }
+        __syncthreads();  // sc / sh are reused by the next item only after its own barriers
+        return;
     }
-    // (m, l) of every live (head, split)
-    u32x4 mlv[NP];
+    // The head's last split combines all of them (attn_row_finish,
+    // attn_common.h: the same factors, the same accumulation order) and
+    // publishes the head's attention output.
+    float ov[kAttnSplits];
+    float mv = -__builtin_inff(), lv = 0.0f;
+    const int slot = lane & (kAttnSplits - 1);
     wt.start();
     for (;;) {
-#pragma unroll
-        for (int j = 0; j < NP; j++) {
-            const int pi = tid + j * kST, h = pi / kAttnSplits, s = pi % kAttnSplits;
-            const bool live = h < a.nh && s < ns;
-            mlv[j] = ll_ld2(ml + (live ? ((size_t)s * a.nh + h) * 2 : 0));
-        }
-        vm_wait<0>();
         bool ok = true;
+        if (tid < HD)
 #pragma unroll
-        for (int j = 0; j < NP; j++) {
-            pin(mlv[j]);
-            const int pi = tid + j * kST, h = pi / kAttnSplits, s = pi % kAttnSplits;
-            if (h < a.nh && s < ns) ok = ok && ready2(mlv[j], want);
+            for (int q = 0; q < kAttnSplits - 1; q++) {
+                if (q >= ns - 1) break;
+                const u64 v = __hip_atomic_load((const LBT_GLOBAL u64*)(a.llpart + (size_t)q * a.H + (size_t)h * HD + tid),
+                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                ok = ok && (unsigned)(v >> 32) == want2;
+                ov[q] = __uint_as_float((uint32_t)v);
+            }
+        if (w == 0 && slot < ns - 1) {
+            const u64 vm = __hip_atomic_load((const LBT_GLOBAL u64*)(ml + ((size_t)slot * a.nh + h) * 2),
+                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const u64 vl = __hip_atomic_load((const LBT_GLOBAL u64*)(ml + ((size_t)slot * a.nh + h) * 2 + 1),
+                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            ok = ok && (unsigned)(vm >> 32) == want2 && (unsigned)(vl >> 32) == want2;
+            mv = __uint_as_float((uint32_t)vm);
+            lv = __uint_as_float((uint32_t)vl);
         }
         if (__all(ok) || wt.give_up()) break;
     }
-#pragma unroll
-    for (int j = 0; j < NP; j++) {
-        const int pi = tid + j * kST, h = pi / kAttnSplits, s = pi % kAttnSplits;
-        if (j * kST >= a.nh * kAttnSplits) break;  // uniform
-        const bool live = h < a.nh && s < ns;
-        const float mm = live ? __uint_as_float(mlv[j].x) : -__builtin_inff();
+    ATR(25)
+    if (w == 0) {
+        const bool live = slot < ns;
+        const float mm = slot == ns - 1 ? m : (live ? mv : -__builtin_inff());
+        const float ll = slot == ns - 1 ? l_own : lv;
         float M = xor_max<8>(mm);
         M = xor_max<4>(M);
         M = xor_max<2>(M);
         M = xor_max<1>(M);
         const float f = live ? lbt_expf(mm - M) : 0.0f;
-        const float Ls = xor_sum_down<8>(live ? __uint_as_float(mlv[j].z) * f : 0.0f);
-        if (h < a.nh) {
-            tab.f[h][s] = f;
-            if (s == 0) tab.L[h] = 1.0f / Ls;
-        }
+        const float Ls = xor_sum_down<8>(live ? ll * f : 0.0f);
+        if (lane < kAttnSplits) sh.fs[lane] = f;
+        if (lane == 0) sh.linv = 1.0f / Ls;
     }
     __syncthreads();
-    float O[EPT];
+    if (tid < HD) {
+        float O = 0.0f;
 #pragma unroll
-    for (int e = 0; e < EPT; e++) O[e] = 0.0f;
-    // split outputs, four splits per poll
-    for (int s0 = 0; s0 < ns; s0 += 4) {
-        u32x4 ov[NG][4][2];
-        wt.start();
-        for (;;) {
-#pragma unroll
-            for (int g = 0; g < NG; g++)
-#pragma unroll
-                for (int sb = 0; sb < 4; sb++) {
-                    const int i0 = 4 * (kST * g + tid), s = s0 + sb;
-                    const u64* p = a.llpart + ((i0 < a.H && s < ns) ? (size_t)s * a.H + i0 : 0);
-                    ov[g][sb][0] = ll_ld2(p);
-                    ov[g][sb][1] = ll_ld2(p + 2);
-                }
-            vm_wait<0>();
-            bool ok = true;
-#pragma unroll
-            for (int g = 0; g < NG; g++)
-#pragma unroll
-                for (int sb = 0; sb < 4; sb++) {
-                    pin(ov[g][sb][0]);
-                    pin(ov[g][sb][1]);
-                    const int i0 = 4 * (kST * g + tid);
-                    if (i0 < a.H && s0 + sb < ns)
-                        ok = ok && ready2(ov[g][sb][0], want) && ready2(ov[g][sb][1], want);
-                }
-            if (__all(ok) || wt.give_up()) break;
+        for (int q = 0; q < kAttnSplits; q++) {
+            if (q >= ns) break;
+            O = __builtin_fmaf(q == ns - 1 ? o_own : ov[q], sh.fs[q], O);
         }
-#pragma unroll
-        for (int g = 0; g < NG; g++) {
-            const int i0 = 4 * (kST * g + tid);
-            if (i0 >= a.H) continue;
-            const float* fh = tab.f[i0 >> hs];
-#pragma unroll
-            for (int sb = 0; sb < 4; sb++) {
-                const int s = s0 + sb;
-                if (s < ns) {
-                    const float f = fh[s];
-                    O[4 * g] = __builtin_fmaf(__uint_as_float(ov[g][sb][0].x), f, O[4 * g]);
-                    O[4 * g + 1] = __builtin_fmaf(__uint_as_float(ov[g][sb][0].z), f, O[4 * g + 1]);
-                    O[4 * g + 2] = __builtin_fmaf(__uint_as_float(ov[g][sb][1].x), f, O[4 * g + 2]);
-                    O[4 * g + 3] = __builtin_fmaf(__uint_as_float(ov[g][sb][1].z), f, O[4 * g + 3]);
-                }
-            }
-        }
+        ll_put(a.llatt + (size_t)h * HD + tid, ep, O * sh.linv);
     }
-#pragma unroll
-    for (int g = 0; g < NG; g++) {
-        const int i0 = 4 * (kST * g + tid);
-        const bool in = i0 < a.H;
-        const float rl = in ? tab.L[i0 >> hs] : 0.0f;
-#pragma unroll
-        for (int k = 0; k < 4; k++) r.v[4 * g + k] = O[4 * g + k] * rl;
-    }
+    ATR(26)
+#undef ATR
+    __syncthreads();  // sc / sh are reused by the next item only after its own barriers
 }
 
 // ---- the step ------------------------------------------------------------
 // Kernel arguments live in device memory and are re-read through a laundered
 // pointer in each phase (scalar loads), so the compiler keeps no uniform value
 // alive across the layer loop (which would exhaust the scalar registers).
+// Matrix k of layer l and norm k of layer l: the model keeps every layer's
+// matrices (and norm gains) at one stride from the previous layer's.
+#define WP(l, k) (a.w0[k] + (size_t)(l) * a.wstride)
+#define NP(l, k) (a.n0[k] + (size_t)(l) * a.nstride)
+
 template <int LK, int EH, int EI>
 __global__ __launch_bounds__(kST) void decode_step_kernel(const StepArgs* __restrict__ pa) {
     extern __shared__ __align__(16) int8_t dyn[];  // weight slices, row tables, xq image, scores
     __shared__ __align__(16) float red[kRedFloats];
     __shared__ float sa_s;
-    __shared__ AttnShared<LK> ash;
-    __shared__ AttnTab tab;
+    __shared__ StepAttnShared<LK> ash;
     __shared__ float xown[kStepMaxRows];
     __shared__ f32x2 rope[kStepMaxRows];  // (cos, sin) of this workgroup's q/k row pairs at position p
+    float* wsc = (float*)(dyn + kld(&launder(pa)->ws_off));  // per-tensor weight scales [layers * 7]
     const int G = (int)gridDim.x, b = (int)blockIdx.x, tid = (int)threadIdx.x;
 
     int p, slot, layers;
@@ -670,18 +666,82 @@ __global__ __launch_bounds__(kST) void decode_step_kernel(const StepArgs* __rest
             }
             rope[q] = cs;
         }
+        for (int i = tid; i < a.layers * 7; i += kST) wsc[i] = gload(a.wscale + i);
         // the residual rows of this workgroup (its o / down rows) start as the embedding
         const uint16_t* erow = a.embed + (size_t)tok * H;
         if (ho)
             for (int r = tid; r < a.t[1].rpw; r += kST) xown[r] = vo0 + r < H ? bf16_to_f32(gload(erow + vo0 + r)) : 0.0f;
         __syncthreads();  // row tables
-        if (hq) tile_load(a.t[0], kld(a.w + (0)), kld(a.w + (1)), kld(a.w + (2)), a.CH, (const uint32_t*)(dyn + a.rt_off[0]), dyn);
     }
     Waiter wt{nullptr, 0ull, 0};
+    // Weight slices of the next layer, loaded into LDS a tile at a time at
+    // each phase's start (a few tiles per phase, so the HBM stream stays
+    // spread over the layer instead of bursting while other workgroups poll):
+    // pend[P] = the layer slice P is being loaded for (-1: none), cur[P] = its
+    // next tile of this wavefront, last[P] = the load count nl after its last
+    // tile (the loads issued since may still be in flight when P is used).
+    int pend[4] = {-1, -1, -1, -1}, cur[4] = {0, 0, 0, 0}, last[4] = {0, 0, 0, 0};
+    int nl = 0;
+    auto load_tile = [&](const StepArgs& a, int P, int ly, int lt) -> int {
+        const uint32_t* rt = (const uint32_t*)(dyn + a.rt_off[P]);
+        switch (P) {
+            case 0: return tile_load_slot(a.t[0], WP(ly, 0), WP(ly, 1), WP(ly, 2), a.CH, rt, dyn, lt);
+            case 1: return tile_load_slot(a.t[1], WP(ly, 3), WP(ly, 3), WP(ly, 3), a.CH, rt, dyn, lt);
+            case 2: return tile_load_slot(a.t[2], WP(ly, 4), WP(ly, 5), WP(ly, 5), a.CH, rt, dyn, lt);
+            default: return tile_load_slot(a.t[3], WP(ly, 6), WP(ly, 6), WP(ly, 6), a.CI, rt, dyn, lt);
+        }
+    };
+    // up to `quota` tiles of the pending slices
+    auto feed = [&](int quota) {
+        if ((pend[0] & pend[1] & pend[2] & pend[3]) == -1) return;  // uniform
+        const StepArgs a = kargs(pa);
+#pragma unroll
+        for (int P = 0; P < 4; P++) {
+            if (pend[P] >= 0) {
+                const int ns_ = tile_slots(a.t[P]);
+                while (quota > 0 && cur[P] < ns_) {
+                    nl += load_tile(a, P, pend[P], cur[P]);
+                    cur[P]++;
+                    quota--;
+                }
+                if (cur[P] >= ns_) {
+                    pend[P] = -1;
+                    last[P] = nl;
+                }
+            }
+        }
+    };
+    // Before the dots of slice P: its loads issued (now if still pending)
+    // and landed; loads issued after it may stay in flight.
+    auto slice_ready = [&](int P) {
+        if (pend[P] >= 0) {
+            const StepArgs a = kargs(pa);
+            const int ns_ = tile_slots(a.t[P]);
+            while (cur[P] < ns_) {
+                nl += load_tile(a, P, pend[P], cur[P]);
+                cur[P]++;
+            }
+            pend[P] = -1;
+            last[P] = nl;
+            vm_wait<0>();
+        } else {
+            vm_wait_n(nl - last[P]);
+        }
+    };
+    auto enqueue = [&](int P, int ly) {
+        pend[P] = ly;
+        cur[P] = 0;
+    };
+    // layer 0's slices (those of phases this workgroup takes part in)
+    if (hq) enqueue(0, 0);
+    if (ho) enqueue(1, 0);
+    if (hg) enqueue(2, 0);
+    if (ho) enqueue(3, 0);
+    feed(64);
 #define STEP_TR(k)                                                                        \
-    if (tid == 0 && (b == 0 || b == G - 1)) {                                             \
+    if (tid == 0) {                                                                       \
         unsigned long long* tr_ = kld(&launder(pa)->trace);                               \
-        if (tr_) gstore(tr_ + (b ? (size_t)layers * 32 : 0) + (size_t)l * 32 + (k), (unsigned long long)wall_clock64()); \
+        if (tr_) gstore(tr_ + ((size_t)b * layers + l) * 32 + (k), (unsigned long long)wall_clock64()); \
     }
 
     for (int l = 0; l < layers; l++) {
@@ -692,16 +752,16 @@ __global__ __launch_bounds__(kST) void decode_step_kernel(const StepArgs* __rest
             const StepArgs a = kargs(pa);
             wt.err = a.err;
             const int H = a.H, KV = a.KV, hd = a.hd, h2 = hd >> 1, hs = __builtin_ctz((unsigned)hd);
-            const float* nw = kld(a.norm + (l * 4 + 0));
+            const float* nw = NP(l, 0);
             RowRegs<EH> r;
             if (l == 0) row_load<EH, kST>(SrcBf16{a.embed + (size_t)tok * H}, H, nw, r);
             else ll_row<EH>(a.llx, H, e0, nw, r, wt);
             STEP_TR(1)
             const Quant qa = prologue<EH>(r, H, nw, a.eps, dyn + a.xq_off, red, &sa_s);
             STEP_TR(2)
-            vm_wait<0>();  // this wavefront's weight tiles (layer 0: issued above)
+            slice_ready(0);
             STEP_TR(3)
-            const float sw0 = kld(a.wscale + (l * 7)), sw1 = kld(a.wscale + (l * 7 + 1)), sw2 = kld(a.wscale + (l * 7 + 2));
+            const float sw0 = wsc[l * 7], sw1 = wsc[l * 7 + 1], sw2 = wsc[l * 7 + 2];
             uint16_t* kcl = a.kc + (size_t)l * a.layer_kv;
             uint16_t* vcl = a.vc + (size_t)l * a.layer_kv;
             u64* q_out = a.llqkv;
@@ -741,58 +801,35 @@ __global__ __launch_bounds__(kST) void decode_step_kernel(const StepArgs* __rest
                           }
                       });
             STEP_TR(4)
-            if (l + 1 < layers)
-                tile_load(a.t[0], kld(a.w + ((l + 1) * 7)), kld(a.w + ((l + 1) * 7 + 1)), kld(a.w + ((l + 1) * 7 + 2)), a.CH, rt, dyn);
+            if (l + 1 < layers) {
+                enqueue(0, l + 1);
+                feed(64);
+            }
         }
         STEP_TR(5)
-        if (l == 0 && ho) {
-            const StepArgs a = kargs(pa);
-            tile_load(a.t[1], kld(a.w + (3)), kld(a.w + (3)), kld(a.w + (3)), a.CH, (const uint32_t*)(dyn + a.rt_off[1]), dyn);
-        }
         // ---- attention over keys 0..p (model.rs:341-357)
         {
             const StepArgs a = kargs(pa);
             wt.err = a.err;
             const int ns = attn_splits(p + 1);
             for (int it = b; it < a.nh * ns; it += G)
-                attn_item<LK>(a, l, it / ns, it % ns, p, e0 + 1u, e0 + 2u, (float*)(dyn + a.sc_off), ash, wt);
+                attn_item<LK>(a, l, it / ns, it % ns, ns, p, e0 + 1u, e0 + 2u, (float*)(dyn + a.sc_off), ash, wt);
             STEP_TR(6)
-            if (l == 0 && hg)
-                tile_load(a.t[2], kld(a.w + (4)), kld(a.w + (5)), kld(a.w + (5)), a.CH, (const uint32_t*)(dyn + a.rt_off[2]), dyn);
         }
         // ---- o_proj(attn_sub_norm(attn)), x += o (model.rs:358-359)
         if (ho) {
             const StepArgs a = kargs(pa);
             wt.err = a.err;
             const int H = a.H;
-            const float* nw = kld(a.norm + (l * 4 + 2));
+            const float* nw = NP(l, 2);
             RowRegs<EH> r;
-            combine_row<EH>(a, attn_splits(p + 1), e0 + 2u, nw, r, tab, wt);
+            ll_row<EH>(a.llatt, H, e0 + 2u, nw, r, wt);
             STEP_TR(7)
             const Quant qa = prologue<EH>(r, H, nw, a.eps, dyn + a.xq_off, red, &sa_s);
             STEP_TR(8)
-            vm_wait<0>();
+            slice_ready(1);
             STEP_TR(9)
-#ifdef STEP_EXP
-            const unsigned long long ck0 = clock64();
-            {
-                int dummy = 0;
-                tile_dots(a.t[1], a.CH, H - b * a.t[1].rpw, (const uint32_t*)(dyn + a.rt_off[1]), dyn, dyn + a.xq_off, qa.qs,
-                          [&](int lr, uint32_t, int d0, int) { dummy += d0; });
-                if (dummy == 0x7fffffff) xown[0] = 1.0f;
-            }
-            STEP_TR(22)
-            if (tid == 0 && b == 0) {
-                unsigned long long* tr_ = kld(&launder(pa)->trace);
-                if (tr_) gstore(tr_ + (size_t)l * 32 + 24, (unsigned long long)(clock64() - ck0));
-            }
-            {
-                const float t_ = kld(a.wscale + (l * 7 + 3));
-                if (t_ == 12345.0f) xown[0] = 1.0f;
-            }
-            STEP_TR(23)
-#endif
-            const float inv = 1.0f / (qa.sa * kld(a.wscale + (l * 7 + 3)));
+            const float inv = 1.0f / (qa.sa * wsc[l * 7 + 3]);
             const int vo0 = b * a.t[1].rpw;
             u64* xo = a.llx + vo0;
             const unsigned ep = e0 + 3u;
@@ -804,12 +841,8 @@ __global__ __launch_bounds__(kST) void decode_step_kernel(const StepArgs* __rest
             });
             STEP_TR(10)
             if (l + 1 < layers) {
-                const uint8_t* w = kld(a.w + ((l + 1) * 7 + 3));
-                tile_load(a.t[1], w, w, w, a.CH, rt, dyn);
-            }
-            if (l == 0) {
-                const uint8_t* w = kld(a.w + (6));
-                tile_load(a.t[3], w, w, w, a.CI, (const uint32_t*)(dyn + a.rt_off[3]), dyn);
+                enqueue(1, l + 1);
+                feed(64);
             }
         }
         STEP_TR(11)
@@ -818,15 +851,15 @@ __global__ __launch_bounds__(kST) void decode_step_kernel(const StepArgs* __rest
             const StepArgs a = kargs(pa);
             wt.err = a.err;
             const int H = a.H, I = a.I;
-            const float* nw = kld(a.norm + (l * 4 + 1));
+            const float* nw = NP(l, 1);
             RowRegs<EH> r;
             ll_row<EH>(a.llx, H, e0 + 3u, nw, r, wt);
             STEP_TR(12)
             const Quant qa = prologue<EH>(r, H, nw, a.eps, dyn + a.xq_off, red, &sa_s);
             STEP_TR(13)
-            vm_wait<0>();
+            slice_ready(2);
             STEP_TR(14)
-            const float ig = 1.0f / (qa.sa * kld(a.wscale + (l * 7 + 4))), iu = 1.0f / (qa.sa * kld(a.wscale + (l * 7 + 5)));
+            const float ig = 1.0f / (qa.sa * wsc[l * 7 + 4]), iu = 1.0f / (qa.sa * wsc[l * 7 + 5]);
             const int vg0 = b * a.t[2].rpw;
             u64* hout = a.llh + (vg0 >> 1);
             const unsigned ep = e0 + 4u;
@@ -840,8 +873,10 @@ __global__ __launch_bounds__(kST) void decode_step_kernel(const StepArgs* __rest
                           ll_put(hout + (lr >> 1), ep, (rl * rl) * u);
                       });
             STEP_TR(15)
-            if (l + 1 < layers)
-                tile_load(a.t[2], kld(a.w + ((l + 1) * 7 + 4)), kld(a.w + ((l + 1) * 7 + 5)), kld(a.w + ((l + 1) * 7 + 5)), a.CH, rt, dyn);
+            if (l + 1 < layers) {
+                enqueue(2, l + 1);
+                feed(64);
+            }
         }
         STEP_TR(16)
         // ---- down on ffn_sub_norm(h), x += down (model.rs:364-365)
@@ -849,15 +884,15 @@ __global__ __launch_bounds__(kST) void decode_step_kernel(const StepArgs* __rest
             const StepArgs a = kargs(pa);
             wt.err = a.err;
             const int H = a.H, I = a.I;
-            const float* nw = kld(a.norm + (l * 4 + 3));
+            const float* nw = NP(l, 3);
             RowRegs<EI> r;
             ll_row<EI>(a.llh, I, e0 + 4u, nw, r, wt);
             STEP_TR(17)
             const Quant qa = prologue<EI>(r, I, nw, a.eps, dyn + a.xq_off, red, &sa_s);
             STEP_TR(18)
-            vm_wait<0>();
+            slice_ready(3);
             STEP_TR(19)
-            const float inv = 1.0f / (qa.sa * kld(a.wscale + (l * 7 + 6)));
+            const float inv = 1.0f / (qa.sa * wsc[l * 7 + 6]);
             const int vo0 = b * a.t[1].rpw;
             const bool last = l + 1 == layers;
             u64* xo = a.llx + vo0;
@@ -872,8 +907,8 @@ __global__ __launch_bounds__(kST) void decode_step_kernel(const StepArgs* __rest
             });
             STEP_TR(20)
             if (!last) {
-                const uint8_t* w = kld(a.w + ((l + 1) * 7 + 6));
-                tile_load(a.t[3], w, w, w, a.CI, rt, dyn);
+                enqueue(3, l + 1);
+                feed(64);
             }
         }
         STEP_TR(21)
@@ -987,6 +1022,8 @@ int step_plan(const lbt_config& c, int cap, int G, StepPlan& pl, const char** wh
     off = (off + 15) & ~15;
     pl.sc_off = off;
     off += attn_split_keys(cap) * 4;
+    pl.ws_off = off;
+    off += c.num_hidden_layers * 7 * 4;
     pl.lds = (size_t)off;
     pl.fn = f.fn;
     const size_t lim = dyn_limit(f.fn);
@@ -1005,6 +1042,7 @@ void step_fill(const StepPlan& pl, const lbt_config& c, StepArgs& a) {
     }
     a.xq_off = pl.xq_off;
     a.sc_off = pl.sc_off;
+    a.ws_off = pl.ws_off;
     a.CH = (int)(padded_cols((size_t)c.hidden_size) / 64);
     a.CI = (int)(padded_cols((size_t)c.intermediate_size) / 64);
 }

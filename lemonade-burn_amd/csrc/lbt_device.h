@@ -520,10 +520,22 @@ __device__ __forceinline__ float row_sumsq(const RowRegs<EPT>& r, int cols, floa
         for (int k = 0; k < 4; k++)
             if (act && row_elem<NT>(tid, 4 * g + k) < cols)
                 acc[g % A] = __builtin_fmaf(r.v[4 * g + k], r.v[4 * g + k], acc[g % A]);
+    if constexpr (A == 4) {
+        // the four wavefront sums together: recursive halving over lane bits
+        // 5 and 4 (each kept sum is v[l] + v[l^m], the butterfly's sums), then
+        // the butterfly's last four steps; accumulator 2*b5 + b4 ends in the
+        // lanes with those bits (lanes 0, 16, 32, 48 write them)
+        float h2[2], h1[1];
+        halve<32, 4>(acc, h2);
+        halve<16, 2>(h2, h1);
+        const float s = xor_sum_down<8>(h1[0]);
+        if ((lane & 15) == 0 && act) red[(tid >> 6) + (lane >> 4) * (NT / 64)] = s;
+    } else {
 #pragma unroll
-    for (int j = 0; j < A; j++) {
-        const float s = wave_sum(acc[j]);
-        if (lane == 0 && act) red[(tid >> 6) + j * (NT / 64)] = s;
+        for (int j = 0; j < A; j++) {
+            const float s = wave_sum(acc[j]);
+            if (lane == 0 && act) red[(tid >> 6) + j * (NT / 64)] = s;
+        }
     }
     __syncthreads();
     return tree16(red);

@@ -21,6 +21,7 @@
 #include <sys/stat.h>
 #include <unistd.h>
 
+#include <algorithm>
 #include <map>
 #include <memory>
 #include <string>
@@ -606,7 +607,7 @@ int ensure_state(lbt_model* m) {
 
 // Words of the epoch-tagged activation buffers of the one-dispatch step.
 struct StepWords {
-    size_t x, qkv, part, h, total;
+    size_t x, qkv, part, att, h, total;
 };
 StepWords step_words(const lbt_config& c, int hd) {
     StepWords w;
@@ -614,8 +615,9 @@ StepWords step_words(const lbt_config& c, int hd) {
     w.x = (H + 1) & ~(size_t)1;
     w.qkv = (H + 2 * KV + 1) & ~(size_t)1;
     w.part = ((size_t)kAttnSplits * H + (size_t)kAttnSplits * c.num_attention_heads * 2 + 1) & ~(size_t)1;
+    w.att = w.x;
     w.h = ((size_t)c.intermediate_size + 1) & ~(size_t)1;
-    w.total = w.x + w.qkv + w.part + w.h + 2;  // + the error word
+    w.total = w.x + w.qkv + w.part + w.att + w.h + 2;  // + the error word
     return w;
 }
 
@@ -628,6 +630,14 @@ int step_ready(lbt_model* m, lbt_cache* c) {
     lbt::StepPlan pl;
     pl.G = m->ctx->cus;
     if (!step_plan(m->cfg, c->cap, pl.G, pl, &why)) return 0;
+    // the step addresses layer l's matrices and norms at a fixed stride
+    const int L = m->cfg.num_hidden_layers;
+    for (int l = 1; l < L; l++) {
+        for (int k = 0; k < 7; k++)
+            if (m->lin[l * 7 + k].d - m->lin[k].d != (ptrdiff_t)l * (m->lin[7].d - m->lin[0].d)) return 0;
+        for (int k = 0; k < 4; k++)
+            if (m->norm[l * 4 + k] - m->norm[k] != (ptrdiff_t)l * (m->norm[4] - m->norm[0])) return 0;
+    }
     double bytes = 0.0;
     for (int i = 0; i < 7 * m->cfg.num_hidden_layers; i++) bytes += (double)m->lin[i].rows * (double)(m->lin[i].kp / 4);
     pl.bytes = bytes;
@@ -643,19 +653,10 @@ int step_prepare(lbt_model* m, lbt_cache* c, StepArgs& a) {
     int rc;
     if ((rc = ensure_state(m))) return rc;
     if (!m->ptab) {
-        std::vector<const void*> wp(L * 7), np(L * 4);
         std::vector<float> ws(L * 7);
-        for (int i = 0; i < L * 7; i++) {
-            wp[i] = m->lin[i].d;
-            ws[i] = m->lin[i].scale;
-        }
-        for (int i = 0; i < L * 4; i++) np[i] = m->norm[i];
-        const size_t b0 = wp.size() * 8, b1 = ws.size() * 4, b2 = np.size() * 8;
-        LBT_HIP(ctx, hipMalloc(&m->ptab, b0 + b1 + b2 + 64));
-        char* t = (char*)m->ptab;
-        LBT_HIP(ctx, hipMemcpy(t, wp.data(), b0, hipMemcpyHostToDevice));
-        LBT_HIP(ctx, hipMemcpy(t + b0, ws.data(), b1, hipMemcpyHostToDevice));
-        LBT_HIP(ctx, hipMemcpy(t + ((b0 + b1 + 7) & ~(size_t)7), np.data(), b2, hipMemcpyHostToDevice));
+        for (int i = 0; i < L * 7; i++) ws[i] = m->lin[i].scale;
+        LBT_HIP(ctx, hipMalloc(&m->ptab, ws.size() * 4));
+        LBT_HIP(ctx, hipMemcpy(m->ptab, ws.data(), ws.size() * 4, hipMemcpyHostToDevice));
     }
     const StepWords sw = step_words(cf, m->hd);
     const double per_step = 5.0 * L;
@@ -670,11 +671,12 @@ int step_prepare(lbt_model* m, lbt_cache* c, StepArgs& a) {
         LBT_HIP(ctx, hipMemsetAsync(m->state + 2, 0, sizeof(int), ctx->stream));
         m->epochs = 0.0;
     }
-    const size_t b0 = (size_t)L * 7 * 8, b1 = (size_t)L * 7 * 4;
     a = StepArgs{};
-    a.w = (const uint8_t* const*)m->ptab;
-    a.wscale = (const float*)((char*)m->ptab + b0);
-    a.norm = (const float* const*)((char*)m->ptab + ((b0 + b1 + 7) & ~(size_t)7));
+    for (int k = 0; k < 7; k++) a.w0[k] = m->lin[k].d;
+    a.wstride = L > 1 ? (size_t)(m->lin[7].d - m->lin[0].d) : 0;
+    for (int k = 0; k < 4; k++) a.n0[k] = m->norm[k];
+    a.nstride = L > 1 ? (size_t)(m->norm[4] - m->norm[0]) : 0;
+    a.wscale = (const float*)m->ptab;
     a.embed = m->embed;
     a.cos_t = m->cos_t;
     a.sin_t = m->sin_t;
@@ -699,9 +701,13 @@ int step_prepare(lbt_model* m, lbt_cache* c, StepArgs& a) {
     a.llx = m->ll;
     a.llqkv = a.llx + sw.x;
     a.llpart = a.llqkv + sw.qkv;
-    a.llh = a.llpart + sw.part;
+    a.llatt = a.llpart + sw.part;
+    a.llh = a.llatt + sw.att;
     a.err = (unsigned*)(a.llh + sw.h);
-    if (m->want_trace && !m->trace) LBT_HIP(ctx, hipMalloc(&m->trace, (size_t)L * 64 * 8));
+    if (m->want_trace && !m->trace) {
+        LBT_HIP(ctx, hipMalloc(&m->trace, (size_t)m->plan.G * L * 32 * 8));
+        LBT_HIP(ctx, hipMemset(m->trace, 0, (size_t)m->plan.G * L * 32 * 8));
+    }
     a.trace = m->trace;
     step_fill(m->plan, cf, a);
     if (!m->dargs) LBT_HIP(ctx, hipMalloc(&m->dargs, sizeof(StepArgs)));
@@ -725,23 +731,33 @@ int step_check(lbt_model* m) {
         return set_err(ctx, LBT_E_DEVICE, "decode step: a wait for another workgroup timed out");
     }
     if (m->trace) {
-        // measurement aid: mean time of each traced segment of the last step
-        const int L = m->cfg.num_hidden_layers;
-        std::vector<unsigned long long> t((size_t)L * 64);
+        // measurement aid: per traced point k, the median and the latest
+        // workgroup's time after the layer's earliest start, averaged over layers
+        const int L = m->cfg.num_hidden_layers, G = m->plan.G;
+        std::vector<unsigned long long> t((size_t)G * L * 32);
         LBT_HIP(ctx, hipMemcpy(t.data(), m->trace, t.size() * 8, hipMemcpyDeviceToHost));
-        for (int half = 0; half < 2; half++) {
-            double seg[32] = {0};
-            for (int l = 1; l < L; l++) {
-                const unsigned long long* r = &t[(size_t)half * L * 32 + (size_t)l * 32];
-                for (int k = 1; k <= 21; k++) seg[k] += (double)(long long)(r[k] - r[k - 1]) / (L - 1);
-                seg[22] += (double)(long long)(r[22] - r[9]) / (L - 1);
-                seg[23] += (double)(long long)(r[23] - r[22]) / (L - 1);
-                seg[24] += (double)r[24] / (L - 1) * 100.0;
+        double med[32] = {0}, mx[32] = {0};
+        int cnt[32] = {0};
+        for (int l = 1; l < L; l++) {
+            unsigned long long t0 = ~0ull;
+            for (int b = 0; b < G; b++) t0 = std::min(t0, t[((size_t)b * L + l) * 32]);
+            for (int k = 0; k < 32; k++) {
+                std::vector<double> v;
+                for (int b = 0; b < G; b++) {
+                    const unsigned long long x = t[((size_t)b * L + l) * 32 + k];
+                    if (x >= t0 && x - t0 < 100000000ull) v.push_back((double)(x - t0) / 100.0);
+                }
+                if (v.empty()) continue;
+                std::sort(v.begin(), v.end());
+                med[k] += v[v.size() / 2];
+                mx[k] += v.back();
+                cnt[k]++;
             }
-            fprintf(stderr, "step trace wg%s (us):", half ? "-last" : "0");
-            for (int k = 1; k <= 24; k++) fprintf(stderr, " %d:%.2f", k, seg[k] / 100.0);
-            fprintf(stderr, "\n");
         }
+        fprintf(stderr, "step trace (us after the layer's first start; median / latest workgroup):\n");
+        for (int k = 0; k < 32; k++)
+            if (cnt[k]) fprintf(stderr, "  %2d: %7.2f %7.2f\n", k, med[k] / cnt[k], mx[k] / cnt[k]);
+        LBT_HIP(ctx, hipMemset(m->trace, 0, t.size() * 8));
     }
     return LBT_OK;
 }
