@@ -246,7 +246,7 @@ struct lbt_model {
     // for the cache buffers and workspace it was captured with
     int* state = nullptr;  // device {position - 1, output slot, barrier epoch, spare}
     hipGraphExec_t step_exec = nullptr;
-    const void* step_key[6] = {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
+    const void* step_key[7] = {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
     // one-dispatch decode step (decode_step.hip): device tables of the layers,
     // the epoch-tagged activation words, the error word, the plan
     int decode_kind = 1;   // 0: one-dispatch step, 1: multi-kernel graph step
@@ -387,9 +387,32 @@ int model_alloc(lbt_model* m) {
     return LBT_OK;
 }
 
+// The captured decode-step graph holds the addresses of the workspace, the
+// token slots and one cache: it is destroyed (after the stream has drained)
+// before any of them is freed, so no live graph ever refers to freed memory.
+void drop_step_graph(lbt_model* m) {
+    if (!m->step_exec) return;
+    hipStreamSynchronize(m->ctx->stream);
+    hipGraphExecDestroy(m->step_exec);
+    m->step_exec = nullptr;
+}
+
+int grow_tok_out(lbt_model* m, int need) {
+    if (need <= m->tok_out_cap) return LBT_OK;
+    drop_step_graph(m);
+    hipStreamSynchronize(m->ctx->stream);
+    if (m->tok_out) hipFree(m->tok_out);
+    m->tok_out = nullptr;
+    m->tok_out_cap = 0;
+    LBT_HIP(m->ctx, hipMalloc(&m->tok_out, (size_t)need * 4));
+    m->tok_out_cap = need;
+    return LBT_OK;
+}
+
 int ensure_ws(lbt_model* m, int n) {
     if (n <= m->mcap) return LBT_OK;
     lbt_ctx* ctx = m->ctx;
+    drop_step_graph(m);
     hipStreamSynchronize(ctx->stream);
     float** bufs[] = {&m->x, &m->q, &m->k, &m->v, &m->att, &m->h, &m->logits};
     for (auto b : bufs)
@@ -444,6 +467,7 @@ int ensure_cap(lbt_cache* cc, int need) {
                                       L * kvh, hipMemcpyDeviceToDevice, ctx->stream));
     }
     LBT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    drop_step_graph(m);
     if (cc->k) hipFree(cc->k);
     if (cc->v) hipFree(cc->v);
     cc->k = nk;
@@ -791,12 +815,10 @@ int decode_steps(lbt_model* m, lbt_cache* c, int n, int slot0) {
         return LBT_OK;
     }
     if ((rc = ensure_state(m))) return rc;
-    const void* key[6] = {c->k, c->v, (const void*)(intptr_t)c->cap, m->tok_out, m->x, m->key};
+    const void* key[7] = {c->k, c->v, (const void*)(intptr_t)c->cap, m->tok_out, m->x, m->key,
+                          (const void*)(intptr_t)m->head_kind};
     if (!m->step_exec || memcmp(key, m->step_key, sizeof(key)) != 0) {
-        if (m->step_exec) {
-            hipGraphExecDestroy(m->step_exec);
-            m->step_exec = nullptr;
-        }
+        drop_step_graph(m);
         hipGraph_t g = nullptr;
         LBT_HIP(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
         const int len = c->len;
@@ -1053,6 +1075,7 @@ int lbt_cache_new(lbt_model* m, lbt_cache** out) {
 void lbt_cache_free(lbt_cache* c) {
     if (!c) return;
     hipStreamSynchronize(c->m->ctx->stream);
+    drop_step_graph(c->m);
     if (c->k) hipFree(c->k);
     if (c->v) hipFree(c->v);
     delete c;
@@ -1120,12 +1143,7 @@ int lbt_model_generate_greedy(lbt_model* m, const uint32_t* prompt, size_t n, si
     int rc;
     if ((rc = ensure_cap(c, c->len + (int)n + (int)steps))) return rc;
     if ((rc = ensure_ws(m, (int)n))) return rc;
-    if ((int)steps + 1 > m->tok_out_cap) {
-        if (m->tok_out) hipFree(m->tok_out);
-        m->tok_out = nullptr;
-        LBT_HIP(ctx, hipMalloc(&m->tok_out, (steps + 1) * 4));
-        m->tok_out_cap = (int)steps + 1;
-    }
+    if ((rc = grow_tok_out(m, (int)steps + 1))) return rc;
     if ((rc = upload_tokens(m, prompt, n))) return rc;
     hipEvent_t e0, e1, e2;
     LBT_HIP(ctx, hipEventCreate(&e0));
@@ -1166,12 +1184,7 @@ int lbt_model_decode_greedy(lbt_model* m, lbt_cache* c, uint32_t first, size_t s
     int rc;
     if ((rc = ensure_cap(c, c->len + (int)steps))) return rc;
     if ((rc = ensure_ws(m, 1))) return rc;
-    if ((int)steps + 1 > m->tok_out_cap) {
-        if (m->tok_out) hipFree(m->tok_out);
-        m->tok_out = nullptr;
-        LBT_HIP(ctx, hipMalloc(&m->tok_out, (steps + 1) * 4));
-        m->tok_out_cap = (int)steps + 1;
-    }
+    if ((rc = grow_tok_out(m, (int)steps + 1))) return rc;
     LBT_HIP(ctx, hipMemcpyAsync(m->toks, &first, 4, hipMemcpyHostToDevice, ctx->stream));
     hipEvent_t e0, e1;
     LBT_HIP(ctx, hipEventCreate(&e0));
@@ -1218,11 +1231,7 @@ int lbt_model_set_head(lbt_model* m, int kind) {
         m->q8 = q;
         m->q8s = qs;
     }
-    if (kind != m->head_kind && m->step_exec) {
-        LBT_HIP(ctx, hipStreamSynchronize(ctx->stream));
-        hipGraphExecDestroy(m->step_exec);
-        m->step_exec = nullptr;
-    }
+    if (kind != m->head_kind) drop_step_graph(m);
     m->head_kind = kind;
     return LBT_OK;
 }

@@ -144,3 +144,38 @@ def test_batch_int8_head_equals_single(ctx, nseq):
         c.free()
     b.free()
     m.free()
+
+
+def test_graph_step_survives_head_switches_and_regrowth(ctx):
+    """The captured decode-step graph across everything that frees a buffer it
+    refers to: head switches (bf16 -> int8 -> bf16), growth of the token
+    slots, of the workspace (a longer prompt) and of the cache, and a cache
+    freed and replaced.  Every decode is checked against the oracle's greedy
+    tokens with the same head."""
+    d = SMALL
+    hip_cfg = lbt_hip.make_config(d["hidden"], d["intermediate"], d["heads"], d["kv_heads"], d["layers"], d["vocab"],
+                                  d["max_pos"])
+    or_cfg = orc.config(d["hidden"], d["intermediate"], d["heads"], d["kv_heads"], d["layers"], d["vocab"],
+                        d["max_pos"])
+    announce("graph step across head switches and regrowth")
+    m = lbt_hip.Model.synthetic(ctx, hip_cfg, 21)
+    m.set_decode(1)
+
+    def oracle_tokens(head, prompt, steps):
+        om = orc.OracleModel(or_cfg, 21)
+        om.set_head(head)
+        out = [int(om.forward(prompt)[0].argmax())]
+        for _ in range(steps):
+            out.append(int(om.forward([out[-1]])[0].argmax()))
+        om.free()
+        return out
+
+    short = np.array([5, 6, 7], np.uint32)
+    longp = (np.arange(40) * 11 % d["vocab"]).astype(np.uint32)
+    for head, prompt, steps in [(0, short, 4), (1, short, 9), (1, longp, 30), (0, longp, 12), (0, short, 300)]:
+        m.set_head(head)
+        cache = m.new_cache()
+        toks, _, _ = m.generate_greedy(prompt, steps, cache)
+        assert list(toks) == oracle_tokens(head, prompt, steps), f"head {head}, prompt {len(prompt)}, {steps} steps"
+        cache.free()
+    m.free()
