@@ -750,6 +750,41 @@ static void attn_split_group(const float* qg, const uint16_t* K, const uint16_t*
     free(ms); free(ls); free(os); free(e);
 }
 
+/* The synthetic KV fill of a batch of nseq sequences (the device's
+ * lbt_batch_fill_synthetic, a test fixture with no reference counterpart),
+ * restated for sequence `seq` of such a batch: cache rows r = (layer * nseq +
+ * seq) * kv_heads + head hold, at flat index i = (r * len + pos) * hd + d of
+ * the [rows][len][hd] values, bf16((sum of the four 16-bit fields of
+ * splitmix64(splitmix64(s) + i), each / 65536) - 2) * sqrt(3)) with s =
+ * 2 seed + 1 for K and 2 seed + 2 for V.  The model's length becomes len. */
+static uint16_t synth_kv_value(uint64_t base, uint64_t i) {
+    const uint64_t z = or_splitmix64(base + i);
+    float acc = 0.0f;
+    for (int k = 0; k < 4; k++) acc += (float)((z >> (16 * k)) & 0xffffu) * (1.0f / 65536.0f);
+    return or_f32_to_bf16((acc - 2.0f) * 1.7320508075688772f);
+}
+
+int or_model_fill_synth_kv(or_model* m, uint64_t seed, int nseq, int seq, int len) {
+    const or_config* c = &m->c;
+    if (len < 0 || len > m->cap || seq < 0 || seq >= nseq) return -1;
+    const size_t hd = (size_t)(c->hidden / c->heads), kvh = (size_t)c->kv_heads, cap = (size_t)m->cap;
+    const uint64_t bk = or_splitmix64(seed * 2 + 1), bv = or_splitmix64(seed * 2 + 2);
+    for (int l = 0; l < c->layers; l++)
+        for (size_t g = 0; g < kvh; g++) {
+            const uint64_t r = ((uint64_t)l * (uint64_t)nseq + (uint64_t)seq) * kvh + g;
+            uint16_t* K = m->kc + ((size_t)l * kvh + g) * cap * hd;
+            uint16_t* V = m->vc + ((size_t)l * kvh + g) * cap * hd;
+            for (size_t p = 0; p < (size_t)len; p++)
+                for (size_t d = 0; d < hd; d++) {
+                    const uint64_t i = (r * (uint64_t)len + p) * hd + d;
+                    K[p * hd + d] = synth_kv_value(bk, i);
+                    V[p * hd + d] = synth_kv_value(bv, i);
+                }
+        }
+    m->len = len;
+    return 0;
+}
+
 int or_model_forward(or_model* m, const uint32_t* tokens, size_t n, int all_logits, float* logits) {
     const or_config* c = &m->c;
     size_t H = (size_t)c->hidden, I = (size_t)c->intermediate;

@@ -117,6 +117,7 @@ void or_model_reset(or_model* m);       /* empty KV cache */
 int or_model_len(const or_model* m);
 /* BitNet::forward (model.rs:305-374), device reduction order.  Writes logits
  * [all_logits ? m : 1, vocab].  Returns 0, or -1 when the context is exceeded. */
+int or_model_fill_synth_kv(or_model* m, uint64_t seed, int nseq, int seq, int len);
 int or_model_forward(or_model* m, const uint32_t* tokens, size_t n, int all_logits, float* logits);
 /* Internals exposed for layer-level parity: the residual stream after the last
  * forward ([n, hidden]) and the bf16 K/V cache of one layer ([kvh, cap, hd]). */

@@ -70,6 +70,7 @@ _SIGS = {
     "or_model_reset": (None, [vp]),
     "or_model_len": (i32, [vp]),
     "or_model_forward": (i32, [vp, vp, sz, i32, vp]),
+    "or_model_fill_synth_kv": (i32, [vp, u64, i32, i32, i32]),
     "or_model_hidden": (vp, [vp]),
     "or_model_kcache": (vp, [vp, i32]),
     "or_model_vcache": (vp, [vp, i32]),
@@ -369,6 +370,11 @@ class OracleModel:
         if rc != 0:
             raise RuntimeError("oracle: context length exceeded")
         return out
+
+    def fill_synth_kv(self, seed: int, nseq: int, seq: int, length: int):
+        """The cache of sequence `seq` of a batch after lbt_batch_fill_synthetic(length, seed)."""
+        if lib().or_model_fill_synth_kv(self.h, seed, nseq, seq, length) != 0:
+            raise ValueError("fill_synth_kv: bad arguments")
 
     def hidden(self, n: int) -> np.ndarray:
         p = lib().or_model_hidden(self.h)

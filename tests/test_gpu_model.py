@@ -168,19 +168,32 @@ def write_lbt_file(tmp_path, or_cfg, seed):
         "hidden_act": "relu2", "tie_word_embeddings": True, "bos_token_id": 1}))
 
 
-def test_load_lb_convert_file(ctx, tmp_path):
-    hip_cfg, or_cfg = cfgs()
-    announce("model_load")
+@pytest.mark.parametrize("intermediate", [512, 1000])
+def test_load_lb_convert_file(ctx, tmp_path, intermediate):
+    """BitNet::load (crates/lb-model/src/model.rs:149-232) of an lb-convert v1
+    directory holding the oracle's synthetic weights: prefill logits of every
+    row and 12 greedy decode tokens equal the oracle's.  intermediate = 1000
+    is not a multiple of 128: the down projection's packed rows carry padded
+    columns (code 1, weight 0, pack.rs:88-103)."""
+    hip_cfg, or_cfg = cfgs(intermediate=intermediate)
+    announce(f"model_load intermediate={intermediate}")
     write_lbt_file(tmp_path, or_cfg, 33)
     m = lbt_hip.Model.load(ctx, tmp_path)
-    s = lbt_hip.Model.synthetic(ctx, hip_cfg, 33)
+    om = orc.OracleModel(or_cfg, 33)
     toks = np.array([5, 6, 7, 800], np.uint32)
-    c1, c2 = m.new_cache(), s.new_cache()
-    assert np.array_equal(m.forward(toks, c1, True), s.forward(toks, c2, True))
+    c1 = m.new_cache()
+    assert np.array_equal(m.forward(toks, c1, True), om.forward(toks, all_logits=True))
     c1.free()
-    c2.free()
+    om.reset()
+    c1 = m.new_cache()
+    got, _, _ = m.generate_greedy(toks, 12, c1)
+    exp = [int(om.forward(toks)[0].argmax())]
+    for _ in range(12):
+        exp.append(int(om.forward([exp[-1]])[0].argmax()))
+    assert list(got) == exp
+    c1.free()
     m.free()
-    s.free()
+    om.free()
     bad = tmp_path / "config.json"
     bad.write_text(bad.read_text().replace("relu2", "silu"))
     with pytest.raises(lbt_hip.LbtError):
@@ -189,12 +202,18 @@ def test_load_lb_convert_file(ctx, tmp_path):
 
 def test_full_2b_prompt64_decode_matches_oracle(ctx):
     """2B4T-shaped model, 64-token uniform-random prompt,
-    greedy decode; tokens identical to the oracle, logits within 1e-3/1e-2."""
-    steps = 32
+    128 greedy decode steps on the device (graph-replayed step): tokens
+    identical to the oracle's greedy run.  A random-init model's greedy
+    stream settles on a repeated token, so 64 further teacher-forced steps
+    (uniform-random tokens, one per position) check the decode logits at
+    distinct inputs: within 1e-3 rel / 1e-2 abs of the oracle (in fact bit
+    for bit) and the same argmax at every position, with the smallest
+    top-1/top-2 margin printed."""
+    steps, forced = 128, 64
     hip_cfg = lbt_hip.make_config()
     or_cfg = orc.config()
     seed = 2026
-    announce("full 2B synthetic model")
+    announce("full 2B synthetic model, 128 greedy steps")
     m = lbt_hip.Model.synthetic(ctx, hip_cfg, seed)
     prompt = np.random.default_rng(64).integers(0, 128256, 64).astype(np.uint32)
     cache = m.new_cache()
@@ -203,18 +222,26 @@ def test_full_2b_prompt64_decode_matches_oracle(ctx):
     old = orc.set_fast(1)  # same integers and logits, multi-threaded SIMD integer kernels
     try:
         om = orc.OracleModel(or_cfg, seed)
-        cache = m.new_cache()
-        lg = m.forward(prompt, cache)
         le = om.forward(prompt)
-        assert np.allclose(lg, le, rtol=1e-3, atol=1e-2)
-        assert int(le[0].argmax()) == toks[0]
         exp = [int(le[0].argmax())]
-        for s in range(steps):
-            le = om.forward([exp[-1]])
-            lg = m.forward([exp[-1]], cache)
-            assert np.allclose(lg, le, rtol=1e-3, atol=1e-2), s
-            exp.append(int(le[0].argmax()))
+        for _ in range(steps):
+            exp.append(int(om.forward([exp[-1]])[0].argmax()))
         assert list(toks) == exp
+        # teacher-forced decode: the device one token at a time, the oracle in one pass
+        om.reset()
+        cache = m.new_cache()
+        m.forward(prompt, cache)
+        om.forward(prompt)
+        tf = np.random.default_rng(7).integers(0, 128256, forced).astype(np.uint32)
+        lg = np.concatenate([m.forward([int(t)], cache) for t in tf])
+        le = om.forward(tf, all_logits=True)
+        assert np.allclose(lg, le, rtol=1e-3, atol=1e-2)
+        assert (lg.argmax(axis=1) == le.argmax(axis=1)).all()
+        assert np.array_equal(lg, le)  # the oracle follows the device's float order
+        top2 = np.sort(le, axis=1)[:, -2:]
+        margin = float((top2[:, 1] - top2[:, 0]).min())
+        print(f"[2B decode] max |dev - oracle| {float(np.abs(lg - le).max()):.3g}, "
+              f"bit-exact rows {int((lg == le).all(axis=1).sum())}/{forced}, min top-1/top-2 margin {margin:.4g}")
         om.free()
         cache.free()
     finally:
