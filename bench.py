@@ -165,6 +165,72 @@ def prefill_gemm(ctx, reps: int = 10) -> list:
     return res
 
 
+LAYER_SHAPES = [("q", 2560, 2560), ("k", 640, 2560), ("v", 640, 2560), ("o", 2560, 2560),
+                ("gate", 6912, 2560), ("up", 6912, 2560), ("down", 2560, 6912)]
+COLD_BYTES = 288 << 20  # rotated weight bytes per shape: more than the 256 MB MALL holds
+
+
+def synth_packed(rng, rows: int, cols: int) -> np.ndarray:
+    """Packed LB2 rows (pack.rs:1-116) of i.i.d. ternary weights, P(-1, 0, +1)
+    = 0.3 / 0.4 / 0.3; padded columns carry code 1 (weight 0)."""
+    kp = (cols + 127) // 128 * 128
+    codes = rng.choice(np.array([0, 1, 2], np.uint8), size=(rows, kp), p=[0.3, 0.4, 0.3])
+    codes[:, cols:] = 1
+    c4 = codes.reshape(rows, kp // 128, 4, 32)  # block, code group k, byte j
+    return (c4[:, :, 0] | (c4[:, :, 1] << 2) | (c4[:, :, 2] << 4) | (c4[:, :, 3] << 6)).reshape(rows, kp // 4)
+
+
+def gemv_shapes(ctx, reps: int = 4) -> dict:
+    """BASELINE configs 1 and 2 on the device: each decode-layer shape at M = 1
+    (f32 N(0,1) activation, absmax-quantized inside the op, f32 out) through
+    lbt_ternary_linear_dev -- the product decode GEMV with its fused quantizer.
+    "cold": enough distinct copies of the matrix (>= 288 MB) are rotated that
+    none is in the MALL when its turn comes; "warm": one copy called again and
+    again (the reference kbench's method, kbench.rs:44-63).  Per-launch
+    device time from HIP events on the library's stream; bytes = packed
+    weights + the f32 activation row."""
+    import ctypes as C
+
+    lib = ctx.lib
+    rng = np.random.default_rng(1)
+    out = {}
+    for name, rows, cols in LAYER_SHAPES:
+        packed = synth_packed(rng, rows, cols)
+        ncopy = max(64, -(-COLD_BYTES // packed.nbytes))
+        ws = [ctx.upload(packed, rows, cols, 1.0) for _ in range(ncopy)]
+        x = rng.standard_normal(cols).astype(np.float32)
+        dx, do = C.c_void_p(), C.c_void_p()
+        ctx.check(lib.lbt_dev_alloc(ctx.h, x.nbytes, C.byref(dx)))
+        ctx.check(lib.lbt_dev_alloc(ctx.h, rows * 4, C.byref(do)))
+        ctx.check(lib.lbt_memcpy_h2d(ctx.h, dx, x.ctypes.data, x.nbytes))
+        oa = (C.c_void_p * 1)(do.value)
+        was = [(C.c_void_p * 1)(w.h) for w in ws]
+
+        def run(seq):
+            ctx.prof_read(reset=True)
+            ctx.prof_enable(True)
+            for wa in seq:
+                ctx.check(lib.lbt_ternary_linear_dev(ctx.h, wa, 1, dx, 1, cols, oa))
+            p = ctx.prof_read(reset=True)["gemv"]
+            ctx.prof_enable(False)
+            return p["ms"] * 1e3 / max(p["launches"], 1)
+
+        run(was[:4])  # code objects, clocks
+        cold = run(was * reps)
+        warm = run([was[0]] * 256)
+        bytes_ = packed.nbytes + cols * 4
+        rec = {"rows": rows, "cols": cols, "copies": ncopy}
+        for k, us in (("cold", cold), ("warm", warm)):
+            gbs = bytes_ / (us * 1e-6) / 1e9
+            rec[k] = {"us": round(us, 3), "GBs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+        out[name] = rec
+        for w in ws:
+            w.free()
+        lib.lbt_dev_free(ctx.h, dx)
+        lib.lbt_dev_free(ctx.h, do)
+    return out
+
+
 def pmc_pass() -> int:
     """The command profiled for the HBM counters (under rocprofv3 --pmc):
     one copy of CALIB_BYTES with the library's copy kernel (the calibration
@@ -198,37 +264,106 @@ def pmc_pass() -> int:
     return 0
 
 
-def cpu_baseline(budget_s: float = 15.0) -> dict:
-    """Reference CPU path restated (VNNI/AVX-512BW/AVX2 ternary GEMV +
-    AVX-512 bf16 LM head, OpenMP over rows), same model shape and seed,
-    greedy decode on this host's cores for about `budget_s` seconds."""
+def _loop(fn, min_s: float = 0.3) -> float:
+    """kbench's timing (kbench.rs:44-63): one warm-up call, then calls until
+    at least `min_s` seconds have passed; seconds per call."""
+    fn()
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= min_s:
+            return el / n
+
+
+def cpu_baseline(decode_s: float = 12.0, decode_s1: float = 8.0) -> dict:
+    """Reference CPU path restated (VNNI/AVX-512BW/AVX2 ternary GEMV/GEMM +
+    AVX-512 bf16 LM head, OpenMP over rows) timed on this host, on all cores
+    and on one: (1) BASELINE config 4, the 2B-shaped model (same shape and
+    seed as the device run) prefilling the 64-token prompt and then decoding
+    greedily for about `decode_s` (`decode_s1` on one core) seconds; (2) the
+    config-1/2 GEMV shapes at M = 1 (kbench.rs:44-63: warm, >= 0.3 s loop),
+    plus one pass over a 520 MB matrix (kbench.rs:75-127, cold); (3) the
+    config-3 prefill GEMM at M = 128 / 512 / 2048 (one core: M = 128)."""
     sys.path.insert(0, str(REPO / "oracle"))
     import lbt_oracle as orc
 
+    allc = int(orc.lib().port_threads())
+    rng = np.random.default_rng(1)
+    shapes = {}
+    for name, rows, cols in LAYER_SHAPES:
+        packed = synth_packed(rng, rows, cols)
+        x = rng.standard_normal((1, cols)).astype(np.float32)
+        q, sa, qs = orc.quantize_acts(x)
+        rec = {}
+        for nt in (allc, 1):
+            dt = _loop(lambda: orc.port_gemm_i32(packed, rows, cols, q, qs, threads=nt))
+            rec["all" if nt == allc else "one"] = {"us": round(dt * 1e6, 1), "GBs": round(packed.nbytes / dt / 1e9, 2)}
+        shapes[name] = rec
+    # the 520 MB stream: a 2560-column matrix of ~520 MB, read once per call
+    tile = synth_packed(rng, 6912, 2560)
+    reps_ = -(-520_000_000 // tile.nbytes)
+    big = np.tile(tile, (reps_, 1))
+    x = rng.standard_normal((1, 2560)).astype(np.float32)
+    q, sa, qs = orc.quantize_acts(x)
+    stream = {}
+    for nt in (allc, 1):
+        t0 = time.perf_counter()
+        orc.port_gemm_i32(big, big.shape[0], 2560, q, qs, threads=nt)
+        dt = time.perf_counter() - t0
+        stream["all" if nt == allc else "one"] = {"ms": round(dt * 1e3, 1), "GBs": round(big.nbytes / dt / 1e9, 2)}
+    del big
+    prefill = []
+    for rows, cols in [(6912, 2560), (2560, 6912)]:
+        packed = synth_packed(rng, rows, cols)
+        for m, nts in ((128, (allc, 1)), (512, (allc,)), (2048, (allc,))):
+            x = rng.standard_normal((m, cols)).astype(np.float32)
+            q, sa, qs = orc.quantize_acts(x)
+            for nt in nts:
+                dt = _loop(lambda: orc.port_gemm_i32(packed, rows, cols, q, qs, threads=nt))
+                prefill.append({"rows": rows, "cols": cols, "m": m, "threads": nt,
+                                "GOPS": round(2.0 * m * rows * cols / dt / 1e9, 1)})
+
     old = orc.set_fast(2)
+    decode = {}
     try:
         t0 = time.perf_counter()
         om = orc.OracleModel(orc.config(), SEED)
         build_s = time.perf_counter() - t0
-        prompt = np.random.default_rng(64).integers(0, 128256, 8).astype(np.uint32)
-        tok = int(om.forward(prompt)[0].argmax())
-        n, t0 = 0, time.perf_counter()
-        while True:
-            tok = int(om.forward([tok])[0].argmax())
-            n += 1
-            el = time.perf_counter() - t0
-            if el > budget_s or n >= 256:
-                break
+        prompt = np.random.default_rng(64).integers(0, 128256, PROMPT_LEN).astype(np.uint32)
+        for nt, budget in ((allc, decode_s), (1, decode_s1)):
+            orc.set_threads(nt)
+            om.reset()
+            t0 = time.perf_counter()
+            tok = int(om.forward(prompt)[-1].argmax())
+            pf = time.perf_counter() - t0
+            n, t0 = 0, time.perf_counter()
+            while True:
+                tok = int(om.forward([tok])[0].argmax())
+                n += 1
+                el = time.perf_counter() - t0
+                if el > budget or n >= 256:
+                    break
+            decode["all" if nt == allc else "one"] = {"tok_s": round(n / el, 3), "steps": n,
+                                                      "prefill64_s": round(pf, 2)}
         om.free()
     finally:
+        orc.set_threads(0)
         orc.set_fast(old)
     return {
-        "value": round(n / el, 3),
+        "value": decode["all"]["tok_s"],
         "unit": "tok/s",
-        "cores": int(orc.lib().port_threads()),
+        "cores": allc,
         "kind": "port",
-        "sample": f"2B-shaped synthetic model (seed {SEED}), 8-token prompt then {n} greedy decode steps in "
-                  f"{el:.1f}s; ternary {orc.lib().port_isa().decode()} + AVX-512 bf16 head (model build {build_s:.1f}s)",
+        "sample": f"2B-shaped synthetic model (seed {SEED}), the 64-token prompt then "
+                  f"{decode['all']['steps']} greedy decode steps on {allc} threads; ternary "
+                  f"{orc.lib().port_isa().decode()} + AVX-512 bf16 head (model build {build_s:.1f}s)",
+        "decode_one_core": decode["one"],
+        "decode_all_cores": decode["all"],
+        "gemv_shapes_warm": shapes,
+        "gemv_520MB_stream": stream,
+        "prefill_gemm": prefill,
     }
 
 
@@ -242,6 +377,7 @@ def main() -> int:
     ap.add_argument("--pmc-pass", action="store_true", help="the workload profiled for the HBM counters")
     ap.add_argument("--no-batched", action="store_true", help="skip the batched-decode (config 5) figures")
     ap.add_argument("--no-int8-head", action="store_true", help="skip the opt-in int8 LM head figure")
+    ap.add_argument("--no-shapes", action="store_true", help="skip the config-1/2 per-shape GEMV figures")
     ap.add_argument("--int8-head-only", action="store_true",
                     help="only the opt-in int8 LM head decode figure (the workload profiled for its kernel)")
     ap.add_argument("--prefill-only", action="store_true",
@@ -354,6 +490,8 @@ def main() -> int:
         line["batched_decode"] = [batched_decode(model, cfg, bsz) for bsz in (16, 64)]
         line["continuous_batching"] = sched_throughput(model, cfg)
         line["prefill_gemm"] = prefill_gemm(ctx)
+    if not args.no_shapes:
+        line["gemv_shapes"] = gemv_shapes(ctx)
     model.free()
     ctx.close()
     if not args.no_cpu_baseline:

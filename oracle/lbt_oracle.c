@@ -500,6 +500,20 @@ struct or_model {
 
 static int g_fast = 0;
 int or_set_fast(int fast) { int o = g_fast; g_fast = fast; return o; }
+static int g_threads = 0; /* 0: every OpenMP thread */
+/* Thread count of every parallel loop here and of the SIMD port's kernels
+ * (0 = all); returns the previous setting.  Used to time the CPU baseline on
+ * one core and on all cores in one process. */
+int or_set_threads(int n) {
+    int o = g_threads;
+    g_threads = n > 0 ? n : 0;
+#ifdef _OPENMP
+    static int all = 0;
+    if (!all) all = omp_get_max_threads();
+    omp_set_num_threads(n > 0 ? n : all);
+#endif
+    return o;
+}
 
 static const int kLinRows[7] = {0, 1, 1, 0, 2, 2, 0}; /* rows: 0=hidden 1=kv 2=inter */
 
@@ -619,7 +633,7 @@ static void linear(const or_model* m, const float* x, size_t n, size_t k, int la
     int32_t* qs = (int32_t*)malloc(n * sizeof(int32_t));
     or_quantize_acts(x, n, k, q, sa, qs);
     int32_t* d = (int32_t*)malloc(n * rows * sizeof(int32_t));
-    if (g_fast) port_gemm_i32(m->packed[layer * 7 + which], rows, cols, q, qs, n, d, 0);
+    if (g_fast) port_gemm_i32(m->packed[layer * 7 + which], rows, cols, q, qs, n, d, g_threads);
     else or_gemm_i32(m->packed[layer * 7 + which], rows, cols, q, qs, n, d);
     float sw = m->wscale[layer * 7 + which];
     for (size_t t = 0; t < n; t++) {
@@ -833,6 +847,10 @@ int or_model_forward(or_model* m, const uint32_t* tokens, size_t n, int all_logi
         /* GQA attention (model.rs:349-357): q head h reads kv head h / group. */
         for (size_t t = 0; t < n; t++) {
             size_t vis = pos0 + t + 1;
+            if (g_fast >= 2) { /* reference order, SIMD, heads over threads (timed CPU baseline only) */
+                port_attention(q + t * H, K, V, nh, group, cap, vis, hd, scaling, att + t * H, g_threads);
+                continue;
+            }
             for (size_t h = 0; h < nh; h++)
                 attn_split_group(q + t * H + h * hd, K + (h / group) * cap * hd, V + (h / group) * cap * hd, vis, hd,
                                  1, scaling, att + t * H + h * hd);
@@ -864,7 +882,7 @@ int or_model_forward(or_model* m, const uint32_t* tokens, size_t n, int all_logi
         or_rmsnorm(x + t * H, m->final_norm, H, eps, nrm);
         float* lt = logits + (t - first) * (size_t)c->vocab;
         if (m->head_kind == 1) or_q8head_gemv_lanes(m->q8, m->q8s, (size_t)c->vocab, H, nrm, lt);
-        else if (g_fast >= 2) port_bf16_gemv(m->embed, (size_t)c->vocab, H, nrm, lt, 0); /* reference order */
+        else if (g_fast >= 2) port_bf16_gemv(m->embed, (size_t)c->vocab, H, nrm, lt, g_threads); /* reference order */
         else or_bf16_gemv_lanes(m->embed, (size_t)c->vocab, H, nrm, lt);
     }
     free(x); free(nrm); free(q); free(kk); free(vv); free(att); free(y); free(g); free(u);

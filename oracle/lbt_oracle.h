@@ -130,6 +130,7 @@ int or_model_cap(const or_model* m);
  * reference-order AVX-512 bf16 LM head (the CPU baseline; logits then differ
  * from the device order by float rounding).  Returns the previous setting. */
 int or_set_fast(int fast);
+int or_set_threads(int n);
 
 #ifdef __cplusplus
 }

@@ -76,6 +76,7 @@ _SIGS = {
     "or_model_vcache": (vp, [vp, i32]),
     "or_model_cap": (i32, [vp]),
     "or_set_fast": (i32, [i32]),
+    "or_set_threads": (i32, [i32]),
     "port_isa": (C.c_char_p, []),
     "port_gemm_i32": (None, [vp, sz, sz, vp, vp, sz, vp, i32]),
     "port_gemm_f32": (None, [vp, sz, sz, f32, vp, vp, vp, sz, vp, i32]),
@@ -400,3 +401,9 @@ def config(hidden=2560, intermediate=6912, heads=20, kv_heads=5, layers=30, voca
 
 def set_fast(mode: int) -> int:
     return lib().or_set_fast(mode)
+
+
+def set_threads(n: int) -> int:
+    """Threads of the oracle's parallel loops and the port's kernels (0 = all);
+    returns the previous setting."""
+    return lib().or_set_threads(n)

@@ -254,3 +254,80 @@ void port_bf16_gemv(const uint16_t* w, size_t rows, size_t cols, const float* x,
                                      : or_bf16_dot_ref(wr, x, cols);
     }
 }
+
+/* ---- attention over the bf16 cache (model.rs:349-357) ----------------------
+ * One query row per head: scores = q.K^T * scaling, softmax, probs @ V, as the
+ * reference's Flex backend computes them (f32 dot products, max-subtracted
+ * expf, a normalised sum of value rows), with the cache rows read in order. */
+__attribute__((target("avx2,fma"))) static inline __m256 bf16x8_avx2(const uint16_t* p) {
+    __m128i h = _mm_loadu_si128((const __m128i*)p);
+    return _mm256_castsi256_ps(_mm256_slli_epi32(_mm256_cvtepu16_epi32(h), 16));
+}
+
+__attribute__((target("avx2,fma"))) static void attn_head_avx2(const float* q, const uint16_t* K,
+                                                                const uint16_t* V, size_t vis, size_t hd,
+                                                                float scaling, float* e, float* out) {
+    float mx = -INFINITY;
+    for (size_t j = 0; j < vis; j++) {
+        const uint16_t* kr = K + j * hd;
+        __m256 a = _mm256_setzero_ps();
+        for (size_t d = 0; d < hd; d += 8) a = _mm256_fmadd_ps(_mm256_loadu_ps(q + d), bf16x8_avx2(kr + d), a);
+        __m128 s4 = _mm_add_ps(_mm256_castps256_ps128(a), _mm256_extractf128_ps(a, 1));
+        s4 = _mm_add_ps(s4, _mm_movehl_ps(s4, s4));
+        s4 = _mm_add_ss(s4, _mm_shuffle_ps(s4, s4, 1));
+        e[j] = _mm_cvtss_f32(s4) * scaling;
+        if (e[j] > mx) mx = e[j];
+    }
+    float sum = 0.0f;
+    for (size_t j = 0; j < vis; j++) {
+        e[j] = expf(e[j] - mx);
+        sum += e[j];
+    }
+    float acc[512];
+    for (size_t d = 0; d < hd; d++) acc[d] = 0.0f;
+    for (size_t j = 0; j < vis; j++) {
+        const uint16_t* vr = V + j * hd;
+        __m256 p = _mm256_set1_ps(e[j]);
+        for (size_t d = 0; d < hd; d += 8)
+            _mm256_storeu_ps(acc + d, _mm256_fmadd_ps(p, bf16x8_avx2(vr + d), _mm256_loadu_ps(acc + d)));
+    }
+    float inv = 1.0f / sum;
+    for (size_t d = 0; d < hd; d++) out[d] = acc[d] * inv;
+}
+
+void port_attention(const float* q, const uint16_t* K, const uint16_t* V, size_t nh, size_t group,
+                    size_t cap, size_t vis, size_t hd, float scaling, float* out, int threads) {
+    int nt = threads > 0 ? threads : port_threads();
+    int fast = detect_isa() >= ISA_AVX2 && hd % 8 == 0 && hd <= 512;
+#pragma omp parallel num_threads(nt)
+    {
+        float* e = (float*)malloc(vis * sizeof(float));
+#pragma omp for schedule(static)
+        for (long h = 0; h < (long)nh; h++) {
+            const uint16_t* Kh = K + (size_t)(h / (long)group) * cap * hd;
+            const uint16_t* Vh = V + (size_t)(h / (long)group) * cap * hd;
+            const float* qh = q + (size_t)h * hd;
+            float* oh = out + (size_t)h * hd;
+            if (fast) {
+                attn_head_avx2(qh, Kh, Vh, vis, hd, scaling, e, oh);
+                continue;
+            }
+            float mx = -INFINITY, sum = 0.0f;
+            for (size_t j = 0; j < vis; j++) {
+                float a = 0.0f;
+                for (size_t d = 0; d < hd; d++) a += qh[d] * or_bf16_to_f32(Kh[j * hd + d]);
+                e[j] = a * scaling;
+                if (e[j] > mx) mx = e[j];
+            }
+            for (size_t j = 0; j < vis; j++) {
+                e[j] = expf(e[j] - mx);
+                sum += e[j];
+            }
+            for (size_t d = 0; d < hd; d++) oh[d] = 0.0f;
+            for (size_t j = 0; j < vis; j++)
+                for (size_t d = 0; d < hd; d++) oh[d] += e[j] * or_bf16_to_f32(Vh[j * hd + d]);
+            for (size_t d = 0; d < hd; d++) oh[d] /= sum;
+        }
+        free(e);
+    }
+}

@@ -29,6 +29,10 @@ void port_gemm_f32(const uint8_t* packed, size_t rows, size_t cols, float s_w, c
 float port_quantize_row(const float* x, size_t k, int8_t* q, int32_t* sum);
 /* bf16_gemv (bf16.rs:14-25) with dot_avx512 (bf16.rs:84-105) / dot_avx2 (:58-81). */
 void port_bf16_gemv(const uint16_t* w, size_t rows, size_t cols, const float* x, float* out, int threads);
+/* GQA attention of one token (model.rs:349-357): head h of nh reads kv head
+ * h / group of K/V [kv_heads][cap][hd] (bf16) over positions 0..vis-1. */
+void port_attention(const float* q, const uint16_t* K, const uint16_t* V, size_t nh, size_t group,
+                    size_t cap, size_t vis, size_t hd, float scaling, float* out, int threads);
 int port_threads(void);
 
 #ifdef __cplusplus

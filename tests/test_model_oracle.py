@@ -66,3 +66,29 @@ def test_fast_mode_same_logits():
     assert np.array_equal(la, lb)
     a.free()
     b.free()
+
+
+def test_cpu_baseline_mode_close_to_device_order():
+    """The timed CPU baseline (fast mode 2: SIMD attention and bf16 head in the
+    reference's plain order, any thread count) computes the same model: logits
+    within float tolerance of the device-order oracle, same argmax."""
+    cfg = small_cfg()
+    toks = np.array([1, 2, 3, 4, 5, 6, 7, 8], np.uint32)
+    a = orc.OracleModel(cfg, 3)
+    la = a.forward(toks, all_logits=True)
+    la2 = a.forward([9])
+    old = orc.set_fast(2)
+    try:
+        for nt in (1, 0):
+            orc.set_threads(nt)
+            b = orc.OracleModel(cfg, 3)
+            lb = b.forward(toks, all_logits=True)
+            lb2 = b.forward([9])
+            b.free()
+            np.testing.assert_allclose(lb, la, rtol=1e-3, atol=1e-3)
+            np.testing.assert_allclose(lb2, la2, rtol=1e-3, atol=1e-3)
+            assert np.array_equal(lb.argmax(1), la.argmax(1))
+    finally:
+        orc.set_threads(0)
+        orc.set_fast(old)
+    a.free()
