@@ -783,7 +783,7 @@ int launch_embed(lbt_ctx* ctx, const uint16_t* embed, int hidden, int vocab, con
 namespace {
 
 template <int LK>
-hipError_t launch_attn_lk(int gh, bool grouped, dim3 grid, size_t lds, hipStream_t st, hipEvent_t e0, hipEvent_t e1,
+hipError_t launch_attn_lk(int gh, bool grouped, bool force_wide, dim3 grid, size_t lds, hipStream_t st, hipEvent_t e0, hipEvent_t e1,
                           const float* q, int nh, int kvh, const RowPos& rp, const uint16_t* kc, const uint16_t* vc,
                           int cap, float scaling, float* o, float* ml) {
     if (!grouped) {
@@ -791,7 +791,7 @@ hipError_t launch_attn_lk(int gh, bool grouped, dim3 grid, size_t lds, hipStream
                               cap, scaling, o, ml);
         return hipGetLastError();
     }
-    const int wide = (long)grid.x * grid.y >= 4096 || getenv("LBT_ATTN_WIDE") ? 1 : 0;
+    const int wide = (long)grid.x * grid.y >= 4096 || force_wide ? 1 : 0;
     switch (gh) {
         case 1:
             hipExtLaunchKernelGGL((attention_group_kernel<LK, 1>), grid, dim3(kThreads), lds, st, e0, e1, 0, q, nh,
@@ -827,15 +827,15 @@ int launch_attention(lbt_ctx* ctx, const float* q, int m, int nh, int kvh, int h
     hipError_t e;
     switch (hd) {
         case 64:
-            e = launch_attn_lk<8>(gh, grouped, grid, lds, ctx->stream, e0, e1, q, nh, kvh, rp, kc, vc, cap, scaling, o,
+            e = launch_attn_lk<8>(gh, grouped, ctx->tune.attn_wide, grid, lds, ctx->stream, e0, e1, q, nh, kvh, rp, kc, vc, cap, scaling, o,
                                   ml);
             break;
         case 128:
-            e = launch_attn_lk<16>(gh, grouped, grid, lds, ctx->stream, e0, e1, q, nh, kvh, rp, kc, vc, cap, scaling,
+            e = launch_attn_lk<16>(gh, grouped, ctx->tune.attn_wide, grid, lds, ctx->stream, e0, e1, q, nh, kvh, rp, kc, vc, cap, scaling,
                                    o, ml);
             break;
         case 256:
-            e = launch_attn_lk<32>(gh, grouped, grid, lds, ctx->stream, e0, e1, q, nh, kvh, rp, kc, vc, cap, scaling,
+            e = launch_attn_lk<32>(gh, grouped, ctx->tune.attn_wide, grid, lds, ctx->stream, e0, e1, q, nh, kvh, rp, kc, vc, cap, scaling,
                                    o, ml);
             break;
         default:
@@ -882,7 +882,7 @@ int launch_head(lbt_ctx* ctx, const void* w, const float* rscale, int rows, int 
         // more than 8 rows: 16-token groups on 512 threads (the whole LDS of a
         // CU; each weight row is then read from L2 half as often), else
         // 8-token groups on 256 threads (two workgroups per CU)
-        const bool big = m > 8 && (size_t)16 * cols * sizeof(float) <= 160 * 1024 && !getenv("LBT_HEAD_TG8");
+        const bool big = m > 8 && (size_t)16 * cols * sizeof(float) <= 160 * 1024 && !ctx->tune.head_tg8;
         const int tg = big ? 16 : kTG, nt = big ? 512 : kThreads, nw = nt / 64;
         const int ngroups = (m + tg - 1) / tg;
         int tiles = ctx->cus * (big ? 2 : 4) / ngroups;

@@ -11,6 +11,31 @@
 
 namespace lbt {
 
+LbtTuning read_tuning() {
+    LbtTuning t;
+    auto num = [](const char* k, long d) {
+        const char* v = getenv(k);
+        return v && *v ? atol(v) : d;
+    };
+    t.no_graph = getenv("LBT_NO_GRAPH") != nullptr;
+    t.no_mfma = getenv("LBT_NO_MFMA") != nullptr;
+    t.mfma_min = (int)num("LBT_MFMA_MIN", kMfmaMinTokens);
+    if (t.mfma_min < 2) t.mfma_min = 2;
+    t.gemm_mode = (int)num("LBT_GEMM_MODE", 0);
+    if (t.gemm_mode != 4 && t.gemm_mode != 5 && t.gemm_mode != 6) t.gemm_mode = 0;
+    t.small_max = (int)num("LBT_GEMM_SMALL_MAX", kSmallMaxTokens);
+    t.small_tiles = num("LBT_GEMM_SMALL_TILES", 100);
+    t.small_ms = (int)num("LBT_GEMM_SMALL_MS", 1);
+    if (t.small_ms < 1) t.small_ms = 1;
+    t.small_ns = (int)num("LBT_GEMM_SMALL_NS", 0);
+    t.small_pf = num("LBT_GEMM_SMALL_PF", 1) != 0;
+    t.attn_wide = getenv("LBT_ATTN_WIDE") != nullptr;
+    t.head_tg8 = getenv("LBT_HEAD_TG8") != nullptr;
+    t.step_trace = getenv("LBT_STEP_TRACE") != nullptr;
+    return t;
+}
+
+
 int set_err(lbt_ctx* ctx, int code, const std::string& msg) {
     if (ctx) ctx->err = msg;
     return code;
@@ -118,6 +143,7 @@ extern "C" {
 
 const char* lbt_version(void) { return "lbt-hip 0.1 gfx950"; }
 
+
 int lbt_ctx_create(int device, lbt_ctx** out) {
     if (!out) return LBT_E_INVALID;
     *out = nullptr;
@@ -127,6 +153,7 @@ int lbt_ctx_create(int device, lbt_ctx** out) {
     if (hipSetDevice(device) != hipSuccess) return LBT_E_DEVICE;
     lbt_ctx* c = new lbt_ctx();
     c->device = device;
+    c->tune = read_tuning();
     if (hipDeviceGetAttribute(&c->cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || c->cus <= 0)
         c->cus = 256;
     if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {

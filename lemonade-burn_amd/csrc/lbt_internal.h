@@ -10,8 +10,26 @@
 
 #include "../../include/lbt.h"
 
+// Path selection read once from the environment when a context is created
+// (lbt_ctx_create); measurements and tests choose a path per context.
+struct LbtTuning {
+    bool no_graph = false;    // LBT_NO_GRAPH: decode steps as separate launches, no captured graph
+    bool no_mfma = false;     // LBT_NO_MFMA: several-token products on the VALU GEMV
+    int mfma_min = 2;         // LBT_MFMA_MIN: fewest tokens for the MFMA GEMMs
+    int gemm_mode = 0;        // LBT_GEMM_MODE: 0 auto, 4 / 5 = 64 / 128 tiles, 6 = few-token kernel
+    int small_max = 32;       // LBT_GEMM_SMALL_MAX: the few-token kernel serves up to this many tokens
+    long small_tiles = 100;   // LBT_GEMM_SMALL_TILES: ... and up to 64 tokens below this many 64x64 tiles
+    int small_ms = 1;         // LBT_GEMM_SMALL_MS: cap of its token tiles (16 * ms)
+    int small_ns = 0;         // LBT_GEMM_SMALL_NS: 1 / 2 forces its row tile (0 auto)
+    bool small_pf = true;     // LBT_GEMM_SMALL_PF=0: no epilogue prefetch
+    bool attn_wide = false;   // LBT_ATTN_WIDE: eight-pass K/V pipeline of the grouped attention
+    bool head_tg8 = false;    // LBT_HEAD_TG8: 8-token groups in the batched LM head
+    bool step_trace = false;  // LBT_STEP_TRACE: phase timestamps of the one-dispatch decode step
+};
+
 struct lbt_ctx {
     int device = 0;
+    LbtTuning tune;
     int cus = 256;  // compute units of the device
     hipStream_t stream = nullptr;
     std::string err;
@@ -56,6 +74,8 @@ struct lbt_q8head {
 };
 
 namespace lbt {
+// The switches of LbtTuning from the environment.
+LbtTuning read_tuning();
 
 // Error helpers: every entry point converts failures into a status code.
 int set_err(lbt_ctx* ctx, int code, const std::string& msg);

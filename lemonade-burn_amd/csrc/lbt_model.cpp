@@ -326,7 +326,7 @@ int validate_config(lbt_ctx* ctx, const lbt_config& c) {
 // Device buffers and RoPE tables shared by load and synthetic creation.
 int model_alloc(lbt_model* m) {
     lbt_ctx* ctx = m->ctx;
-    m->want_trace = getenv("LBT_STEP_TRACE") != nullptr;
+    m->want_trace = ctx->tune.step_trace;
     const lbt_config& c = m->cfg;
     m->hd = c.hidden_size / c.num_attention_heads;
     size_t wbytes = 0;
@@ -809,7 +809,7 @@ int decode_steps(lbt_model* m, lbt_cache* c, int n, int slot0) {
         m->last_n = 1;
         return LBT_OK;
     }
-    if (ctx->prof || getenv("LBT_NO_GRAPH")) {
+    if (ctx->prof || ctx->tune.no_graph) {
         for (int s = 0; s < n; s++)
             if ((rc = forward_dev(m, c, nullptr, 1, false, false, m->tok_out + slot0 + s))) return rc;
         return LBT_OK;

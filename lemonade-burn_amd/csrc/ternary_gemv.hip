@@ -384,7 +384,7 @@ int make_gemv_args(lbt_ctx* ctx, const TernaryOp& op, GemvArgs& a) {
 }
 
 int launch_ternary_gemv(lbt_ctx* ctx, const TernaryOp& op) {
-    if (op.m == 1 && op.in_mode != kInPreQ && !getenv("LBT_GEMV_CLASSIC")) {
+    if (op.m == 1 && op.in_mode != kInPreQ) {
         const int rc = launch_ternary_gemv_cu(ctx, op);
         if (rc != 1) return rc;  // launched, or an error
     }
@@ -496,9 +496,7 @@ int launch_ternary(lbt_ctx* ctx, const TernaryOp& op_in) {
         op.tok_pos = nullptr;
         op.pos_dev = nullptr;
     }
-    const char* mm = getenv("LBT_MFMA_MIN");
-    const int mfma_min = mm ? atoi(mm) : kMfmaMinTokens;
-    if (op.m >= (mfma_min > 1 ? mfma_min : 2) && !getenv("LBT_NO_MFMA")) return launch_ternary_mfma(ctx, op);
+    if (op.m >= ctx->tune.mfma_min && !ctx->tune.no_mfma) return launch_ternary_mfma(ctx, op);
     return launch_ternary_gemv(ctx, op);
 }
 

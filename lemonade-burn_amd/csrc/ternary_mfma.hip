@@ -1,11 +1,13 @@
-// ternary_mfma.hip -- packed 2-bit ternary x int8 prefill GEMM on the gfx950
-// int8 matrix cores (v_mfma_i32_16x16x64_i8).
+// ternary_mfma.hip -- packed 2-bit ternary x int8 GEMMs on the gfx950 int8
+// matrix cores: the few-token kernel (v_mfma_i32_16x16x64_i8, batched decode
+// and short prefills) and the pipelined prefill GEMM
+// (v_mfma_i32_32x32x32_i8).
 //
 // Replaces the reference's prefill branch of ternary_gemm_multi
 // (crates/lb-ternary/src/gemm.rs:155-194) and its AVX-512 2x4 register tile
 // (tile_rows / tile_avx512bw, gemm.rs:245-268, :483-550).
 //
-// Layout of one MFMA (16 tokens x 16 rows x 64 k): lane l = 16*g + i holds
+// Layout of one 16 x 16 x 64 MFMA (16 tokens x 16 rows x 64 k): lane l = 16*g + i holds
 // A = 16 int8 activations of token i and B = 16 weight codes of row i for the
 // same 16 k values (chunk g).  The 64 k values of one MFMA are taken straight
 // from the LB2 layout: lane group g owns packed chunk c = 4p + g (16 bytes =
@@ -16,11 +18,8 @@
 // dword (no table, no LDS expansion) and fed as int8; the exact i32 result
 // sum(c*q) - sum(q) is the reference's dot (gemm.rs:3-17, :306-308).
 //
-// Tiling: 4 wavefronts (2 x 2), each 16*MS tokens x 16*NS rows; activations
-// are staged through LDS in 256-byte k-slices (double-buffered, rows padded to
-// 272 bytes so each 16-lane group reads distinct banks), weights go from HBM
-// straight into registers one super step ahead.  The epilogues are those of
-// the decode GEMV (ternary_common.h), so outputs are identical.
+// The epilogues are those of the decode GEMV (ternary_common.h), so outputs
+// are identical.
 #include <stdlib.h>
 
 #include <type_traits>
@@ -215,96 +214,6 @@ __device__ __forceinline__ void mfma_epilogue(const GemvArgs& a, AccT (&acc)[MS]
     }
 }
 
-template <int MS, int NS, int OUT>
-__global__ __launch_bounds__(kThreads) void tgemm_kernel(GemvArgs a) {
-    constexpr int BM = 32 * MS, BN = 32 * NS, AST = 256 + 16, APT = BM / 16;
-    __shared__ __align__(16) int8_t As[2][BM * AST];
-    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
-    const int wm = w & 1, wn = w >> 1;
-    const int li = lane & 15, lg = lane >> 4;
-    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-    const int C = a.C, kp = a.kp, M = a.m;
-    const int nsteps = (C + 3) / 4;
-
-    const uint4* brow[NS];
-    bool bval[NS];
-#pragma unroll
-    for (int s = 0; s < NS; s++) {
-        const int vr = n0 + wn * (BN / 2) + s * 16 + li;
-        bval[s] = vr < a.total_rows;
-        int mat, r;
-        resolve_row<OUT>(a, bval[s] ? vr : 0, mat, r);
-        brow[s] = (const uint4*)(sel3(a.w, mat) + (size_t)r * (size_t)(kp >> 2));
-    }
-
-    int4 ast[APT];
-    uint4 bw[NS];
-    auto a_load = [&](int p) {
-#pragma unroll
-        for (int e = 0; e < APT; e++) {
-            const int idx = tid + kThreads * e, row = idx >> 4, col = idx & 15;
-            const int tok = m0 + row, kb = p * 256 + col * 16;
-            ast[e] = (tok < M && kb < kp) ? *(const int4*)(a.q + (size_t)tok * kp + kb) : make_int4(0, 0, 0, 0);
-        }
-    };
-    auto a_store = [&](int buf) {
-#pragma unroll
-        for (int e = 0; e < APT; e++) {
-            const int idx = tid + kThreads * e, row = idx >> 4, col = idx & 15;
-            *(int4*)(As[buf] + row * AST + col * 16) = ast[e];
-        }
-    };
-    auto b_load = [&](int p) {
-#pragma unroll
-        for (int s = 0; s < NS; s++) {
-            const int c = 4 * p + lg;
-            bw[s] = (bval[s] && c < C) ? ld_stream(brow[s] + c) : make_uint4(0, 0, 0, 0);
-        }
-    };
-
-    v4i acc[MS][NS];
-#pragma unroll
-    for (int ms = 0; ms < MS; ms++)
-#pragma unroll
-        for (int s = 0; s < NS; s++) acc[ms][s] = v4i{0, 0, 0, 0};
-
-    a_load(0);
-    b_load(0);
-    a_store(0);
-    __syncthreads();
-    for (int p = 0; p < nsteps; p++) {
-        const int buf = p & 1;
-        uint4 bcur[NS];
-#pragma unroll
-        for (int s = 0; s < NS; s++) bcur[s] = bw[s];
-        if (p + 1 < nsteps) {
-            a_load(p + 1);
-            b_load(p + 1);
-        }
-        const int8_t* Ab = As[buf] + (wm * (BM / 2) + li) * AST + (lg >> 1) * 128 + (lg & 1) * 16;
-#pragma unroll
-        for (int kk = 0; kk < 4; kk++) {
-            const int sh = 2 * kk;
-            v4i bop[NS];
-#pragma unroll
-            for (int s = 0; s < NS; s++)
-                bop[s] = v4i{(int)((bcur[s].x >> sh) & 0x03030303u), (int)((bcur[s].y >> sh) & 0x03030303u),
-                             (int)((bcur[s].z >> sh) & 0x03030303u), (int)((bcur[s].w >> sh) & 0x03030303u)};
-#pragma unroll
-            for (int ms = 0; ms < MS; ms++) {
-                const v4i aop = *(const v4i*)(Ab + ms * 16 * AST + kk * 32);
-#pragma unroll
-                for (int s = 0; s < NS; s++)
-                    acc[ms][s] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aop, bop[s], acc[ms][s], 0, 0, 0);
-            }
-        }
-        if (p + 1 < nsteps) a_store(buf ^ 1);
-        __syncthreads();
-    }
-
-    mfma_epilogue<OUT, 16>(a, acc, m0 + wm * (BM / 2), n0 + wn * (BN / 2));
-}
-
 // ---------------------------------------------------------------------------
 // Few-token GEMM (batched decode and short prefills, 2..32 tokens, and up to
 // 64 for the shapes with few 64 x 64 tiles): the
@@ -317,7 +226,7 @@ __global__ __launch_bounds__(kThreads) void tgemm_kernel(GemvArgs a) {
 // per lane and row tile), reads the activations (L2-resident, 16 MS tokens)
 // straight from global memory one step ahead, and the three partial int32
 // tiles are added to wavefront 0's through LDS (exact, any order) before the
-// shared epilogue.  Operand layout as tgemm_kernel: lane (li, lg) takes chunk
+// shared epilogue.  Operand layout: lane (li, lg) takes chunk
 // 4p + lg of row li and, for MFMA kk of step p, the 16 activations of token
 // li at k = 256 p + 128 (lg >> 1) + 32 kk + 16 (lg & 1).
 // Loads of mfma_epilogue's per-token values (16 x 16 tiles), the same
@@ -357,7 +266,6 @@ __device__ __forceinline__ void epi_prefetch(const GemvArgs& a, int tok0, int ro
 
 constexpr int kSmallMaxSteps = 8;  // 256-k steps per wavefront: K <= 8192
 constexpr int kSmallWideRowTiles = 384;  // 32-row tiles from 384 * 32 rows
-constexpr long kSmallFewTiles = 100;
 
 template <int OUT, int MS, int NS, bool PF = false>
 __global__ __launch_bounds__(kThreads) void tgemm_small_kernel(GemvArgs a) {
@@ -654,18 +562,6 @@ __global__ __launch_bounds__(kThreads) void tgemm2_kernel(GemvArgs a) {
 
 namespace {
 
-template <int MS, int NS>
-hipError_t launch_tiles(const GemvArgs& a, int out_mode, dim3 grid, hipStream_t s, hipEvent_t e0, hipEvent_t e1) {
-    switch (out_mode) {
-        case kOutI32: hipExtLaunchKernelGGL((tgemm_kernel<MS, NS, kOutI32>), grid, dim3(kThreads), 0, s, e0, e1, 0, a); break;
-        case kOutF32: hipExtLaunchKernelGGL((tgemm_kernel<MS, NS, kOutF32>), grid, dim3(kThreads), 0, s, e0, e1, 0, a); break;
-        case kOutF32Add: hipExtLaunchKernelGGL((tgemm_kernel<MS, NS, kOutF32Add>), grid, dim3(kThreads), 0, s, e0, e1, 0, a); break;
-        case kOutRelu2: hipExtLaunchKernelGGL((tgemm_kernel<MS, NS, kOutRelu2>), grid, dim3(kThreads), 0, s, e0, e1, 0, a); break;
-        default: hipExtLaunchKernelGGL((tgemm_kernel<MS, NS, kOutQKV>), grid, dim3(kThreads), 0, s, e0, e1, 0, a); break;
-    }
-    return hipGetLastError();
-}
-
 template <int MS, int NS, int KB>
 hipError_t launch_tiles2(const GemvArgs& a, int out_mode, dim3 grid, hipStream_t s, hipEvent_t e0, hipEvent_t e1) {
     constexpr size_t lds = (size_t)kG2Stages * (64 * MS) * (128 * KB);
@@ -703,11 +599,11 @@ hipError_t launch_small_pf(const GemvArgs& a, int out_mode, dim3 grid, hipStream
 }
 
 template <int MS, int NS>
-hipError_t launch_small(const GemvArgs& a, int out_mode, dim3 grid, hipStream_t s, hipEvent_t e0, hipEvent_t e1) {
+hipError_t launch_small(const GemvArgs& a, int out_mode, bool pf, dim3 grid, hipStream_t s, hipEvent_t e0,
+                        hipEvent_t e1) {
     // 16-token tiles: the epilogue's per-token loads go out with the weight
-    // stream (measured +1.5-2% at B = 8..64); LBT_GEMM_SMALL_PF=0 turns it off
+    // stream (measured +1.5-2% at B = 8..64)
     if constexpr (MS == 1) {
-        static const bool pf = !getenv("LBT_GEMM_SMALL_PF") || atoi(getenv("LBT_GEMM_SMALL_PF")) != 0;
         if (pf) return launch_small_pf<MS, NS, true>(a, out_mode, grid, s, e0, e1);
     }
     return launch_small_pf<MS, NS, false>(a, out_mode, grid, s, e0, e1);
@@ -754,60 +650,45 @@ int launch_ternary_mfma(lbt_ctx* ctx, const TernaryOp& op_in) {
     int rc = make_gemv_args(ctx, op, a);
     if (rc) return rc;
     const int total = a.total_rows;
-    const bool big = (long)((total + 127) / 128) * ((op.m + 127) / 128) >= 240;
     hipEvent_t e0, e1;
     prof_pair(ctx, &e0, &e1);
     hipError_t e;
-    // LBT_GEMM_MODE (tests and measurements): 1 = 16x16x64 kernel, 2 / 3 =
-    // 32x32x32 with 256-k steps (128 / 64 tiles), 4 / 5 = 128-k steps with 64 /
-    // 128 tiles, 6 = few-token kernel (16-row tiles, K split over the
-    // wavefronts); default: the few-token kernel up to kSmallMaxTokens tokens
-    // (LBT_GEMM_SMALL_MAX overrides), then 128 tiles when there are >= 200 of
-    // them, else 64
-    const char* gm = getenv("LBT_GEMM_MODE");
-    const int gmode = gm ? atoi(gm) : 0;
+    // path (LBT_GEMM_MODE forces one, for tests and measurements): 6 = the
+    // few-token kernel, 4 / 5 = 64 / 128 tiles of the pipelined GEMM; by
+    // default the few-token kernel up to tune.small_max tokens, then 128
+    // tiles when there are >= 200 of them, else 64
+    const LbtTuning& tu = ctx->tune;
+    const int gmode = tu.gemm_mode;
     const long t128 = (long)((total + 127) / 128) * ((op.m + 127) / 128);
     const dim3 g128((unsigned)((total + 127) / 128), (unsigned)((op.m + 127) / 128));
     const dim3 g64((unsigned)((total + 63) / 64), (unsigned)((op.m + 63) / 64));
-    const char* sm = getenv("LBT_GEMM_SMALL_MAX");
-    const int small_max = sm ? atoi(sm) : kSmallMaxTokens;
     const bool small_ok = a.kp <= 256 * 4 * kSmallMaxSteps;
     // up to 64 tokens the few-token kernel also serves the shapes the 64 x 64
-    // tiling would give fewer than kSmallFewTiles tiles (q/k/v, o, down of
-    // the 2B model at B = 33..64; LBT_GEMM_SMALL_TILES overrides)
-    const char* st = getenv("LBT_GEMM_SMALL_TILES");
+    // tiling would give fewer than tune.small_tiles tiles (q/k/v, o, down of
+    // the 2B model at B = 33..64)
     const long t64 = (long)((total + 63) / 64) * ((op.m + 63) / 64);
-    const bool few_tiles = op.m <= 64 && t64 < (st ? atol(st) : kSmallFewTiles);
-    if (small_ok && (gmode == 6 || (gmode == 0 && (op.m <= small_max || few_tiles)))) {
+    const bool few_tiles = op.m <= 64 && t64 < tu.small_tiles;
+    if (small_ok && (gmode == 6 || (gmode == 0 && (op.m <= tu.small_max || few_tiles)))) {
         // 16-token tiles (more workgroups) measured faster than 32..64-token
-        // ones at every batch served here; LBT_GEMM_SMALL_MS = 2..4 selects
-        // the wider tiles
-        const char* mc = getenv("LBT_GEMM_SMALL_MS");
-        const int mcap = mc ? atoi(mc) : 1;
+        // ones at every batch served here; tune.small_ms = 2..4 allows the
+        // wider tiles
         int ms = op.m <= 16 ? 1 : op.m <= 32 ? 2 : op.m <= 48 ? 3 : 4;
-        if (ms > mcap) ms = mcap < 1 ? 1 : mcap;
+        if (ms > tu.small_ms) ms = tu.small_ms;
         // 32-row tiles (half the activation re-reads) where they still give
-        // >= 256 workgroups per token tile; LBT_GEMM_SMALL_NS = 1 / 2 forces
-        const char* nc = getenv("LBT_GEMM_SMALL_NS");
-        const int ns = nc ? (atoi(nc) == 2 ? 2 : 1) : (total >= 32 * kSmallWideRowTiles ? 2 : 1);
+        // >= 256 workgroups per token tile; tune.small_ns = 1 / 2 forces
+        const int ns = tu.small_ns ? (tu.small_ns == 2 ? 2 : 1) : (total >= 32 * kSmallWideRowTiles ? 2 : 1);
         const dim3 g((unsigned)((total + 16 * ns - 1) / (16 * ns)), (unsigned)((op.m + 16 * ms - 1) / (16 * ms)));
+        const bool pf = tu.small_pf;
         if (ns == 2)
-            e = ms == 1   ? launch_small<1, 2>(a, op.out_mode, g, ctx->stream, e0, e1)
-                : ms == 2 ? launch_small<2, 2>(a, op.out_mode, g, ctx->stream, e0, e1)
-                : ms == 3 ? launch_small<3, 2>(a, op.out_mode, g, ctx->stream, e0, e1)
-                          : launch_small<4, 2>(a, op.out_mode, g, ctx->stream, e0, e1);
+            e = ms == 1   ? launch_small<1, 2>(a, op.out_mode, pf, g, ctx->stream, e0, e1)
+                : ms == 2 ? launch_small<2, 2>(a, op.out_mode, pf, g, ctx->stream, e0, e1)
+                : ms == 3 ? launch_small<3, 2>(a, op.out_mode, pf, g, ctx->stream, e0, e1)
+                          : launch_small<4, 2>(a, op.out_mode, pf, g, ctx->stream, e0, e1);
         else
-            e = ms == 1   ? launch_small<1, 1>(a, op.out_mode, g, ctx->stream, e0, e1)
-                : ms == 2 ? launch_small<2, 1>(a, op.out_mode, g, ctx->stream, e0, e1)
-                : ms == 3 ? launch_small<3, 1>(a, op.out_mode, g, ctx->stream, e0, e1)
-                          : launch_small<4, 1>(a, op.out_mode, g, ctx->stream, e0, e1);
-    } else if (gmode == 1) {
-        e = big ? launch_tiles<4, 4>(a, op.out_mode, g128, ctx->stream, e0, e1)
-                : launch_tiles<2, 2>(a, op.out_mode, g64, ctx->stream, e0, e1);
-    } else if (gmode == 2 && a.kp % 256 == 0) {
-        e = launch_tiles2<2, 2, 2>(a, op.out_mode, g128, ctx->stream, e0, e1);
-    } else if (gmode == 3 && a.kp % 256 == 0) {
-        e = launch_tiles2<1, 1, 2>(a, op.out_mode, g64, ctx->stream, e0, e1);
+            e = ms == 1   ? launch_small<1, 1>(a, op.out_mode, pf, g, ctx->stream, e0, e1)
+                : ms == 2 ? launch_small<2, 1>(a, op.out_mode, pf, g, ctx->stream, e0, e1)
+                : ms == 3 ? launch_small<3, 1>(a, op.out_mode, pf, g, ctx->stream, e0, e1)
+                          : launch_small<4, 1>(a, op.out_mode, pf, g, ctx->stream, e0, e1);
     } else if (gmode == 4) {
         e = launch_tiles2<1, 1, 1>(a, op.out_mode, g64, ctx->stream, e0, e1);
     } else if (t128 >= 200 || gmode == 5) {
@@ -815,7 +696,7 @@ int launch_ternary_mfma(lbt_ctx* ctx, const TernaryOp& op_in) {
     } else {
         e = launch_tiles2<1, 1, 1>(a, op.out_mode, g64, ctx->stream, e0, e1);
     }
-    if (e != hipSuccess) return hip_err(ctx, e, "tgemm_kernel launch");
+    if (e != hipSuccess) return hip_err(ctx, e, "ternary GEMM launch");
     prof_commit(ctx, e0, e1, kProfGemm, 2.0 * op.m * (double)total * a.kp);
     return LBT_OK;
 }

@@ -29,3 +29,26 @@ def ctx():
 def announce(msg: str):
     """Names the case on stdout before a GPU step, so a fault is attributable."""
     print(f"[gpu-case] {msg}", flush=True)
+
+
+@pytest.fixture
+def ctx_with(monkeypatch):
+    """Factory of fresh HIP contexts created under LBT_* environment switches
+    (the library reads them once, when a context is created); each is closed
+    after the test, so everything made on it must be freed by then."""
+    made = []
+
+    def make(**env):
+        import lbt_hip
+
+        for k, v in env.items():
+            monkeypatch.setenv(k, v)
+        c = lbt_hip.Ctx(0)
+        for k in env:
+            monkeypatch.delenv(k)
+        made.append(c)
+        return c
+
+    yield make
+    for c in made:
+        c.close()

@@ -64,12 +64,12 @@ def test_batch_matches_single_sequence_oracle(ctx, shape, nseq):
 
 
 @pytest.mark.parametrize("wide", [False, True])
-def test_batch_long_context_matches_oracle(ctx, monkeypatch, wide):
+def test_batch_long_context_matches_oracle(ctx, ctx_with, wide):
     """Prompts of 1100+ tokens (65-key and longer splits: the four- and, with
     LBT_ATTN_WIDE, eight-pass K/V pipelines of the grouped attention); the
     batched step's logits bit-exact to single-sequence oracles."""
     if wide:
-        monkeypatch.setenv("LBT_ATTN_WIDE", "1")
+        ctx = ctx_with(LBT_ATTN_WIDE="1")
     hip_cfg, or_cfg = cfgs(max_pos=2048, layers=1)
     announce(f"batch long context wide={wide}")
     seed = 41

@@ -249,7 +249,7 @@ def test_full_2b_prompt64_decode_matches_oracle(ctx):
     m.free()
 
 
-def test_graph_decode_replays_match_eager_and_oracle(ctx, monkeypatch):
+def test_graph_decode_replays_match_eager_and_oracle(ctx, ctx_with):
     """Decode steps run as a replayed HIP graph; replays interleaved with eager
     forwards and a cache regrowth (re-capture) give the oracle's tokens, and
     the same tokens as the eager path (LBT_NO_GRAPH)."""
@@ -281,8 +281,10 @@ def test_graph_decode_replays_match_eager_and_oracle(ctx, monkeypatch):
     assert list(toks2) == oracle_run(nxt, 250)
     assert len(cache) == len(prompt) + 12 + 1 + 250
     cache.free()
+    m.free()
+    # the same model on a context without graphs (separate launches)
+    m = lbt_hip.Model.synthetic(ctx_with(LBT_NO_GRAPH="1"), hip_cfg, 12)
     c2 = m.new_cache()
-    monkeypatch.setenv("LBT_NO_GRAPH", "1")
     f2 = m.forward_argmax(prompt, c2)
     t_eager, _ = m.decode_greedy(c2, f2, 12)
     assert list(t_eager) == list(toks)

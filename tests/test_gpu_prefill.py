@@ -70,12 +70,10 @@ def test_few_token_gemm_bitexact(ctx, rows, cols, m):
 @pytest.mark.parametrize("rows,cols,m", [(23, 384, 17), (37, 2560, 33), (130, 300, 65), (5, 129, 16), (100, 1000, 200),
                                          (1, 256, 20), (257, 768, 130), (31, 8192, 64)])
 @pytest.mark.parametrize("ms,ns", [("1", "1"), ("2", "1"), ("3", "2"), ("4", "1"), ("1", "2"), ("4", "2")])
-def test_few_token_kernel_ragged(ctx, monkeypatch, rows, cols, m, ms, ns):
+def test_few_token_kernel_ragged(ctx_with, rows, cols, m, ms, ns):
     # LBT_GEMM_MODE=6 forces the few-token kernel at any token count;
     # LBT_GEMM_SMALL_MS / _NS its tile (16 * ms tokens x 16 * ns rows)
-    monkeypatch.setenv("LBT_GEMM_MODE", "6")
-    monkeypatch.setenv("LBT_GEMM_SMALL_MS", ms)
-    monkeypatch.setenv("LBT_GEMM_SMALL_NS", ns)
+    ctx = ctx_with(LBT_GEMM_MODE="6", LBT_GEMM_SMALL_MS=ms, LBT_GEMM_SMALL_NS=ns)
     announce(f"few-token ragged {rows}x{cols} m={m} ms={ms} ns={ns}")
     t, scale, x = golden_case(rows, cols, m, 7 * rows + cols + m)
     p = orc.pack(t)
@@ -117,7 +115,7 @@ def test_fused_multi_mfma_equals_separate(ctx, m):
 
 
 @pytest.mark.parametrize("n", [2, 5, 16, 40, 130])
-def test_model_prefill_mfma_matches_oracle_and_gemv(ctx, monkeypatch, n):
+def test_model_prefill_mfma_matches_oracle_and_gemv(ctx, ctx_with, n):
     cfg = dict(hidden=512, intermediate=1536, heads=4, kv_heads=1, layers=2, vocab=1000, max_pos=1024)
     hip_cfg = lbt_hip.make_config(**cfg)
     or_cfg = orc.config(**cfg)
@@ -129,7 +127,8 @@ def test_model_prefill_mfma_matches_oracle_and_gemv(ctx, monkeypatch, n):
     got = m.forward(toks, c, all_logits=True)
     assert np.array_equal(got, om.forward(toks, all_logits=True))
     c.free()
-    monkeypatch.setenv("LBT_NO_MFMA", "1")
+    m.free()
+    m = lbt_hip.Model.synthetic(ctx_with(LBT_NO_MFMA="1"), hip_cfg, 3)
     c = m.new_cache()
     assert np.array_equal(m.forward(toks, c, all_logits=True), got)
     c.free()
@@ -137,14 +136,14 @@ def test_model_prefill_mfma_matches_oracle_and_gemv(ctx, monkeypatch, n):
     om.free()
 
 
-@pytest.mark.parametrize("mode", ["1", "4", "5", "6"])
-def test_model_prefill_every_gemm_tiling_matches_oracle(ctx, monkeypatch, mode):
+@pytest.mark.parametrize("mode", ["4", "5", "6"])
+def test_model_prefill_every_gemm_tiling_matches_oracle(ctx_with, mode):
     # every epilogue (q/k/v + RoPE + KV append, residual add, relu^2*up) through
-    # each MFMA tiling: 16x16x64 kernel, 64x64 and 128x128 tiles of the 32x32x32 one,
-    # the few-token kernel
+    # each MFMA tiling: 64x64 and 128x128 tiles of the 32x32x32 GEMM, the
+    # few-token kernel
     cfg = dict(hidden=512, intermediate=1536, heads=4, kv_heads=1, layers=2, vocab=1000, max_pos=1024)
     n = 200
-    monkeypatch.setenv("LBT_GEMM_MODE", mode)
+    ctx = ctx_with(LBT_GEMM_MODE=mode)
     announce(f"model prefill gemm mode {mode} n={n}")
     m = lbt_hip.Model.synthetic(ctx, lbt_hip.make_config(**cfg), 5)
     om = orc.OracleModel(orc.config(**cfg), 5)
