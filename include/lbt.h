@@ -112,6 +112,18 @@ int lbt_ternary_linear(lbt_ctx* ctx, const lbt_weight* const* ws, size_t n, cons
                        size_t cols, float* const* outs);
 int lbt_ternary_linear_dev(lbt_ctx* ctx, const lbt_weight* const* ws, size_t n, const float* x,
                            size_t m, size_t cols, float* const* outs);
+/* lbt_ternary_linear_dev that allocates nothing.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, serving loops, harnesses that forbid hipMalloc).  The
+ * several-row paths keep their quantized activations in a static 4 MiB
+ * scratch per device instead of the context's grow-only buffer, so
+ * round256(m * padded(cols)) + 8 m must be <= 4 MiB (LBT_E_INVALID beyond,
+ * e.g. about 600 rows at cols = 6912); profiling must be off.  Results equal
+ * lbt_ternary_linear_dev's bit for bit.  Every call on a device shares that
+ * device's scratch: calls that overlap on one device (several contexts or
+ * host threads) race. */
+int lbt_ternary_linear_dev_noalloc(lbt_ctx* ctx, const lbt_weight* const* ws, size_t n, const float* x,
+                                   size_t m, size_t cols, float* const* outs);
 
 /* ---- bf16 linear (tied LM head) ---------------------------------------------
  * bf16_gemv (crates/lb-ternary/src/bf16.rs:14-25) / TernaryBackend::bf16_linear

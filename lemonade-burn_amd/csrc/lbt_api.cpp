@@ -154,6 +154,10 @@ int lbt_ctx_create(int device, lbt_ctx** out) {
     lbt_ctx* c = new lbt_ctx();
     c->device = device;
     c->tune = read_tuning();
+    if (noalloc_scratch_init(device, &c->noalloc, &c->noalloc_bytes) != LBT_OK) {
+        delete c;
+        return LBT_E_DEVICE;
+    }
     if (hipDeviceGetAttribute(&c->cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || c->cus <= 0)
         c->cus = 256;
     if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
@@ -390,6 +394,34 @@ int lbt_ternary_linear_dev(lbt_ctx* ctx, const lbt_weight* const* ws, size_t n, 
     op.in_mode = kInF32;
     op.out_mode = kOutF32;
     op.x = x;
+    for (size_t i = 0; i < n; i++) op.out[i] = outs[i];
+    return launch_ternary(ctx, op);
+}
+
+int lbt_ternary_linear_dev_noalloc(lbt_ctx* ctx, const lbt_weight* const* ws, size_t n, const float* x, size_t m,
+                                   size_t cols, float* const* outs) {
+    if (!ctx) return LBT_E_INVALID;
+    int rc = check_ws(ctx, ws, n, cols, true);
+    if (rc) return rc;
+    if (m == 0) return LBT_OK;
+    const size_t kp = ws[0]->kp;
+    const size_t need = ((m * kp + 255) & ~(size_t)255) + m * 8;
+    if (need > ctx->noalloc_bytes) {
+        const size_t max_m = (ctx->noalloc_bytes - 255) / (kp + 8);
+        return set_err(ctx, LBT_E_INVALID,
+                       "lbt_ternary_linear_dev_noalloc: " + std::to_string(m) + " rows of " + std::to_string(kp) +
+                           " packed columns need " + std::to_string(need) + " bytes of scratch, over the static " +
+                           std::to_string(ctx->noalloc_bytes) + " (about " + std::to_string(max_m) +
+                           " rows of this width fit)");
+    }
+    if (ctx->prof)
+        return set_err(ctx, LBT_E_INVALID, "lbt_ternary_linear_dev_noalloc: profiling is on (it creates events)");
+    TernaryOp op = make_op(ws, n, m);
+    op.in_mode = kInF32;
+    op.out_mode = kOutF32;
+    op.x = x;
+    op.scratch = ctx->noalloc;
+    op.scratch_bytes = ctx->noalloc_bytes;
     for (size_t i = 0; i < n; i++) op.out[i] = outs[i];
     return launch_ternary(ctx, op);
 }

@@ -49,6 +49,9 @@ struct lbt_ctx {
     // grow-only device scratch of the prefill GEMM (quantized activations)
     void* qws = nullptr;
     size_t qws_bytes = 0;
+    // this device's static scratch of the allocation-free entry point
+    void* noalloc = nullptr;
+    size_t noalloc_bytes = 0;
 };
 
 struct lbt_weight {
@@ -137,6 +140,10 @@ struct TernaryOp {
     const float* sin_t = nullptr;
     uint16_t* kc = nullptr;
     uint16_t* vc = nullptr;
+    // caller-provided device scratch for the quantized activations of the
+    // several-row paths (null: the context's grow-only buffer)
+    void* scratch = nullptr;
+    size_t scratch_bytes = 0;
 };
 // Dispatches the single-token decode GEMV (m = 1) or the int8-MFMA GEMMs
 // (m >= kMfmaMinTokens; the VALU few-token GEMV tgemv_kernel stays behind
@@ -220,6 +227,12 @@ int launch_attn_quantize(lbt_ctx* ctx, const float* o, const float* ml, int m, i
 lbt_ctx* model_ctx(const lbt_model* m);
 // Grow-only per-context device scratch for quantized activations.
 int qws_reserve(lbt_ctx* ctx, size_t bytes, void** out);
+// Scratch of `bytes` for op's quantized activations: op.scratch when set
+// (an error when it is smaller), else the context's buffer (qws_reserve).
+int act_scratch(lbt_ctx* ctx, const TernaryOp& op, size_t bytes, void** out);
+// Device address of this device's static no-alloc scratch (noalloc.hip),
+// looked up once per device; called by lbt_ctx_create with the device current.
+int noalloc_scratch_init(int device, void** out, size_t* bytes);
 int launch_fill_u64(lbt_ctx* ctx, unsigned long long* p, int n, unsigned long long v);
 // Streaming device copy (16-byte granules, byte tail).
 int launch_copy(lbt_ctx* ctx, void* dst, const void* src, size_t bytes);

@@ -478,7 +478,7 @@ int launch_ternary(lbt_ctx* ctx, const TernaryOp& op_in) {
         const size_t kp = padded_cols((size_t)op.cols);
         const size_t qb = ((size_t)op.m * kp + 255) & ~(size_t)255;
         void* q;
-        int rc = qws_reserve(ctx, qb + (size_t)op.m * 8, &q);
+        int rc = act_scratch(ctx, op, qb + (size_t)op.m * 8, &q);
         if (rc) return rc;
         float* sd = (float*)((char*)q + qb);
         int32_t* ud = (int32_t*)(sd + op.m);

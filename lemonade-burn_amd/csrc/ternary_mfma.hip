@@ -627,6 +627,13 @@ int qws_reserve(lbt_ctx* ctx, size_t bytes, void** out) {
     return LBT_OK;
 }
 
+int act_scratch(lbt_ctx* ctx, const TernaryOp& op, size_t bytes, void** out) {
+    if (!op.scratch) return qws_reserve(ctx, bytes, out);
+    if (bytes > op.scratch_bytes) return set_err(ctx, LBT_E_INVALID, "ternary: activations exceed the given scratch");
+    *out = op.scratch;
+    return LBT_OK;
+}
+
 int launch_ternary_mfma(lbt_ctx* ctx, const TernaryOp& op_in) {
     TernaryOp op = op_in;
     if (op.in_mode == kInF32) {
@@ -635,7 +642,7 @@ int launch_ternary_mfma(lbt_ctx* ctx, const TernaryOp& op_in) {
         const size_t kp = padded_cols((size_t)op.cols);
         void* q;
         const size_t qb = ((size_t)op.m * kp + 255) & ~(size_t)255;
-        int rc = qws_reserve(ctx, qb + (size_t)op.m * 8, &q);
+        int rc = act_scratch(ctx, op, qb + (size_t)op.m * 8, &q);
         if (rc) return rc;
         int8_t* qd = (int8_t*)q;
         float* sd = (float*)((char*)q + qb);

@@ -75,6 +75,7 @@ SIGNATURES = {
     "lbt_gemm_multi_dev": (i32, [vp, vp, sz, vp, vp, vp, sz, vp]),
     "lbt_ternary_linear": (i32, [vp, vp, sz, vp, sz, sz, vp]),
     "lbt_ternary_linear_dev": (i32, [vp, vp, sz, vp, sz, sz, vp]),
+    "lbt_ternary_linear_dev_noalloc": (i32, [vp, vp, sz, vp, sz, sz, vp]),
     "lbt_bf16_upload": (i32, [vp, vp, sz, sz, C.POINTER(vp)]),
     "lbt_bf16_free": (None, [vp]),
     "lbt_bf16_linear": (i32, [vp, vp, vp, sz, vp]),
