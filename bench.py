@@ -100,6 +100,30 @@ def int8_head_decode(model, ctx, prompt, steps: int = 128) -> dict:
             "head_GBs": round(h["bytes"] / (h["ms"] / 1e3) / 1e9, 1) if h["ms"] > 0 else 0.0}
 
 
+def sampled_decode(model, prompt, steps: int = 128) -> dict:
+    """The same decode loop with the device sampler (temperature 0.8, top-p
+    0.95; and top-k 40) instead of the argmax: the lb-server job loop with
+    its Sampler (main.rs:102-160, sample.rs:45-82), ids only over PCIe."""
+    import ctypes as C
+
+    import lbt_hip
+
+    out = {}
+    for name, p in (("t0.8_p0.95", (0.8, 0.95, 0)), ("t0.8_k40", (0.8, 1.0, 40))):
+        params = lbt_hip.LbtSampleParams(*p)
+        st = C.c_uint64(0x5EED)
+        cache = model.new_cache()
+        first = model.forward_sample(prompt, cache, params, st)
+        model.decode_sample(cache, first, 8, params, st)  # builds the step graph
+        cache.free()
+        cache = model.new_cache()
+        first = model.forward_sample(prompt, cache, params, st)
+        _, ms = model.decode_sample(cache, first, steps, params, st)
+        cache.free()
+        out[name] = {"tok_s": round(steps / (ms / 1e3), 2), "ms_per_step": round(ms / steps, 4)}
+    return out
+
+
 def sched_throughput(model, cfg, slots: int = 16, requests: int = 32, prompt_len: int = 64, new: int = 64) -> dict:
     """Continuous batching (lbt_sched_*): `requests` greedy requests of a
     `prompt_len`-token prompt and `new` tokens each through `slots` slots;
@@ -486,6 +510,7 @@ def main() -> int:
     }
     if not args.no_int8_head:
         line["int8_head_decode"] = int8_head_decode(model, ctx, prompt)
+    line["sampled_decode"] = sampled_decode(model, prompt)
     if not args.no_batched:
         line["batched_decode"] = [batched_decode(model, cfg, bsz) for bsz in (16, 64)]
         line["continuous_batching"] = sched_throughput(model, cfg)

@@ -151,6 +151,28 @@ int lbt_q8head_read(lbt_ctx* ctx, const lbt_q8head* h, int8_t* q, float* scale);
 int lbt_q8head_linear(lbt_ctx* ctx, const lbt_q8head* h, const float* x, size_t m, float* out);
 int lbt_q8head_linear_dev(lbt_ctx* ctx, const lbt_q8head* h, const float* x, size_t m, float* out);
 
+/* ---- sampling -------------------------------------------------------------------
+ * SamplingParams (crates/lb-model/src/sample.rs:3-15) without the seed: the
+ * xorshift64 state is the caller's (Sampler::new sets it to seed.max(1),
+ * sample.rs:33-35) and each sample at temperature > 0 advances it by one draw. */
+typedef struct lbt_sample_params {
+    float temperature; /* <= 0: argmax */
+    float top_p;       /* >= 1 (or NaN): no cut */
+    size_t top_k;      /* 0: no truncation */
+} lbt_sample_params;
+
+/* Sampler::sample (sample.rs:45-82) on the device for `rows` rows of logits
+ * [rows][vocab]; states[r] is row r's sampler state (updated), out[r] its id.
+ * The reference's steps in its order; the cumulative probabilities are exact
+ * integer sums of floor(p * 2^45) (the reference's sequential f32 sums pick
+ * the same id except where the draw lies within rounding of a boundary);
+ * equal logits are ordered by ascending index (the reference's unstable sort
+ * leaves it open). */
+int lbt_sample(lbt_ctx* ctx, const float* logits, size_t rows, size_t vocab, const lbt_sample_params* p,
+               uint64_t* states, uint32_t* out);
+int lbt_sample_dev(lbt_ctx* ctx, const float* logits, size_t rows, size_t vocab, const lbt_sample_params* p,
+                   uint64_t* states, uint32_t* out);
+
 /* ---- BitNet b1.58 model ------------------------------------------------------
  * Config (crates/lb-model/src/model.rs:22-42). */
 typedef struct lbt_config {
@@ -208,6 +230,15 @@ int lbt_model_generate_greedy(lbt_model* m, const uint32_t* prompt, size_t n, si
  * gets the `steps` argmax ids.  ms_decode (nullable) gets device-timed ms. */
 int lbt_model_decode_greedy(lbt_model* m, lbt_cache* c, uint32_t first, size_t steps, uint32_t* out_tokens,
                             float* ms_decode);
+/* The lb-server job loop with its Sampler (crates/lb-server/src/main.rs:102-160,
+ * sample.rs:45-82) on the device: forward_sample runs the prompt and samples
+ * the first token; decode_sample feeds `first` and samples `steps` tokens,
+ * each fed back on the device.  *state is the sampler state (seed.max(1) for
+ * a new job), updated.  Only token ids cross to the host. */
+int lbt_model_forward_sample(lbt_model* m, const uint32_t* tokens, size_t n, lbt_cache* c,
+                             const lbt_sample_params* p, uint64_t* state, uint32_t* next);
+int lbt_model_decode_sample(lbt_model* m, lbt_cache* c, uint32_t first, size_t steps, const lbt_sample_params* p,
+                            uint64_t* state, uint32_t* out_tokens, float* ms_decode);
 /* LM head of the model's forwards: 0 = the exact tied bf16 head (default),
  * 1 = the opt-in int8 head (q8head.rs), quantized on the device from the
  * tied embedding when first selected.  A cached decode-step graph is rebuilt. */

@@ -179,6 +179,7 @@ void lbt_ctx_destroy(lbt_ctx* ctx) {
     for (auto e : ctx->free_events) hipEventDestroy(e);
     if (ctx->ws) hipFree(ctx->ws);
     if (ctx->qws) hipFree(ctx->qws);
+    if (ctx->sws) hipFree(ctx->sws);
     hipStreamDestroy(ctx->stream);
     delete ctx;
 }
@@ -396,6 +397,49 @@ int lbt_ternary_linear_dev(lbt_ctx* ctx, const lbt_weight* const* ws, size_t n, 
     op.x = x;
     for (size_t i = 0; i < n; i++) op.out[i] = outs[i];
     return launch_ternary(ctx, op);
+}
+
+int lbt_sample_dev(lbt_ctx* ctx, const float* logits, size_t rows, size_t vocab, const lbt_sample_params* p,
+                   uint64_t* states, uint32_t* out) {
+    if (!ctx) return LBT_E_INVALID;
+    if (!p || !logits || !states || !out || vocab == 0 || vocab > 0x7fffffff || rows > 0x7fffffff)
+        return set_err(ctx, LBT_E_INVALID, "lbt_sample: bad arguments");
+    if (rows == 0) return LBT_OK;
+    size_t need;
+    sample_scratch_bytes((int)rows, (int)vocab, &need);
+    if (need > ctx->sws_bytes) {
+        if (ctx->sws) {
+            hipStreamSynchronize(ctx->stream);
+            hipFree(ctx->sws);
+            ctx->sws = nullptr;
+            ctx->sws_bytes = 0;
+        }
+        LBT_HIP(ctx, hipMalloc(&ctx->sws, need));
+        ctx->sws_bytes = need;
+    }
+    return launch_sample(ctx, logits, (long)vocab, (int)rows, (int)vocab, *p, (unsigned long long*)states, out,
+                         nullptr, ctx->sws);
+}
+
+int lbt_sample(lbt_ctx* ctx, const float* logits, size_t rows, size_t vocab, const lbt_sample_params* p,
+               uint64_t* states, uint32_t* out) {
+    if (!ctx) return LBT_E_INVALID;
+    if (!p || !logits || !states || !out || vocab == 0) return set_err(ctx, LBT_E_INVALID, "lbt_sample: bad arguments");
+    if (rows == 0) return LBT_OK;
+    Carve cv;
+    const size_t ol = cv.add(rows * vocab * 4), os = cv.add(rows * 8), oo = cv.add(rows * 4);
+    void* wsp;
+    int rc = ws_reserve(ctx, cv.total(), &wsp);
+    if (rc) return rc;
+    char* b = (char*)wsp;
+    LBT_HIP(ctx, hipMemcpyAsync(b + ol, logits, rows * vocab * 4, hipMemcpyHostToDevice, ctx->stream));
+    LBT_HIP(ctx, hipMemcpyAsync(b + os, states, rows * 8, hipMemcpyHostToDevice, ctx->stream));
+    rc = lbt_sample_dev(ctx, (const float*)(b + ol), rows, vocab, p, (uint64_t*)(b + os), (uint32_t*)(b + oo));
+    if (rc) return rc;
+    LBT_HIP(ctx, hipMemcpyAsync(states, b + os, rows * 8, hipMemcpyDeviceToHost, ctx->stream));
+    LBT_HIP(ctx, hipMemcpyAsync(out, b + oo, rows * 4, hipMemcpyDeviceToHost, ctx->stream));
+    LBT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return LBT_OK;
 }
 
 int lbt_ternary_linear_dev_noalloc(lbt_ctx* ctx, const lbt_weight* const* ws, size_t n, const float* x, size_t m,

@@ -49,6 +49,9 @@ struct lbt_ctx {
     // grow-only device scratch of the prefill GEMM (quantized activations)
     void* qws = nullptr;
     size_t qws_bytes = 0;
+    // grow-only scratch of lbt_sample_dev
+    void* sws = nullptr;
+    size_t sws_bytes = 0;
     // this device's static scratch of the allocation-free entry point
     void* noalloc = nullptr;
     size_t noalloc_bytes = 0;
@@ -178,6 +181,12 @@ int launch_q8_quantize(lbt_ctx* ctx, const uint16_t* w, int rows, int cols, int8
 // ---- model pieces --------------------------------------------------------
 // state (nullable, device): {position, output slot}; when set, the kernel
 // advances the position by one and writes the token to tok_out[slot++].
+// Sampler::sample on `rows` rows of logits (sample.hip); the token of row r
+// goes to out_tok[r] and/or, as an argmax-key word the next embedding reads,
+// to out_key[r]; scratch: sample_scratch_bytes.
+int launch_sample(lbt_ctx* ctx, const float* logits, long ld, int rows, int vocab, const lbt_sample_params& p,
+                  unsigned long long* states, uint32_t* out_tok, unsigned long long* out_key, void* scratch);
+int sample_scratch_bytes(int rows, int vocab, size_t* bytes);
 int launch_embed(lbt_ctx* ctx, const uint16_t* embed, int hidden, int vocab, const uint32_t* tokens,
                  const unsigned long long* key, uint32_t* tok_out, int m, float* x, int* state = nullptr);
 // Split-key attention (attn_common.h): keys per split for vis visible keys,

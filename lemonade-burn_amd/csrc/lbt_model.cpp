@@ -246,7 +246,12 @@ struct lbt_model {
     // for the cache buffers and workspace it was captured with
     int* state = nullptr;  // device {position - 1, output slot, barrier epoch, spare}
     hipGraphExec_t step_exec = nullptr;
-    const void* step_key[7] = {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
+    static constexpr int kStepKey = 11;
+    const void* step_key[kStepKey] = {};
+    // device sampler (sample.hip) of the sampling decode loop: the sampler
+    // state and the candidate scratch of one row
+    unsigned long long* sstate = nullptr;
+    void* sscratch = nullptr;
     // one-dispatch decode step (decode_step.hip): device tables of the layers,
     // the epoch-tagged activation words, the error word, the plan
     int decode_kind = 1;   // 0: one-dispatch step, 1: multi-kernel graph step
@@ -786,12 +791,32 @@ int step_check(lbt_model* m) {
     return LBT_OK;
 }
 
+int ensure_sampler(lbt_model* m) {
+    if (m->sstate) return LBT_OK;
+    lbt_ctx* ctx = m->ctx;
+    size_t bytes;
+    sample_scratch_bytes(1, m->cfg.vocab_size, &bytes);
+    LBT_HIP(ctx, hipMalloc(&m->sscratch, bytes));
+    LBT_HIP(ctx, hipMalloc(&m->sstate, 8));
+    return LBT_OK;
+}
+
+// The token after the last LM head: the sampler's pick written as the
+// argmax-key word the next embedding reads (sp null: the head's argmax stays).
+int sample_key(lbt_model* m, const lbt_sample_params* sp) {
+    if (!sp) return LBT_OK;
+    return launch_sample(m->ctx, m->logits, m->cfg.vocab_size, 1, m->cfg.vocab_size, *sp, m->sstate, nullptr, m->key,
+                         m->sscratch);
+}
+
 // Runs n decode steps, each fed with the previous step's argmax (the key);
 // the token consumed by step s goes to m->tok_out[slot0 + s].  Outside
 // profiling one captured step is replayed as a HIP graph (positions and
 // output slots advance on the device); the graph is re-captured when the
 // cache or workspace buffers change.
-int decode_steps(lbt_model* m, lbt_cache* c, int n, int slot0) {
+// With `sp`, each step's LM head also writes its logits and the sampler
+// (state m->sstate) replaces the argmax in the key.
+int decode_steps(lbt_model* m, lbt_cache* c, int n, int slot0, const lbt_sample_params* sp = nullptr) {
     lbt_ctx* ctx = m->ctx;
     if (n <= 0) return LBT_OK;
     int rc;
@@ -803,26 +828,46 @@ int decode_steps(lbt_model* m, lbt_cache* c, int n, int slot0) {
         for (int s = 0; s < n; s++) {
             if ((rc = launch_decode_step(ctx, m->plan, m->dargs, ctx->stream))) return rc;
             m->epochs += 5.0 * cf.num_hidden_layers;
-            if ((rc = model_head(m, m->x, 1, (float)cf.rms_norm_eps, nullptr, m->key, nullptr))) return rc;
+            if ((rc = model_head(m, m->x, 1, (float)cf.rms_norm_eps, sp ? m->logits : nullptr, m->key, nullptr)))
+                return rc;
+            if ((rc = sample_key(m, sp))) return rc;
         }
         c->len += n;
         m->last_n = 1;
         return LBT_OK;
     }
     if (ctx->prof || ctx->tune.no_graph) {
-        for (int s = 0; s < n; s++)
-            if ((rc = forward_dev(m, c, nullptr, 1, false, false, m->tok_out + slot0 + s))) return rc;
+        for (int s = 0; s < n; s++) {
+            if ((rc = forward_dev(m, c, nullptr, 1, false, sp != nullptr, m->tok_out + slot0 + s))) return rc;
+            if ((rc = sample_key(m, sp))) return rc;
+        }
         return LBT_OK;
     }
     if ((rc = ensure_state(m))) return rc;
-    const void* key[7] = {c->k, c->v, (const void*)(intptr_t)c->cap, m->tok_out, m->x, m->key,
-                          (const void*)(intptr_t)m->head_kind};
+    // what the captured step depends on: buffers, head, sampler and its parameters
+    uint32_t tb = 0, pb = 0;
+    if (sp) {
+        memcpy(&tb, &sp->temperature, 4);
+        memcpy(&pb, &sp->top_p, 4);
+    }
+    const void* key[lbt_model::kStepKey] = {c->k,
+                                            c->v,
+                                            (const void*)(intptr_t)c->cap,
+                                            m->tok_out,
+                                            m->x,
+                                            m->key,
+                                            (const void*)(intptr_t)m->head_kind,
+                                            (const void*)(intptr_t)(sp ? 1 : 0),
+                                            (const void*)(uintptr_t)tb,
+                                            (const void*)(uintptr_t)pb,
+                                            (const void*)(uintptr_t)(sp ? sp->top_k : 0)};
     if (!m->step_exec || memcmp(key, m->step_key, sizeof(key)) != 0) {
         drop_step_graph(m);
         hipGraph_t g = nullptr;
         LBT_HIP(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
         const int len = c->len;
-        rc = forward_dev(m, c, nullptr, 1, false, false, m->tok_out, m->state);
+        rc = forward_dev(m, c, nullptr, 1, false, sp != nullptr, m->tok_out, m->state);
+        if (!rc) rc = sample_key(m, sp);
         c->len = len;
         hipError_t e = hipStreamEndCapture(ctx->stream, &g);
         if (rc) {
@@ -1045,6 +1090,8 @@ void lbt_model_free(lbt_model* m) {
     if (m->ll) hipFree(m->ll);
     if (m->trace) hipFree(m->trace);
     if (m->dargs) hipFree(m->dargs);
+    if (m->sstate) hipFree(m->sstate);
+    if (m->sscratch) hipFree(m->sscratch);
     void* bufs[] = {m->wbuf, m->fbuf, m->embed, m->cos_t, m->sin_t, m->x,   m->q,       m->k,
                     m->v,    m->att,  m->h,     m->logits, m->toks, m->key, m->tok_out, m->state,
                     m->ao,   m->aml,  m->q8,    m->q8s};
@@ -1202,6 +1249,65 @@ int lbt_model_decode_greedy(lbt_model* m, lbt_cache* c, uint32_t first, size_t s
         hipEventElapsedTime(&a, e0, e1);
         if (ms_decode) *ms_decode = a;
         e = hipMemcpy(out_tokens, m->tok_out, steps * 4, hipMemcpyDeviceToHost);
+        if (e != hipSuccess) rc = hip_err(ctx, e, "read tokens");
+    }
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    return rc;
+}
+
+int lbt_model_forward_sample(lbt_model* m, const uint32_t* tokens, size_t n, lbt_cache* c,
+                             const lbt_sample_params* p, uint64_t* state, uint32_t* next) {
+    if (!m || !c || !tokens || n == 0 || !next || !p || !state)
+        return set_err(m ? m->ctx : nullptr, LBT_E_INVALID, "bad arguments");
+    lbt_ctx* ctx = m->ctx;
+    int rc;
+    if ((rc = ensure_cap(c, c->len + (int)n))) return rc;
+    if ((rc = ensure_ws(m, (int)n))) return rc;
+    if ((rc = ensure_sampler(m))) return rc;
+    if ((rc = upload_tokens(m, tokens, n))) return rc;
+    LBT_HIP(ctx, hipMemcpyAsync(m->sstate, state, 8, hipMemcpyHostToDevice, ctx->stream));
+    if ((rc = forward_dev(m, c, m->toks, (int)n, false, true, nullptr))) return rc;
+    if ((rc = sample_key(m, p))) return rc;
+    unsigned long long key = 0;
+    LBT_HIP(ctx, hipMemcpyAsync(&key, m->key, 8, hipMemcpyDeviceToHost, ctx->stream));
+    LBT_HIP(ctx, hipMemcpyAsync(state, m->sstate, 8, hipMemcpyDeviceToHost, ctx->stream));
+    LBT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    *next = 0xffffffffu - (uint32_t)(key & 0xffffffffull);
+    return LBT_OK;
+}
+
+int lbt_model_decode_sample(lbt_model* m, lbt_cache* c, uint32_t first, size_t steps, const lbt_sample_params* p,
+                            uint64_t* state, uint32_t* out_tokens, float* ms_decode) {
+    if (!m || !c || !out_tokens || steps == 0 || !p || !state)
+        return set_err(m ? m->ctx : nullptr, LBT_E_INVALID, "bad arguments");
+    lbt_ctx* ctx = m->ctx;
+    if (first >= (uint32_t)m->cfg.vocab_size) return set_err(ctx, LBT_E_INVALID, "token id out of range");
+    int rc;
+    if ((rc = ensure_cap(c, c->len + (int)steps))) return rc;
+    if ((rc = ensure_ws(m, 1))) return rc;
+    if ((rc = grow_tok_out(m, (int)steps + 1))) return rc;
+    if ((rc = ensure_sampler(m))) return rc;
+    LBT_HIP(ctx, hipMemcpyAsync(m->toks, &first, 4, hipMemcpyHostToDevice, ctx->stream));
+    LBT_HIP(ctx, hipMemcpyAsync(m->sstate, state, 8, hipMemcpyHostToDevice, ctx->stream));
+    hipEvent_t e0, e1;
+    LBT_HIP(ctx, hipEventCreate(&e0));
+    LBT_HIP(ctx, hipEventCreate(&e1));
+    hipEventRecord(e0, ctx->stream);
+    rc = forward_dev(m, c, m->toks, 1, false, true, nullptr);
+    if (!rc) rc = sample_key(m, p);
+    if (!rc) rc = decode_steps(m, c, (int)steps - 1, 0, p);
+    if (!rc) rc = launch_embed(ctx, m->embed, 0, m->cfg.vocab_size, nullptr, m->key, m->tok_out + steps - 1, 1, m->x);
+    hipEventRecord(e1, ctx->stream);
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (!rc && e != hipSuccess) rc = hip_err(ctx, e, "decode");
+    if (!rc) rc = step_check(m);
+    if (!rc) {
+        float a = 0;
+        hipEventElapsedTime(&a, e0, e1);
+        if (ms_decode) *ms_decode = a;
+        e = hipMemcpy(out_tokens, m->tok_out, steps * 4, hipMemcpyDeviceToHost);
+        if (e == hipSuccess) e = hipMemcpy(state, m->sstate, 8, hipMemcpyDeviceToHost);
         if (e != hipSuccess) rc = hip_err(ctx, e, "read tokens");
     }
     hipEventDestroy(e0);

@@ -1,0 +1,392 @@
+// sample.hip -- token sampling on the device: Sampler::sample
+// (crates/lb-model/src/sample.rs:45-82) for rows of logits, so that only
+// token ids leave the GPU (the reference ships every 128256-float logit row
+// to the host and sorts it there, lb-server/src/main.rs:141-160).
+//
+// One workgroup of 1024 threads per row.  The reference's steps, in its
+// order: temperature <= 0 is the argmax (sample.rs:17-25); otherwise the
+// logits are ordered by descending total_cmp (ties: ascending index -- the
+// reference's unstable sort leaves their order open), truncated to top_k,
+// p = exp((l - max) / t), cut to the shortest prefix whose cumulative
+// probability reaches top_p, and one xorshift64 draw r = (state >> 40) / 2^24
+// (sample.rs:36-43) picks the first element whose cumulative probability
+// exceeds r.  The probabilities are summed as exact integers,
+// w = floor(p * 2^45) (p <= 1, so 2^17 of them stay below 2^62):
+//   c >= top_p  <=>  sum(w) >= ceil(top_p * W),
+//   r < c       <=>  sum(w) >= floor(draw * W_keep / 2^24) + 1,
+// so no float sum depends on an order and no sort is needed: each "first
+// element in sorted order whose prefix reaches T" is a radix select over the
+// keys (~total order << index bits | index) with weight histograms, 9 bits a
+// round.  Elements with w = 0 can never be chosen, so only elements with
+// w > 0 (a prefix of the sorted order) are kept as candidates -- in LDS when
+// they fit, else in a global scratch of 16 bytes per logit.  A NaN among the
+// top-k p (a NaN logit in the set, max = +inf, all -inf, a NaN temperature)
+// makes every comparison of the reference false: it returns the last element
+// of the set, and so does this kernel.
+#include "lbt_device.h"
+#include "lbt_internal.h"
+
+namespace lbt {
+
+namespace {
+
+constexpr int kST = 1024;  // threads
+constexpr int kDigit = 9, kBins = 1 << kDigit;
+constexpr int kLdsCand = 4096;  // candidates kept in LDS
+constexpr unsigned long long kNone = ~0ull;
+
+struct Cand {
+    unsigned long long s, w;
+};
+
+struct SampleShared {
+    Cand cand[kLdsCand];
+    unsigned long long hist[kBins];
+    unsigned long long red[kST / 64];
+    unsigned long long red2[kST / 64];
+    unsigned long long sel_below, sel_through;
+    unsigned sel_bin;
+    unsigned cnt;
+    float fred[kST / 64];
+    unsigned ired[kST / 64];
+};
+
+// Ascending key of the IEEE total order (total_cmp) of x's bits.
+__device__ __forceinline__ unsigned total_asc(float x) {
+    const unsigned b = __float_as_uint(x);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+// Sorted-order key of element i: ascending keys = descending logits, then
+// ascending index (ib index bits, so keys stay below 2^(32 + ib)).
+__device__ __forceinline__ unsigned long long sample_key(float x, unsigned i, int ib) {
+    return ((unsigned long long)(~total_asc(x)) << ib) | i;
+}
+
+__device__ __forceinline__ unsigned long long wave_sum(unsigned long long v) {
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
+    return v;
+}
+__device__ __forceinline__ unsigned long long wave_min(unsigned long long v) {
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) {
+        const unsigned long long o = __shfl_xor(v, d, 64);
+        v = o < v ? o : v;
+    }
+    return v;
+}
+__device__ __forceinline__ unsigned long long wave_max(unsigned long long v) {
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) {
+        const unsigned long long o = __shfl_xor(v, d, 64);
+        v = o > v ? o : v;
+    }
+    return v;
+}
+
+// Block reductions (every thread gets the result); kind 0 sum, 1 min, 2 max.
+template <int KIND>
+__device__ unsigned long long block_red(unsigned long long v, unsigned long long* buf) {
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    v = KIND == 0 ? wave_sum(v) : KIND == 1 ? wave_min(v) : wave_max(v);
+    __syncthreads();
+    if (lane == 0) buf[w] = v;
+    __syncthreads();
+    unsigned long long r = buf[0];
+    for (int i = 1; i < kST / 64; i++) {
+        const unsigned long long o = buf[i];
+        r = KIND == 0 ? r + o : KIND == 1 ? (o < r ? o : r) : (o > r ? o : r);
+    }
+    return r;
+}
+
+// ceil(top_p * W) for top_p < 1 (0 for top_p <= 0), exactly: top_p = M 2^-sh
+// with M < 2^24, M * W < 2^86 held as two 64-bit words.
+__device__ unsigned long long top_p_target(float top_p, unsigned long long W) {
+    if (!(top_p > 0.0f)) return 0;
+    const unsigned b = __float_as_uint(top_p);
+    const int be = (int)((b >> 23) & 0xff);
+    const unsigned long long M = be ? ((b & 0x7fffffu) | 0x800000u) : (b & 0x7fffffu);
+    const int sh = be ? 150 - be : 149;  // top_p = M 2^-sh
+    if (sh >= 128) return 1;
+    const unsigned long long lo = M * W, hi = __umul64hi(M, W);
+    unsigned long long q, rem;
+    if (sh >= 64) {
+        q = sh == 64 ? hi : hi >> (sh - 64);
+        rem = lo | (sh == 64 ? 0ull : (hi & ((1ull << (sh - 64)) - 1)));
+    } else {
+        q = (lo >> sh) | (hi << (64 - sh));
+        rem = lo & ((1ull << sh) - 1);
+    }
+    return q + (rem ? 1 : 0);
+}
+
+// The smallest key s* among candidates with s <= lim whose cumulative weight
+// (w with MASS, else 1 each) through s* reaches `target` (which must not
+// exceed their total); `through` = that cumulative weight.  All threads call.
+// Source of (key, weight) pairs: the candidate list, or every logit of the
+// row with weight 1.
+struct CandSrc {
+    const Cand* c;
+    __device__ unsigned long long key(unsigned i) const { return c[i].s; }
+    __device__ unsigned long long w(unsigned i) const { return c[i].w; }
+};
+struct LogitSrc {
+    const float* lg;
+    int ib;
+    __device__ unsigned long long key(unsigned i) const { return sample_key(lg[i], i, ib); }
+    __device__ unsigned long long w(unsigned) const { return 1ull; }
+};
+
+template <bool MASS, class Src>
+__device__ unsigned long long radix_select(const Src& c, unsigned n, unsigned long long lim,
+                                           unsigned long long target, int rounds, SampleShared& sh,
+                                           unsigned long long& through) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    unsigned long long prefix = 0, below = 0;
+    for (int r = rounds - 1; r >= 0; r--) {
+        const int shift = r * kDigit;
+        for (int b = tid; b < kBins; b += kST) sh.hist[b] = 0;
+        __syncthreads();
+        for (unsigned i = tid; i < n; i += kST) {
+            const unsigned long long s = c.key(i);
+            if (s <= lim && (s >> (shift + kDigit)) == prefix)
+                atomicAdd(&sh.hist[(s >> shift) & (kBins - 1)], MASS ? c.w(i) : 1ull);
+        }
+        __syncthreads();
+        if (tid < 64) {
+            constexpr int PL = kBins / 64;
+            unsigned long long h[PL], sum = 0;
+#pragma unroll
+            for (int j = 0; j < PL; j++) {
+                h[j] = sh.hist[PL * lane + j];
+                sum += h[j];
+            }
+            unsigned long long inc = sum;
+#pragma unroll
+            for (int d = 1; d < 64; d <<= 1) {
+                const unsigned long long v = __shfl_up(inc, d, 64);
+                if (lane >= d) inc += v;
+            }
+            unsigned long long run = below + inc - sum, bel = 0, thr = 0;
+            unsigned found = kBins;
+#pragma unroll
+            for (int j = 0; j < PL; j++) {
+                if (h[j] && found == kBins && run + h[j] >= target) {
+                    found = PL * lane + j;
+                    bel = run;
+                    thr = run + h[j];
+                }
+                run += h[j];
+            }
+            const unsigned long long fmin = wave_min(found);
+            if (found == fmin && found < kBins) {
+                sh.sel_bin = found;
+                sh.sel_below = bel;
+                sh.sel_through = thr;
+            }
+        }
+        __syncthreads();
+        prefix = (prefix << kDigit) | sh.sel_bin;
+        below = sh.sel_below;
+        through = sh.sel_through;
+    }
+    return prefix;
+}
+
+struct SampleArgs {
+    const float* logits;
+    long ld;  // floats between rows
+    int V;
+    float temperature, top_p;
+    unsigned long long top_k;  // 0: no truncation
+    unsigned long long* states;  // [rows] xorshift states, advanced by one draw when temperature > 0
+    uint32_t* out_tok;            // [rows] (nullable)
+    unsigned long long* out_key;  // [rows] argmax-key words the next embedding reads (nullable)
+    Cand* scratch;                // [rows][V]
+};
+
+__global__ __launch_bounds__(kST) void sample_kernel(SampleArgs a) {
+    __shared__ SampleShared sh;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int row = blockIdx.x, V = a.V;
+    const float* lg = a.logits + (size_t)row * a.ld;
+    const float t = a.temperature;
+    unsigned out = 0;
+    if (t <= 0.0f) {
+        // argmax (sample.rs:17-25): the first index of the largest value under
+        // float comparison; a NaN never wins, and a NaN at index 0 stays
+        float bv = 0.0f;
+        int bi = V;
+        for (int i = tid; i < V; i += kST) {
+            const float v = lg[i];
+            if (v == v && (bi == V || v > bv)) {
+                bv = v;
+                bi = i;
+            }
+        }
+        for (int d = 32; d >= 1; d >>= 1) {
+            const float ov = __shfl_xor(bv, d, 64);
+            const int oi = __shfl_xor(bi, d, 64);
+            if (oi != V && (bi == V || ov > bv || (ov == bv && oi < bi))) {
+                bv = ov;
+                bi = oi;
+            }
+        }
+        if (lane == 0) {
+            sh.fred[wv] = bv;
+            sh.ired[wv] = (unsigned)bi;
+        }
+        __syncthreads();
+        if (tid == 0) {
+            for (int w = 0; w < kST / 64; w++) {
+                const float ov = sh.fred[w];
+                const int oi = (int)sh.ired[w];
+                if (oi != V && (bi == V || ov > bv || (ov == bv && oi < bi))) {
+                    bv = ov;
+                    bi = oi;
+                }
+            }
+            const float l0 = lg[0];
+            out = (l0 != l0 || bi == V) ? 0u : (unsigned)bi;
+            if (a.out_tok) a.out_tok[row] = out;
+            if (a.out_key) a.out_key[row] = 0xffffffffull - out;
+        }
+        return;
+    }
+
+    // max under the total order (sorted element 0)
+    unsigned mk = 0;
+    for (int i = tid; i < V; i += kST) {
+        const unsigned k = total_asc(lg[i]);
+        mk = k > mk ? k : mk;
+    }
+    mk = (unsigned)block_red<2>(mk, sh.red);
+    const float mx = __uint_as_float((mk & 0x80000000u) ? (mk & 0x7fffffffu) : ~mk);
+
+    int ib = 1;
+    while (ib < 32 && (1u << ib) < (unsigned)V) ib++;
+    const int rounds = (32 + ib + kDigit - 1) / kDigit;
+    const unsigned long long imask = (1ull << ib) - 1;
+
+    // candidates (w > 0) with their keys; NaN p: the smallest such key
+    if (tid == 0) sh.cnt = 0;
+    __syncthreads();
+    Cand* gc = a.scratch + (size_t)row * V;
+    unsigned long long wsum = 0, nan_s = kNone, smax = 0;
+    for (int i0 = 0; i0 < V; i0 += kST) {
+        const int i = i0 + tid;
+        bool keep = false;
+        unsigned long long s = 0, w = 0;
+        if (i < V) {
+            const float l = lg[i];
+            s = sample_key(l, (unsigned)i, ib);
+            smax = s > smax ? s : smax;
+            const float p = lbt_expf((l - mx) / t);
+            if (p != p) {
+                nan_s = s < nan_s ? s : nan_s;
+            } else {
+                w = (unsigned long long)(p * 0x1p45f);
+                keep = w != 0;
+                wsum += w;
+            }
+        }
+        const unsigned long long m = __ballot(keep);
+        if (m) {
+            unsigned base = 0;
+            if (lane == 0) base = atomicAdd(&sh.cnt, (unsigned)__popcll(m));
+            base = __shfl(base, 0, 64);
+            if (keep) {
+                const unsigned slot = base + (unsigned)__popcll(m & ((1ull << lane) - 1));
+                const Cand e{s, w};
+                if (slot < (unsigned)kLdsCand) sh.cand[slot] = e;
+                else gc[slot] = e;
+            }
+        }
+    }
+    const unsigned long long Wall = block_red<0>(wsum, sh.red);
+    nan_s = block_red<1>(nan_s, sh.red2);
+    smax = block_red<2>(smax, sh.red);
+    const unsigned n = sh.cnt;
+    CandSrc c{sh.cand};
+    if (n > (unsigned)kLdsCand) {
+        for (int i = tid; i < kLdsCand; i += kST) gc[i] = sh.cand[i];
+        __syncthreads();
+        c.c = gc;
+    }
+    // one draw per call (sample.rs:36-43, 71)
+    unsigned long long st = a.states[row];
+    st ^= st << 13;
+    st ^= st >> 7;
+    st ^= st << 17;
+    const unsigned long long u = st >> 40;
+    __syncthreads();
+    if (tid == 0) a.states[row] = st;
+
+    const unsigned long long kk = (a.top_k > 0 && a.top_k < (unsigned long long)V) ? a.top_k : (unsigned long long)V;
+    unsigned long long lim = kNone, W = Wall, thr;
+    if (kk < n) {
+        lim = radix_select<false>(c, n, kNone, kk, rounds, sh, thr);
+        unsigned long long part = 0;
+        for (unsigned i = tid; i < n; i += kST)
+            if (c.key(i) <= lim) part += c.w(i);
+        W = block_red<0>(part, sh.red);
+    }
+    bool bad = false;
+    unsigned long long last = smax;  // last element of the top-k set
+    if (nan_s != kNone) {
+        if (kk < (unsigned long long)V) {
+            if (kk < n) {
+                last = lim;
+            } else {
+                // the k-th element lies beyond the candidates: select over all logits
+                last = radix_select<false>(LogitSrc{lg, ib}, (unsigned)V, kNone, kk, rounds, sh, thr);
+            }
+        }
+        bad = nan_s <= last;
+    }
+    if (bad) {
+        out = (unsigned)(last & imask);
+    } else {
+        unsigned long long keep_lim = lim, WK = W;
+        if (a.top_p < 1.0f) keep_lim = radix_select<true>(c, n, lim, top_p_target(a.top_p, W), rounds, sh, WK);
+        const unsigned long long Td = ((u * (WK & 0xffffffull)) >> 24) + u * (WK >> 24) + 1;
+        const unsigned long long sd = radix_select<true>(c, n, keep_lim, Td, rounds, sh, thr);
+        out = (unsigned)(sd & imask);
+    }
+    if (tid == 0) {
+        if (a.out_tok) a.out_tok[row] = out;
+        if (a.out_key) a.out_key[row] = 0xffffffffull - out;
+    }
+}
+
+}  // namespace
+
+int sample_scratch_bytes(int rows, int vocab, size_t* bytes) {
+    *bytes = (size_t)rows * (size_t)vocab * sizeof(Cand);
+    return LBT_OK;
+}
+
+int launch_sample(lbt_ctx* ctx, const float* logits, long ld, int rows, int vocab, const lbt_sample_params& p,
+                  unsigned long long* states, uint32_t* out_tok, unsigned long long* out_key, void* scratch) {
+    if (rows <= 0) return LBT_OK;
+    if (vocab <= 0 || ld < vocab || !logits || !states || !scratch)
+        return set_err(ctx, LBT_E_INVALID, "sample: bad arguments");
+    SampleArgs a;
+    a.logits = logits;
+    a.ld = ld;
+    a.V = vocab;
+    a.temperature = p.temperature;
+    a.top_p = p.top_p;
+    a.top_k = (unsigned long long)p.top_k;
+    a.states = states;
+    a.out_tok = out_tok;
+    a.out_key = out_key;
+    a.scratch = (Cand*)scratch;
+    hipLaunchKernelGGL(sample_kernel, dim3(rows), dim3(kST), 0, ctx->stream, a);
+    LBT_HIP(ctx, hipGetLastError());
+    return LBT_OK;
+}
+
+}  // namespace lbt

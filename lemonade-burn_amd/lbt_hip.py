@@ -29,6 +29,10 @@ f32 = C.c_float
 u64 = C.c_uint64
 
 
+class LbtSampleParams(C.Structure):
+    _fields_ = [("temperature", C.c_float), ("top_p", C.c_float), ("top_k", C.c_size_t)]
+
+
 class LbtConfig(C.Structure):
     _fields_ = [
         ("hidden_size", C.c_int32),
@@ -98,6 +102,10 @@ SIGNATURES = {
     "lbt_model_forward_argmax": (i32, [vp, vp, sz, vp, vp]),
     "lbt_model_generate_greedy": (i32, [vp, vp, sz, sz, vp, vp, vp, vp]),
     "lbt_model_decode_greedy": (i32, [vp, vp, C.c_uint32, sz, vp, vp]),
+    "lbt_model_forward_sample": (i32, [vp, vp, sz, vp, vp, vp, vp]),
+    "lbt_model_decode_sample": (i32, [vp, vp, C.c_uint32, sz, vp, vp, vp, vp]),
+    "lbt_sample": (i32, [vp, vp, sz, sz, vp, vp, vp]),
+    "lbt_sample_dev": (i32, [vp, vp, sz, sz, vp, vp, vp]),
     "lbt_model_read_hidden": (i32, [vp, vp, sz]),
     "lbt_model_set_head": (i32, [vp, i32]),
     "lbt_model_set_decode": (i32, [vp, i32]),
@@ -220,6 +228,18 @@ class Ctx:
         oa = (C.c_void_p * len(ws))(*[o.ctypes.data for o in outs])
         self.check(self.lib.lbt_gemm_multi(self.h, wa, len(ws), _ptr(q), _ptr(scale), _ptr(qsum), m, oa))
         return outs
+
+    def sample(self, logits: np.ndarray, temperature: float, top_p: float, top_k: int, states: np.ndarray) -> np.ndarray:
+        """Sampler::sample on the device for each row of `logits`; `states`
+        (uint64 per row) is updated in place."""
+        lg = np.ascontiguousarray(logits, dtype=np.float32)
+        if lg.ndim == 1:
+            lg = lg[None]
+        assert states.dtype == np.uint64 and states.flags.c_contiguous and states.size == lg.shape[0]
+        out = np.zeros(lg.shape[0], np.uint32)
+        p = LbtSampleParams(temperature, top_p, top_k)
+        self.check(self.lib.lbt_sample(self.h, _ptr(lg), lg.shape[0], lg.shape[1], C.byref(p), _ptr(states), _ptr(out)))
+        return out
 
     def ternary_linear(self, ws: list["Weight"], x: np.ndarray) -> list[np.ndarray]:
         x = np.ascontiguousarray(x, dtype=np.float32)
@@ -377,6 +397,21 @@ class Model:
         self.ctx.check(self.ctx.lib.lbt_model_forward(self.h, _ptr(t), len(t), cache.h, 1 if all_logits else 0,
                                                       _ptr(out)))
         return out
+
+    def forward_sample(self, tokens, cache: "Cache", params: "LbtSampleParams", state: C.c_uint64) -> int:
+        """Prompt forward, then one device sample (state updated in place)."""
+        t = np.ascontiguousarray(tokens, dtype=np.uint32)
+        nxt = C.c_uint32()
+        self.ctx.check(self.ctx.lib.lbt_model_forward_sample(self.h, _ptr(t), len(t), cache.h, C.byref(params),
+                                                             C.byref(state), C.byref(nxt)))
+        return int(nxt.value)
+
+    def decode_sample(self, cache: "Cache", first: int, steps: int, params: "LbtSampleParams", state: C.c_uint64):
+        out = np.zeros(steps, np.uint32)
+        md = C.c_float()
+        self.ctx.check(self.ctx.lib.lbt_model_decode_sample(self.h, cache.h, C.c_uint32(first), steps, C.byref(params),
+                                                            C.byref(state), _ptr(out), C.byref(md)))
+        return out, md.value
 
     def forward_argmax(self, tokens, cache: "Cache") -> int:
         t = np.ascontiguousarray(tokens, dtype=np.uint32)

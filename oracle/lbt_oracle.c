@@ -404,6 +404,107 @@ uint32_t or_argmax(const float* v, size_t n) {
 }
 
 /* ------------------------------------------------------------------------ */
+/* Sampler::sample (sample.rs:45-82) as the device sampler computes it        */
+/* ------------------------------------------------------------------------ */
+/* Order of sort_unstable_by(total_cmp, descending) made total: larger logit
+ * first (IEEE total order, so -0.0 after +0.0 and NaNs by sign), equal logits
+ * by ascending index.  Ascending keys give that order. */
+uint64_t or_sample_key(float x, uint32_t i) {
+    uint32_t b;
+    memcpy(&b, &x, 4);
+    uint32_t asc = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return ((uint64_t)(~asc) << 32) | i;
+}
+
+static int cmp_u64(const void* a, const void* b) {
+    uint64_t x = *(const uint64_t*)a, y = *(const uint64_t*)b;
+    return x < y ? -1 : x > y;
+}
+
+/* ceil(top_p * W) for 0 < top_p < 1, exactly (top_p = M 2^-sh, M < 2^24). */
+uint64_t or_top_p_target(float top_p, uint64_t W) {
+    if (!(top_p > 0.0f)) return 0;
+    int e;
+    float m = frexpf(top_p, &e);
+    uint64_t M = (uint64_t)ldexpf(m, 24);
+    int sh = 24 - e;
+    if (sh >= 128) return 1;
+    unsigned __int128 x = (unsigned __int128)M * W;
+    uint64_t q = (uint64_t)(x >> sh);
+    return q + (((x & ((((unsigned __int128)1) << sh) - 1)) != 0) ? 1 : 0);
+}
+
+/* The step of sample.rs:36-43 (xorshift64, seed.max(1) initially); returns
+ * the 24-bit draw, r = draw / 2^24. */
+uint32_t or_sample_uniform(uint64_t* state) {
+    uint64_t s = *state;
+    s ^= s << 13;
+    s ^= s >> 7;
+    s ^= s << 17;
+    *state = s;
+    return (uint32_t)(s >> 40);
+}
+
+/* temperature <= 0: argmax (state untouched).  Otherwise the reference's
+ * steps in its order -- sort, top-k truncation, p = exp((l - max) / t), top-p
+ * cut, one uniform draw, first cumulative mass above the draw -- with the
+ * masses in exact integers: w = floor(p 2^45) (p <= 1, so any 2^17 of them
+ * sum below 2^62), c >= top_p as sum(w) >= ceil(top_p W), r < c as
+ * sum(w) > draw W_keep / 2^24.  The reference sums f32 in sorted order; the
+ * two agree except where the draw lies within rounding of a boundary.  A NaN
+ * among the top-k p (a NaN logit in the set, max = +inf, all -inf, a NaN
+ * temperature) makes every reference comparison false: the last element of
+ * the set is returned, as there. */
+uint32_t or_sample(const float* logits, size_t V, float temperature, float top_p, size_t top_k, uint64_t* state) {
+    if (temperature <= 0.0f) return or_argmax(logits, V);
+    uint64_t* s = (uint64_t*)malloc(V * sizeof(uint64_t));
+    for (size_t i = 0; i < V; i++) s[i] = or_sample_key(logits[i], (uint32_t)i);
+    qsort(s, V, sizeof(uint64_t), cmp_u64);
+    const size_t k = (top_k > 0 && top_k < V) ? top_k : V;
+    const float mx = logits[(uint32_t)s[0]];
+    uint64_t* w = (uint64_t*)malloc(k * sizeof(uint64_t));
+    int bad = 0;
+    for (size_t j = 0; j < k; j++) {
+        float p = or_expf((logits[(uint32_t)s[j]] - mx) / temperature);
+        if (p != p) bad = 1;
+        w[j] = p != p ? 0 : (uint64_t)(p * 0x1p45f);
+    }
+    const uint64_t u = or_sample_uniform(state);
+    uint32_t out = (uint32_t)s[k - 1];
+    if (!bad) {
+        uint64_t W = 0;
+        for (size_t j = 0; j < k; j++) W += w[j];
+        size_t keep = k;
+        if (top_p < 1.0f) {
+            const uint64_t T = or_top_p_target(top_p, W);
+            uint64_t c = 0;
+            for (size_t j = 0; j < k; j++) {
+                c += w[j];
+                if (c >= T) {
+                    keep = j + 1;
+                    break;
+                }
+            }
+        }
+        uint64_t WK = 0;
+        for (size_t j = 0; j < keep; j++) WK += w[j];
+        const uint64_t Td = (uint64_t)(((unsigned __int128)u * WK) >> 24) + 1;
+        uint64_t c = 0;
+        out = (uint32_t)s[keep - 1];
+        for (size_t j = 0; j < keep; j++) {
+            c += w[j];
+            if (c >= Td) {
+                out = (uint32_t)s[j];
+                break;
+            }
+        }
+    }
+    free(w);
+    free(s);
+    return out;
+}
+
+/* ------------------------------------------------------------------------ */
 /* RoPE tables (model.rs:213-230)                                            */
 /* ------------------------------------------------------------------------ */
 void or_rope_tables(size_t hd, size_t max_pos, double theta, float* cos_t, float* sin_t) {

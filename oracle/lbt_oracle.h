@@ -74,6 +74,12 @@ float or_sumsq(const float* x, size_t n);                     /* canonical order
 void or_rmsnorm(const float* x, const float* w, size_t n, float eps, float* out);
 float or_expf(float x);                                       /* Cody-Waite + Taylor(7) */
 uint32_t or_argmax(const float* v, size_t n);                 /* sample.rs:17-25 */
+/* Sampler::sample (sample.rs:45-82) with exact integer masses; the helpers
+ * are exported for the tests. */
+uint32_t or_sample(const float* logits, size_t V, float temperature, float top_p, size_t top_k, uint64_t* state);
+uint64_t or_sample_key(float x, uint32_t i);
+uint64_t or_top_p_target(float top_p, uint64_t W);
+uint32_t or_sample_uniform(uint64_t* state);
 
 /* ---- RoPE tables (crates/lb-model/src/model.rs:213-230) ---------------- */
 /* cos/sin are [max_pos, hd/2]: entry i serves dims i and i + hd/2. */

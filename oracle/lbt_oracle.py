@@ -54,6 +54,10 @@ _SIGS = {
     "or_rmsnorm": (None, [vp, vp, sz, f32, vp]),
     "or_expf": (f32, [f32]),
     "or_argmax": (C.c_uint32, [vp, sz]),
+    "or_sample": (C.c_uint32, [vp, sz, f32, f32, sz, vp]),
+    "or_sample_key": (C.c_uint64, [f32, C.c_uint32]),
+    "or_top_p_target": (C.c_uint64, [f32, C.c_uint64]),
+    "or_sample_uniform": (C.c_uint32, [vp]),
     "or_rope_tables": (None, [sz, sz, C.c_double, vp, vp]),
     "or_synth_hash": (u64, [u64, u64, u64]),
     "or_synth_ternary": (C.c_int8, [u64, u64, u64]),
@@ -407,3 +411,16 @@ def set_threads(n: int) -> int:
     """Threads of the oracle's parallel loops and the port's kernels (0 = all);
     returns the previous setting."""
     return lib().or_set_threads(n)
+
+
+class Sampler:
+    """Sampler (sample.rs:28-82) in the device sampler's arithmetic:
+    state = seed.max(1), one draw per sample at temperature > 0."""
+
+    def __init__(self, temperature: float, top_p: float = 1.0, top_k: int = 0, seed: int = 0x5EED):
+        self.t, self.top_p, self.top_k = float(temperature), float(top_p), int(top_k)
+        self.state = C.c_uint64(max(int(seed), 1))
+
+    def sample(self, logits: np.ndarray) -> int:
+        lg = np.ascontiguousarray(logits, np.float32)
+        return int(lib().or_sample(_p(lg), lg.size, self.t, self.top_p, self.top_k, C.byref(self.state)))
