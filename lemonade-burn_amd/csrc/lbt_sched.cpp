@@ -90,11 +90,16 @@ int lbt_sched_step(lbt_sched* s, int* pending) {
     for (int k = 0; k < s->slots && !s->queue.empty(); k++) {
         if (s->slot_req[k] >= 0) continue;
         const uint64_t id = s->queue.front();
-        s->queue.pop_front();
         lbt_sched::Req& r = s->reqs[id];
+        // the request leaves the queue only once its slot holds it: a failed
+        // reset or prefill leaves it first in line for the next step
         if ((rc = lbt_batch_reset(s->b, k))) return rc;
         uint32_t first = 0;
-        if ((rc = lbt_batch_prefill(s->b, k, r.prompt.data(), r.prompt.size(), &first))) return rc;
+        if ((rc = lbt_batch_prefill(s->b, k, r.prompt.data(), r.prompt.size(), &first))) {
+            lbt_batch_reset(s->b, k);
+            return rc;
+        }
+        s->queue.pop_front();
         r.out.push_back(first);
         if (finished(r)) {
             r.done = true;
