@@ -402,6 +402,9 @@ def main() -> int:
     ap.add_argument("--no-batched", action="store_true", help="skip the batched-decode (config 5) figures")
     ap.add_argument("--no-int8-head", action="store_true", help="skip the opt-in int8 LM head figure")
     ap.add_argument("--no-shapes", action="store_true", help="skip the config-1/2 per-shape GEMV figures")
+    ap.add_argument("--no-sampled", action="store_true", help="skip the device-sampling decode figure")
+    ap.add_argument("--shapes-only", action="store_true",
+                    help="only the config-1/2 per-shape GEMV figures (the workload profiled for them)")
     ap.add_argument("--int8-head-only", action="store_true",
                     help="only the opt-in int8 LM head decode figure (the workload profiled for its kernel)")
     ap.add_argument("--prefill-only", action="store_true",
@@ -413,6 +416,11 @@ def main() -> int:
         import lbt_hip
 
         print(json.dumps({"prefill_gemm": prefill_gemm(lbt_hip.Ctx(0))}), flush=True)
+        return 0
+    if args.shapes_only:
+        import lbt_hip
+
+        print(json.dumps({"gemv_shapes": gemv_shapes(lbt_hip.Ctx(0))}), flush=True)
         return 0
     if args.int8_head_only:
         import lbt_hip
@@ -510,7 +518,8 @@ def main() -> int:
     }
     if not args.no_int8_head:
         line["int8_head_decode"] = int8_head_decode(model, ctx, prompt)
-    line["sampled_decode"] = sampled_decode(model, prompt)
+    if not args.no_sampled:
+        line["sampled_decode"] = sampled_decode(model, prompt)
     if not args.no_batched:
         line["batched_decode"] = [batched_decode(model, cfg, bsz) for bsz in (16, 64)]
         line["continuous_batching"] = sched_throughput(model, cfg)
