@@ -23,6 +23,7 @@
 #include <stdlib.h>
 
 #include <type_traits>
+#include <utility>
 
 #include "ternary_common.h"
 
@@ -207,7 +208,13 @@ __device__ __forceinline__ void mfma_epilogue(const GemvArgs& a, AccT (&acc)[MS]
                     } else {
                         const float inv = sw[s] == sw[0] ? inv0 : 1.0f / (sa[ms][r] * sw[s]);
                         const float y = (float)d * inv;
-                        gstore((float*)base[s] + o, OUT == kOutF32Add ? old[mi][s][r] + y : y);
+                        const float v = OUT == kOutF32Add ? old[mi][s][r] + y : y;
+                        // the prefill GEMM's output streams past L2 (nontemporal):
+                        // measured 2-10% faster on the config-3 shapes
+                        if constexpr (TM == 32)
+                            __builtin_nontemporal_store(v, (LBT_GLOBAL float*)((float*)base[s] + o));
+                        else
+                            gstore((float*)base[s] + o, v);
                     }
                 }
             }
@@ -362,12 +369,12 @@ __global__ __launch_bounds__(kThreads) void tgemm_small_kernel(GemvArgs a) {
 // covers KB 128-k blocks (8 KB MFMAs per tile).
 //
 // Activations go HBM -> LDS with global_load_lds_dwordx4 (no registers) into
-// a ring of 4 stages of one step's slice each, 4 slices ahead; the MFMA A
+// a ring of ST stages of one step's slice each, ST slices ahead; the MFMA A
 // operands of slice p+1 are read from LDS while the MFMAs of slice p run.
-// Packed weights go to registers 4 steps ahead and are unpacked per MFMA.
-// One barrier per step.  With KB = 1 and MS = NS = 2 the ring is 64 KB, so
-// two workgroups share a CU and one's prologue and epilogue overlap the
-// other's MFMAs.
+// Packed weights go to registers ST steps ahead and are unpacked per MFMA.
+// One barrier per step.  With KB = 1, MS = NS = 2 and three stages the ring
+// is 48 KB, so two workgroups (register-bound) share a CU and one's prologue
+// and epilogue overlap the other's MFMAs.
 //
 // LDS slice layout: token T of the tile owns RB = 128 KB bytes; its 16-byte
 // chunk c sits at T*RB + ((c ^ swz(T)) * 16), swz(T) = T & 15 for 256-byte
@@ -382,15 +389,29 @@ __global__ __launch_bounds__(kThreads) void tgemm_small_kernel(GemvArgs a) {
 // step, shifted right by 2 (kc & 3).
 typedef __attribute__((address_space(3))) void lds_void_t;
 
-constexpr int kG2Stages = 4;
+// LDS ring stages of tgemm2_kernel (slices in flight ahead of the MFMAs):
+// 3 measured 1-3% faster than 4 at M = 2048 (one stage less of LDS per
+// workgroup) and as fast below; 2 is slower at M = 512.
+constexpr int kG2Stages = 3;
+
+// f(integral_constant<I>) for I = 0, 1, ... while it returns true.
+template <int... I, class F>
+__device__ __forceinline__ void seq_while(std::integer_sequence<int, I...>, F&& f) {
+    (f(std::integral_constant<int, I>{}) && ...);
+}
 
 template <int KB>
 __device__ __forceinline__ int g2_swz(int T) {
     return KB == 2 ? (T & 15) : ((T >> 1) & 7);
 }
 
-template <int OUT, int MS, int NS, int KB>
-__global__ __launch_bounds__(kThreads) void tgemm2_kernel(GemvArgs a) {
+template <int OUT, int MS, int NS, int KB, int ST = kG2Stages>
+// Two wavefronts per SIMD: without the bound the compiler moved the
+// accumulators to AGPRs beyond 256 registers (one wavefront per SIMD, 20%
+// slower); three per SIMD needs a single-buffered A operand (164 VGPRs),
+// measured no faster.
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void tgemm2_kernel(GemvArgs a) {
     constexpr int TM = 32, BM = 2 * TM * MS, BN = 2 * TM * NS;
     constexpr int RB = 128 * KB;                 // LDS bytes per token per stage
     constexpr int KC = 4 * KB;                   // 32-k chunks per step
@@ -398,7 +419,7 @@ __global__ __launch_bounds__(kThreads) void tgemm2_kernel(GemvArgs a) {
     constexpr int NA = kSlice / 16 / kThreads;   // A chunks per lane per step
     constexpr int NB = NS * KB;                  // weight uint4 loads per lane per step
     constexpr int TPB = 1024 / RB;               // tokens per 1 KB DMA block
-    extern __shared__ __align__(16) int8_t As[];  // [kG2Stages][kSlice]
+    extern __shared__ __align__(16) int8_t As[];  // [ST][kSlice]
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const int wm = w & 1, wn = w >> 1;
     const int l32 = lane & 31, g = lane >> 5;
@@ -442,7 +463,7 @@ __global__ __launch_bounds__(kThreads) void tgemm2_kernel(GemvArgs a) {
     // loop-carried loads falls back to waiting for everything); the step's
     // explicit s_waitcnt covers them, and pin() after it keeps every use of
     // the registers below the wait.
-    u32x4 bw[kG2Stages][NB];  // [slot][s * KB + 128-k block]
+    u32x4 bw[ST][NB];  // [slot][s * KB + 128-k block]
     auto b_issue = [&](int p, u32x4 (&dst)[NB]) {
 #pragma unroll
         for (int s = 0; s < NS; s++)
@@ -490,34 +511,36 @@ __global__ __launch_bounds__(kThreads) void tgemm2_kernel(GemvArgs a) {
     // operands of step 0.
     const int plast = nsteps - 1;
 #pragma unroll
-    for (int p = 0; p < kG2Stages; p++) {
+    for (int p = 0; p < ST; p++) {
         const int pi = p < plast ? p : plast;
         a_issue(pi, p);
         b_issue(pi, bw[p]);
     }
     MTR(1)
-    wait_vm(std::integral_constant<int, NB + 3 * (NA + NB)>{});
+    wait_vm(std::integral_constant<int, NB + (ST - 1) * (NA + NB)>{});
     __builtin_amdgcn_s_barrier();
     MTR(2)
     a_read(0, aop[0]);
 
-    // Step p (ring slot p % 4 and operand buffer p % 2 as constants: no
+    // Step p (ring slot p % ST and operand buffer p % 2 as constants: no
     // register rotation, which would wait for every load in flight):
     //   wait for slice p+1 (own chunks) and weights p, barrier (all chunks of
     //   slice p+1; every wave has read slice p into registers);
-    //   slice p+4 -> stage p % 4; LDS reads of slice p+1 into the other
-    //   operand buffer while the MFMAs of step p run; weights p+4 into the
-    //   registers of weights p once they are unpacked.
-    auto step = [&](int p, auto slot_c) {
+    //   slice p+ST -> stage p % ST; LDS reads of slice p+1 into the other
+    //   operand buffer while the MFMAs of step p run; weights p+ST into the
+    //   registers of weights p once they are unpacked.  Loads are issued in
+    //   the order A_0 B_0 A_1 B_1 ..., so "slice p+1 and weights p done"
+    //   leaves B_{p+1} and the ST-2 later pairs in flight.
+    auto step = [&](int p, auto slot_c, auto cur_c) {
         constexpr int slot = decltype(slot_c)::value;
-        constexpr int cur = slot & 1;
-        wait_vm(std::integral_constant<int, NB + 2 * (NA + NB)>{});
+        constexpr int cur = decltype(cur_c)::value;
+        wait_vm(std::integral_constant<int, NB + (ST - 2) * (NA + NB)>{});
 #pragma unroll
         for (int i = 0; i < NB; i++) pin(bw[slot][i]);
         __builtin_amdgcn_s_barrier();
-        const int pn = p + kG2Stages < plast ? p + kG2Stages : plast;
+        const int pn = p + ST < plast ? p + ST : plast;
         a_issue(pn, slot);
-        a_read((slot + 1) % kG2Stages, aop[cur ^ 1]);
+        a_read((slot + 1) % ST, aop[cur ^ 1]);
 #pragma unroll
         for (int kc = 0; kc < KC; kc++) {
             const int sh = 2 * (kc & 3), b = kc >> 2;
@@ -536,19 +559,23 @@ __global__ __launch_bounds__(kThreads) void tgemm2_kernel(GemvArgs a) {
         }
         b_issue(pn, bw[slot]);
     };
-    for (int p = 0; p < nsteps; p += kG2Stages) {
-        step(p, std::integral_constant<int, 0>{});
-        if (p + 1 < nsteps) step(p + 1, std::integral_constant<int, 1>{});
-        if (p + 2 < nsteps) step(p + 2, std::integral_constant<int, 2>{});
-        if (p + 3 < nsteps) step(p + 3, std::integral_constant<int, 3>{});
-    }
+    // unrolled over a multiple of both the ring (slot) and the operand
+    // double buffer (cur), so both are constants in every step
+    constexpr int U = ST % 2 == 0 ? ST : 2 * ST;
+    for (int p = 0; p < nsteps; p += U)
+        seq_while(std::make_integer_sequence<int, U>{}, [&](auto ic) {
+            constexpr int i = decltype(ic)::value;
+            if (p + i >= nsteps) return false;
+            step(p + i, std::integral_constant<int, i % ST>{}, std::integral_constant<int, i & 1>{});
+            return true;
+        });
     // No load in flight past this point.  The weight registers of the last
     // steps are never read, so each is used here, after the wait: until then
     // the compiler cannot give a register to anything else while a load
     // untracked by it is still to write it.
     __builtin_amdgcn_s_waitcnt(0);
 #pragma unroll
-    for (int k = 0; k < kG2Stages; k++)
+    for (int k = 0; k < ST; k++)
 #pragma unroll
         for (int i = 0; i < NB; i++) asm volatile("" ::"v"(bw[k][i]));
     MTR(3)
@@ -562,25 +589,25 @@ __global__ __launch_bounds__(kThreads) void tgemm2_kernel(GemvArgs a) {
 
 namespace {
 
-template <int MS, int NS, int KB>
+template <int MS, int NS, int KB, int ST = kG2Stages>
 hipError_t launch_tiles2(const GemvArgs& a, int out_mode, dim3 grid, hipStream_t s, hipEvent_t e0, hipEvent_t e1) {
-    constexpr size_t lds = (size_t)kG2Stages * (64 * MS) * (128 * KB);
+    constexpr size_t lds = (size_t)ST * (64 * MS) * (128 * KB);
     static bool attr = false;
     if (!attr) {
-        const void* fns[] = {(const void*)tgemm2_kernel<kOutI32, MS, NS, KB>, (const void*)tgemm2_kernel<kOutF32, MS, NS, KB>,
-                             (const void*)tgemm2_kernel<kOutF32Add, MS, NS, KB>,
-                             (const void*)tgemm2_kernel<kOutRelu2, MS, NS, KB>,
-                             (const void*)tgemm2_kernel<kOutQKV, MS, NS, KB>};
+        const void* fns[] = {(const void*)tgemm2_kernel<kOutI32, MS, NS, KB, ST>, (const void*)tgemm2_kernel<kOutF32, MS, NS, KB, ST>,
+                             (const void*)tgemm2_kernel<kOutF32Add, MS, NS, KB, ST>,
+                             (const void*)tgemm2_kernel<kOutRelu2, MS, NS, KB, ST>,
+                             (const void*)tgemm2_kernel<kOutQKV, MS, NS, KB, ST>};
         for (const void* f : fns) (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         (void)hipGetLastError();
         attr = true;
     }
     switch (out_mode) {
-        case kOutI32: hipExtLaunchKernelGGL((tgemm2_kernel<kOutI32, MS, NS, KB>), grid, dim3(kThreads), lds, s, e0, e1, 0, a); break;
-        case kOutF32: hipExtLaunchKernelGGL((tgemm2_kernel<kOutF32, MS, NS, KB>), grid, dim3(kThreads), lds, s, e0, e1, 0, a); break;
-        case kOutF32Add: hipExtLaunchKernelGGL((tgemm2_kernel<kOutF32Add, MS, NS, KB>), grid, dim3(kThreads), lds, s, e0, e1, 0, a); break;
-        case kOutRelu2: hipExtLaunchKernelGGL((tgemm2_kernel<kOutRelu2, MS, NS, KB>), grid, dim3(kThreads), lds, s, e0, e1, 0, a); break;
-        default: hipExtLaunchKernelGGL((tgemm2_kernel<kOutQKV, MS, NS, KB>), grid, dim3(kThreads), lds, s, e0, e1, 0, a); break;
+        case kOutI32: hipExtLaunchKernelGGL((tgemm2_kernel<kOutI32, MS, NS, KB, ST>), grid, dim3(kThreads), lds, s, e0, e1, 0, a); break;
+        case kOutF32: hipExtLaunchKernelGGL((tgemm2_kernel<kOutF32, MS, NS, KB, ST>), grid, dim3(kThreads), lds, s, e0, e1, 0, a); break;
+        case kOutF32Add: hipExtLaunchKernelGGL((tgemm2_kernel<kOutF32Add, MS, NS, KB, ST>), grid, dim3(kThreads), lds, s, e0, e1, 0, a); break;
+        case kOutRelu2: hipExtLaunchKernelGGL((tgemm2_kernel<kOutRelu2, MS, NS, KB, ST>), grid, dim3(kThreads), lds, s, e0, e1, 0, a); break;
+        default: hipExtLaunchKernelGGL((tgemm2_kernel<kOutQKV, MS, NS, KB, ST>), grid, dim3(kThreads), lds, s, e0, e1, 0, a); break;
     }
     return hipGetLastError();
 }
@@ -696,9 +723,7 @@ int launch_ternary_mfma(lbt_ctx* ctx, const TernaryOp& op_in) {
                 : ms == 2 ? launch_small<2, 1>(a, op.out_mode, pf, g, ctx->stream, e0, e1)
                 : ms == 3 ? launch_small<3, 1>(a, op.out_mode, pf, g, ctx->stream, e0, e1)
                           : launch_small<4, 1>(a, op.out_mode, pf, g, ctx->stream, e0, e1);
-    } else if (gmode == 4) {
-        e = launch_tiles2<1, 1, 1>(a, op.out_mode, g64, ctx->stream, e0, e1);
-    } else if (t128 >= 200 || gmode == 5) {
+    } else if (gmode != 4 && (t128 >= 200 || gmode == 5)) {
         e = launch_tiles2<2, 2, 1>(a, op.out_mode, g128, ctx->stream, e0, e1);
     } else {
         e = launch_tiles2<1, 1, 1>(a, op.out_mode, g64, ctx->stream, e0, e1);
