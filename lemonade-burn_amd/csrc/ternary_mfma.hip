@@ -221,6 +221,94 @@ __device__ __forceinline__ void mfma_epilogue(const GemvArgs& a, AccT (&acc)[MS]
     }
 }
 
+// The same values for a wavefront block whose rows all lie in one matrix
+// and whose tokens are all below M (every full tile of an unpaired output):
+// no per-store bounds branch, one division per token (the per-row-block
+// scale is the block's one matrix scale), 32-bit offsets from the matrix's
+// base (the compiler then uses scalar-base stores), the residual's old
+// values loaded half a tile ahead of its stores.  Instruction count, not
+// memory, bounds the epilogue of a 128 x 128 tile (2088 instructions per
+// wavefront in the general form).
+// Per-token values of a wavefront block's 32 MS tokens: lane j holds token
+// tok0 + j's sum(q) and 1/(s_a*s_w) of matrix mt (one load pair and one
+// division per lane, instead of one per lane and D-tile element); the
+// epilogue fetches them across lanes.  Loaded ahead of the main loop
+// (divide = false), divided once the first slices' loads are out.
+struct Epi32Tok {
+    int qs;
+    float inv;
+};
+
+template <int OUT, int MS>
+__device__ __forceinline__ void epi32_pre(const GemvArgs& a, int tok0, float swm, Epi32Tok& t, bool divide) {
+    static_assert(MS <= 2, "one token per lane");
+    const int lane = (int)threadIdx.x & 63;
+    const int tok = tok0 + (lane < 32 * MS ? lane : 0);
+    if (!divide) {
+        t.qs = gload(a.qsum + tok);
+        t.inv = a.qscale ? gload(a.qscale + tok) : 1.0f;  // s_a until divided
+    } else {
+        t.inv = OUT == kOutI32 ? 0.0f : 1.0f / (t.inv * swm);
+    }
+}
+
+template <int OUT, int MS, int NS>
+__device__ __forceinline__ void epi32_full(const GemvArgs& a, v16i (&acc)[MS][NS], int tok0, int mt_v, int ro0_v,
+                                           const Epi32Tok& t) {
+    using L = DLayout<32>;
+    constexpr int R = L::R;
+    const int lane = (int)threadIdx.x & 63, lr = L::row(lane);
+    // wavefront-uniform: scalar registers, scalar selects
+    const int mt = __builtin_amdgcn_readfirstlane(mt_v), ro0 = __builtin_amdgcn_readfirstlane(ro0_v);
+    const int ld = mt == 0 ? a.rows[0] : (mt == 1 ? a.rows[1] : a.rows[2]);
+    const float swm = mt == 0 ? a.sw[0] : (mt == 1 ? a.sw[1] : a.sw[2]);
+    void* const outv = mt == 0 ? a.out[0] : (mt == 1 ? a.out[1] : a.out[2]);
+    // stores through a buffer resource: the matrix base in scalar registers,
+    // a 32-bit byte offset per lane (the caller checks M * ld < 2^30)
+    const __amdgpu_buffer_rsrc_t ob = buf_rsrc(outv, 0xffffffffu);
+    (void)swm;
+    int qs[MS][R];
+    float inv[MS][R];
+#pragma unroll
+    for (int ms = 0; ms < MS; ms++)
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const int src = ms * 32 + L::tok(lane, r);
+            qs[ms][r] = __shfl(t.qs, src, 64);
+            inv[ms][r] = __shfl(t.inv, src, 64);
+        }
+#pragma unroll
+    for (int ms = 0; ms < MS; ms++) {
+        float old[NS][R];
+        if (OUT == kOutF32Add) {
+#pragma unroll
+            for (int s = 0; s < NS; s++)
+#pragma unroll
+                for (int r = 0; r < R; r++) {
+                    const int tok = tok0 + ms * 32 + L::tok(lane, r);
+                    const uint32_t off = (uint32_t)(tok * ld + ro0 + s * 32 + lr) * 4u;
+                    old[s][r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ob, off, 0, 0));
+                }
+        }
+#pragma unroll
+        for (int s = 0; s < NS; s++)
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const int tok = tok0 + ms * 32 + L::tok(lane, r);
+                const uint32_t off = (uint32_t)(tok * ld + ro0 + s * 32 + lr) * 4u;
+                const int d = acc[ms][s][r] - qs[ms][r];
+                if (OUT == kOutI32) {
+                    __builtin_amdgcn_raw_buffer_store_b32((uint32_t)d, ob, off, 0, 0);
+                } else {
+                    const float y = (float)d * inv[ms][r];
+                    const float v = OUT == kOutF32Add ? old[s][r] + y : y;
+                    // nontemporal: the output streams past L2
+                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), ob, off, 0, 2);
+                }
+            }
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Few-token GEMM (batched decode and short prefills, 2..32 tokens, and up to
 // 64 for the shapes with few 64 x 64 tiles): the
@@ -453,6 +541,23 @@ void tgemm2_kernel(GemvArgs a) {
     const int kp = a.kp, M = a.m;
     const int nsteps = kp / RB;
     MTR(0)
+    // a full wavefront block of one matrix takes the lean epilogue; its
+    // per-token values are loaded now and divided once the loads of the
+    // first slices are out (they arrive during the main loop's prologue)
+    const int tok0 = m0 + wm * (BM / 2), row0 = n0 + wn * (BN / 2);
+    bool fast = false;
+    int mt0 = 0, ro0 = 0;
+    float swm = 1.0f;
+    Epi32Tok et{0, 1.0f};
+    if constexpr (OUT == kOutF32 || OUT == kOutF32Add || OUT == kOutI32) {
+        int mt1, ro1;
+        resolve_row<OUT>(a, row0, mt0, ro0);
+        resolve_row<OUT>(a, row0 + NS * TM - 1, mt1, ro1);
+        const int ldm = mt0 == 0 ? a.rows[0] : (mt0 == 1 ? a.rows[1] : a.rows[2]);
+        swm = mt0 == 0 ? a.sw[0] : (mt0 == 1 ? a.sw[1] : a.sw[2]);
+        fast = tok0 + MS * TM <= M && row0 + NS * TM <= a.total_rows && mt0 == mt1 && (long)M * ldm < (1L << 30);
+        if (fast) epi32_pre<OUT, MS>(a, tok0, swm, et, false);
+    }
 
     // weights: row tile s of this wave, row l32; packed uint4 2b + g of a step
     const uint4* brow[NS];
@@ -543,6 +648,8 @@ void tgemm2_kernel(GemvArgs a) {
         b_issue(pi, bw[p]);
     }
     MTR(1)
+    if constexpr (OUT == kOutF32 || OUT == kOutF32Add || OUT == kOutI32)
+        if (fast) epi32_pre<OUT, MS>(a, tok0, swm, et, true);
     wait_vm(std::integral_constant<int, NB + (ST - 1) * (NA + NB)>{});
     __builtin_amdgcn_s_barrier();
     MTR(2)
@@ -606,7 +713,17 @@ void tgemm2_kernel(GemvArgs a) {
         for (int i = 0; i < NB; i++) asm volatile("" ::"v"(bw[k][i]));
     MTR(3)
 
-    mfma_epilogue<OUT, TM>(a, acc, m0 + wm * (BM / 2), n0 + wn * (BN / 2));
+    if constexpr (OUT == kOutF32 || OUT == kOutF32Add || OUT == kOutI32) {
+        if (fast) {
+            epi32_full<OUT, MS, NS>(a, acc, tok0, mt0, ro0, et);
+#ifdef LBT_GEMM_TRACE
+            __builtin_amdgcn_s_waitcnt(0);
+#endif
+            MTR(4)
+            return;
+        }
+    }
+    mfma_epilogue<OUT, TM>(a, acc, tok0, row0);
 #ifdef LBT_GEMM_TRACE
     __builtin_amdgcn_s_waitcnt(0);
 #endif
