@@ -59,7 +59,8 @@ int lbt_memcpy_d2h(lbt_ctx* ctx, void* dst, const void* src, size_t bytes);
  * reference kernel when HBM counters are calibrated.  No counterpart in the
  * reference (its tensors live in host memory). */
 int lbt_memcpy_d2d(lbt_ctx* ctx, void* dst, const void* src, size_t bytes);
-/* Library build id (kernel set + arch). */
+/* Library build id (kernel set + arch; "+step" when the one-dispatch decode
+ * step is built in). */
 const char* lbt_version(void);
 
 /* ---- packed ternary weights ------------------------------------------------
@@ -248,7 +249,8 @@ int lbt_model_set_head(lbt_model* m, int kind);
  * crates/lb-model/src/model.rs:305-374, on the CPU): 0 = all decoder layers of
  * a token in one dispatch, 1 = one dispatch per kernel, replayed as a
  * captured graph (default).  Both give the same bits; shapes the one-dispatch step
- * does not take use the multi-kernel step. */
+ * does not take use the multi-kernel step.  Kind 0 (measured slower) is in
+ * builds made with LBT_WITH_STEP=1 only; otherwise it is LBT_E_INVALID. */
 int lbt_model_set_decode(lbt_model* m, int kind);
 /* Residual stream of the last forward ([n, hidden] f32) for layer-level tests. */
 int lbt_model_read_hidden(lbt_model* m, float* out, size_t n);

@@ -33,6 +33,9 @@ FLAGS = [
     "-Wno-unused-result",
     f"-I{REPO / 'include'}",
 ]
+# the one-dispatch decode step (measured slower than the graph step) only on request
+if os.environ.get("LBT_WITH_STEP") == "1":
+    FLAGS.append("-DLBT_WITH_STEP=1")
 
 
 def sources() -> list[Path]:

@@ -39,6 +39,10 @@
 #include "ternary_common.h"
 #include "decode_step.h"
 
+// Measured slower than the multi-kernel graph step it equals bit for bit, so
+// it is built only on request (LBT_WITH_STEP=1 in the build environment).
+#if LBT_WITH_STEP
+
 namespace lbt {
 
 constexpr int kST = 256;  // threads per workgroup
@@ -1060,3 +1064,19 @@ int launch_decode_step(lbt_ctx* ctx, const StepPlan& pl, const StepArgs* dargs, 
 }
 
 }  // namespace lbt
+
+#else
+
+namespace lbt {
+int step_plan(const lbt_config&, int, int, StepPlan&, const char** why) {
+    if (why) *why = "the one-dispatch step is not in this build (LBT_WITH_STEP=1)";
+    return 0;
+}
+void step_fill(const StepPlan&, const lbt_config&, StepArgs&) {}
+int launch_decode_step(lbt_ctx* ctx, const StepPlan&, const StepArgs*, hipStream_t) {
+    return set_err(ctx, LBT_E_INVALID, "the one-dispatch step is not in this build (LBT_WITH_STEP=1)");
+}
+}  // namespace lbt
+
+#endif
+

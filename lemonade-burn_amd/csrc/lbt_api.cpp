@@ -141,7 +141,13 @@ TernaryOp make_op(const lbt_weight* const* ws, size_t n, size_t m) {
 
 extern "C" {
 
-const char* lbt_version(void) { return "lbt-hip 0.1 gfx950"; }
+const char* lbt_version(void) {
+#if LBT_WITH_STEP
+    return "lbt-hip 0.2 gfx950 +step";
+#else
+    return "lbt-hip 0.2 gfx950";
+#endif
+}
 
 
 int lbt_ctx_create(int device, lbt_ctx** out) {

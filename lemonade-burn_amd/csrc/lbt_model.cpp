@@ -1346,6 +1346,10 @@ int lbt_model_set_decode(lbt_model* m, int kind) {
     if (!m) return LBT_E_INVALID;
     if (kind != 0 && kind != 1)
         return set_err(m->ctx, LBT_E_INVALID, "set_decode: kind must be 0 (one dispatch) or 1 (multi-kernel)");
+#if !LBT_WITH_STEP
+    if (kind == 0)
+        return set_err(m->ctx, LBT_E_INVALID, "set_decode: the one-dispatch step is not in this build (LBT_WITH_STEP=1)");
+#endif
     m->decode_kind = kind;
     return LBT_OK;
 }

@@ -8,9 +8,10 @@ import pytest
 
 import lbt_hip
 import lbt_oracle as orc
-from conftest import announce
+from conftest import announce, step_built
 
-pytestmark = pytest.mark.gpu
+pytestmark = [pytest.mark.gpu,
+              pytest.mark.skipif(not step_built(), reason="one-dispatch step not built (LBT_WITH_STEP=1)")]
 
 
 def run_decode(m, prompt, steps):
