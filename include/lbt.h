@@ -278,6 +278,15 @@ int lbt_batch_forward(lbt_batch* b, const uint32_t* tokens, float* logits, uint3
 /* `steps` greedy steps of every sequence starting from first[s]:
  * out_tokens[i * nseq + s] is sequence s's token produced by step i;
  * *ms_decode (nullable) the device time of the steps. */
+/* lbt_batch_prefill / lbt_batch_forward with the device sampler
+ * (sample.rs:45-82): the first token of `seq` drawn with *p and its sampler
+ * state *state; one step of every sequence, sequence s drawn with params[s]
+ * and states[s] (host arrays of nseq; states updated; temperature 0 is the
+ * argmax).  Only token ids return to the host. */
+int lbt_batch_prefill_sample(lbt_batch* b, int seq, const uint32_t* tokens, size_t n, const lbt_sample_params* p,
+                             uint64_t* state, uint32_t* next);
+int lbt_batch_forward_sample(lbt_batch* b, const uint32_t* tokens, const lbt_sample_params* params,
+                             uint64_t* states, uint32_t* next);
 int lbt_batch_decode_greedy(lbt_batch* b, const uint32_t* first, size_t steps, uint32_t* out_tokens,
                             float* ms_decode);
 
@@ -302,6 +311,11 @@ int lbt_sched_submit(lbt_sched* s, const uint32_t* prompt, size_t n, size_t max_
 /* One step: admit queued requests into free slots (prefill, first token),
  * then one batched decode step of the active slots.  *pending (nullable):
  * requests still queued or active afterwards. */
+/* lbt_sched_submit for a request sampled with *p (the job's SamplingParams,
+ * lb-server/src/main.rs:102-109) from a sampler seeded with `seed`
+ * (seed.max(1), sample.rs:33-35); requests of both kinds share the steps. */
+int lbt_sched_submit_sample(lbt_sched* s, const uint32_t* prompt, size_t n, size_t max_new, uint32_t stop,
+                            const lbt_sample_params* p, uint64_t seed, uint64_t* id);
 int lbt_sched_step(lbt_sched* s, int* pending);
 /* The tokens of request id so far (up to cap of them into tokens, nullable),
  * their count in *n and whether it is finished in *done. */

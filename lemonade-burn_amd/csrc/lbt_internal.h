@@ -185,7 +185,8 @@ int launch_q8_quantize(lbt_ctx* ctx, const uint16_t* w, int rows, int cols, int8
 // goes to out_tok[r] and/or, as an argmax-key word the next embedding reads,
 // to out_key[r]; scratch: sample_scratch_bytes.
 int launch_sample(lbt_ctx* ctx, const float* logits, long ld, int rows, int vocab, const lbt_sample_params& p,
-                  unsigned long long* states, uint32_t* out_tok, unsigned long long* out_key, void* scratch);
+                  unsigned long long* states, uint32_t* out_tok, unsigned long long* out_key, void* scratch,
+                  const lbt_sample_params* rowp = nullptr);
 int sample_scratch_bytes(int rows, int vocab, size_t* bytes);
 int launch_embed(lbt_ctx* ctx, const uint16_t* embed, int hidden, int vocab, const uint32_t* tokens,
                  const unsigned long long* key, uint32_t* tok_out, int m, float* x, int* state = nullptr);

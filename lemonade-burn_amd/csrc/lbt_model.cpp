@@ -303,6 +303,11 @@ struct lbt_batch {
     int* pos = nullptr;        // device positions of the current step [nseq]
     uint32_t* tok_out = nullptr;
     size_t tok_out_cap = 0;
+    // device sampler of the batch: per-sequence parameters and states, and
+    // the candidate scratch of nseq rows (allocated on first use)
+    lbt_sample_params* sp = nullptr;
+    unsigned long long* sst = nullptr;
+    void* sscratch = nullptr;
     size_t seq_stride() const;
     size_t layer_stride() const { return (size_t)nseq * seq_stride(); }
 };
@@ -1416,7 +1421,7 @@ int lbt_batch_new(lbt_model* m, int nseq, int cap, lbt_batch** out) {
 void lbt_batch_free(lbt_batch* b) {
     if (!b) return;
     hipStreamSynchronize(b->m->ctx->stream);
-    void* bufs[] = {b->k, b->v, b->pos, b->tok_out};
+    void* bufs[] = {b->k, b->v, b->pos, b->tok_out, b->sp, b->sst, b->sscratch};
     for (void* p : bufs)
         if (p) hipFree(p);
     delete b;
@@ -1453,6 +1458,80 @@ int lbt_batch_prefill(lbt_batch* b, int seq, const uint32_t* tokens, size_t n, u
     LBT_HIP(ctx, hipMemcpyAsync(&key, m->key, 8, hipMemcpyDeviceToHost, ctx->stream));
     LBT_HIP(ctx, hipStreamSynchronize(ctx->stream));
     if (next) *next = 0xffffffffu - (uint32_t)(key & 0xffffffffull);
+    return LBT_OK;
+}
+
+namespace {
+int batch_sampler(lbt_batch* b) {
+    if (b->sp) return LBT_OK;
+    lbt_ctx* ctx = b->m->ctx;
+    size_t bytes;
+    sample_scratch_bytes(b->nseq, b->m->cfg.vocab_size, &bytes);
+    LBT_HIP(ctx, hipMalloc(&b->sscratch, bytes));
+    LBT_HIP(ctx, hipMalloc(&b->sst, (size_t)b->nseq * 8));
+    LBT_HIP(ctx, hipMalloc(&b->sp, (size_t)b->nseq * sizeof(lbt_sample_params)));
+    return LBT_OK;
+}
+}  // namespace
+
+int lbt_batch_prefill_sample(lbt_batch* b, int seq, const uint32_t* tokens, size_t n, const lbt_sample_params* p,
+                             uint64_t* state, uint32_t* next) {
+    if (!b || !tokens || n == 0 || seq < 0 || seq >= b->nseq || !p || !state)
+        return set_err(b ? b->m->ctx : nullptr, LBT_E_INVALID, "bad arguments");
+    lbt_model* m = b->m;
+    lbt_ctx* ctx = m->ctx;
+    if (b->len[seq] + (int)n > b->cap) return set_err(ctx, LBT_E_RANGE, "batch: sequence capacity exceeded");
+    int rc;
+    if ((rc = ensure_ws(m, (int)n))) return rc;
+    if ((rc = batch_sampler(b))) return rc;
+    if ((rc = upload_tokens(m, tokens, n))) return rc;
+    LBT_HIP(ctx, hipMemcpyAsync(b->sst + seq, state, 8, hipMemcpyHostToDevice, ctx->stream));
+    const size_t off = (size_t)seq * b->seq_stride();
+    KvView kv{b->k + off, b->v + off, b->layer_stride(), b->cap};
+    RowPos rp;
+    rp.pos0 = b->len[seq];
+    rp.vis_max = b->len[seq] + (int)n;
+    if ((rc = forward_rows(m, kv, rp, m->toks, (int)n, false, true, nullptr, nullptr, (int)n > 1))) return rc;
+    b->len[seq] += (int)n;
+    if ((rc = launch_sample(ctx, m->logits, m->cfg.vocab_size, 1, m->cfg.vocab_size, *p, b->sst + seq, nullptr, m->key,
+                            b->sscratch)))
+        return rc;
+    unsigned long long key = 0;
+    LBT_HIP(ctx, hipMemcpyAsync(&key, m->key, 8, hipMemcpyDeviceToHost, ctx->stream));
+    LBT_HIP(ctx, hipMemcpyAsync(state, b->sst + seq, 8, hipMemcpyDeviceToHost, ctx->stream));
+    LBT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    if (next) *next = 0xffffffffu - (uint32_t)(key & 0xffffffffull);
+    return LBT_OK;
+}
+
+int lbt_batch_forward_sample(lbt_batch* b, const uint32_t* tokens, const lbt_sample_params* params, uint64_t* states,
+                             uint32_t* next) {
+    if (!b || !tokens || !params || !states || !next)
+        return set_err(b ? b->m->ctx : nullptr, LBT_E_INVALID, "bad arguments");
+    lbt_model* m = b->m;
+    lbt_ctx* ctx = m->ctx;
+    for (int s = 0; s < b->nseq; s++) {
+        if (b->len[s] + 1 > b->cap) return set_err(ctx, LBT_E_RANGE, "batch: sequence capacity exceeded");
+        if (tokens[s] >= (uint32_t)m->cfg.vocab_size) return set_err(ctx, LBT_E_INVALID, "token id out of range");
+    }
+    int rc;
+    if ((rc = ensure_ws(m, b->nseq))) return rc;
+    if ((rc = batch_sampler(b))) return rc;
+    if ((rc = upload_tokens(m, tokens, (size_t)b->nseq))) return rc;
+    LBT_HIP(ctx, hipMemcpyAsync(b->sp, params, (size_t)b->nseq * sizeof(lbt_sample_params), hipMemcpyHostToDevice,
+                                ctx->stream));
+    LBT_HIP(ctx, hipMemcpyAsync(b->sst, states, (size_t)b->nseq * 8, hipMemcpyHostToDevice, ctx->stream));
+    if ((rc = batch_upload_pos(b))) return rc;
+    if ((rc = batch_step(b, m->toks, true, nullptr))) return rc;
+    for (int s = 0; s < b->nseq; s++) b->len[s] += 1;
+    if ((rc = launch_sample(ctx, m->logits, m->cfg.vocab_size, b->nseq, m->cfg.vocab_size, params[0], b->sst,
+                            nullptr, m->key, b->sscratch, b->sp)))
+        return rc;
+    std::vector<unsigned long long> keys((size_t)b->nseq);
+    LBT_HIP(ctx, hipMemcpyAsync(keys.data(), m->key, keys.size() * 8, hipMemcpyDeviceToHost, ctx->stream));
+    LBT_HIP(ctx, hipMemcpyAsync(states, b->sst, (size_t)b->nseq * 8, hipMemcpyDeviceToHost, ctx->stream));
+    LBT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    for (int s = 0; s < b->nseq; s++) next[s] = 0xffffffffu - (uint32_t)(keys[s] & 0xffffffffull);
     return LBT_OK;
 }
 

@@ -1,4 +1,5 @@
-// lbt_sched.cpp -- continuous batching of greedy requests over one lbt_batch.
+// lbt_sched.cpp -- continuous batching of requests over one lbt_batch, greedy
+// or drawn by the device sampler with each request's own parameters.
 //
 // Not in the reference: lb-server runs one request at a time
 // (crates/lb-server/src/main.rs:92-100).  A request waits in a FIFO until a
@@ -24,6 +25,10 @@ struct lbt_sched {
         uint32_t stop = 0xffffffffu;
         std::vector<uint32_t> out;
         bool done = false;
+        // sampled requests: the job's SamplingParams and sampler state
+        // (sample.rs:28-35); greedy ones keep temperature 0
+        lbt_sample_params sp{0.0f, 1.0f, 0};
+        uint64_t state = 1;
     };
     std::map<uint64_t, Req> reqs;
     std::deque<uint64_t> queue;
@@ -83,6 +88,17 @@ int lbt_sched_submit(lbt_sched* s, const uint32_t* prompt, size_t n, size_t max_
     return LBT_OK;
 }
 
+int lbt_sched_submit_sample(lbt_sched* s, const uint32_t* prompt, size_t n, size_t max_new, uint32_t stop,
+                            const lbt_sample_params* p, uint64_t seed, uint64_t* id) {
+    if (!p) return lbt::set_err(ctx_of(s), LBT_E_INVALID, "bad arguments");
+    int rc = lbt_sched_submit(s, prompt, n, max_new, stop, id);
+    if (rc) return rc;
+    lbt_sched::Req& r = s->reqs[*id];
+    r.sp = *p;
+    r.state = seed > 1 ? seed : 1;  // Sampler::new: seed.max(1)
+    return LBT_OK;
+}
+
 int lbt_sched_step(lbt_sched* s, int* pending) {
     if (!s) return LBT_E_INVALID;
     int rc;
@@ -95,11 +111,15 @@ int lbt_sched_step(lbt_sched* s, int* pending) {
         // reset or prefill leaves it first in line for the next step
         if ((rc = lbt_batch_reset(s->b, k))) return rc;
         uint32_t first = 0;
-        if ((rc = lbt_batch_prefill(s->b, k, r.prompt.data(), r.prompt.size(), &first))) {
+        uint64_t st = r.state;
+        if ((rc = r.sp.temperature != 0.0f
+                      ? lbt_batch_prefill_sample(s->b, k, r.prompt.data(), r.prompt.size(), &r.sp, &st, &first)
+                      : lbt_batch_prefill(s->b, k, r.prompt.data(), r.prompt.size(), &first))) {
             lbt_batch_reset(s->b, k);
             return rc;
         }
         s->queue.pop_front();
+        r.state = st;
         r.out.push_back(first);
         if (finished(r)) {
             r.done = true;
@@ -109,21 +129,31 @@ int lbt_sched_step(lbt_sched* s, int* pending) {
         }
     }
     // one batched decode step of the active slots (free slots at position 0)
-    bool any = false;
+    bool any = false, sampled = false;
     std::vector<uint32_t> toks((size_t)s->slots, 0), next((size_t)s->slots, 0);
+    std::vector<lbt_sample_params> sp((size_t)s->slots, lbt_sample_params{0.0f, 1.0f, 0});
+    std::vector<uint64_t> st((size_t)s->slots, 1);
     for (int k = 0; k < s->slots; k++) {
         if (s->slot_req[k] < 0) {
             if ((rc = lbt_batch_reset(s->b, k))) return rc;
             continue;
         }
         any = true;
-        toks[k] = s->reqs[(uint64_t)s->slot_req[k]].out.back();
+        const lbt_sched::Req& r = s->reqs[(uint64_t)s->slot_req[k]];
+        toks[k] = r.out.back();
+        sp[k] = r.sp;
+        st[k] = r.state;
+        sampled |= r.sp.temperature != 0.0f;
     }
     if (any) {
-        if ((rc = lbt_batch_forward(s->b, toks.data(), nullptr, next.data()))) return rc;
+        // greedy slots ride along in a sampling step at temperature 0 (the argmax)
+        if ((rc = sampled ? lbt_batch_forward_sample(s->b, toks.data(), sp.data(), st.data(), next.data())
+                          : lbt_batch_forward(s->b, toks.data(), nullptr, next.data())))
+            return rc;
         for (int k = 0; k < s->slots; k++) {
             if (s->slot_req[k] < 0) continue;
             lbt_sched::Req& r = s->reqs[(uint64_t)s->slot_req[k]];
+            r.state = st[k];
             r.out.push_back(next[k]);
             if (finished(r)) {
                 r.done = true;

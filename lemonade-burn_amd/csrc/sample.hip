@@ -201,6 +201,7 @@ struct SampleArgs {
     int V;
     float temperature, top_p;
     unsigned long long top_k;  // 0: no truncation
+    const lbt_sample_params* rowp;  // [rows] per-row parameters in device memory (null: the ones above)
     unsigned long long* states;  // [rows] xorshift states, advanced by one draw when temperature > 0
     uint32_t* out_tok;            // [rows] (nullable)
     unsigned long long* out_key;  // [rows] argmax-key words the next embedding reads (nullable)
@@ -212,6 +213,11 @@ __global__ __launch_bounds__(kST) void sample_kernel(SampleArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int row = blockIdx.x, V = a.V;
     const float* lg = a.logits + (size_t)row * a.ld;
+    if (a.rowp) {
+        a.temperature = gload(&a.rowp[row].temperature);
+        a.top_p = gload(&a.rowp[row].top_p);
+        a.top_k = (unsigned long long)gload(&a.rowp[row].top_k);
+    }
     const float t = a.temperature;
     unsigned out = 0;
     if (t <= 0.0f) {
@@ -369,7 +375,8 @@ int sample_scratch_bytes(int rows, int vocab, size_t* bytes) {
 }
 
 int launch_sample(lbt_ctx* ctx, const float* logits, long ld, int rows, int vocab, const lbt_sample_params& p,
-                  unsigned long long* states, uint32_t* out_tok, unsigned long long* out_key, void* scratch) {
+                  unsigned long long* states, uint32_t* out_tok, unsigned long long* out_key, void* scratch,
+                  const lbt_sample_params* rowp) {
     if (rows <= 0) return LBT_OK;
     if (vocab <= 0 || ld < vocab || !logits || !states || !scratch)
         return set_err(ctx, LBT_E_INVALID, "sample: bad arguments");
@@ -380,6 +387,7 @@ int launch_sample(lbt_ctx* ctx, const float* logits, long ld, int rows, int voca
     a.temperature = p.temperature;
     a.top_p = p.top_p;
     a.top_k = (unsigned long long)p.top_k;
+    a.rowp = rowp;
     a.states = states;
     a.out_tok = out_tok;
     a.out_key = out_key;

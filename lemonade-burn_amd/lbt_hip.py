@@ -115,11 +115,14 @@ SIGNATURES = {
     "lbt_batch_prefill": (i32, [vp, i32, vp, sz, vp]),
     "lbt_batch_fill_synthetic": (i32, [vp, i32, C.c_uint64]),
     "lbt_batch_forward": (i32, [vp, vp, vp, vp]),
+    "lbt_batch_prefill_sample": (i32, [vp, i32, vp, sz, vp, vp, vp]),
+    "lbt_batch_forward_sample": (i32, [vp, vp, vp, vp, vp]),
     "lbt_batch_decode_greedy": (i32, [vp, vp, sz, vp, vp]),
     "lbt_batch_reset": (i32, [vp, i32]),
     "lbt_sched_new": (i32, [vp, i32, i32, C.POINTER(vp)]),
     "lbt_sched_free": (None, [vp]),
     "lbt_sched_submit": (i32, [vp, vp, sz, sz, C.c_uint32, C.POINTER(C.c_uint64)]),
+    "lbt_sched_submit_sample": (i32, [vp, vp, sz, sz, C.c_uint32, vp, C.c_uint64, C.POINTER(C.c_uint64)]),
     "lbt_sched_step": (i32, [vp, C.POINTER(i32)]),
     "lbt_sched_result": (i32, [vp, C.c_uint64, vp, sz, C.POINTER(sz), C.POINTER(i32)]),
     "lbt_sched_release": (i32, [vp, C.c_uint64]),
@@ -491,6 +494,23 @@ class Batch:
         self._check(self.model.ctx.lib.lbt_batch_prefill(self.h, seq, _ptr(t), t.size, C.byref(nxt)))
         return int(nxt.value)
 
+    def prefill_sample(self, seq: int, tokens, params: "LbtSampleParams", state: C.c_uint64) -> int:
+        t = np.ascontiguousarray(tokens, np.uint32)
+        nxt = C.c_uint32()
+        self._check(self.model.ctx.lib.lbt_batch_prefill_sample(self.h, seq, _ptr(t), t.size, C.byref(params),
+                                                                C.byref(state), C.byref(nxt)))
+        return int(nxt.value)
+
+    def forward_sample(self, tokens, params: list, states: np.ndarray) -> np.ndarray:
+        """One step of every sequence, sequence s drawn with params[s]
+        ((temperature, top_p, top_k)) and states[s] (uint64, updated)."""
+        t = np.ascontiguousarray(tokens, np.uint32)
+        assert t.size == self.nseq and len(params) == self.nseq and states.dtype == np.uint64
+        pa = (LbtSampleParams * self.nseq)(*[LbtSampleParams(*p) for p in params])
+        nxt = np.zeros(self.nseq, np.uint32)
+        self._check(self.model.ctx.lib.lbt_batch_forward_sample(self.h, _ptr(t), pa, _ptr(states), _ptr(nxt)))
+        return nxt
+
     def fill_synthetic(self, length: int, seed: int):
         self._check(self.model.ctx.lib.lbt_batch_fill_synthetic(self.h, length, C.c_uint64(seed)))
 
@@ -527,6 +547,15 @@ class Sched:
 
     def _check(self, rc):
         self.model.ctx.check(rc)
+
+    def submit_sample(self, prompt, max_new: int, params, seed: int, stop: int = NO_STOP) -> int:
+        """A request drawn by the device sampler: params = (temperature, top_p, top_k)."""
+        t = np.ascontiguousarray(prompt, np.uint32)
+        rid = C.c_uint64()
+        p = LbtSampleParams(*params)
+        self._check(self.model.ctx.lib.lbt_sched_submit_sample(self.h, _ptr(t), t.size, max_new, C.c_uint32(stop),
+                                                               C.byref(p), C.c_uint64(seed), C.byref(rid)))
+        return int(rid.value)
 
     def submit(self, prompt, max_new: int, stop: int = NO_STOP) -> int:
         t = np.ascontiguousarray(prompt, np.uint32)

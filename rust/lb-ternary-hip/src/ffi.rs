@@ -321,6 +321,22 @@ extern "C" {
     pub fn lbt_batch_prefill(b: *mut LbtBatch, seq: c_int, tokens: *const u32, n: usize, next: *mut u32) -> c_int;
     pub fn lbt_batch_fill_synthetic(b: *mut LbtBatch, len: c_int, seed: u64) -> c_int;
     pub fn lbt_batch_forward(b: *mut LbtBatch, tokens: *const u32, logits: *mut f32, next: *mut u32) -> c_int;
+    pub fn lbt_batch_prefill_sample(
+        b: *mut LbtBatch,
+        seq: c_int,
+        tokens: *const u32,
+        n: usize,
+        p: *const LbtSampleParams,
+        state: *mut u64,
+        next: *mut u32,
+    ) -> c_int;
+    pub fn lbt_batch_forward_sample(
+        b: *mut LbtBatch,
+        tokens: *const u32,
+        params: *const LbtSampleParams,
+        states: *mut u64,
+        next: *mut u32,
+    ) -> c_int;
     pub fn lbt_batch_decode_greedy(
         b: *mut LbtBatch,
         first: *const u32,
@@ -337,6 +353,16 @@ extern "C" {
         n: usize,
         max_new: usize,
         stop: u32,
+        id: *mut u64,
+    ) -> c_int;
+    pub fn lbt_sched_submit_sample(
+        s: *mut LbtSched,
+        prompt: *const u32,
+        n: usize,
+        max_new: usize,
+        stop: u32,
+        p: *const LbtSampleParams,
+        seed: u64,
         id: *mut u64,
     ) -> c_int;
     pub fn lbt_sched_step(s: *mut LbtSched, pending: *mut c_int) -> c_int;
