@@ -36,6 +36,7 @@ FLAGS = [
 # the one-dispatch decode step (measured slower than the graph step) only on request
 if os.environ.get("LBT_WITH_STEP") == "1":
     FLAGS.append("-DLBT_WITH_STEP=1")
+FLAGS += os.environ.get("LBT_EXTRA_FLAGS", "").split()
 
 
 def sources() -> list[Path]:

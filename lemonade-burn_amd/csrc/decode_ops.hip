@@ -86,22 +86,24 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(const float* q, int
 // taking all GH query heads of the KV head.  Grid (kvh * splits, m).
 // wide: eight key passes in flight per split of more than 64 keys (grids of
 // many workgroups, where occupancy is not the limit); same partials.
-template <int LK, int GH>
+template <int LK, int GH, bool WIDE>
 __global__ __launch_bounds__(kThreads) void attention_group_kernel(const float* q, int nh, int kvh, RowPos rp,
                                                                    const uint16_t* kc, const uint16_t* vc, int cap,
-                                                                   float scaling, float* o, float* ml, int wide) {
-    extern __shared__ float sc[];  // [GH][attn_split_keys(visible keys)]
+                                                                   float scaling, float* o, float* ml) {
+    extern __shared__ __align__(16) float sc[];  // [attn_group_score_keys(split keys)][GH]
     __shared__ AttnGroupShared<LK, GH> sh;
     const int nsg = (int)gridDim.x / kvh;  // splits in the grid (the most any row has)
     const int g = blockIdx.x / nsg, s = blockIdx.x % nsg, t = blockIdx.y;
     const int H = nh * LK * 8;
     const size_t kvoff = row_cache_offset(rp, t) + (size_t)g * cap * LK * 8;
     const int p = row_position(rp, t);
+    // the eight-pass path is its own instantiation: its register buffers
+    // would otherwise set the occupancy of the narrower paths too
     if (attn_split_keys(p + 1) <= 2 * (kThreads / LK))
         attention_split_group<LK, GH, 2>(q + (size_t)t * H, g, nh, s, p, kc + kvoff, vc + kvoff, scaling,
                                          o + (size_t)t * kAttnSplits * H, ml + (size_t)t * kAttnSplits * nh * 2, sc,
                                          sh);
-    else if (!wide || attn_split_keys(p + 1) <= 4 * (kThreads / LK))
+    else if (!WIDE || attn_split_keys(p + 1) <= 4 * (kThreads / LK))
         attention_split_group<LK, GH, 4>(q + (size_t)t * H, g, nh, s, p, kc + kvoff, vc + kvoff, scaling,
                                          o + (size_t)t * kAttnSplits * H, ml + (size_t)t * kAttnSplits * nh * 2, sc,
                                          sh);
@@ -783,7 +785,7 @@ int launch_embed(lbt_ctx* ctx, const uint16_t* embed, int hidden, int vocab, con
 namespace {
 
 template <int LK>
-hipError_t launch_attn_lk(int gh, bool grouped, bool force_wide, dim3 grid, size_t lds, hipStream_t st, hipEvent_t e0, hipEvent_t e1,
+hipError_t launch_attn_lk(int gh, bool grouped, int force_wide, dim3 grid, size_t lds, hipStream_t st, hipEvent_t e0, hipEvent_t e1,
                           const float* q, int nh, int kvh, const RowPos& rp, const uint16_t* kc, const uint16_t* vc,
                           int cap, float scaling, float* o, float* ml) {
     if (!grouped) {
@@ -791,21 +793,20 @@ hipError_t launch_attn_lk(int gh, bool grouped, bool force_wide, dim3 grid, size
                               cap, scaling, o, ml);
         return hipGetLastError();
     }
-    const int wide = (long)grid.x * grid.y >= 4096 || force_wide ? 1 : 0;
+    const bool wide = force_wide < 0 ? (long)grid.x * grid.y >= 4096 : force_wide != 0;
+#define LBT_ATTN_GROUP(GH)                                                                                      \
+    if (wide)                                                                                                   \
+        hipExtLaunchKernelGGL((attention_group_kernel<LK, GH, true>), grid, dim3(kThreads), lds, st, e0, e1, 0, q, \
+                              nh, kvh, rp, kc, vc, cap, scaling, o, ml);                                        \
+    else                                                                                                        \
+        hipExtLaunchKernelGGL((attention_group_kernel<LK, GH, false>), grid, dim3(kThreads), lds, st, e0, e1, 0, q, \
+                              nh, kvh, rp, kc, vc, cap, scaling, o, ml);
     switch (gh) {
-        case 1:
-            hipExtLaunchKernelGGL((attention_group_kernel<LK, 1>), grid, dim3(kThreads), lds, st, e0, e1, 0, q, nh,
-                                  kvh, rp, kc, vc, cap, scaling, o, ml, wide);
-            break;
-        case 2:
-            hipExtLaunchKernelGGL((attention_group_kernel<LK, 2>), grid, dim3(kThreads), lds, st, e0, e1, 0, q, nh,
-                                  kvh, rp, kc, vc, cap, scaling, o, ml, wide);
-            break;
-        default:
-            hipExtLaunchKernelGGL((attention_group_kernel<LK, 4>), grid, dim3(kThreads), lds, st, e0, e1, 0, q, nh,
-                                  kvh, rp, kc, vc, cap, scaling, o, ml, wide);
-            break;
+        case 1: LBT_ATTN_GROUP(1); break;
+        case 2: LBT_ATTN_GROUP(2); break;
+        default: LBT_ATTN_GROUP(4); break;
     }
+#undef LBT_ATTN_GROUP
     return hipGetLastError();
 }
 
@@ -817,7 +818,8 @@ int launch_attention(lbt_ctx* ctx, const float* q, int m, int nh, int kvh, int h
     if (kvh <= 0 || nh % kvh) return set_err(ctx, LBT_E_INVALID, "attention: heads must be a multiple of kv heads");
     const int gh = nh / kvh;
     if (gh != 1 && gh != 2 && gh != 4) grouped = false;
-    const size_t lds = (size_t)(grouped ? gh : 1) * attn_split_keys(rp.vis_max) * sizeof(float);
+    const size_t lds = grouped ? (size_t)gh * attn_group_score_keys(attn_split_keys(rp.vis_max), hd / 8) * sizeof(float)
+                               : (size_t)attn_split_keys(rp.vis_max) * sizeof(float);
     if (lds > 64 * 1024) return set_err(ctx, LBT_E_RANGE, "attention: context too long for the LDS score buffer");
     hipEvent_t e0, e1;
     prof_pair(ctx, &e0, &e1);

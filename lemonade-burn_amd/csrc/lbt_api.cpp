@@ -29,7 +29,10 @@ LbtTuning read_tuning() {
     if (t.small_ms < 1) t.small_ms = 1;
     t.small_ns = (int)num("LBT_GEMM_SMALL_NS", 0);
     t.small_pf = num("LBT_GEMM_SMALL_PF", 1) != 0;
-    t.attn_wide = getenv("LBT_ATTN_WIDE") != nullptr;
+    {
+        const char* v = getenv("LBT_ATTN_WIDE");
+        t.attn_wide = v ? (atoi(v) != 0 ? 1 : 0) : -1;
+    }
     t.head_tg8 = getenv("LBT_HEAD_TG8") != nullptr;
     t.step_trace = getenv("LBT_STEP_TRACE") != nullptr;
     return t;

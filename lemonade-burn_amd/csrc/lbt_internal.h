@@ -22,7 +22,7 @@ struct LbtTuning {
     int small_ms = 1;         // LBT_GEMM_SMALL_MS: cap of its token tiles (16 * ms)
     int small_ns = 0;         // LBT_GEMM_SMALL_NS: 1 / 2 forces its row tile (0 auto)
     bool small_pf = true;     // LBT_GEMM_SMALL_PF=0: no epilogue prefetch
-    bool attn_wide = false;   // LBT_ATTN_WIDE: eight-pass K/V pipeline of the grouped attention
+    int attn_wide = -1;       // LBT_ATTN_WIDE=1/0: eight-pass K/V pipeline of the grouped attention on/off (-1: by grid size)
     bool head_tg8 = false;    // LBT_HEAD_TG8: 8-token groups in the batched LM head
     bool step_trace = false;  // LBT_STEP_TRACE: phase timestamps of the one-dispatch decode step
 };

@@ -315,7 +315,7 @@ __device__ __forceinline__ void epi32_full(const GemvArgs& a, v16i (&acc)[MS][NS
 // weight stream is the whole cost, so the grid is cut as finely as the
 // 16 x 16 x 64 MFMA allows -- one workgroup per 16 rows (o/down of the 2B
 // model: 160 workgroups instead of 40 tiles of 64 rows; 32 rows, NS = 2, where
-// that still leaves >= 384 workgroups, halving the activation re-reads) --
+// that still leaves >= 256 workgroups, halving the activation re-reads) --
 // and its 4 wavefronts split K into contiguous step ranges.  Each wavefront
 // issues every weight load of its range at once (at most kSmallMaxSteps uint4
 // per lane and row tile), reads the activations (L2-resident, 16 MS tokens)
@@ -360,7 +360,7 @@ __device__ __forceinline__ void epi_prefetch(const GemvArgs& a, int tok0, int ro
 }
 
 constexpr int kSmallMaxSteps = 8;  // 256-k steps per wavefront: K <= 8192
-constexpr int kSmallWideRowTiles = 384;  // 32-row tiles from 384 * 32 rows
+constexpr int kSmallWideGroups = 256;  // 32-row tiles from 256 workgroups of them
 
 template <int OUT, int MS, int NS, bool PF = false>
 __global__ __launch_bounds__(kThreads) void tgemm_small_kernel(GemvArgs a) {
@@ -851,9 +851,14 @@ int launch_ternary_mfma(lbt_ctx* ctx, const TernaryOp& op_in) {
         // wider tiles
         int ms = op.m <= 16 ? 1 : op.m <= 32 ? 2 : op.m <= 48 ? 3 : 4;
         if (ms > tu.small_ms) ms = tu.small_ms;
-        // 32-row tiles (half the activation re-reads) where they still give
-        // >= 256 workgroups per token tile; tune.small_ns = 1 / 2 forces
-        const int ns = tu.small_ns ? (tu.small_ns == 2 ? 2 : 1) : (total >= 32 * kSmallWideRowTiles ? 2 : 1);
+        // 32-row tiles (half the activation and weight re-reads) where they
+        // still give >= kSmallWideGroups workgroups over all token tiles
+        // (measured at 2B, 64 tokens: q/k/v 9.4 -> 7.6 us, o 8.1 -> 7.4,
+        // down 14.2 -> 12.0; 16 tokens keep 16-row tiles there);
+        // tune.small_ns = 1 / 2 forces
+        const long tt = (op.m + 16 * ms - 1) / (16 * ms);
+        const int ns = tu.small_ns ? (tu.small_ns == 2 ? 2 : 1)
+                                   : ((long)((total + 31) / 32) * tt >= kSmallWideGroups ? 2 : 1);
         const dim3 g((unsigned)((total + 16 * ns - 1) / (16 * ns)), (unsigned)((op.m + 16 * ms - 1) / (16 * ms)));
         const bool pf = tu.small_pf;
         if (ns == 2)
