@@ -16,9 +16,10 @@
 //   r < c       <=>  sum(w) >= floor(draw * W_keep / 2^24) + 1,
 // so no float sum depends on an order and no sort is needed: each "first
 // element in sorted order whose prefix reaches T" is a radix select over the
-// keys (~total order << index bits | index) with weight histograms, 9 bits a
-// round.  Elements with w = 0 can never be chosen, so only elements with
-// w > 0 (a prefix of the sorted order) are kept as candidates -- in LDS when
+// keys (~total order << index bits | index) with weight histograms: three
+// rounds over the value, then the index bits only where values tie.
+// Elements with w = 0 can never be chosen, so only elements with w > 0 (a
+// prefix of the sorted order) are kept as candidates -- in LDS when
 // they fit, else in a global scratch of 16 bytes per logit.  A NaN among the
 // top-k p (a NaN logit in the set, max = +inf, all -inf, a NaN temperature)
 // makes every comparison of the reference false: it returns the last element
@@ -31,7 +32,7 @@ namespace lbt {
 namespace {
 
 constexpr int kST = 1024;  // threads
-constexpr int kDigit = 9, kBins = 1 << kDigit;
+constexpr int kBins = 2048;  // histogram bins: digits of up to 11 bits
 constexpr int kLdsCand = 4096;  // candidates kept in LDS
 constexpr unsigned long long kNone = ~0ull;
 
@@ -42,10 +43,14 @@ struct Cand {
 struct SampleShared {
     Cand cand[kLdsCand];
     unsigned long long hist[kBins];
+    unsigned long long minkey[kBins];  // smallest key per bin (last value round)
+    unsigned bcnt[kBins];              // elements per bin (last value round)
     unsigned long long red[kST / 64];
     unsigned long long red2[kST / 64];
     unsigned long long sel_below, sel_through;
     unsigned sel_bin;
+    unsigned long long sel_min;
+    unsigned sel_cnt;
     unsigned cnt;
     float fred[kST / 64];
     unsigned ired[kST / 64];
@@ -139,58 +144,107 @@ struct LogitSrc {
     __device__ unsigned long long w(unsigned) const { return 1ull; }
 };
 
+// One round of the select: the histogram of digit (s >> shift) & (2^bits - 1)
+// over the elements with s <= lim whose bits above shift + bits equal
+// `prefix`, then the first bin (ascending) whose cumulative weight from
+// `below` reaches `target`.  LAST also counts the elements of each bin and
+// keeps its smallest key.
+template <bool MASS, bool LAST, class Src>
+__device__ void select_round(const Src& c, unsigned n, unsigned long long lim, unsigned long long target, int shift,
+                             int bits, unsigned long long prefix, unsigned long long below, SampleShared& sh) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int nb = 1 << bits;
+    for (int b = tid; b < nb; b += kST) {
+        sh.hist[b] = 0;
+        if (LAST) {
+            sh.bcnt[b] = 0;
+            sh.minkey[b] = kNone;
+        }
+    }
+    __syncthreads();
+    for (unsigned i = tid; i < n; i += kST) {
+        const unsigned long long s = c.key(i);
+        if (s <= lim && (s >> (shift + bits)) == prefix) {
+            const unsigned bin = (unsigned)(s >> shift) & (unsigned)(nb - 1);
+            atomicAdd(&sh.hist[bin], MASS ? c.w(i) : 1ull);
+            if (LAST) {
+                atomicAdd(&sh.bcnt[bin], 1u);
+                atomicMin(&sh.minkey[bin], s);
+            }
+        }
+    }
+    __syncthreads();
+    if (tid < 64) {
+        // PL bins per lane; bins past nb (rounds of fewer than 64 bins) are
+        // empty, whatever an earlier round left there
+        const int PL = nb >= 64 ? nb / 64 : 1;
+        auto hbin = [&](int b) { return b < nb ? sh.hist[b] : 0ull; };
+        unsigned long long sum = 0;
+        for (int j = 0; j < PL; j++) sum += hbin(PL * lane + j);
+        unsigned long long inc = sum;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const unsigned long long v = __shfl_up(inc, d, 64);
+            if (lane >= d) inc += v;
+        }
+        unsigned long long run = below + inc - sum, bel = 0, thr = 0;
+        unsigned found = kBins;
+        for (int j = 0; j < PL; j++) {
+            const unsigned long long h = hbin(PL * lane + j);
+            if (h && found == kBins && run + h >= target) {
+                found = PL * lane + j;
+                bel = run;
+                thr = run + h;
+            }
+            run += h;
+        }
+        const unsigned long long fmin = wave_min((unsigned long long)found);
+        if (found == fmin && found < kBins) {
+            sh.sel_bin = found;
+            sh.sel_below = bel;
+            sh.sel_through = thr;
+            if (LAST) {
+                sh.sel_cnt = sh.bcnt[found];
+                sh.sel_min = sh.minkey[found];
+            }
+        }
+    }
+    __syncthreads();
+}
+
+// The smallest key s* among candidates with s <= lim whose cumulative weight
+// (w with MASS, else 1 each) through s* reaches `target` (which must not
+// exceed their total); `through` = that cumulative weight.  All threads call.
+// Keys are (value key << ib) | index: three rounds over the 32-bit value key
+// (11, 11 and 10 bits); when the selected value is held by one element (no
+// tie) that element is s*, else rounds over the ib index bits among the
+// elements of that value follow.  The same s* as a radix select over the
+// whole key, in fewer passes.
 template <bool MASS, class Src>
 __device__ unsigned long long radix_select(const Src& c, unsigned n, unsigned long long lim,
-                                           unsigned long long target, int rounds, SampleShared& sh,
+                                           unsigned long long target, int ib, SampleShared& sh,
                                            unsigned long long& through) {
-    const int tid = threadIdx.x, lane = tid & 63;
     unsigned long long prefix = 0, below = 0;
-    for (int r = rounds - 1; r >= 0; r--) {
-        const int shift = r * kDigit;
-        for (int b = tid; b < kBins; b += kST) sh.hist[b] = 0;
-        __syncthreads();
-        for (unsigned i = tid; i < n; i += kST) {
-            const unsigned long long s = c.key(i);
-            if (s <= lim && (s >> (shift + kDigit)) == prefix)
-                atomicAdd(&sh.hist[(s >> shift) & (kBins - 1)], MASS ? c.w(i) : 1ull);
-        }
-        __syncthreads();
-        if (tid < 64) {
-            constexpr int PL = kBins / 64;
-            unsigned long long h[PL], sum = 0;
-#pragma unroll
-            for (int j = 0; j < PL; j++) {
-                h[j] = sh.hist[PL * lane + j];
-                sum += h[j];
-            }
-            unsigned long long inc = sum;
-#pragma unroll
-            for (int d = 1; d < 64; d <<= 1) {
-                const unsigned long long v = __shfl_up(inc, d, 64);
-                if (lane >= d) inc += v;
-            }
-            unsigned long long run = below + inc - sum, bel = 0, thr = 0;
-            unsigned found = kBins;
-#pragma unroll
-            for (int j = 0; j < PL; j++) {
-                if (h[j] && found == kBins && run + h[j] >= target) {
-                    found = PL * lane + j;
-                    bel = run;
-                    thr = run + h[j];
-                }
-                run += h[j];
-            }
-            const unsigned long long fmin = wave_min(found);
-            if (found == fmin && found < kBins) {
-                sh.sel_bin = found;
-                sh.sel_below = bel;
-                sh.sel_through = thr;
-            }
-        }
-        __syncthreads();
-        prefix = (prefix << kDigit) | sh.sel_bin;
+    select_round<MASS, false>(c, n, lim, target, ib + 21, 11, prefix, below, sh);
+    prefix = sh.sel_bin;
+    below = sh.sel_below;
+    select_round<MASS, false>(c, n, lim, target, ib + 10, 11, prefix, below, sh);
+    prefix = (prefix << 11) | sh.sel_bin;
+    below = sh.sel_below;
+    select_round<MASS, true>(c, n, lim, target, ib, 10, prefix, below, sh);
+    prefix = (prefix << 10) | sh.sel_bin;
+    below = sh.sel_below;
+    through = sh.sel_through;
+    if (sh.sel_cnt == 1) return sh.sel_min;
+    // a tie of values: the index bits, high digits first (11 bits at most)
+    for (int done = 0; done < ib;) {
+        const int bits = ib - done < 11 ? ib - done : 11;
+        const int shift = ib - done - bits;
+        select_round<MASS, false>(c, n, lim, target, shift, bits, prefix, below, sh);
+        prefix = (prefix << bits) | sh.sel_bin;
         below = sh.sel_below;
         through = sh.sel_through;
+        done += bits;
     }
     return prefix;
 }
@@ -273,7 +327,6 @@ __global__ __launch_bounds__(kST) void sample_kernel(SampleArgs a) {
 
     int ib = 1;
     while (ib < 32 && (1u << ib) < (unsigned)V) ib++;
-    const int rounds = (32 + ib + kDigit - 1) / kDigit;
     const unsigned long long imask = (1ull << ib) - 1;
 
     // candidates (w > 0) with their keys; NaN p: the smallest such key
@@ -333,7 +386,7 @@ __global__ __launch_bounds__(kST) void sample_kernel(SampleArgs a) {
     const unsigned long long kk = (a.top_k > 0 && a.top_k < (unsigned long long)V) ? a.top_k : (unsigned long long)V;
     unsigned long long lim = kNone, W = Wall, thr;
     if (kk < n) {
-        lim = radix_select<false>(c, n, kNone, kk, rounds, sh, thr);
+        lim = radix_select<false>(c, n, kNone, kk, ib, sh, thr);
         unsigned long long part = 0;
         for (unsigned i = tid; i < n; i += kST)
             if (c.key(i) <= lim) part += c.w(i);
@@ -347,7 +400,7 @@ __global__ __launch_bounds__(kST) void sample_kernel(SampleArgs a) {
                 last = lim;
             } else {
                 // the k-th element lies beyond the candidates: select over all logits
-                last = radix_select<false>(LogitSrc{lg, ib}, (unsigned)V, kNone, kk, rounds, sh, thr);
+                last = radix_select<false>(LogitSrc{lg, ib}, (unsigned)V, kNone, kk, ib, sh, thr);
             }
         }
         bad = nan_s <= last;
@@ -356,9 +409,9 @@ __global__ __launch_bounds__(kST) void sample_kernel(SampleArgs a) {
         out = (unsigned)(last & imask);
     } else {
         unsigned long long keep_lim = lim, WK = W;
-        if (a.top_p < 1.0f) keep_lim = radix_select<true>(c, n, lim, top_p_target(a.top_p, W), rounds, sh, WK);
+        if (a.top_p < 1.0f) keep_lim = radix_select<true>(c, n, lim, top_p_target(a.top_p, W), ib, sh, WK);
         const unsigned long long Td = ((u * (WK & 0xffffffull)) >> 24) + u * (WK >> 24) + 1;
-        const unsigned long long sd = radix_select<true>(c, n, keep_lim, Td, rounds, sh, thr);
+        const unsigned long long sd = radix_select<true>(c, n, keep_lim, Td, ib, sh, thr);
         out = (unsigned)(sd & imask);
     }
     if (tid == 0) {
