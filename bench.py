@@ -409,6 +409,8 @@ def main() -> int:
                     help="only the opt-in int8 LM head decode figure (the workload profiled for its kernel)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the config-3 prefill GEMM sweep (the workload profiled for the MFMA counters)")
+    ap.add_argument("--batched-only", action="store_true",
+                    help="only the config-5 batched-decode figures (the workload profiled for its kernels)")
     args = ap.parse_args()
     if args.pmc_pass:
         return pmc_pass()
@@ -421,6 +423,14 @@ def main() -> int:
         import lbt_hip
 
         print(json.dumps({"gemv_shapes": gemv_shapes(lbt_hip.Ctx(0))}), flush=True)
+        return 0
+    if args.batched_only:
+        import lbt_hip
+
+        ctx = lbt_hip.Ctx(0)
+        cfg = lbt_hip.make_config()
+        model = lbt_hip.Model.synthetic(ctx, cfg, SEED)
+        print(json.dumps({"batched_decode": [batched_decode(model, cfg, b) for b in (16, 64)]}), flush=True)
         return 0
     if args.int8_head_only:
         import lbt_hip
