@@ -801,8 +801,15 @@ int ensure_sampler(lbt_model* m) {
     lbt_ctx* ctx = m->ctx;
     size_t bytes;
     sample_scratch_bytes(1, m->cfg.vocab_size, &bytes);
-    LBT_HIP(ctx, hipMalloc(&m->sscratch, bytes));
-    LBT_HIP(ctx, hipMalloc(&m->sstate, 8));
+    void *scr = nullptr, *st = nullptr;
+    hipError_t e = hipMalloc(&scr, bytes);
+    if (e == hipSuccess) e = hipMalloc(&st, 8);
+    if (e != hipSuccess) {  // all or nothing: a later call allocates afresh
+        if (scr) hipFree(scr);
+        return hip_err(ctx, e, "sampler scratch");
+    }
+    m->sscratch = scr;
+    m->sstate = (unsigned long long*)st;
     return LBT_OK;
 }
 
@@ -1467,9 +1474,18 @@ int batch_sampler(lbt_batch* b) {
     lbt_ctx* ctx = b->m->ctx;
     size_t bytes;
     sample_scratch_bytes(b->nseq, b->m->cfg.vocab_size, &bytes);
-    LBT_HIP(ctx, hipMalloc(&b->sscratch, bytes));
-    LBT_HIP(ctx, hipMalloc(&b->sst, (size_t)b->nseq * 8));
-    LBT_HIP(ctx, hipMalloc(&b->sp, (size_t)b->nseq * sizeof(lbt_sample_params)));
+    void *scr = nullptr, *st = nullptr, *sp = nullptr;
+    hipError_t e = hipMalloc(&scr, bytes);
+    if (e == hipSuccess) e = hipMalloc(&st, (size_t)b->nseq * 8);
+    if (e == hipSuccess) e = hipMalloc(&sp, (size_t)b->nseq * sizeof(lbt_sample_params));
+    if (e != hipSuccess) {  // all or nothing: a later call allocates afresh
+        if (scr) hipFree(scr);
+        if (st) hipFree(st);
+        return hip_err(ctx, e, "batch sampler scratch");
+    }
+    b->sscratch = scr;
+    b->sst = (unsigned long long*)st;
+    b->sp = (lbt_sample_params*)sp;
     return LBT_OK;
 }
 }  // namespace
