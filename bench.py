@@ -1,5 +1,5 @@
 """Benchmark: batch-1 greedy decode of a BitNet-b1.58-2B4T-shaped model on one
-MI355X (30 layers, hidden 2560, FFN 6912 ReLU^2-gated,
+MI355X (the decode benchmark: 30 layers, hidden 2560, FFN 6912 ReLU^2-gated,
 20/5 heads, head_dim 128, vocab 128256 bf16 tied head, random-init weights,
 64-token uniform-random prompt, then greedy decode).
 
@@ -44,7 +44,7 @@ def gemv_traffic() -> float | None:
 
 
 def batched_decode(model, cfg, batch: int, cap: int = 4096, steps: int = 8) -> dict:
-    """`batch` sequences, each with a `cap`-position bf16
+    """Batched decode: `batch` sequences, each with a `cap`-position bf16
     KV cache (the model's max_position_embeddings) pre-filled with synthetic
     values (approximately N(0,1)) up to cap - steps - 1, decoded together;
     greedy steps timed on the device after one untimed step.  Bytes per step:
@@ -143,7 +143,7 @@ def sched_throughput(model, cfg, slots: int = 16, requests: int = 32, prompt_len
 
 
 def prefill_gemm(ctx, reps: int = 10) -> list:
-    """the prefill GEMM (int8 MFMA) on the FFN shapes
+    """The prefill GEMM benchmark: the prefill GEMM (int8 MFMA) on the FFN shapes
     2560->6912 and 6912->2560 at M = 128, 512, 2048 tokens; seeded ternary
     weights (P = 0.3/0.4/0.3) and int8 activations resident on the device;
     HIP events around each launch (the library's profiling pass)."""
@@ -205,7 +205,7 @@ def synth_packed(rng, rows: int, cols: int) -> np.ndarray:
 
 
 def gemv_shapes(ctx, reps: int = 4) -> dict:
-    """BASELINE configs 1 and 2 on the device: each decode-layer shape at M = 1
+    """The per-shape GEMV benchmark (one shape, then every decoder-layer shape) on the device: each decode-layer shape at M = 1
     (f32 N(0,1) activation, absmax-quantized inside the op, f32 out) through
     lbt_ternary_linear_dev -- the product decode GEMV with its fused quantizer.
     "cold": enough distinct copies of the matrix (>= 288 MB) are rotated that
@@ -304,7 +304,7 @@ def _loop(fn, min_s: float = 0.3) -> float:
 def cpu_baseline(decode_s: float = 12.0, decode_s1: float = 8.0) -> dict:
     """Reference CPU path restated (VNNI/AVX-512BW/AVX2 ternary GEMV/GEMM +
     AVX-512 bf16 LM head, OpenMP over rows) timed on this host, on all cores
-    and on one: (1) BASELINE config 4, the 2B-shaped model (same shape and
+    and on one: (1) the decode benchmark, the 2B-shaped model (same shape and
     seed as the device run) prefilling the 64-token prompt and then decoding
     greedily for about `decode_s` (`decode_s1` on one core) seconds; (2) the
     config-1/2 GEMV shapes at M = 1 (kbench.rs:44-63: warm, >= 0.3 s loop),

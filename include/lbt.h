@@ -255,7 +255,7 @@ int lbt_model_set_decode(lbt_model* m, int kind);
 /* Residual stream of the last forward ([n, hidden] f32) for layer-level tests. */
 int lbt_model_read_hidden(lbt_model* m, float* out, size_t n);
 
-/* ---- batched decode ------------------------------------
+/* ---- batched decode (several sequences per step) ------------------------------------
  * No counterpart in the reference, which decodes one sequence at a time
  * (lb-server main.rs:92-100).  `nseq` independent sequences, each with its own
  * bf16 KV cache of fixed capacity `cap` positions; a step appends one token to
@@ -294,7 +294,7 @@ int lbt_batch_decode_greedy(lbt_batch* b, const uint32_t* first, size_t steps, u
  * the next prefill.  No counterpart in the reference (one cache per request). */
 int lbt_batch_reset(lbt_batch* b, int seq);
 
-/* ---- continuous batching (SURVEY next row; no counterpart in the reference,
+/* ---- continuous batching (no counterpart in the reference,
  * whose server runs one request at a time, lb-server main.rs:92-100) ---------
  * Greedy requests share one lbt_batch of `slots` sequences: a queued request
  * takes a free slot (its prompt prefilled there), every step advances all

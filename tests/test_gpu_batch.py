@@ -1,4 +1,4 @@
-"""Batched decode (BASELINE config 5 path): every sequence of a batch gets
+"""Batched decode (the B = 16 / 64 benchmark path): every sequence of a batch gets
 exactly the single-sequence results of the oracle model on its own tokens —
 greedy next token after its prompt, logits of a batched step (bit-exact) and
 the greedy continuation — for the small-M GEMV and the int8-MFMA batch

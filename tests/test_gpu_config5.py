@@ -1,4 +1,4 @@
-"""BASELINE config 5 at its real workload: the 2B-shaped model decoding B = 16
+"""Batched decode at its benchmark workload: the 2B-shaped model decoding B = 16
 and 64 sequences together, each over a 4096-position bf16 KV cache filled to
 4087 positions with the synthetic fill; sampled sequences' step logits are
 bit-exact to the single-sequence oracle holding the same cache contents."""

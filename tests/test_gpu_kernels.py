@@ -89,7 +89,7 @@ BITNET = [(2560, 2560), (640, 2560), (6912, 2560), (2560, 6912)]
 @pytest.mark.parametrize("rows,cols", BITNET)
 @pytest.mark.parametrize("m", [1, 2, 5, 8, 64])
 def test_bitnet_shapes_bitexact(ctx, rows, cols, m):
-    # BASELINE configs 1-3 shapes, benchmark distribution P(-1,0,1)=(.3,.4,.3), N(0,1) activations
+    # the benchmark GEMV/GEMM shapes (one decoder layer, the FFN prefill shapes), distribution P(-1,0,1)=(.3,.4,.3), N(0,1) activations
     announce(f"bitnet shape {rows}x{cols} m={m}")
     rng = np.random.default_rng(rows * 7 + cols + m)
     t = ternary_iid(rng, rows, cols)

@@ -201,7 +201,7 @@ def test_load_lb_convert_file(ctx, tmp_path, intermediate):
 
 
 def test_full_2b_prompt64_decode_matches_oracle(ctx):
-    """2B4T-shaped model, 64-token uniform-random prompt,
+    """The decode benchmark workload: 2B4T-shaped model, 64-token uniform-random prompt,
     128 greedy decode steps on the device (graph-replayed step): tokens
     identical to the oracle's greedy run.  A random-init model's greedy
     stream settles on a repeated token, so 64 further teacher-forced steps

@@ -1,5 +1,5 @@
 """Prefill GEMM on the int8 matrix cores (v_mfma_i32_16x16x64_i8): exact
-integers and bit-identical f32 outputs vs the oracle at BASELINE config 3
+integers and bit-identical f32 outputs vs the oracle on the prefill benchmark shapes
 (FFN shapes 2560->6912 and 6912->2560 at M = 128, 512, 2048), ragged tiles,
 the reference's prefill overflow case, and the model prefill through the
 MFMA path equal to the decode GEMV path."""
