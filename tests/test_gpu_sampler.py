@@ -45,6 +45,25 @@ def test_sample_rows_match_oracle(ctx, V, scale):
         assert np.array_equal(st, st_o), pi
 
 
+@pytest.mark.parametrize("V", [2047, 2048, 2049, 4096, 4097, 6145])
+def test_sample_chunk_and_lds_boundaries_match_oracle(ctx, V):
+    """Rows around the candidate pass's 2048-logit chunks and the 4096
+    candidates kept in LDS: flat logits (every logit a candidate), so the
+    candidate count is V itself."""
+    rng = np.random.default_rng(V + 1)
+    rows = 3
+    for t, top_p, top_k in [(1.0, 1.0, 0), (0.9, 0.95, 0), (1.2, 1.0, 4000), (0.7, 0.5, 2049)]:
+        announce(f"sample boundaries V={V} params={t},{top_p},{top_k}")
+        lg = (rng.standard_normal((rows, V)) * 0.5).astype(np.float32)
+        lg[1, ::3] = lg[1, 0]  # exact ties across chunks
+        st = rng.integers(1, 2**63, rows).astype(np.uint64)
+        st_o = st.copy()
+        got = ctx.sample(lg, t, top_p, top_k, st)
+        exp = oracle_rows(lg, t, top_p, top_k, st_o)
+        assert np.array_equal(got, exp), (V, t, top_p, top_k, got, exp)
+        assert np.array_equal(st, st_o)
+
+
 def test_sample_edge_cases_match_oracle(ctx):
     nan = np.float32("nan")
     neg_nan = np.frombuffer(np.uint32(0xFFC00000).tobytes(), np.float32)[0]
