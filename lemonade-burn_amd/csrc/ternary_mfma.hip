@@ -730,6 +730,184 @@ void tgemm2_kernel(GemvArgs a) {
     MTR(4)
 }
 
+// Prefill GEMM with one workgroup of 8 wavefronts per CU (two per SIMD, the
+// pair that keeps the matrix pipe fed): WM x WN wavefronts of (32 MS) x
+// (32 NS) each, so a tile is BM = 32 MS WM tokens x BN = 32 NS WN rows; the
+// product uses <WM, WN, MS, NS, KB> = <2, 4, 2, 2, 1>, 128 tokens x 256 rows.
+// Operands as in tgemm2_kernel (the same LDS slice layout and swizzle, the
+// weights unpacked in registers); the ring holds ST slices and slice
+// p + ST - 1 is issued once every wavefront has passed the barrier of step
+// p, so ST - 1 slices are in flight during a step.  A operands are read from
+// LDS one 32-k chunk ahead of the MFMAs.  Same accumulators, same epilogues:
+// the same bits as every other GEMM path.  Measured against the 128 x 128
+// tiles of tgemm2_kernel (two workgroups per CU), config-3 shapes: 2560 x
+// 6912 at M = 2048 46.9 -> 44.5 us (160 tiles, one round), 6912 x 2560 at
+// M = 1024 24.1 -> 23.4 us, at M = 2048 the same; slower where it leaves
+// fewer than ~150 tiles (M = 512: 15.4 -> 19.4 us and 19.1 -> 39.2 us).
+// Measured and not kept: 256 x 256 tiles (MS = 2, NS = 4: 216 tiles on
+// 6912 x 2560 at M = 2048 in one round, 44.9 us, no faster; 74-79 us on the
+// 2560-row matrix), 128 x 192 and 256 x 128, and 256-k steps (KB = 2: 2-10%
+// slower).
+constexpr int kG3MinTiles = 150;
+constexpr int kG3Stages = 3;
+
+template <int OUT, int WM, int WN, int MS, int NS, int KB>
+__global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void tgemm3_kernel(GemvArgs a) {
+    constexpr int NT = 64 * WM * WN, ST = kG3Stages;
+    static_assert(NT == 512, "two wavefronts per SIMD from one workgroup");
+    constexpr int TM = 32, BM = TM * MS * WM, BN = TM * NS * WN;
+    constexpr int RB = 128 * KB, KC = 4 * KB;
+    constexpr int kSlice = BM * RB;
+    constexpr int NA = kSlice / 16 / NT;  // A chunks per lane per step
+    static_assert(NA * 16 * NT == kSlice, "slice splits into whole 1 KB blocks per wavefront");
+    constexpr int NB = NS * KB;           // weight uint4 loads per lane per step
+    constexpr int TPB = 1024 / RB;
+    extern __shared__ __align__(16) int8_t As[];  // [ST][kSlice]
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int wm = w % WM, wn = w / WM;
+    const int l32 = lane & 31, g = lane >> 5;
+    int tx, ty;
+    g2_tile(tx, ty);
+    const int m0 = ty * BM, n0 = tx * BN;
+    const int kp = a.kp, M = a.m;
+    const int nsteps = kp / RB;
+    const int tok0 = m0 + wm * (TM * MS), row0 = n0 + wn * (TM * NS);
+    bool fast = false;
+    int mt0 = 0, ro0 = 0;
+    float swm = 1.0f;
+    Epi32Tok et{0, 1.0f};
+    if constexpr (OUT == kOutF32 || OUT == kOutF32Add || OUT == kOutI32) {
+        int mt1, ro1;
+        resolve_row<OUT>(a, row0, mt0, ro0);
+        resolve_row<OUT>(a, row0 + NS * TM - 1, mt1, ro1);
+        const int ldm = mt0 == 0 ? a.rows[0] : (mt0 == 1 ? a.rows[1] : a.rows[2]);
+        swm = mt0 == 0 ? a.sw[0] : (mt0 == 1 ? a.sw[1] : a.sw[2]);
+        fast = tok0 + MS * TM <= M && row0 + NS * TM <= a.total_rows && mt0 == mt1 && (long)M * ldm < (1L << 30);
+        if (fast) epi32_pre<OUT, MS>(a, tok0, swm, et, false);
+    }
+    const uint4* brow[NS];
+#pragma unroll
+    for (int s = 0; s < NS; s++) {
+        const int vr = row0 + s * TM + l32;
+        int mat, r;
+        resolve_row<OUT>(a, vr < a.total_rows ? vr : 0, mat, r);
+        brow[s] = (const uint4*)(sel3(a.w, mat) + (size_t)r * (size_t)(kp >> 2)) + g;
+    }
+    const int8_t* asrc[NA];
+    int adst[NA];
+#pragma unroll
+    for (int j = 0; j < NA; j++) {
+        const int blk = w * NA + j;
+        const int T = blk * TPB + lane / (RB / 16), cs = lane % (RB / 16);
+        const int c = cs ^ g2_swz<KB>(T);
+        const int tok = m0 + T < M ? m0 + T : M - 1;  // past M: any valid row, never stored
+        asrc[j] = a.q + (size_t)tok * kp + c * 16;
+        adst[j] = blk * 1024;
+    }
+    auto a_issue = [&](int p, int stage) {
+        int8_t* dst = As + stage * kSlice;
+#pragma unroll
+        for (int j = 0; j < NA; j++)
+            __builtin_amdgcn_global_load_lds((const void*)(asrc[j] + p * RB), (lds_void_t*)(dst + adst[j]), 16, 0, 0);
+    };
+    // untracked weight loads (inline asm), covered by the explicit waits
+    u32x4 bw[ST][NB];
+    auto b_issue = [&](int p, u32x4 (&dst)[NB]) {
+#pragma unroll
+        for (int s = 0; s < NS; s++)
+#pragma unroll
+            for (int b = 0; b < KB; b++)
+                asm volatile("global_load_dwordx4 %0, %1, off"
+                             : "=v"(dst[s * KB + b])
+                             : "v"(brow[s] + 2 * (KB * p + b))
+                             : "memory");
+    };
+    auto pin = [](u32x4& v) { asm volatile("" : "+v"(v)); };
+    auto wait_vm = [](auto n_c) {
+        constexpr int n = decltype(n_c)::value;
+        __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (0 << 8));
+    };
+    v16i acc[MS][NS];
+#pragma unroll
+    for (int ms = 0; ms < MS; ms++)
+#pragma unroll
+        for (int s = 0; s < NS; s++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[ms][s][r] = 0;
+    const int arow = (wm * (TM * MS) + l32) * RB;
+    int axo[KC];
+#pragma unroll
+    for (int kc = 0; kc < KC; kc++) axo[kc] = ((2 * kc + g) ^ g2_swz<KB>(l32)) << 4;
+
+    const int plast = nsteps - 1;
+#pragma unroll
+    for (int p = 0; p < ST - 1; p++) {
+        const int pi = p < plast ? p : plast;
+        a_issue(pi, p);
+        b_issue(pi, bw[p]);
+    }
+    if constexpr (OUT == kOutF32 || OUT == kOutF32Add || OUT == kOutI32)
+        if (fast) epi32_pre<OUT, MS>(a, tok0, swm, et, true);
+
+    // Step p: slice p and weights p landed (own loads), barrier (every
+    // wavefront's chunks of slice p; every wavefront done with slice p - 1),
+    // slice and weights p + ST - 1 into the slots of p - 1, then the MFMAs of
+    // slice p with each chunk's A operands read one chunk ahead.
+    auto step = [&](int p, auto slot_c) {
+        constexpr int slot = decltype(slot_c)::value;
+        constexpr int nslot = (slot + ST - 1) % ST;
+        wait_vm(std::integral_constant<int, (ST - 2) * (NA + NB)>{});
+#pragma unroll
+        for (int i = 0; i < NB; i++) pin(bw[slot][i]);
+        __builtin_amdgcn_s_barrier();
+        const int pn = p + ST - 1 < plast ? p + ST - 1 : plast;
+        a_issue(pn, nslot);
+        const int8_t* Ab = As + slot * kSlice + arow;
+        v4i aop[2][MS];
+#pragma unroll
+        for (int ms = 0; ms < MS; ms++) aop[0][ms] = *(const v4i*)(Ab + axo[0] + ms * TM * RB);
+#pragma unroll
+        for (int kc = 0; kc < KC; kc++) {
+            if (kc + 1 < KC) {
+#pragma unroll
+                for (int ms = 0; ms < MS; ms++)
+                    aop[(kc + 1) & 1][ms] = *(const v4i*)(Ab + axo[kc + 1] + ms * TM * RB);
+            }
+            const int sh = 2 * (kc & 3), b = kc >> 2;
+#pragma unroll
+            for (int s = 0; s < NS; s++) {
+                const u32x4 v = bw[slot][s * KB + b];
+                const v4i bop = v4i{(int)((v.x >> sh) & 0x03030303u), (int)((v.y >> sh) & 0x03030303u),
+                                    (int)((v.z >> sh) & 0x03030303u), (int)((v.w >> sh) & 0x03030303u)};
+#pragma unroll
+                for (int ms = 0; ms < MS; ms++)
+                    acc[ms][s] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop[kc & 1][ms], bop, acc[ms][s], 0, 0, 0);
+            }
+        }
+        b_issue(pn, bw[nslot]);
+    };
+    for (int p = 0; p < nsteps; p += ST)
+        seq_while(std::make_integer_sequence<int, ST>{}, [&](auto ic) {
+            constexpr int i = decltype(ic)::value;
+            if (p + i >= nsteps) return false;
+            step(p + i, std::integral_constant<int, i>{});
+            return true;
+        });
+    __builtin_amdgcn_s_waitcnt(0);
+#pragma unroll
+    for (int k = 0; k < ST; k++)
+#pragma unroll
+        for (int i = 0; i < NB; i++) asm volatile("" ::"v"(bw[k][i]));
+    if constexpr (OUT == kOutF32 || OUT == kOutF32Add || OUT == kOutI32) {
+        if (fast) {
+            epi32_full<OUT, MS, NS>(a, acc, tok0, mt0, ro0, et);
+            return;
+        }
+    }
+    mfma_epilogue<OUT, TM>(a, acc, tok0, row0);
+}
+
 namespace {
 
 template <int MS, int NS, int KB, int ST = kG2Stages>
@@ -755,6 +933,31 @@ hipError_t launch_tiles2(const GemvArgs& a, int out_mode, dim3 grid, hipStream_t
     return hipGetLastError();
 }
 
+
+template <int WM, int WN, int MS, int NS, int KB>
+hipError_t launch_tiles3(const GemvArgs& a, int out_mode, dim3 grid, hipStream_t s, hipEvent_t e0, hipEvent_t e1) {
+    constexpr int NT = 64 * WM * WN;
+    constexpr size_t lds = (size_t)kG3Stages * (32 * MS * WM) * (128 * KB);
+    static bool attr = false;
+    if (!attr) {
+        const void* fns[] = {(const void*)tgemm3_kernel<kOutI32, WM, WN, MS, NS, KB>,
+                             (const void*)tgemm3_kernel<kOutF32, WM, WN, MS, NS, KB>,
+                             (const void*)tgemm3_kernel<kOutF32Add, WM, WN, MS, NS, KB>,
+                             (const void*)tgemm3_kernel<kOutRelu2, WM, WN, MS, NS, KB>,
+                             (const void*)tgemm3_kernel<kOutQKV, WM, WN, MS, NS, KB>};
+        for (const void* f : fns) (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        (void)hipGetLastError();
+        attr = true;
+    }
+    switch (out_mode) {
+        case kOutI32: hipExtLaunchKernelGGL((tgemm3_kernel<kOutI32, WM, WN, MS, NS, KB>), grid, dim3(NT), lds, s, e0, e1, 0, a); break;
+        case kOutF32: hipExtLaunchKernelGGL((tgemm3_kernel<kOutF32, WM, WN, MS, NS, KB>), grid, dim3(NT), lds, s, e0, e1, 0, a); break;
+        case kOutF32Add: hipExtLaunchKernelGGL((tgemm3_kernel<kOutF32Add, WM, WN, MS, NS, KB>), grid, dim3(NT), lds, s, e0, e1, 0, a); break;
+        case kOutRelu2: hipExtLaunchKernelGGL((tgemm3_kernel<kOutRelu2, WM, WN, MS, NS, KB>), grid, dim3(NT), lds, s, e0, e1, 0, a); break;
+        default: hipExtLaunchKernelGGL((tgemm3_kernel<kOutQKV, WM, WN, MS, NS, KB>), grid, dim3(NT), lds, s, e0, e1, 0, a); break;
+    }
+    return hipGetLastError();
+}
 
 template <int MS, int NS, bool PF>
 hipError_t launch_small_pf(const GemvArgs& a, int out_mode, dim3 grid, hipStream_t s, hipEvent_t e0, hipEvent_t e1) {
@@ -831,14 +1034,18 @@ int launch_ternary_mfma(lbt_ctx* ctx, const TernaryOp& op_in) {
     prof_pair(ctx, &e0, &e1);
     hipError_t e;
     // path (LBT_GEMM_MODE forces one, for tests and measurements): 6 = the
-    // few-token kernel, 4 / 5 = 64 / 128 tiles of the pipelined GEMM; by
-    // default the few-token kernel up to tune.small_max tokens, then 128
-    // tiles when there are >= 200 of them, else 64
+    // few-token kernel, 4 / 5 = 64 / 128 tiles of the pipelined GEMM, 7 =
+    // the 128 x 256 tiles of one 8-wavefront workgroup per CU; by default
+    // the few-token kernel up to tune.small_max tokens, then 128 x 256 tiles
+    // when there are >= kG3MinTiles of them, else 128 x 128 tiles when there
+    // are >= 200, else 64 x 64
     const LbtTuning& tu = ctx->tune;
     const int gmode = tu.gemm_mode;
     const long t128 = (long)((total + 127) / 128) * ((op.m + 127) / 128);
     const dim3 g128((unsigned)((total + 127) / 128), (unsigned)((op.m + 127) / 128));
     const dim3 g64((unsigned)((total + 63) / 64), (unsigned)((op.m + 63) / 64));
+    const dim3 g3((unsigned)((total + 255) / 256), (unsigned)((op.m + 127) / 128));
+    const long t3 = (long)g3.x * g3.y;
     const bool small_ok = a.kp <= 256 * 4 * kSmallMaxSteps;
     // up to 64 tokens the few-token kernel also serves the shapes the 64 x 64
     // tiling would give fewer than tune.small_tiles tiles (q/k/v, o, down of
@@ -871,6 +1078,8 @@ int launch_ternary_mfma(lbt_ctx* ctx, const TernaryOp& op_in) {
                 : ms == 2 ? launch_small<2, 1>(a, op.out_mode, pf, g, ctx->stream, e0, e1)
                 : ms == 3 ? launch_small<3, 1>(a, op.out_mode, pf, g, ctx->stream, e0, e1)
                           : launch_small<4, 1>(a, op.out_mode, pf, g, ctx->stream, e0, e1);
+    } else if (gmode == 7 || (gmode == 0 && t3 >= kG3MinTiles)) {
+        e = launch_tiles3<2, 4, 2, 2, 1>(a, op.out_mode, g3, ctx->stream, e0, e1);
     } else if (gmode != 4 && (t128 >= 200 || gmode == 5)) {
         e = launch_tiles2<2, 2, 1>(a, op.out_mode, g128, ctx->stream, e0, e1);
     } else {

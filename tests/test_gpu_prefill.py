@@ -47,6 +47,23 @@ def test_ragged_tiles(ctx, rows, cols, m):
     w.free()
 
 
+@pytest.mark.parametrize("rows,cols,m", [(23, 384, 17), (300, 512, 257), (257, 768, 1000), (1000, 2560, 129),
+                                         (600, 1280, 300)])
+def test_ragged_tiles_8wave_kernel(ctx_with, rows, cols, m):
+    # the 128 x 256 tiles forced at sizes that leave partial token and row
+    # tiles (and a partial wavefront block inside a tile)
+    ctx = ctx_with(LBT_GEMM_MODE="7")
+    announce(f"prefill 8-wave ragged {rows}x{cols} m={m}")
+    t, scale, x = golden_case(rows, cols, m, rows + cols + m)
+    p = orc.pack(t)
+    q, sa, su = orc.quantize_acts(x)
+    w = ctx.upload(p, rows, cols, float(scale))
+    assert np.array_equal(ctx.gemm_i32(w, q, su), q[:, :cols].astype(np.int64) @ t.T.astype(np.int64))
+    (y,) = ctx.ternary_linear([w], x)
+    assert np.array_equal(y, orc.gemm_f32(p, rows, cols, scale, q, sa, su))
+    w.free()
+
+
 @pytest.mark.parametrize("rows,cols", [(6912, 2560), (2560, 6912), (640, 2560), (13824, 2560)])
 @pytest.mark.parametrize("m", [2, 7, 16, 17, 32, 48, 64])
 def test_few_token_gemm_bitexact(ctx, rows, cols, m):
@@ -136,11 +153,11 @@ def test_model_prefill_mfma_matches_oracle_and_gemv(ctx, ctx_with, n):
     om.free()
 
 
-@pytest.mark.parametrize("mode", ["4", "5", "6"])
+@pytest.mark.parametrize("mode", ["4", "5", "6", "7"])
 def test_model_prefill_every_gemm_tiling_matches_oracle(ctx_with, mode):
     # every epilogue (q/k/v + RoPE + KV append, residual add, relu^2*up) through
     # each MFMA tiling: 64x64 and 128x128 tiles of the 32x32x32 GEMM, the
-    # few-token kernel
+    # few-token kernel, the 128x256 tiles of the 8-wavefront kernel
     cfg = dict(hidden=512, intermediate=1536, heads=4, kv_heads=1, layers=2, vocab=1000, max_pos=1024)
     n = 200
     ctx = ctx_with(LBT_GEMM_MODE=mode)
