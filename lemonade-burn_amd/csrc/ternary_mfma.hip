@@ -234,27 +234,33 @@ __device__ __forceinline__ void mfma_epilogue(const GemvArgs& a, AccT (&acc)[MS]
 // division per lane, instead of one per lane and D-tile element); the
 // epilogue fetches them across lanes.  Loaded ahead of the main loop
 // (divide = false), divided once the first slices' loads are out.
+// A block of 32 MS tokens: lane j holds tokens tok0 + j + 64 i, i < (MS + 1) / 2.
+template <int MS>
 struct Epi32Tok {
-    int qs;
-    float inv;
+    static constexpr int N = (MS + 1) / 2;
+    int qs[N];
+    float inv[N];
 };
 
 template <int OUT, int MS>
-__device__ __forceinline__ void epi32_pre(const GemvArgs& a, int tok0, float swm, Epi32Tok& t, bool divide) {
-    static_assert(MS <= 2, "one token per lane");
+__device__ __forceinline__ void epi32_pre(const GemvArgs& a, int tok0, float swm, Epi32Tok<MS>& t, bool divide) {
     const int lane = (int)threadIdx.x & 63;
-    const int tok = tok0 + (lane < 32 * MS ? lane : 0);
-    if (!divide) {
-        t.qs = gload(a.qsum + tok);
-        t.inv = a.qscale ? gload(a.qscale + tok) : 1.0f;  // s_a until divided
-    } else {
-        t.inv = OUT == kOutI32 ? 0.0f : 1.0f / (t.inv * swm);
+#pragma unroll
+    for (int i = 0; i < Epi32Tok<MS>::N; i++) {
+        const int j = 64 * i + lane;
+        const int tok = tok0 + (j < 32 * MS ? j : 0);
+        if (!divide) {
+            t.qs[i] = gload(a.qsum + tok);
+            t.inv[i] = a.qscale ? gload(a.qscale + tok) : 1.0f;  // s_a until divided
+        } else {
+            t.inv[i] = OUT == kOutI32 ? 0.0f : 1.0f / (t.inv[i] * swm);
+        }
     }
 }
 
 template <int OUT, int MS, int NS>
 __device__ __forceinline__ void epi32_full(const GemvArgs& a, v16i (&acc)[MS][NS], int tok0, int mt_v, int ro0_v,
-                                           const Epi32Tok& t) {
+                                           const Epi32Tok<MS>& t) {
     using L = DLayout<32>;
     constexpr int R = L::R;
     const int lane = (int)threadIdx.x & 63, lr = L::row(lane);
@@ -267,18 +273,17 @@ __device__ __forceinline__ void epi32_full(const GemvArgs& a, v16i (&acc)[MS][NS
     // a 32-bit byte offset per lane (the caller checks M * ld < 2^30)
     const __amdgpu_buffer_rsrc_t ob = buf_rsrc(outv, 0xffffffffu);
     (void)swm;
-    int qs[MS][R];
-    float inv[MS][R];
-#pragma unroll
-    for (int ms = 0; ms < MS; ms++)
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-            const int src = ms * 32 + L::tok(lane, r);
-            qs[ms][r] = __shfl(t.qs, src, 64);
-            inv[ms][r] = __shfl(t.inv, src, 64);
-        }
 #pragma unroll
     for (int ms = 0; ms < MS; ms++) {
+        // this block's tokens 32 ms .. 32 ms + 31 sit in slot ms / 2 of lanes 32 (ms & 1) + ..
+        int qs[R];
+        float inv[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const int src = (ms & 1) * 32 + L::tok(lane, r);
+            qs[r] = __shfl(t.qs[ms >> 1], src, 64);
+            inv[r] = __shfl(t.inv[ms >> 1], src, 64);
+        }
         float old[NS][R];
         if (OUT == kOutF32Add) {
 #pragma unroll
@@ -296,11 +301,11 @@ __device__ __forceinline__ void epi32_full(const GemvArgs& a, v16i (&acc)[MS][NS
             for (int r = 0; r < R; r++) {
                 const int tok = tok0 + ms * 32 + L::tok(lane, r);
                 const uint32_t off = (uint32_t)(tok * ld + ro0 + s * 32 + lr) * 4u;
-                const int d = acc[ms][s][r] - qs[ms][r];
+                const int d = acc[ms][s][r] - qs[r];
                 if (OUT == kOutI32) {
                     __builtin_amdgcn_raw_buffer_store_b32((uint32_t)d, ob, off, 0, 0);
                 } else {
-                    const float y = (float)d * inv[ms][r];
+                    const float y = (float)d * inv[r];
                     const float v = OUT == kOutF32Add ? old[s][r] + y : y;
                     // nontemporal: the output streams past L2
                     __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), ob, off, 0, 2);
@@ -548,7 +553,7 @@ void tgemm2_kernel(GemvArgs a) {
     bool fast = false;
     int mt0 = 0, ro0 = 0;
     float swm = 1.0f;
-    Epi32Tok et{0, 1.0f};
+    Epi32Tok<MS> et{};
     if constexpr (OUT == kOutF32 || OUT == kOutF32Add || OUT == kOutI32) {
         int mt1, ro1;
         resolve_row<OUT>(a, row0, mt0, ro0);
@@ -732,8 +737,12 @@ void tgemm2_kernel(GemvArgs a) {
 
 // Prefill GEMM with one workgroup of 8 wavefronts per CU (two per SIMD, the
 // pair that keeps the matrix pipe fed): WM x WN wavefronts of (32 MS) x
-// (32 NS) each, so a tile is BM = 32 MS WM tokens x BN = 32 NS WN rows; the
-// product uses <WM, WN, MS, NS, KB> = <2, 4, 2, 2, 1>, 128 tokens x 256 rows.
+// (32 NS) each, so a tile is BM = 32 MS WM tokens x BN = 32 NS WN rows.  The
+// product uses <WM, WN, MS, NS, KB> = <1, 8, 4, 1, 1>: 128 tokens x 256 rows,
+// every wavefront all 128 tokens of 32 rows of its own, so each weight row
+// is unpacked by one wavefront only (the unpacking -- a shift and a mask
+// per dword and 32-k chunk -- is most of the main loop's VALU work; with
+// 2 x 4 wavefronts of 64 x 64 every row was unpacked twice).
 // Operands as in tgemm2_kernel (the same LDS slice layout and swizzle, the
 // weights unpacked in registers); the ring holds ST slices and slice
 // p + ST - 1 is issued once every wavefront has passed the barrier of step
@@ -741,20 +750,23 @@ void tgemm2_kernel(GemvArgs a) {
 // LDS one 32-k chunk ahead of the MFMAs.  Same accumulators, same epilogues:
 // the same bits as every other GEMM path.  Measured against the 128 x 128
 // tiles of tgemm2_kernel (two workgroups per CU), config-3 shapes: 2560 x
-// 6912 at M = 2048 46.9 -> 44.5 us (160 tiles, one round), 6912 x 2560 at
-// M = 1024 24.1 -> 23.4 us, at M = 2048 the same; slower where it leaves
-// fewer than ~150 tiles (M = 512: 15.4 -> 19.4 us and 19.1 -> 39.2 us).
-// Measured and not kept: 256 x 256 tiles (MS = 2, NS = 4: 216 tiles on
-// 6912 x 2560 at M = 2048 in one round, 44.9 us, no faster; 74-79 us on the
-// 2560-row matrix), 128 x 192 and 256 x 128, and 256-k steps (KB = 2: 2-10%
-// slower).
+// 6912 at M = 2048 44.6 -> 42.5 us (160 tiles, one round), 6912 x 2560 at
+// M = 1024 23.1 -> 22.0 us and at M = 2048 44.9 -> 43.1 us; slower where
+// it leaves fewer than ~150 tiles (M = 512: 15.4 -> 19.4 us and 19.1 ->
+// 39.2 us in the 2 x 4 form).  Measured and not kept: 2 x 4 wavefronts of
+// 64 x 64 (3-5% slower), with the next slice's A operands read a whole
+// step ahead as in tgemm2_kernel (2 x 4: 1-4% faster than per chunk; 1 x 8:
+// 3-5% slower), ring depths of 4 and 6 slices (no faster), 256 x 256 tiles
+// (216 tiles on 6912 x 2560 at M = 2048 in one round: 44.9 us; 74-79 us on
+// the 2560-row matrix), 128 x 192 and 256 x 128 tiles, and 256-k steps
+// (KB = 2: 2-10% slower).
 constexpr int kG3MinTiles = 150;
 constexpr int kG3Stages = 3;
 
-template <int OUT, int WM, int WN, int MS, int NS, int KB>
+template <int OUT, int WM, int WN, int MS, int NS, int KB, int ST>
 __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void tgemm3_kernel(GemvArgs a) {
-    constexpr int NT = 64 * WM * WN, ST = kG3Stages;
+    constexpr int NT = 64 * WM * WN;
     static_assert(NT == 512, "two wavefronts per SIMD from one workgroup");
     constexpr int TM = 32, BM = TM * MS * WM, BN = TM * NS * WN;
     constexpr int RB = 128 * KB, KC = 4 * KB;
@@ -776,7 +788,7 @@ void tgemm3_kernel(GemvArgs a) {
     bool fast = false;
     int mt0 = 0, ro0 = 0;
     float swm = 1.0f;
-    Epi32Tok et{0, 1.0f};
+    Epi32Tok<MS> et{};
     if constexpr (OUT == kOutF32 || OUT == kOutF32Add || OUT == kOutI32) {
         int mt1, ro1;
         resolve_row<OUT>(a, row0, mt0, ro0);
@@ -840,7 +852,7 @@ void tgemm3_kernel(GemvArgs a) {
 #pragma unroll
     for (int kc = 0; kc < KC; kc++) axo[kc] = ((2 * kc + g) ^ g2_swz<KB>(l32)) << 4;
 
-    const int plast = nsteps - 1;
+const int plast = nsteps - 1;
 #pragma unroll
     for (int p = 0; p < ST - 1; p++) {
         const int pi = p < plast ? p : plast;
@@ -894,6 +906,7 @@ void tgemm3_kernel(GemvArgs a) {
             step(p + i, std::integral_constant<int, i>{});
             return true;
         });
+
     __builtin_amdgcn_s_waitcnt(0);
 #pragma unroll
     for (int k = 0; k < ST; k++)
@@ -905,7 +918,18 @@ void tgemm3_kernel(GemvArgs a) {
             return;
         }
     }
-    mfma_epilogue<OUT, TM>(a, acc, tok0, row0);
+    // the general epilogue in blocks of at most two token tiles (its
+    // per-token tables for four would not fit beside the accumulators)
+    constexpr int EH = MS > 2 ? 2 : MS;
+#pragma unroll
+    for (int h = 0; h < MS; h += EH) {
+        v16i part[EH][NS];
+#pragma unroll
+        for (int i = 0; i < EH; i++)
+#pragma unroll
+            for (int s = 0; s < NS; s++) part[i][s] = acc[h + i][s];
+        mfma_epilogue<OUT, TM>(a, part, tok0 + h * TM, row0);
+    }
 }
 
 namespace {
@@ -934,27 +958,27 @@ hipError_t launch_tiles2(const GemvArgs& a, int out_mode, dim3 grid, hipStream_t
 }
 
 
-template <int WM, int WN, int MS, int NS, int KB>
+template <int WM, int WN, int MS, int NS, int KB, int ST>
 hipError_t launch_tiles3(const GemvArgs& a, int out_mode, dim3 grid, hipStream_t s, hipEvent_t e0, hipEvent_t e1) {
     constexpr int NT = 64 * WM * WN;
-    constexpr size_t lds = (size_t)kG3Stages * (32 * MS * WM) * (128 * KB);
+    constexpr size_t lds = (size_t)ST * (32 * MS * WM) * (128 * KB);
     static bool attr = false;
     if (!attr) {
-        const void* fns[] = {(const void*)tgemm3_kernel<kOutI32, WM, WN, MS, NS, KB>,
-                             (const void*)tgemm3_kernel<kOutF32, WM, WN, MS, NS, KB>,
-                             (const void*)tgemm3_kernel<kOutF32Add, WM, WN, MS, NS, KB>,
-                             (const void*)tgemm3_kernel<kOutRelu2, WM, WN, MS, NS, KB>,
-                             (const void*)tgemm3_kernel<kOutQKV, WM, WN, MS, NS, KB>};
+        const void* fns[] = {(const void*)tgemm3_kernel<kOutI32, WM, WN, MS, NS, KB, ST>,
+                             (const void*)tgemm3_kernel<kOutF32, WM, WN, MS, NS, KB, ST>,
+                             (const void*)tgemm3_kernel<kOutF32Add, WM, WN, MS, NS, KB, ST>,
+                             (const void*)tgemm3_kernel<kOutRelu2, WM, WN, MS, NS, KB, ST>,
+                             (const void*)tgemm3_kernel<kOutQKV, WM, WN, MS, NS, KB, ST>};
         for (const void* f : fns) (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         (void)hipGetLastError();
         attr = true;
     }
     switch (out_mode) {
-        case kOutI32: hipExtLaunchKernelGGL((tgemm3_kernel<kOutI32, WM, WN, MS, NS, KB>), grid, dim3(NT), lds, s, e0, e1, 0, a); break;
-        case kOutF32: hipExtLaunchKernelGGL((tgemm3_kernel<kOutF32, WM, WN, MS, NS, KB>), grid, dim3(NT), lds, s, e0, e1, 0, a); break;
-        case kOutF32Add: hipExtLaunchKernelGGL((tgemm3_kernel<kOutF32Add, WM, WN, MS, NS, KB>), grid, dim3(NT), lds, s, e0, e1, 0, a); break;
-        case kOutRelu2: hipExtLaunchKernelGGL((tgemm3_kernel<kOutRelu2, WM, WN, MS, NS, KB>), grid, dim3(NT), lds, s, e0, e1, 0, a); break;
-        default: hipExtLaunchKernelGGL((tgemm3_kernel<kOutQKV, WM, WN, MS, NS, KB>), grid, dim3(NT), lds, s, e0, e1, 0, a); break;
+        case kOutI32: hipExtLaunchKernelGGL((tgemm3_kernel<kOutI32, WM, WN, MS, NS, KB, ST>), grid, dim3(NT), lds, s, e0, e1, 0, a); break;
+        case kOutF32: hipExtLaunchKernelGGL((tgemm3_kernel<kOutF32, WM, WN, MS, NS, KB, ST>), grid, dim3(NT), lds, s, e0, e1, 0, a); break;
+        case kOutF32Add: hipExtLaunchKernelGGL((tgemm3_kernel<kOutF32Add, WM, WN, MS, NS, KB, ST>), grid, dim3(NT), lds, s, e0, e1, 0, a); break;
+        case kOutRelu2: hipExtLaunchKernelGGL((tgemm3_kernel<kOutRelu2, WM, WN, MS, NS, KB, ST>), grid, dim3(NT), lds, s, e0, e1, 0, a); break;
+        default: hipExtLaunchKernelGGL((tgemm3_kernel<kOutQKV, WM, WN, MS, NS, KB, ST>), grid, dim3(NT), lds, s, e0, e1, 0, a); break;
     }
     return hipGetLastError();
 }
@@ -1079,7 +1103,7 @@ int launch_ternary_mfma(lbt_ctx* ctx, const TernaryOp& op_in) {
                 : ms == 3 ? launch_small<3, 1>(a, op.out_mode, pf, g, ctx->stream, e0, e1)
                           : launch_small<4, 1>(a, op.out_mode, pf, g, ctx->stream, e0, e1);
     } else if (gmode == 7 || (gmode == 0 && t3 >= kG3MinTiles)) {
-        e = launch_tiles3<2, 4, 2, 2, 1>(a, op.out_mode, g3, ctx->stream, e0, e1);
+        e = launch_tiles3<1, 8, 4, 1, 1, kG3Stages>(a, op.out_mode, g3, ctx->stream, e0, e1);
     } else if (gmode != 4 && (t128 >= 200 || gmode == 5)) {
         e = launch_tiles2<2, 2, 1>(a, op.out_mode, g128, ctx->stream, e0, e1);
     } else {
