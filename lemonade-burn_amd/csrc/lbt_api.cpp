@@ -22,7 +22,7 @@ LbtTuning read_tuning() {
     t.mfma_min = (int)num("LBT_MFMA_MIN", kMfmaMinTokens);
     if (t.mfma_min < 2) t.mfma_min = 2;
     t.gemm_mode = (int)num("LBT_GEMM_MODE", 0);
-    if (t.gemm_mode < 4 || t.gemm_mode > 7) t.gemm_mode = 0;
+    if (t.gemm_mode < 4 || t.gemm_mode > 8) t.gemm_mode = 0;
     t.small_max = (int)num("LBT_GEMM_SMALL_MAX", kSmallMaxTokens);
     t.small_tiles = num("LBT_GEMM_SMALL_TILES", 100);
     t.small_ms = (int)num("LBT_GEMM_SMALL_MS", 1);

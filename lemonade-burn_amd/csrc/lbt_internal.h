@@ -16,7 +16,7 @@ struct LbtTuning {
     bool no_graph = false;    // LBT_NO_GRAPH: decode steps as separate launches, no captured graph
     bool no_mfma = false;     // LBT_NO_MFMA: several-token products on the VALU GEMV
     int mfma_min = 2;         // LBT_MFMA_MIN: fewest tokens for the MFMA GEMMs
-    int gemm_mode = 0;        // LBT_GEMM_MODE: 0 auto, 4 / 5 = 64 / 128 tiles, 6 = few-token kernel, 7 = 128 x 256 tiles
+    int gemm_mode = 0;        // LBT_GEMM_MODE: 0 auto, 4 / 5 = 64 / 128 tiles, 6 = few-token kernel, 7 / 8 = 128 x 256 / 64 x 320 tiles
     int small_max = 32;       // LBT_GEMM_SMALL_MAX: the few-token kernel serves up to this many tokens
     long small_tiles = 100;   // LBT_GEMM_SMALL_TILES: ... and up to 64 tokens below this many 64x64 tiles
     int small_ms = 1;         // LBT_GEMM_SMALL_MS: cap of its token tiles (16 * ms)

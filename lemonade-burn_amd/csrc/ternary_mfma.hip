@@ -735,14 +735,20 @@ void tgemm2_kernel(GemvArgs a) {
     MTR(4)
 }
 
-// Prefill GEMM with one workgroup of 8 wavefronts per CU (two per SIMD, the
-// pair that keeps the matrix pipe fed): WM x WN wavefronts of (32 MS) x
-// (32 NS) each, so a tile is BM = 32 MS WM tokens x BN = 32 NS WN rows.  The
-// product uses <WM, WN, MS, NS, KB> = <1, 8, 4, 1, 1>: 128 tokens x 256 rows,
-// every wavefront all 128 tokens of 32 rows of its own, so each weight row
-// is unpacked by one wavefront only (the unpacking -- a shift and a mask
-// per dword and 32-k chunk -- is most of the main loop's VALU work; with
-// 2 x 4 wavefronts of 64 x 64 every row was unpacked twice).
+// Prefill GEMM with one workgroup per CU of 8 or more wavefronts (at least
+// two per SIMD, what keeps the matrix pipe fed): WM x WN wavefronts of
+// (32 MS) x (32 NS) each, so a tile is BM = 32 MS WM tokens x BN = 32 NS WN
+// rows.  The product uses <WM, WN, MS, NS, KB> = <1, 8, 4, 1, 1>: 128 tokens
+// x 256 rows, every wavefront all 128 tokens of 32 rows of its own, so each
+// weight row is unpacked by one wavefront only (the unpacking -- a shift and
+// a mask per dword and 32-k chunk -- is most of the main loop's VALU work;
+// with 2 x 4 wavefronts of 64 x 64 every row was unpacked twice); and
+// <1, 10, 2, 1, 1>: 64 tokens x 320 rows from 10 wavefronts (at most three
+// per SIMD, 2 MFMA tiles each: 6 per SIMD and step against 8), for the
+// matrices whose 128 x 256 tiles leave CUs idle -- 2560 rows at M = 2048
+// give 256 tiles of 64 x 320 (44.0 -> 36.8 us, 39% of the int8 peak)
+// against 160 of 128 x 256.  Workgroups of more than 8 wavefronts load each
+// activation slice from the first LW of them only.
 // Operands as in tgemm2_kernel (the same LDS slice layout and swizzle, the
 // weights unpacked in registers); the ring holds ST slices and slice
 // p + ST - 1 is issued once every wavefront has passed the barrier of step
@@ -763,21 +769,35 @@ void tgemm2_kernel(GemvArgs a) {
 constexpr int kG3MinTiles = 150;
 constexpr int kG3Stages = 3;
 
+// waves_per_eu bound of a workgroup of NW wavefronts, one workgroup per CU
+template <int NW>
+constexpr int g3_wpe = (NW + 3) / 4 < 2 ? 2 : (NW + 3) / 4;
+// wavefronts that load the activation slices: the largest count <= NW that
+// divides the slice's 1 KB blocks
+template <int NW, int NBLK>
+constexpr int g3_loaders() {
+    int l = NW < NBLK ? NW : NBLK;
+    while (NBLK % l) l--;
+    return l;
+}
+
 template <int OUT, int WM, int WN, int MS, int NS, int KB, int ST>
-__global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(g3_wpe<WM * WN>, g3_wpe<WM * WN>)))
 void tgemm3_kernel(GemvArgs a) {
     constexpr int NT = 64 * WM * WN;
-    static_assert(NT == 512, "two wavefronts per SIMD from one workgroup");
+    static_assert(NT >= 512, "at least two wavefronts per SIMD from one workgroup");
     constexpr int TM = 32, BM = TM * MS * WM, BN = TM * NS * WN;
     constexpr int RB = 128 * KB, KC = 4 * KB;
     constexpr int kSlice = BM * RB;
-    constexpr int NA = kSlice / 16 / NT;  // A chunks per lane per step
-    static_assert(NA * 16 * NT == kSlice, "slice splits into whole 1 KB blocks per wavefront");
+    constexpr int LW = g3_loaders<WM * WN, kSlice / 1024>();  // loading wavefronts
+    constexpr int NA = kSlice / 1024 / LW;  // A chunks per lane per step (loading wavefronts)
+    static_assert(NA * 1024 * LW == kSlice, "slice splits into whole 1 KB blocks per loading wavefront");
     constexpr int NB = NS * KB;           // weight uint4 loads per lane per step
     constexpr int TPB = 1024 / RB;
     extern __shared__ __align__(16) int8_t As[];  // [ST][kSlice]
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const int wm = w % WM, wn = w / WM;
+    const bool loader = __builtin_amdgcn_readfirstlane(w) < LW;
     const int l32 = lane & 31, g = lane >> 5;
     int tx, ty;
     g2_tile(tx, ty);
@@ -810,7 +830,7 @@ void tgemm3_kernel(GemvArgs a) {
     int adst[NA];
 #pragma unroll
     for (int j = 0; j < NA; j++) {
-        const int blk = w * NA + j;
+        const int blk = (loader ? w : 0) * NA + j;
         const int T = blk * TPB + lane / (RB / 16), cs = lane % (RB / 16);
         const int c = cs ^ g2_swz<KB>(T);
         const int tok = m0 + T < M ? m0 + T : M - 1;  // past M: any valid row, never stored
@@ -818,6 +838,7 @@ void tgemm3_kernel(GemvArgs a) {
         adst[j] = blk * 1024;
     }
     auto a_issue = [&](int p, int stage) {
+        if (!loader) return;
         int8_t* dst = As + stage * kSlice;
 #pragma unroll
         for (int j = 0; j < NA; j++)
@@ -869,7 +890,10 @@ const int plast = nsteps - 1;
     auto step = [&](int p, auto slot_c) {
         constexpr int slot = decltype(slot_c)::value;
         constexpr int nslot = (slot + ST - 1) % ST;
-        wait_vm(std::integral_constant<int, (ST - 2) * (NA + NB)>{});
+        if (loader)
+            wait_vm(std::integral_constant<int, (ST - 2) * (NA + NB)>{});
+        else
+            wait_vm(std::integral_constant<int, (ST - 2) * NB>{});
 #pragma unroll
         for (int i = 0; i < NB; i++) pin(bw[slot][i]);
         __builtin_amdgcn_s_barrier();
@@ -1058,18 +1082,25 @@ int launch_ternary_mfma(lbt_ctx* ctx, const TernaryOp& op_in) {
     prof_pair(ctx, &e0, &e1);
     hipError_t e;
     // path (LBT_GEMM_MODE forces one, for tests and measurements): 6 = the
-    // few-token kernel, 4 / 5 = 64 / 128 tiles of the pipelined GEMM, 7 =
-    // the 128 x 256 tiles of one 8-wavefront workgroup per CU; by default
-    // the few-token kernel up to tune.small_max tokens, then 128 x 256 tiles
-    // when there are >= kG3MinTiles of them, else 128 x 128 tiles when there
-    // are >= 200, else 64 x 64
+    // few-token kernel, 4 / 5 = 64 / 128 tiles of the pipelined GEMM, 7 / 8 =
+    // the 128 x 256 / 64 x 320 tiles of one workgroup per CU; by default the
+    // few-token kernel up to tune.small_max tokens, then the one-workgroup-
+    // per-CU tiles as picked below, else 128 x 128 tiles when there are
+    // >= 200, else 64 x 64
     const LbtTuning& tu = ctx->tune;
     const int gmode = tu.gemm_mode;
     const long t128 = (long)((total + 127) / 128) * ((op.m + 127) / 128);
     const dim3 g128((unsigned)((total + 127) / 128), (unsigned)((op.m + 127) / 128));
     const dim3 g64((unsigned)((total + 63) / 64), (unsigned)((op.m + 63) / 64));
+    // the 8-wavefront kernel: 128 x 256 tiles (two wavefronts of 4 MFMA
+    // tiles per SIMD) or 64 x 320 tiles from 10 wavefronts (at most three of
+    // 2 tiles per SIMD), whichever needs fewer rounds x MFMA tiles per SIMD
+    // over the 256 CUs; only where the chosen one has >= kG3MinTiles tiles
     const dim3 g3((unsigned)((total + 255) / 256), (unsigned)((op.m + 127) / 128));
-    const long t3 = (long)g3.x * g3.y;
+    const dim3 g3n((unsigned)((total + 319) / 320), (unsigned)((op.m + 63) / 64));
+    const long t3 = (long)g3.x * g3.y, t3n = (long)g3n.x * g3n.y;
+    const long c3 = (t3 + 255) / 256 * 8, c3n = (t3n + 255) / 256 * 6;
+    const int g3pick = c3n < c3 ? (t3n >= kG3MinTiles ? 2 : 0) : (t3 >= kG3MinTiles ? 1 : 0);
     const bool small_ok = a.kp <= 256 * 4 * kSmallMaxSteps;
     // up to 64 tokens the few-token kernel also serves the shapes the 64 x 64
     // tiling would give fewer than tune.small_tiles tiles (q/k/v, o, down of
@@ -1102,8 +1133,11 @@ int launch_ternary_mfma(lbt_ctx* ctx, const TernaryOp& op_in) {
                 : ms == 2 ? launch_small<2, 1>(a, op.out_mode, pf, g, ctx->stream, e0, e1)
                 : ms == 3 ? launch_small<3, 1>(a, op.out_mode, pf, g, ctx->stream, e0, e1)
                           : launch_small<4, 1>(a, op.out_mode, pf, g, ctx->stream, e0, e1);
-    } else if (gmode == 7 || (gmode == 0 && t3 >= kG3MinTiles)) {
-        e = launch_tiles3<1, 8, 4, 1, 1, kG3Stages>(a, op.out_mode, g3, ctx->stream, e0, e1);
+    } else if (gmode == 7 || gmode == 8 || (gmode == 0 && g3pick != 0)) {
+        if (gmode == 8 || (gmode == 0 && g3pick == 2))
+            e = launch_tiles3<1, 10, 2, 1, 1, kG3Stages>(a, op.out_mode, g3n, ctx->stream, e0, e1);
+        else
+            e = launch_tiles3<1, 8, 4, 1, 1, kG3Stages>(a, op.out_mode, g3, ctx->stream, e0, e1);
     } else if (gmode != 4 && (t128 >= 200 || gmode == 5)) {
         e = launch_tiles2<2, 2, 1>(a, op.out_mode, g128, ctx->stream, e0, e1);
     } else {

@@ -49,11 +49,13 @@ def test_ragged_tiles(ctx, rows, cols, m):
 
 @pytest.mark.parametrize("rows,cols,m", [(23, 384, 17), (300, 512, 257), (257, 768, 1000), (1000, 2560, 129),
                                          (600, 1280, 300)])
-def test_ragged_tiles_8wave_kernel(ctx_with, rows, cols, m):
-    # the 128 x 256 tiles forced at sizes that leave partial token and row
-    # tiles (and a partial wavefront block inside a tile)
-    ctx = ctx_with(LBT_GEMM_MODE="7")
-    announce(f"prefill 8-wave ragged {rows}x{cols} m={m}")
+@pytest.mark.parametrize("mode", ["7", "8"])
+def test_ragged_tiles_one_workgroup_per_cu(ctx_with, rows, cols, m, mode):
+    # the 128 x 256 (8 wavefronts) and 64 x 320 (10 wavefronts) tiles forced
+    # at sizes that leave partial token and row tiles (and a partial
+    # wavefront block inside a tile)
+    ctx = ctx_with(LBT_GEMM_MODE=mode)
+    announce(f"prefill one-wg-per-cu mode {mode} ragged {rows}x{cols} m={m}")
     t, scale, x = golden_case(rows, cols, m, rows + cols + m)
     p = orc.pack(t)
     q, sa, su = orc.quantize_acts(x)
@@ -153,11 +155,12 @@ def test_model_prefill_mfma_matches_oracle_and_gemv(ctx, ctx_with, n):
     om.free()
 
 
-@pytest.mark.parametrize("mode", ["4", "5", "6", "7"])
+@pytest.mark.parametrize("mode", ["4", "5", "6", "7", "8"])
 def test_model_prefill_every_gemm_tiling_matches_oracle(ctx_with, mode):
     # every epilogue (q/k/v + RoPE + KV append, residual add, relu^2*up) through
     # each MFMA tiling: 64x64 and 128x128 tiles of the 32x32x32 GEMM, the
-    # few-token kernel, the 128x256 tiles of the 8-wavefront kernel
+    # few-token kernel, the 128x256 and 64x320 tiles of the one-workgroup-per-CU
+    # kernel
     cfg = dict(hidden=512, intermediate=1536, heads=4, kv_heads=1, layers=2, vocab=1000, max_pos=1024)
     n = 200
     ctx = ctx_with(LBT_GEMM_MODE=mode)
