@@ -1099,8 +1099,14 @@ int launch_ternary_mfma(lbt_ctx* ctx, const TernaryOp& op_in) {
     const dim3 g3((unsigned)((total + 255) / 256), (unsigned)((op.m + 127) / 128));
     const dim3 g3n((unsigned)((total + 319) / 320), (unsigned)((op.m + 63) / 64));
     const long t3 = (long)g3.x * g3.y, t3n = (long)g3n.x * g3n.y;
+    // MFMA tiles per SIMD on the busiest CU: 8 per round of 128 x 256, 6 per
+    // round of 64 x 320, 4 per 128 x 128 tile of tgemm2_kernel (one wavefront
+    // of 2 x 2 per SIMD, two workgroups per CU), 1 per 64 x 64 tile; ties go
+    // to the one-workgroup-per-CU kernel
     const long c3 = (t3 + 255) / 256 * 8, c3n = (t3n + 255) / 256 * 6;
-    const int g3pick = c3n < c3 ? (t3n >= kG3MinTiles ? 2 : 0) : (t3 >= kG3MinTiles ? 1 : 0);
+    const long c2 = t128 >= 200 ? (t128 + 255) / 256 * 4 : ((long)g64.x * g64.y + 255) / 256;
+    int g3pick = c3n < c3 ? (t3n >= kG3MinTiles ? 2 : 0) : (t3 >= kG3MinTiles ? 1 : 0);
+    if (g3pick != 0 && (g3pick == 2 ? c3n : c3) > c2) g3pick = 0;
     const bool small_ok = a.kp <= 256 * 4 * kSmallMaxSteps;
     // up to 64 tokens the few-token kernel also serves the shapes the 64 x 64
     // tiling would give fewer than tune.small_tiles tiles (q/k/v, o, down of
