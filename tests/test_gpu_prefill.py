@@ -174,3 +174,24 @@ def test_model_prefill_every_gemm_tiling_matches_oracle(ctx_with, mode):
     c.free()
     m.free()
     om.free()
+
+
+@pytest.mark.parametrize("n", [1024, 2048])
+def test_2b_width_long_prefill_tilings_agree(ctx, ctx_with, n):
+    # a 2B-width prefill of n tokens takes the one-workgroup-per-CU tilings
+    # for q/k/v, o, gate/up and down (every fused epilogue at full width);
+    # its logits and KV cache equal the 128 x 128 tiling's bit for bit (that
+    # path is checked against the oracle above)
+    cfg = lbt_hip.make_config(layers=2, vocab=1000, max_pos=4096)
+    announce(f"2B-width prefill n={n}: default tilings vs LBT_GEMM_MODE=5")
+    toks = np.random.default_rng(n + 1).integers(0, 1000, n).astype(np.uint32)
+    outs = []
+    for c in (ctx, ctx_with(LBT_GEMM_MODE="5")):
+        m = lbt_hip.Model.synthetic(c, cfg, 13)
+        cache = m.new_cache()
+        logits = m.forward(toks, cache, all_logits=True)
+        outs.append((logits, cache.read(1, False), cache.read(1, True)))
+        cache.free()
+        m.free()
+    for a, b in zip(outs[0], outs[1]):
+        assert np.array_equal(a, b)
