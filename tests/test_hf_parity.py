@@ -1,0 +1,53 @@
+"""Model semantics (RMSNorm and sub-norm placement, RoPE convention and theta,
+GQA head mapping, attention scaling and causal mask, relu^2 gating, tied bf16
+head) pinned against an independent implementation: HF transformers' BitNet
+(5.15.0) with its online-quantized linear, on a tiny random model
+(tests/golden/make_hf_fixture.py writes the logits; the weights are
+regenerated here from its seed).
+
+Tolerance: HF runs in float64 with K and V rounded to bf16 as the device cache
+stores them; the oracle computes K and V in f32 first, so an occasional bf16
+rounding lands on the other side, which moves the logits (range about
+[-3.4, 3.4]) by up to 0.02 (an f64 restatement with the same rounding differs
+from HF by the same 0.019; without the bf16 rounding on either side the two
+agree to 1.3e-5).  The bound 0.05 sits between that and what a plausible
+mistake does to the same comparison (measured on the f64 restatement):
+theta 10000 instead of 500000 0.10, interleaved instead of rotate-half RoPE
+0.15, q-head h on KV head h % kv_heads 0.26, no 1/sqrt(hd) 1.04, relu without
+the square 1.09, gate and up swapped 2.7, no causal mask 3.7, no attention
+sub-norm 4.2."""
+import numpy as np
+
+import hf_tiny
+import lbt_oracle as orc
+
+
+def _oracle():
+    logits, prompt, seed = hf_tiny.load_fixture()
+    packed, ws, norms, final, emb16, _ = hf_tiny.weights(orc, seed)
+    om = orc.OracleModel.wrap(hf_tiny.oracle_config(orc), packed, ws, norms, final, emb16)
+    return om, logits, prompt
+
+
+def _check(got, exp):
+    assert np.abs(got - exp).max() <= hf_tiny.TOL
+    top2 = np.sort(exp, axis=1)[:, -2:]
+    clear = (top2[:, 1] - top2[:, 0]) > 2 * hf_tiny.TOL
+    assert (got.argmax(1) == exp.argmax(1))[clear].all()
+
+
+def test_oracle_prefill_matches_hf_bitnet():
+    om, exp, prompt = _oracle()
+    got = om.forward(np.array(prompt, np.uint32), all_logits=True)
+    _check(got, exp)
+    om.free()
+
+
+def test_oracle_decode_matches_hf_bitnet():
+    # 10-token prefill, then one token at a time through the KV cache
+    om, exp, prompt = _oracle()
+    rows = [om.forward(np.array(prompt[:10], np.uint32), all_logits=True)]
+    for t in prompt[10:]:
+        rows.append(om.forward(np.array([t], np.uint32)))
+    _check(np.concatenate(rows), exp)
+    om.free()
