@@ -25,11 +25,19 @@ from pathlib import Path
 
 import numpy as np
 
-CFG = dict(vocab=300, hidden=256, intermediate=512, heads=4, kv_heads=2, layers=2, max_pos=256, eps=1e-5,
+CFG = dict(vocab=300, hidden=256, intermediate=512, heads=4, kv_heads=2, layers=2, max_pos=2048, eps=1e-5,
            theta=500000.0)
 SEED = 20260
 PROMPT = [3, 77, 150, 299, 1, 42, 42, 208, 9, 120, 64, 255, 17, 5, 180, 91]
+# a long prompt (uniform ids from this seed): RoPE at large positions and
+# attention over more than 1024 keys; only the rows LONG_ROWS are stored
+LONG_LEN, LONG_SEED = 1100, 11
+LONG_ROWS = list(range(8)) + list(range(1020, 1030)) + list(range(1090, 1100))
 OUT = Path(__file__).with_name("hf_bitnet_tiny.npz")
+
+
+def long_prompt() -> list:
+    return [int(t) for t in np.random.default_rng(LONG_SEED).integers(0, CFG["vocab"], LONG_LEN)]
 
 
 def tiny_weights(seed: int = SEED):
@@ -58,7 +66,7 @@ def tiny_weights(seed: int = SEED):
     return layers, final, emb
 
 
-def hf_logits() -> np.ndarray:
+def hf_logits(prompt=PROMPT) -> np.ndarray:
     import torch
     import transformers.models.bitnet.modeling_bitnet as mb
     from transformers import BitNetConfig, BitNetForCausalLM
@@ -110,7 +118,7 @@ def hf_logits() -> np.ndarray:
         model.model.norm.weight.copy_(torch.from_numpy(final.astype(np.float64)))
         model.model.embed_tokens.weight.copy_(torch.from_numpy(emb.astype(np.float64)))
         assert model.lm_head.weight.data_ptr() == model.model.embed_tokens.weight.data_ptr(), "tied head"
-        ids = torch.tensor([PROMPT], dtype=torch.long)
+        ids = torch.tensor([prompt], dtype=torch.long)
         out = model(input_ids=ids, use_cache=False)
     mb.apply_rotary_pos_emb = rope
     return out.logits[0].numpy()
@@ -118,5 +126,7 @@ def hf_logits() -> np.ndarray:
 
 if __name__ == "__main__":
     lg = hf_logits()
-    np.savez_compressed(OUT, logits=lg.astype(np.float64), prompt=np.array(PROMPT, np.int64), seed=np.int64(SEED))
-    print(f"wrote {OUT}: logits {lg.shape}, max |logit| {np.abs(lg).max():.3f}")
+    ll = hf_logits(long_prompt())[LONG_ROWS]
+    np.savez_compressed(OUT, logits=lg.astype(np.float64), prompt=np.array(PROMPT, np.int64), seed=np.int64(SEED),
+                        long_logits=ll.astype(np.float32), long_rows=np.array(LONG_ROWS, np.int64))
+    print(f"wrote {OUT}: logits {lg.shape}, long-prompt rows {ll.shape}, max |logit| {np.abs(lg).max():.3f}")

@@ -14,11 +14,18 @@ import make_hf_fixture as mk  # noqa: E402
 
 FIXTURE = Path(__file__).with_name("golden") / "hf_bitnet_tiny.npz"
 TOL = 0.05  # max |logit - HF|; see test_hf_parity.py
+TOL_LONG = 0.1  # the same for the rows of the 1100-token prompt
 
 
 def load_fixture():
     fx = np.load(FIXTURE)
     return fx["logits"], [int(t) for t in fx["prompt"]], int(fx["seed"])
+
+
+def load_long():
+    """(HF logits of the stored rows, their row indices, the 1100-token prompt)."""
+    fx = np.load(FIXTURE)
+    return fx["long_logits"].astype(np.float64), [int(r) for r in fx["long_rows"]], mk.long_prompt()
 
 
 def weights(orc, seed):
