@@ -70,6 +70,17 @@ def batched_decode(model, cfg, batch: int, cap: int = 4096, steps: int = 8) -> d
 MFMA_INT8_PEAK_TOPS = 5000.0
 
 
+def batched_mfma_head(model, cfg) -> list:
+    """The batched-decode figures with head kind 2 (the bf16 head of the
+    batch's rows on the matrix cores, logits within tolerance of the exact
+    head); reported beside `batched_decode`, never as it."""
+    model.set_head(2)
+    try:
+        return [batched_decode(model, cfg, b) for b in (16, 64)]
+    finally:
+        model.set_head(0)
+
+
 def int8_head_decode(model, ctx, prompt, steps: int = 128) -> dict:
     """Decode tok/s with the opt-in int8 LM head (q8head.rs), the same loop as
     `value`; its logits are not the exact bf16 head's, so it is reported
@@ -430,7 +441,8 @@ def main() -> int:
         ctx = lbt_hip.Ctx(0)
         cfg = lbt_hip.make_config()
         model = lbt_hip.Model.synthetic(ctx, cfg, SEED)
-        print(json.dumps({"batched_decode": [batched_decode(model, cfg, b) for b in (16, 64)]}), flush=True)
+        print(json.dumps({"batched_decode": [batched_decode(model, cfg, b) for b in (16, 64)],
+                          "batched_decode_mfma_head": batched_mfma_head(model, cfg)}), flush=True)
         return 0
     if args.int8_head_only:
         import lbt_hip
@@ -532,6 +544,7 @@ def main() -> int:
         line["sampled_decode"] = sampled_decode(model, prompt)
     if not args.no_batched:
         line["batched_decode"] = [batched_decode(model, cfg, bsz) for bsz in (16, 64)]
+        line["batched_decode_mfma_head"] = batched_mfma_head(model, cfg)
         line["continuous_batching"] = sched_throughput(model, cfg)
         line["prefill_gemm"] = prefill_gemm(ctx)
     if not args.no_shapes:

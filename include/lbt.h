@@ -242,7 +242,12 @@ int lbt_model_decode_sample(lbt_model* m, lbt_cache* c, uint32_t first, size_t s
                             uint64_t* state, uint32_t* out_tokens, float* ms_decode);
 /* LM head of the model's forwards: 0 = the exact tied bf16 head (default),
  * 1 = the opt-in int8 head (q8head.rs), quantized on the device from the
- * tied embedding when first selected.  A cached decode-step graph is rebuilt. */
+ * tied embedding when first selected, 2 = the tied bf16 head with heads of
+ * 33..64 rows (batched steps, prefill logits) on the bf16 matrix cores
+ * (activations as bf16 hi + lo parts, f32 accumulation: logits within
+ * tolerance of kind 0; other heads exact).  A cached decode-step graph is
+ * rebuilt.  No counterpart in the reference for kind 2: it serves batched
+ * decode, which the reference does not have. */
 int lbt_model_set_head(lbt_model* m, int kind);
 /* How batch-1 decode steps (generate_greedy / decode_greedy) run; no
  * reference counterpart (the reference's step is BitNet::forward on one token,

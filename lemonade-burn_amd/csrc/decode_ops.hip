@@ -941,6 +941,205 @@ int launch_head(lbt_ctx* ctx, const void* w, const float* rscale, int rows, int 
 }
 }  // namespace
 
+// ---------------------------------------------------------------------------
+// The tied bf16 head of several rows on the bf16 matrix cores (head kind 2):
+// each normalized row x is split into bf16 parts hi = bf16(x) and
+// lo = bf16(x - hi) (x - hi is exact in f32; x - hi - lo is below 2^-17 |x|),
+// and logits = W.hi + W.lo accumulate in f32 in v_mfma_f32_32x32x16_bf16
+// (the bf16 x bf16 products are exact in f32).  The sum order is the matrix
+// core's, so these logits match the exact head within tolerance, not bit for
+// bit; a one-row head never takes this path.
+
+// xh / xl [mp][cols] (rows past m zero)
+__global__ __launch_bounds__(kThreads) void bf16_split_kernel(const float* xn, int m, int cols, uint16_t* xh,
+                                                              uint16_t* xl) {
+    const int t = blockIdx.x;
+    for (int i = threadIdx.x; i < cols; i += kThreads) {
+        const float x = t < m ? xn[(size_t)t * cols + i] : 0.0f;
+        const uint16_t h = f32_to_bf16(x);
+        xh[(size_t)t * cols + i] = h;
+        xl[(size_t)t * cols + i] = f32_to_bf16(x - bf16_to_f32(h));
+    }
+}
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// Workgroup of 4 wavefronts: TT token tiles of 32 x 4 / TT groups of NV
+// vocab tiles of 32 rows; a wavefront takes one token tile and NV vocab tiles
+// (each activation load feeds NV MFMA pairs).  k is visited in blocks of 64:
+// lane l (half h = l >> 5) holds, for the four 16-k steps s of block b, the
+// 8 k values 64 b + 32 h + 8 s .. + 7 of its token (A) and vocab row (B) --
+// the same k in both operands, so the products are those of the dot -- which
+// makes each lane's loads of a block 64 contiguous bytes per row.  D: vocab
+// row l & 31 of the tile, tokens 8 (r >> 2) + 4 (l >> 5) + (r & 3).  The
+// first-max keys of a token meet in LDS: one atomic per token and workgroup.
+template <int TT, int NV>
+__global__ __launch_bounds__(kThreads) void lmhead_mfma_kernel(const uint16_t* W, int rows, int cols,
+                                                               const uint16_t* xh, const uint16_t* xl, int m,
+                                                               float* logits, unsigned long long* key) {
+    constexpr int VG = 4 / TT;
+    __shared__ unsigned long long kb[4][64];
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int tt = w % TT, vg = w / TT;
+    const int row0 = (blockIdx.x * VG + vg) * 32 * NV;
+    const bool live = row0 < rows;  // wavefront-uniform
+    const int l32 = lane & 31, h = lane >> 5;
+    if (lane < 32) {
+        kb[w][lane] = 0ull;
+        kb[w][lane + 32] = 0ull;
+    }
+    f32x16 acc[NV];
+#pragma unroll
+    for (int v = 0; v < NV; v++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[v][r] = 0.0f;
+    if (live) {
+        const uint4* wp[NV];
+#pragma unroll
+        for (int v = 0; v < NV; v++) {
+            const int r = row0 + 32 * v + l32;
+            wp[v] = (const uint4*)(W + (size_t)(r < rows ? r : rows - 1) * cols + 32 * h);
+        }
+        const int tok = tt * 32 + l32;
+        const uint4* hp = (const uint4*)(xh + (size_t)tok * cols + 32 * h);
+        const uint4* lp = (const uint4*)(xl + (size_t)tok * cols + 32 * h);
+        const int nb = cols / 64;
+        // untracked loads (inline asm) with explicit waits: the compiler's
+        // own tracking of these loop-carried buffers waits for every load in
+        // flight, which left no block of loads ahead of the MFMAs
+        constexpr int NL = 4 * NV + 8;  // 16-byte loads per lane and block
+        u32x4 bw[2][NV][4], ah[2][4], al[2][4];
+        auto gl = [](u32x4& d, const uint4* p) {
+            asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(d) : "v"(p) : "memory");
+        };
+        auto load = [&](int b, u32x4 (&bb)[NV][4], u32x4 (&hh)[4], u32x4 (&ll)[4]) {
+            const int bc = b < nb ? b : nb - 1;  // past the end: the last block again (same count)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+#pragma unroll
+                for (int v = 0; v < NV; v++) gl(bb[v][i], wp[v] + 8 * bc + i);
+                gl(hh[i], hp + 8 * bc + i);
+                gl(ll[i], lp + 8 * bc + i);
+            }
+        };
+        auto land = [&](u32x4 (&bb)[NV][4], u32x4 (&hh)[4], u32x4 (&ll)[4]) {
+            __builtin_amdgcn_s_waitcnt((NL & 15) | ((NL >> 4) << 14) | (7 << 4) | (15 << 8));
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+#pragma unroll
+                for (int v = 0; v < NV; v++) asm volatile("" : "+v"(bb[v][i]));
+                asm volatile("" : "+v"(hh[i]));
+                asm volatile("" : "+v"(ll[i]));
+            }
+        };
+        auto mfma = [&](const u32x4 (&bb)[NV][4], const u32x4 (&hh)[4], const u32x4 (&ll)[4]) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const bf16x8 a0 = __builtin_bit_cast(bf16x8, hh[i]), a1 = __builtin_bit_cast(bf16x8, ll[i]);
+#pragma unroll
+                for (int v = 0; v < NV; v++) {
+                    const bf16x8 bv = __builtin_bit_cast(bf16x8, bb[v][i]);
+                    acc[v] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, bv, acc[v], 0, 0, 0);
+                    acc[v] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, bv, acc[v], 0, 0, 0);
+                }
+            }
+        };
+        load(0, bw[0], ah[0], al[0]);
+        for (int b = 0; b < nb; b += 2) {
+            load(b + 1, bw[1], ah[1], al[1]);
+            land(bw[0], ah[0], al[0]);
+            mfma(bw[0], ah[0], al[0]);
+            load(b + 2, bw[0], ah[0], al[0]);
+            land(bw[1], ah[1], al[1]);
+            if (b + 1 < nb) mfma(bw[1], ah[1], al[1]);
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+#pragma unroll
+        for (int k = 0; k < 2; k++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+#pragma unroll
+                for (int v = 0; v < NV; v++) asm volatile("" ::"v"(bw[k][v][i]));
+                asm volatile("" ::"v"(ah[k][i]));
+                asm volatile("" ::"v"(al[k][i]));
+            }
+        // this wavefront's best key per token of its tile (lanes of one half
+        // share a token per r), then its logits
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int tl = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            unsigned long long k = 0ull;
+#pragma unroll
+            for (int v = 0; v < NV; v++) {
+                const int row = row0 + 32 * v + l32;
+                if (row < rows) {
+                    const unsigned long long kv = argmax_key(acc[v][r], (uint32_t)row);
+                    k = kv > k ? kv : k;
+                }
+            }
+#pragma unroll
+            for (int msk = 16; msk >= 1; msk >>= 1) {
+                const unsigned long long o = __shfl_xor(k, msk, 64);
+                k = o > k ? o : k;
+            }
+            if (l32 == 0) kb[w][tl] = k;
+        }
+        if (logits) {
+#pragma unroll
+            for (int v = 0; v < NV; v++) {
+                const int row = row0 + 32 * v + l32;
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int t = tt * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                    if (row < rows && t < m) logits[(size_t)t * rows + row] = acc[v][r];
+                }
+            }
+        }
+    }
+    __syncthreads();
+    // token t = 32 tt' + tl: the best of the wavefronts of token tile tt'
+    const int t = (int)threadIdx.x;
+    if (key && t < m && t < 32 * TT) {
+        const int ttt = t / 32, tl = t % 32;
+        unsigned long long b = 0ull;
+#pragma unroll
+        for (int j = 0; j < VG; j++) {
+            const unsigned long long kv = kb[j * TT + ttt][tl];
+            b = kv > b ? kv : b;
+        }
+        if (b) atomicMax(&key[t], b);
+    }
+}
+
+constexpr int kHeadMfmaNV = 2;
+
+int launch_bf16_mfma_head(lbt_ctx* ctx, const uint16_t* w, int rows, int cols, const float* x, int m,
+                          const float* norm_w, float eps, float* logits, unsigned long long* key, float* xn,
+                          uint16_t* xs, size_t xs_bytes) {
+    if (m < 2 || m > 64 || !xn || cols % 64 || cols > 16 * kThreads)
+        return set_err(ctx, LBT_E_INVALID, "bf16 matrix-core head: 2..64 rows, cols a multiple of 64");
+    const int tt = m <= 32 ? 1 : 2, mp = 32 * tt;
+    if ((size_t)2 * mp * cols * 2 > xs_bytes) return set_err(ctx, LBT_E_INVALID, "bf16 matrix-core head: scratch");
+    uint16_t* xh = xs;
+    uint16_t* xl = xs + (size_t)mp * cols;
+    hipEvent_t e0, e1;
+    prof_pair(ctx, &e0, &e1);
+    hipLaunchKernelGGL(row_norm_kernel, dim3(m), dim3(kThreads), 0, ctx->stream, x, cols, norm_w, eps, xn);
+    hipLaunchKernelGGL(bf16_split_kernel, dim3(mp), dim3(kThreads), 0, ctx->stream, xn, m, cols, xh, xl);
+    const int rows_per_wg = 32 * kHeadMfmaNV * (4 / tt);
+    const dim3 grid((unsigned)((rows + rows_per_wg - 1) / rows_per_wg));
+    if (tt == 1)
+        hipExtLaunchKernelGGL((lmhead_mfma_kernel<1, kHeadMfmaNV>), grid, dim3(kThreads), 0, ctx->stream, e0, e1, 0, w,
+                              rows, cols, xh, xl, m, logits, key);
+    else
+        hipExtLaunchKernelGGL((lmhead_mfma_kernel<2, kHeadMfmaNV>), grid, dim3(kThreads), 0, ctx->stream, e0, e1, 0, w,
+                              rows, cols, xh, xl, m, logits, key);
+    LBT_HIP(ctx, hipGetLastError());
+    prof_commit(ctx, e0, e1, kProfHead, (double)rows * cols * 2.0);
+    return LBT_OK;
+}
+
 int launch_bf16_linear(lbt_ctx* ctx, const uint16_t* w, int rows, int cols, const float* x, int m,
                        const float* norm_w, float eps, float* logits, unsigned long long* key, float* xn) {
     return launch_head(ctx, w, nullptr, rows, cols, x, m, norm_w, eps, logits, key, xn);

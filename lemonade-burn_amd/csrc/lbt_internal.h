@@ -171,6 +171,14 @@ int launch_quantize(lbt_ctx* ctx, const float* x, const float* norm_w, float eps
 // If key != nullptr, the first-max key of row t is atomically maxed into key[t].
 int launch_bf16_linear(lbt_ctx* ctx, const uint16_t* w, int rows, int cols, const float* x, int m,
                        const float* norm_w, float eps, float* logits, unsigned long long* key, float* xn = nullptr);
+// The same head for 2..64 rows on the bf16 matrix cores (head kind 2 uses it
+// for 33..64 rows):
+// xn = rmsnorm(x) split into bf16 hi + lo parts in xs (2 * 32 * ceil(m/32)
+// * cols bf16), f32 accumulation in the matrix core's order (logits within
+// tolerance of launch_bf16_linear's, the same first-max key contract).
+int launch_bf16_mfma_head(lbt_ctx* ctx, const uint16_t* w, int rows, int cols, const float* x, int m,
+                          const float* norm_w, float eps, float* logits, unsigned long long* key, float* xn,
+                          uint16_t* xs, size_t xs_bytes);
 // The opt-in int8 head (q8head.rs): logits[t*rows + r] = scale[r] *
 // sum_k xn[t,k] * q[r,k]; same norm, key and xn contract as above.
 int launch_q8_linear(lbt_ctx* ctx, const int8_t* q, const float* scale, int rows, int cols, const float* x, int m,

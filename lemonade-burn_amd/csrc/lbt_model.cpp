@@ -229,6 +229,8 @@ struct lbt_model {
     int head_kind = 0;
     int8_t* q8 = nullptr;
     float* q8s = nullptr;
+    uint16_t* hx = nullptr;  // head kind 2: bf16 hi / lo parts of up to 64 normalized rows
+    size_t hx_bytes = 0;
     float* cos_t = nullptr;
     float* sin_t = nullptr;
     float scaling = 0.0f;
@@ -279,6 +281,11 @@ int model_head(lbt_model* m, const float* x, int rows, float eps, float* logits,
     if (m->head_kind == 1)
         return launch_q8_linear(m->ctx, m->q8, m->q8s, c.vocab_size, c.hidden_size, x, rows, m->final_norm, eps,
                                 logits, key, xn);
+    // kind 2 from 33 rows (two token tiles per workgroup): below that the
+    // f32 head is faster (B = 16: 267 us against 380)
+    if (m->head_kind == 2 && rows > 32 && rows <= 64 && xn)
+        return launch_bf16_mfma_head(m->ctx, m->embed, c.vocab_size, c.hidden_size, x, rows, m->final_norm, eps,
+                                     logits, key, xn, m->hx, m->hx_bytes);
     return launch_bf16_linear(m->ctx, m->embed, c.vocab_size, c.hidden_size, x, rows, m->final_norm, eps, logits,
                               key, xn);
 }
@@ -1106,7 +1113,7 @@ void lbt_model_free(lbt_model* m) {
     if (m->sscratch) hipFree(m->sscratch);
     void* bufs[] = {m->wbuf, m->fbuf, m->embed, m->cos_t, m->sin_t, m->x,   m->q,       m->k,
                     m->v,    m->att,  m->h,     m->logits, m->toks, m->key, m->tok_out, m->state,
-                    m->ao,   m->aml,  m->q8,    m->q8s};
+                    m->ao,   m->aml,  m->q8,    m->q8s,     m->hx};
     for (void* b : bufs)
         if (b) hipFree(b);
     delete m;
@@ -1330,8 +1337,18 @@ int lbt_model_decode_sample(lbt_model* m, lbt_cache* c, uint32_t first, size_t s
 int lbt_model_set_head(lbt_model* m, int kind) {
     if (!m) return LBT_E_INVALID;
     lbt_ctx* ctx = m->ctx;
-    if (kind != 0 && kind != 1) return set_err(ctx, LBT_E_INVALID, "set_head: kind must be 0 (bf16) or 1 (int8)");
+    if (kind < 0 || kind > 2)
+        return set_err(ctx, LBT_E_INVALID, "set_head: kind must be 0 (bf16), 1 (int8) or 2 (bf16 matrix cores)");
     const lbt_config& c = m->cfg;
+    if (kind == 2 && !m->hx) {
+        if (c.hidden_size % 64) return set_err(ctx, LBT_E_INVALID, "set_head: kind 2 needs hidden_size % 64 == 0");
+        const size_t bytes = (size_t)2 * 64 * c.hidden_size * 2;
+        void* p = nullptr;
+        hipError_t e = hipMalloc(&p, bytes);
+        if (e != hipSuccess) return hip_err(ctx, e, "bf16 matrix-core head scratch");
+        m->hx = (uint16_t*)p;
+        m->hx_bytes = bytes;
+    }
     if (kind == 1 && !m->q8) {
         const size_t n = (size_t)c.vocab_size * c.hidden_size;
         int8_t* q = nullptr;

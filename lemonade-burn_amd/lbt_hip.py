@@ -390,7 +390,8 @@ class Model:
         self.ctx.check(self.ctx.lib.lbt_model_set_decode(self.h, kind))
 
     def set_head(self, kind: int):
-        """0 = the exact tied bf16 head, 1 = the opt-in int8 head (q8head.rs)."""
+        """0 = the exact tied bf16 head, 1 = the opt-in int8 head (q8head.rs), 2 = the
+        bf16 head on the matrix cores for heads of 33..64 rows (within tolerance)."""
         self.ctx.check(self.ctx.lib.lbt_model_set_head(self.h, kind))
 
     def forward(self, tokens, cache: "Cache", all_logits: bool = False) -> np.ndarray:
