@@ -573,12 +573,14 @@ __device__ __forceinline__ void attn_row_issue(const AttnRow& a, const float* no
     }
 }
 
+// attn_row_finish in two steps around its barrier: attn_row_tab builds the
+// per-(head, split) factors in LDS, attn_row_combine (after a barrier) forms
+// the row.  Threads past NT take no part in either (a caller may skip them
+// for whole wavefronts).
 template <int EPT, int NSB, int NT = kThreads>
-__device__ __forceinline__ void attn_row_finish(const AttnRow& a, AttnRegs<EPT, NSB, NT>& ar, RowRegs<EPT>& r,
-                                                AttnTab& tab) {
+__device__ __forceinline__ void attn_row_tab(const AttnRow& a, AttnRegs<EPT, NSB, NT>& ar, AttnTab& tab) {
     const int tid = (int)threadIdx.x;
     const bool act = tid < NT;
-    const int hs = __builtin_ctz((unsigned)a.hd);  // head_dim is a power of two
     LBT_CTR(6)
     // (head, split) pairs sit in 16 consecutive lanes per head: M, the split
     // factors f_s and L come from lane butterflies, no LDS round trip
@@ -601,8 +603,14 @@ __device__ __forceinline__ void attn_row_finish(const AttnRow& a, AttnRegs<EPT, 
         }
     }
     LBT_CTR(9)
-    __syncthreads();
-    LBT_CTR(10)
+}
+
+template <int EPT, int NSB, int NT = kThreads>
+__device__ __forceinline__ void attn_row_combine(const AttnRow& a, AttnRegs<EPT, NSB, NT>& ar, RowRegs<EPT>& r,
+                                                 const AttnTab& tab) {
+    const int tid = (int)threadIdx.x;
+    const bool act = tid < NT;
+    const int hs = __builtin_ctz((unsigned)a.hd);  // head_dim is a power of two
     float O[EPT];
 #pragma unroll
     for (int e = 0; e < EPT; e++) O[e] = 0.0f;
@@ -645,6 +653,15 @@ __device__ __forceinline__ void attn_row_finish(const AttnRow& a, AttnRegs<EPT, 
 #pragma unroll
         for (int k = 0; k < 4; k++) r.v[4 * g + k] = O[4 * g + k] * rl;
     }
+}
+
+template <int EPT, int NSB, int NT = kThreads>
+__device__ __forceinline__ void attn_row_finish(const AttnRow& a, AttnRegs<EPT, NSB, NT>& ar, RowRegs<EPT>& r,
+                                                AttnTab& tab) {
+    attn_row_tab<EPT, NSB, NT>(a, ar, tab);
+    __syncthreads();
+    LBT_CTR(10)
+    attn_row_combine<EPT, NSB, NT>(a, ar, r, tab);
 }
 
 }  // namespace lbt

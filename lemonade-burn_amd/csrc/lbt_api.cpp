@@ -35,6 +35,8 @@ LbtTuning read_tuning() {
     }
     t.head_tg8 = getenv("LBT_HEAD_TG8") != nullptr;
     t.step_trace = getenv("LBT_STEP_TRACE") != nullptr;
+    t.gemv_pw = num("LBT_GEMV_PW", 4) == 16 ? 16 : 4;
+    t.gemv_pwo = num("LBT_GEMV_PWO", 16) == 4 ? 4 : 16;
     return t;
 }
 

@@ -504,9 +504,10 @@ __device__ __forceinline__ float tree16(const float* w) {
 // elements in ascending order; the 16 virtual wavefronts (vt / 64) reduce
 // by xor butterflies, then tree16.  A kernel with NT threads holds
 // A = 1024 / NT virtual threads per thread (vt = t + NT*j).  Uses red[0..15]
-// (reduction slots 0..3); one barrier.
+// (reduction slots 0..3).  row_sumsq_part leaves the 16 virtual-wavefront
+// sums in red[0..15] (threads past NT take no part; no barrier).
 template <int EPT, int NT = kThreads>
-__device__ __forceinline__ float row_sumsq(const RowRegs<EPT>& r, int cols, float* red) {
+__device__ __forceinline__ void row_sumsq_part(const RowRegs<EPT>& r, int cols, float* red) {
     static_assert(NT == 256 || NT == 512 || NT == 1024, "threads of a row prologue");
     constexpr int A = 1024 / NT;
     const int tid = (int)threadIdx.x, lane = tid & 63;
@@ -537,6 +538,11 @@ __device__ __forceinline__ float row_sumsq(const RowRegs<EPT>& r, int cols, floa
             if (lane == 0 && act) red[(tid >> 6) + j * (NT / 64)] = s;
         }
     }
+}
+// The partials of row_sumsq_part, published by a barrier, summed.
+template <int EPT, int NT = kThreads>
+__device__ __forceinline__ float row_sumsq(const RowRegs<EPT>& r, int cols, float* red) {
+    row_sumsq_part<EPT, NT>(r, cols, red);
     __syncthreads();
     return tree16(red);
 }

@@ -25,6 +25,8 @@ struct LbtTuning {
     int attn_wide = -1;       // LBT_ATTN_WIDE=1/0: eight-pass K/V pipeline of the grouped attention on/off (-1: by grid size)
     bool head_tg8 = false;    // LBT_HEAD_TG8: 8-token groups in the batched LM head
     bool step_trace = false;  // LBT_STEP_TRACE: phase timestamps of the one-dispatch decode step
+    int gemv_pw = 4;          // LBT_GEMV_PW=16: single-token GEMV prologue (f32 rows) on all 16 wavefronts (default 4)
+    int gemv_pwo = 16;        // LBT_GEMV_PWO=4: ... of the o projection (attention-combine rows) on four (default 16)
 };
 
 struct lbt_ctx {

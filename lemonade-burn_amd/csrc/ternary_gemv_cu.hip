@@ -63,10 +63,62 @@ constexpr int kCuThreads = 1024;
 constexpr int kCuEPT = 8;       // row elements per thread: rows up to 8192 (4: rows up to 4096)
 constexpr int kCuMaxRows = 64;  // rows per workgroup (16 wavefronts x 64 / L, L >= 16)
 
-template <int L, int CPL, int IN, int OUT, int EPT>
+// RMSNorm + ActQuant of a row held by the first PW wavefronts only (the
+// element layout of row_elem<64 * PW>), the other wavefronts skipping every
+// step but the barriers: the reductions' per-wavefront work (butterflies,
+// the divisions and square root of the norm factor and scale) then runs
+// once per SIMD instead of four times.  The same values as quantize_row_regs
+// (canonical sum-of-squares order; max and integer sums are order
+// independent).  s_a goes to *sa; wavefront w < PW leaves its sum(q)
+// partial at ((int*)(red + 32))[w], published by the caller's next barrier.
+template <int EPT, int PW, int NORM, typename Pos>
+__device__ __forceinline__ void quant_row_waves(RowRegs<EPT>& r, int cols, int kp, const float* norm_w, float eps,
+                                                int8_t* dst, Pos pos, float* sa, float* red) {
+    constexpr int NT = 64 * PW;
+    const int tid = (int)threadIdx.x, w = tid >> 6;
+    const bool part = w < PW;  // uniform per wavefront
+    if constexpr (NORM != 0) {
+        if (part) row_sumsq_part<EPT, NT>(r, cols, red);
+        __syncthreads();
+    }
+    if (part) {
+        if constexpr (NORM != 0) {
+            const float f = 1.0f / __builtin_sqrtf(tree16(red) / (float)cols + eps);
+#pragma unroll
+            for (int e = 0; e < EPT; e++) r.v[e] = (r.v[e] * f) * r.nw[e];
+        }
+        float am = 0.0f;
+#pragma unroll
+        for (int e = 0; e < EPT; e++) am = fmaxf(am, fabsf(r.v[e]));
+        am = wave_max(am);
+        if ((tid & 63) == 0) red[16 + w] = am;
+    }
+    __syncthreads();
+    if (part) {
+        float am = red[16];
+#pragma unroll
+        for (int i = 1; i < PW; i++) am = fmaxf(am, red[16 + i]);
+        const float scale = 127.0f / fmaxf(am, 1e-5f);
+        int s = 0;
+#pragma unroll
+        for (int g = 0; g < EPT / 4; g++) {
+            const int i0 = 4 * NT * g + 4 * tid;
+            if (i0 < kp) *(uint32_t*)(dst + pos(i0)) = quant4(&r.v[4 * g], scale, s);
+        }
+        s = wave_sum_i(s);
+        if ((tid & 63) == 0) ((int*)(red + 32))[w] = s;
+        if (tid == 0) *sa = scale;
+    }
+}
+
+// PW: wavefronts of the activation prologue (16: all, EPT elements per
+// thread; 4: the first four, EPT elements per thread of 256).
+template <int L, int CPL, int IN, int OUT, int EPT, int PW>
 __global__ __launch_bounds__(kCuThreads) void tgemv_cu_kernel(GemvArgs a, int rpw) {
+    static_assert(PW == 16 || PW == 4, "prologue wavefronts");
     constexpr int RPWV = 64 / L;  // rows per wavefront
-    __shared__ __align__(16) int8_t xq[EPT * kCuThreads];
+    constexpr int PNT = 64 * PW;  // threads of the prologue
+    __shared__ __align__(16) int8_t xq[EPT * PNT];
     __shared__ __align__(16) float red[kRedFloats];
     __shared__ float sa_s;
     const int tid = (int)threadIdx.x, w = tid >> 6, lane = tid & 63;
@@ -82,18 +134,20 @@ __global__ __launch_bounds__(kCuThreads) void tgemv_cu_kernel(GemvArgs a, int rp
 
     // the activation row's loads first
     RowRegs<EPT> row;
-    AttnRegs<IN == kInAttn ? EPT : 4, IN == kInAttn ? 4 : 1, kCuThreads> arow;
+    AttnRegs<IN == kInAttn ? EPT : 4, IN == kInAttn ? 4 : 1, PNT> arow;
     AttnRow attn{a.att_o, a.att_ml, 0, a.att_nh, a.hd, a.cols};
     const float* norm_w = a.norm_w ? launder(a.norm_w) : nullptr;
     // the decode position (attention splits): an untracked load issued first,
     // waited for with the row (below), so no wait on it covers the weights
     float posf = 0.0f;
     // (without a device position, a harmless word of the partials is read)
-    if constexpr (IN == kInAttn) posf = ld_f32_async(a.pos_dev ? (const float*)a.pos_dev : a.att_ml);
-    if constexpr (IN == kInAttn)
-        attn_row_issue<EPT, 4, kCuThreads>(attn, norm_w, arow, row);
-    else
-        row_load_buf<EPT, kCuThreads>(launder(a.x), a.cols, norm_w, row);
+    if constexpr (IN == kInAttn) {
+        if (PW == 16 || w < PW) {
+            posf = ld_f32_async(a.pos_dev ? (const float*)a.pos_dev : a.att_ml);
+            attn_row_issue<EPT, 4, PNT>(attn, norm_w, arow, row);
+        }
+    } else if (PW == 16 || w < PW)
+        row_load_buf<EPT, PNT>(launder(a.x), a.cols, norm_w, row);
 
     // then every weight load of this workgroup, once every wavefront's row
     // loads are queued ahead of them (a bare barrier: no wait for the data)
@@ -119,14 +173,25 @@ __global__ __launch_bounds__(kCuThreads) void tgemv_cu_kernel(GemvArgs a, int rp
     // prologue: (attention combine,) RMSNorm + ActQuant into the permuted LDS image
     if constexpr (IN == kInAttn) {
         __shared__ AttnTab tab;
-        vm_wait<CPL>();  // all but the weight loads: the position and the row
-        pin(posf);
-        attn.ns = attn_splits((a.pos_dev ? __float_as_int(posf) : a.pos0) + 1);
-        attn_row_finish<EPT, 4, kCuThreads>(attn, arow, row, tab);
+        if (PW == 16 || w < PW) {
+            vm_wait<CPL>();  // all but the weight loads: the position and the row
+            pin(posf);
+            attn.ns = attn_splits((a.pos_dev ? __float_as_int(posf) : a.pos0) + 1);
+            attn_row_tab<EPT, 4, PNT>(attn, arow, tab);
+        }
+        __syncthreads();
+        if (PW == 16 || w < PW) attn_row_combine<EPT, 4, PNT>(attn, arow, row, tab);
         CTR(3)
     }
-    quantize_row_regs<EPT, kCuThreads, -1, true>(row, a.cols, a.kp, norm_w, a.eps, xq,
-                                                    [C](int i) { return perm_pos(i, C); }, &sa_s, nullptr, red);
+    if constexpr (PW == 16)
+        quantize_row_regs<EPT, kCuThreads, -1, true>(row, a.cols, a.kp, norm_w, a.eps, xq,
+                                                        [C](int i) { return perm_pos(i, C); }, &sa_s, nullptr, red);
+    else if (norm_w)
+        quant_row_waves<EPT, PW, 1>(row, a.cols, a.kp, norm_w, a.eps, xq, [C](int i) { return perm_pos(i, C); },
+                                    &sa_s, red);
+    else
+        quant_row_waves<EPT, PW, 0>(row, a.cols, a.kp, norm_w, a.eps, xq, [C](int i) { return perm_pos(i, C); },
+                                    &sa_s, red);
     __syncthreads();
     CTR(9)
     // sum(q): the wavefronts' partials left by the quantizer
@@ -134,7 +199,7 @@ __global__ __launch_bounds__(kCuThreads) void tgemv_cu_kernel(GemvArgs a, int rp
     {
         const int4* qp = (const int4*)(red + 32);
 #pragma unroll
-        for (int i = 0; i < kCuThreads / 256; i++) {
+        for (int i = 0; i < PW / 4; i++) {
             const int4 v = qp[i];
             qsum += (v.x + v.y) + (v.z + v.w);
         }
@@ -195,15 +260,19 @@ __global__ __launch_bounds__(kCuThreads) void tgemv_cu_kernel(GemvArgs a, int rp
 
 namespace {
 
-template <int L, int CPL, int EPT>
+template <int L, int CPL, int EPT, int PW>
 hipError_t launch_cu(const GemvArgs& a, int in_mode, int out_mode, int rpw, dim3 grid, hipStream_t s, hipEvent_t e0,
                      hipEvent_t e1) {
-#define LBT_CU_LAUNCH(IN, OUT)                                                                                   \
-    hipExtLaunchKernelGGL((tgemv_cu_kernel<L, CPL, IN, OUT, EPT>), grid, dim3(kCuThreads), 0, s, e0, e1, 0, a, \
+#define LBT_CU_LAUNCH(IN, OUT)                                                                                       \
+    hipExtLaunchKernelGGL((tgemv_cu_kernel<L, CPL, IN, OUT, EPT, PW>), grid, dim3(kCuThreads), 0, s, e0, e1, 0, a, \
                           rpw)
     if (in_mode == kInAttn) {
-        LBT_CU_LAUNCH(kInAttn, kOutF32Add);
-        return hipGetLastError();
+        if constexpr (PW == 16 || EPT <= 16) {
+            LBT_CU_LAUNCH(kInAttn, kOutF32Add);
+            return hipGetLastError();
+        } else {
+            return hipErrorInvalidValue;
+        }
     }
     switch (out_mode) {
         case kOutI32: LBT_CU_LAUNCH(kInF32, kOutI32); break;
@@ -227,19 +296,25 @@ hipError_t launch_cu(const GemvArgs& a, int in_mode, int out_mode, int rpw, dim3
 // groups beyond the row are skipped either way).
 template <int L, int CPL>
 hipError_t launch_cu_e(const GemvArgs& a, int in_mode, int out_mode, int rpw, dim3 grid, hipStream_t s,
-                       hipEvent_t e0, hipEvent_t e1) {
-    if (a.kp <= 4 * kCuThreads) return launch_cu<L, CPL, 4>(a, in_mode, out_mode, rpw, grid, s, e0, e1);
-    return launch_cu<L, CPL, 8>(a, in_mode, out_mode, rpw, grid, s, e0, e1);
+                       hipEvent_t e0, hipEvent_t e1, int pw) {
+    if (pw == 4) {
+        if (a.kp <= 12 * 256) return launch_cu<L, CPL, 12, 4>(a, in_mode, out_mode, rpw, grid, s, e0, e1);
+        if (in_mode == kInAttn) return launch_cu<L, CPL, 16, 4>(a, in_mode, out_mode, rpw, grid, s, e0, e1);
+        if (a.kp <= 28 * 256) return launch_cu<L, CPL, 28, 4>(a, in_mode, out_mode, rpw, grid, s, e0, e1);
+        return launch_cu<L, CPL, 32, 4>(a, in_mode, out_mode, rpw, grid, s, e0, e1);
+    }
+    if (a.kp <= 4 * kCuThreads) return launch_cu<L, CPL, 4, 16>(a, in_mode, out_mode, rpw, grid, s, e0, e1);
+    return launch_cu<L, CPL, 8, 16>(a, in_mode, out_mode, rpw, grid, s, e0, e1);
 }
 
 template <int L>
 hipError_t launch_cu_l(const GemvArgs& a, int cpl, int in_mode, int out_mode, int rpw, dim3 grid, hipStream_t s,
-                       hipEvent_t e0, hipEvent_t e1) {
+                       hipEvent_t e0, hipEvent_t e1, int pw) {
     switch (cpl) {
-        case 1: return launch_cu_e<L, 1>(a, in_mode, out_mode, rpw, grid, s, e0, e1);
-        case 2: return launch_cu_e<L, 2>(a, in_mode, out_mode, rpw, grid, s, e0, e1);
-        case 4: return launch_cu_e<L, 4>(a, in_mode, out_mode, rpw, grid, s, e0, e1);
-        default: return launch_cu_e<L, 8>(a, in_mode, out_mode, rpw, grid, s, e0, e1);
+        case 1: return launch_cu_e<L, 1>(a, in_mode, out_mode, rpw, grid, s, e0, e1, pw);
+        case 2: return launch_cu_e<L, 2>(a, in_mode, out_mode, rpw, grid, s, e0, e1, pw);
+        case 4: return launch_cu_e<L, 4>(a, in_mode, out_mode, rpw, grid, s, e0, e1, pw);
+        default: return launch_cu_e<L, 8>(a, in_mode, out_mode, rpw, grid, s, e0, e1, pw);
     }
 }
 
@@ -269,9 +344,10 @@ int launch_ternary_gemv_cu(lbt_ctx* ctx, const TernaryOp& op) {
     hipEvent_t e0, e1;
     prof_pair(ctx, &e0, &e1);
     hipError_t e;
-    if (L == 64) e = launch_cu_l<64>(a, cpl, op.in_mode, op.out_mode, rpw, grid, ctx->stream, e0, e1);
-    else if (L == 32) e = launch_cu_l<32>(a, cpl, op.in_mode, op.out_mode, rpw, grid, ctx->stream, e0, e1);
-    else e = launch_cu_l<16>(a, cpl, op.in_mode, op.out_mode, rpw, grid, ctx->stream, e0, e1);
+    const int pw = op.in_mode == kInAttn ? ctx->tune.gemv_pwo : ctx->tune.gemv_pw;
+    if (L == 64) e = launch_cu_l<64>(a, cpl, op.in_mode, op.out_mode, rpw, grid, ctx->stream, e0, e1, pw);
+    else if (L == 32) e = launch_cu_l<32>(a, cpl, op.in_mode, op.out_mode, rpw, grid, ctx->stream, e0, e1, pw);
+    else e = launch_cu_l<16>(a, cpl, op.in_mode, op.out_mode, rpw, grid, ctx->stream, e0, e1, pw);
     if (e != hipSuccess) return hip_err(ctx, e, "tgemv_cu_kernel launch");
     const double bytes = (double)total * (a.kp / 4) + (double)op.cols * 4.0;
     prof_commit(ctx, e0, e1, kProfGemv, bytes);
