@@ -59,8 +59,7 @@ int lbt_memcpy_d2h(lbt_ctx* ctx, void* dst, const void* src, size_t bytes);
  * reference kernel when HBM counters are calibrated.  No counterpart in the
  * reference (its tensors live in host memory). */
 int lbt_memcpy_d2d(lbt_ctx* ctx, void* dst, const void* src, size_t bytes);
-/* Library build id (kernel set + arch; "+step" when the one-dispatch decode
- * step is built in). */
+/* Library build id (version + arch). */
 const char* lbt_version(void);
 
 /* ---- packed ternary weights ------------------------------------------------
@@ -249,14 +248,6 @@ int lbt_model_decode_sample(lbt_model* m, lbt_cache* c, uint32_t first, size_t s
  * rebuilt.  No counterpart in the reference for kind 2: it serves batched
  * decode, which the reference does not have. */
 int lbt_model_set_head(lbt_model* m, int kind);
-/* How batch-1 decode steps (generate_greedy / decode_greedy) run; no
- * reference counterpart (the reference's step is BitNet::forward on one token,
- * crates/lb-model/src/model.rs:305-374, on the CPU): 0 = all decoder layers of
- * a token in one dispatch, 1 = one dispatch per kernel, replayed as a
- * captured graph (default).  Both give the same bits; shapes the one-dispatch step
- * does not take use the multi-kernel step.  Kind 0 (measured slower) is in
- * builds made with LBT_WITH_STEP=1 only; otherwise it is LBT_E_INVALID. */
-int lbt_model_set_decode(lbt_model* m, int kind);
 /* Residual stream of the last forward ([n, hidden] f32) for layer-level tests. */
 int lbt_model_read_hidden(lbt_model* m, float* out, size_t n);
 
@@ -332,7 +323,7 @@ int lbt_sched_release(lbt_sched* s, uint64_t id);
  * When enabled, every ternary GEMV/GEMM launch of the model loop is bracketed
  * by HIP events on the context stream; totals are per kernel class
  * (0 = ternary decode GEMV, 1 = ternary prefill GEMM, 2 = bf16 LM head,
- * 3 = attention, 4 = other, 5 = one-dispatch decode step of all layers). */
+ * 3 = attention, 4 = other; slot 5 is unused). */
 typedef struct lbt_prof {
     double ms[6];
     double bytes[6];

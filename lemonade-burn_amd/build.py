@@ -33,12 +33,7 @@ FLAGS = [
     "-Wno-unused-result",
     f"-I{REPO / 'include'}",
 ]
-# the one-dispatch decode step (measured slower than the graph step) only on request
-if os.environ.get("LBT_WITH_STEP") == "1":
-    FLAGS.append("-DLBT_WITH_STEP=1")
 FLAGS += os.environ.get("LBT_EXTRA_FLAGS", "").split()
-# the phase-trace variant of the decode GEMV (gemv_phases.py): python build.py trace
-TRACE_LIB = PKG / "liblbt_hip_trace.so"
 
 
 def sources() -> list[Path]:
@@ -71,22 +66,5 @@ def build(verbose: bool = True) -> Path:
     return LIB
 
 
-def build_trace(verbose: bool = True) -> Path:
-    """The same library with -DLBT_GEMV_TRACE, as liblbt_hip_trace.so (own
-    object folder): only gemv_phases.py loads it."""
-    global BUILD, LIB
-    saved = (BUILD, LIB, list(FLAGS))
-    BUILD, LIB = PKG / "_build_trace", TRACE_LIB
-    FLAGS.append("-DLBT_GEMV_TRACE")
-    try:
-        return build(verbose)
-    finally:
-        BUILD, LIB = saved[0], saved[1]
-        FLAGS[:] = saved[2]
-
-
 if __name__ == "__main__":
-    if sys.argv[1:] == ["trace"]:
-        build_trace()
-    else:
-        build()
+    build()

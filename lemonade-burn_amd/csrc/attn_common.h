@@ -46,15 +46,6 @@ struct AttnShared {
     __align__(16) float pv[4][LK * 8];
 };
 
-// Optional phase stamps (debug builds of the attention kernel and of the
-// combine).
-#ifndef LBT_ATR
-#define LBT_ATR(i)
-#endif
-#ifndef LBT_CTR
-#define LBT_CTR(i)
-#endif
-
 // Splits of vis visible keys.
 __host__ __device__ __forceinline__ int attn_splits(int vis) {
     const int ks = attn_split_keys(vis);
@@ -140,8 +131,6 @@ __device__ __forceinline__ void attention_split_ku(const float* q, int h, int nh
     }
     const uint16_t* K = K0 + (size_t)j0 * HD;
     const uint16_t* V = V0 + (size_t)j0 * HD;
-    LBT_ATR(1)
-    LBT_ATR(2)
     const float q8[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
 
     // ---- scores and the split max
@@ -177,9 +166,7 @@ __device__ __forceinline__ void attention_split_ku(const float* q, int h, int nh
     }
     mx = wave_max(mx);
     if (lane == 0 && w < 4) sh.rmax[w] = mx;
-    LBT_ATR(3)
     __syncthreads();  // publishes the scores and the wave maxima
-    LBT_ATR(4)
     const float m = fmaxf(fmaxf(sh.rmax[0], sh.rmax[1]), fmaxf(sh.rmax[2], sh.rmax[3]));
     float ps = 0.0f;
     if (act)
@@ -191,7 +178,6 @@ __device__ __forceinline__ void attention_split_ku(const float* q, int h, int nh
     ps = wave_sum(ps);
     if (lane == 0 && w < 4) sh.rsum[w] = ps;
     __syncthreads();  // publishes the exponentials and the wave sums
-    LBT_ATR(5)
 
     // ---- unnormalised probs @ V
     float acc[8];
@@ -222,7 +208,6 @@ __device__ __forceinline__ void attention_split_ku(const float* q, int h, int nh
             if (b0 + KU * NK >= cnt) break;
         }
     }
-    LBT_ATR(6)
     if constexpr (GW > 1) {
 #pragma unroll
         for (int e = 0; e < 8; e++) acc[e] = xor_sum_up<LK>(acc[e]);
@@ -240,7 +225,6 @@ __device__ __forceinline__ void attention_split_ku(const float* q, int h, int nh
         ml[((size_t)s * nh + h) * 2] = m;
         ml[((size_t)s * nh + h) * 2 + 1] = (sh.rsum[0] + sh.rsum[1]) + (sh.rsum[2] + sh.rsum[3]);
     }
-    LBT_ATR(8)
 }
 
 // attention_split_ku with the load batch sized to the split: four key passes
@@ -581,7 +565,6 @@ template <int EPT, int NSB, int NT = kThreads>
 __device__ __forceinline__ void attn_row_tab(const AttnRow& a, AttnRegs<EPT, NSB, NT>& ar, AttnTab& tab) {
     const int tid = (int)threadIdx.x;
     const bool act = tid < NT;
-    LBT_CTR(6)
     // (head, split) pairs sit in 16 consecutive lanes per head: M, the split
     // factors f_s and L come from lane butterflies, no LDS round trip
     static_assert(kAttnSplits == 16 && NT % kAttnSplits == 0, "16-lane head segments");
@@ -602,7 +585,6 @@ __device__ __forceinline__ void attn_row_tab(const AttnRow& a, AttnRegs<EPT, NSB
             if (s == 0) tab.L[h] = 1.0f / L;
         }
     }
-    LBT_CTR(9)
 }
 
 template <int EPT, int NSB, int NT = kThreads>
@@ -660,7 +642,6 @@ __device__ __forceinline__ void attn_row_finish(const AttnRow& a, AttnRegs<EPT, 
                                                 AttnTab& tab) {
     attn_row_tab<EPT, NSB, NT>(a, ar, tab);
     __syncthreads();
-    LBT_CTR(10)
     attn_row_combine<EPT, NSB, NT>(a, ar, r, tab);
 }
 

@@ -9,15 +9,6 @@
 // Float order follows lbt_device.h; the oracle mirrors it.
 #include <hip/hip_runtime.h>
 
-#ifdef LBT_ATTN_TRACE
-// Debug build only: wall-clock stamps of the attention phases per workgroup.
-__device__ unsigned long long lbt_attn_trace[256 * 16];
-#define LBT_ATR(i) \
-    if (threadIdx.x == 0 && blockIdx.y == 0 && blockIdx.x < 256) lbt_attn_trace[blockIdx.x * 16 + (i)] = wall_clock64();
-extern "C" int lbt_debug_attn_trace(unsigned long long* out) {
-    return (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(lbt_attn_trace), sizeof(lbt_attn_trace));
-}
-#endif
 
 #include "lbt_device.h"
 #include "lbt_internal.h"
@@ -65,7 +56,6 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(const float* q, int
                                                              float scaling, float* o, float* ml) {
     extern __shared__ float sc[];  // [attn_split_keys(visible keys)]
     __shared__ AttnShared<LK> sh;
-    LBT_ATR(0)
     const int nsg = (int)gridDim.x / nh;  // splits in the grid (the most any row has)
     const int h = blockIdx.x / nsg, s = blockIdx.x % nsg, t = blockIdx.y;
     const int H = nh * LK * 8, g = h / (nh / kvh);
@@ -79,7 +69,6 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(const float* q, int
     else  // the row's position (a graph-replayed step reads it from the device)
         attention_split<LK>(q + (size_t)t * H, h, nh, s, row_position(rp, t), kc + kvoff, vc + kvoff, scaling, ot,
                             mlt, sc, sh);
-    LBT_ATR(7)
 }
 
 // The same splits with one workgroup per (KV head, key split, query row)

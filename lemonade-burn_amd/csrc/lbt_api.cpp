@@ -34,7 +34,6 @@ LbtTuning read_tuning() {
         t.attn_wide = v ? (atoi(v) != 0 ? 1 : 0) : -1;
     }
     t.head_tg8 = getenv("LBT_HEAD_TG8") != nullptr;
-    t.step_trace = getenv("LBT_STEP_TRACE") != nullptr;
     t.gemv_pw = num("LBT_GEMV_PW", 4) == 16 ? 16 : 4;
     t.gemv_pwo = num("LBT_GEMV_PWO", 16) == 4 ? 4 : 16;
     return t;
@@ -146,13 +145,7 @@ TernaryOp make_op(const lbt_weight* const* ws, size_t n, size_t m) {
 
 extern "C" {
 
-const char* lbt_version(void) {
-#if LBT_WITH_STEP
-    return "lbt-hip 0.2 gfx950 +step";
-#else
-    return "lbt-hip 0.2 gfx950";
-#endif
-}
+const char* lbt_version(void) { return "lbt-hip 0.3 gfx950"; }
 
 
 int lbt_ctx_create(int device, lbt_ctx** out) {

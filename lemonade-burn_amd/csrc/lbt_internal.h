@@ -24,7 +24,6 @@ struct LbtTuning {
     bool small_pf = true;     // LBT_GEMM_SMALL_PF=0: no epilogue prefetch
     int attn_wide = -1;       // LBT_ATTN_WIDE=1/0: eight-pass K/V pipeline of the grouped attention on/off (-1: by grid size)
     bool head_tg8 = false;    // LBT_HEAD_TG8: 8-token groups in the batched LM head
-    bool step_trace = false;  // LBT_STEP_TRACE: phase timestamps of the one-dispatch decode step
     int gemv_pw = 4;          // LBT_GEMV_PW=16: single-token GEMV prologue (f32 rows) on all 16 wavefronts (default 4)
     int gemv_pwo = 16;        // LBT_GEMV_PWO=4: ... of the o projection (attention-combine rows) on four (default 16)
 };
@@ -98,7 +97,7 @@ int hip_err(lbt_ctx* ctx, hipError_t e, const char* what);
 int ws_reserve(lbt_ctx* ctx, size_t bytes, void** out);
 
 // Profiling brackets around one launch (no-ops unless ctx->prof).
-enum ProfClass { kProfGemv = 0, kProfGemm = 1, kProfHead = 2, kProfAttn = 3, kProfOther = 4, kProfStep = 5 };
+enum ProfClass { kProfGemv = 0, kProfGemm = 1, kProfHead = 2, kProfAttn = 3, kProfOther = 4 };
 // prof_pair hands out a start/stop event pair (null when profiling is off)
 // for hipExtLaunchKernelGGL, which timestamps the dispatch itself, so the
 // measured time is the kernel's execution (as rocprofv3 reports it).

@@ -27,7 +27,6 @@
 #include <string>
 #include <vector>
 
-#include "decode_step.h"
 #include "lbt_internal.h"
 
 using namespace lbt;
@@ -254,18 +253,6 @@ struct lbt_model {
     // state and the candidate scratch of one row
     unsigned long long* sstate = nullptr;
     void* sscratch = nullptr;
-    // one-dispatch decode step (decode_step.hip): device tables of the layers,
-    // the epoch-tagged activation words, the error word, the plan
-    int decode_kind = 1;   // 0: one-dispatch step, 1: multi-kernel graph step
-    void* ptab = nullptr;  // [layers*7] weight ptrs, [layers*7] scales, [layers*4] norm ptrs
-    unsigned long long* ll = nullptr;  // x, q/k/v, partials, h words, then the error word
-    size_t ll_bytes = 0;
-    double epochs = 0.0;  // epochs used since the words were last cleared
-    lbt::StepPlan plan;
-    int plan_cap = 0;
-    StepArgs* dargs = nullptr;  // the step's arguments in device memory
-    unsigned long long* trace = nullptr;  // phase timestamps (LBT_STEP_TRACE, read at model creation)
-    bool want_trace = false;
 };
 
 namespace lbt {
@@ -343,7 +330,6 @@ int validate_config(lbt_ctx* ctx, const lbt_config& c) {
 // Device buffers and RoPE tables shared by load and synthetic creation.
 int model_alloc(lbt_model* m) {
     lbt_ctx* ctx = m->ctx;
-    m->want_trace = ctx->tune.step_trace;
     const lbt_config& c = m->cfg;
     m->hd = c.hidden_size / c.num_attention_heads;
     size_t wbytes = 0;
@@ -646,163 +632,6 @@ int ensure_state(lbt_model* m) {
     return LBT_OK;
 }
 
-// Words of the epoch-tagged activation buffers of the one-dispatch step.
-struct StepWords {
-    size_t x, qkv, part, att, h, total;
-};
-StepWords step_words(const lbt_config& c, int hd) {
-    StepWords w;
-    const size_t H = (size_t)c.hidden_size, KV = (size_t)c.num_key_value_heads * hd;
-    w.x = (H + 1) & ~(size_t)1;
-    w.qkv = (H + 2 * KV + 1) & ~(size_t)1;
-    w.part = ((size_t)kAttnSplits * H + (size_t)kAttnSplits * c.num_attention_heads * 2 + 1) & ~(size_t)1;
-    w.att = w.x;
-    w.h = ((size_t)c.intermediate_size + 1) & ~(size_t)1;
-    w.total = w.x + w.qkv + w.part + w.att + w.h + 2;  // + the error word
-    return w;
-}
-
-// Plan of the one-dispatch step for this cache capacity, or 0 when the model
-// uses the multi-kernel step (selected, or a shape the step does not take).
-int step_ready(lbt_model* m, lbt_cache* c) {
-    if (m->decode_kind != 0) return 0;
-    if (m->plan.fn && m->plan_cap == c->cap) return 1;
-    const char* why = nullptr;
-    lbt::StepPlan pl;
-    pl.G = m->ctx->cus;
-    if (!step_plan(m->cfg, c->cap, pl.G, pl, &why)) return 0;
-    // the step addresses layer l's matrices and norms at a fixed stride
-    const int L = m->cfg.num_hidden_layers;
-    for (int l = 1; l < L; l++) {
-        for (int k = 0; k < 7; k++)
-            if (m->lin[l * 7 + k].d - m->lin[k].d != (ptrdiff_t)l * (m->lin[7].d - m->lin[0].d)) return 0;
-        for (int k = 0; k < 4; k++)
-            if (m->norm[l * 4 + k] - m->norm[k] != (ptrdiff_t)l * (m->norm[4] - m->norm[0])) return 0;
-    }
-    double bytes = 0.0;
-    for (int i = 0; i < 7 * m->cfg.num_hidden_layers; i++) bytes += (double)m->lin[i].rows * (double)(m->lin[i].kp / 4);
-    pl.bytes = bytes;
-    m->plan = pl;
-    m->plan_cap = c->cap;
-    return 1;
-}
-
-int step_prepare(lbt_model* m, lbt_cache* c, StepArgs& a) {
-    lbt_ctx* ctx = m->ctx;
-    const lbt_config& cf = m->cfg;
-    const int L = cf.num_hidden_layers;
-    int rc;
-    if ((rc = ensure_state(m))) return rc;
-    if (!m->ptab) {
-        std::vector<float> ws(L * 7);
-        for (int i = 0; i < L * 7; i++) ws[i] = m->lin[i].scale;
-        LBT_HIP(ctx, hipMalloc(&m->ptab, ws.size() * 4));
-        LBT_HIP(ctx, hipMemcpy(m->ptab, ws.data(), ws.size() * 4, hipMemcpyHostToDevice));
-    }
-    const StepWords sw = step_words(cf, m->hd);
-    const double per_step = 5.0 * L;
-    if (!m->ll || m->epochs + per_step * 4096.0 > 2147483648.0) {
-        // fresh words (epoch 0) and epoch base 0; also before the 32-bit epochs
-        // could wrap (a word must never show a future epoch)
-        if (!m->ll) {
-            m->ll_bytes = sw.total * 8;
-            LBT_HIP(ctx, hipMalloc(&m->ll, m->ll_bytes));
-        }
-        LBT_HIP(ctx, hipMemsetAsync(m->ll, 0, m->ll_bytes, ctx->stream));
-        LBT_HIP(ctx, hipMemsetAsync(m->state + 2, 0, sizeof(int), ctx->stream));
-        m->epochs = 0.0;
-    }
-    a = StepArgs{};
-    for (int k = 0; k < 7; k++) a.w0[k] = m->lin[k].d;
-    a.wstride = L > 1 ? (size_t)(m->lin[7].d - m->lin[0].d) : 0;
-    for (int k = 0; k < 4; k++) a.n0[k] = m->norm[k];
-    a.nstride = L > 1 ? (size_t)(m->norm[4] - m->norm[0]) : 0;
-    a.wscale = (const float*)m->ptab;
-    a.embed = m->embed;
-    a.cos_t = m->cos_t;
-    a.sin_t = m->sin_t;
-    a.kc = c->k;
-    a.vc = c->v;
-    a.cap = c->cap;
-    a.layer_kv = (size_t)cf.num_key_value_heads * c->cap * m->hd;
-    a.layers = L;
-    a.H = cf.hidden_size;
-    a.I = cf.intermediate_size;
-    a.nh = cf.num_attention_heads;
-    a.kvh = cf.num_key_value_heads;
-    a.hd = m->hd;
-    a.KV = cf.num_key_value_heads * m->hd;
-    a.vocab = cf.vocab_size;
-    a.eps = (float)cf.rms_norm_eps;
-    a.scaling = m->scaling;
-    a.state = m->state;
-    a.key = m->key;
-    a.tok_out = m->tok_out;
-    a.xout = m->x;
-    a.llx = m->ll;
-    a.llqkv = a.llx + sw.x;
-    a.llpart = a.llqkv + sw.qkv;
-    a.llatt = a.llpart + sw.part;
-    a.llh = a.llatt + sw.att;
-    a.err = (unsigned*)(a.llh + sw.h);
-    if (m->want_trace && !m->trace) {
-        LBT_HIP(ctx, hipMalloc(&m->trace, (size_t)m->plan.G * L * 32 * 8));
-        LBT_HIP(ctx, hipMemset(m->trace, 0, (size_t)m->plan.G * L * 32 * 8));
-    }
-    a.trace = m->trace;
-    step_fill(m->plan, cf, a);
-    if (!m->dargs) LBT_HIP(ctx, hipMalloc(&m->dargs, sizeof(StepArgs)));
-    // stream-ordered: earlier steps have read the previous arguments
-    LBT_HIP(ctx, hipMemcpyAsync(m->dargs, &a, sizeof(StepArgs), hipMemcpyHostToDevice, ctx->stream));
-    return LBT_OK;
-}
-
-// After a synchronize: a wait that timed out inside the step is an error.
-int step_check(lbt_model* m) {
-    if (!m->ll) return LBT_OK;
-    lbt_ctx* ctx = m->ctx;
-    const StepWords sw = step_words(m->cfg, m->hd);
-    unsigned* e = (unsigned*)(m->ll + sw.total - 2);
-    unsigned err = 0;
-    LBT_HIP(ctx, hipMemcpy(&err, e, 4, hipMemcpyDeviceToHost));
-    if (err) {
-        // the words may hold any epoch now: start over from fresh words
-        m->epochs = 1e300;
-        hipMemset(e, 0, 4);
-        return set_err(ctx, LBT_E_DEVICE, "decode step: a wait for another workgroup timed out");
-    }
-    if (m->trace) {
-        // measurement aid: per traced point k, the median and the latest
-        // workgroup's time after the layer's earliest start, averaged over layers
-        const int L = m->cfg.num_hidden_layers, G = m->plan.G;
-        std::vector<unsigned long long> t((size_t)G * L * 32);
-        LBT_HIP(ctx, hipMemcpy(t.data(), m->trace, t.size() * 8, hipMemcpyDeviceToHost));
-        double med[32] = {0}, mx[32] = {0};
-        int cnt[32] = {0};
-        for (int l = 1; l < L; l++) {
-            unsigned long long t0 = ~0ull;
-            for (int b = 0; b < G; b++) t0 = std::min(t0, t[((size_t)b * L + l) * 32]);
-            for (int k = 0; k < 32; k++) {
-                std::vector<double> v;
-                for (int b = 0; b < G; b++) {
-                    const unsigned long long x = t[((size_t)b * L + l) * 32 + k];
-                    if (x >= t0 && x - t0 < 100000000ull) v.push_back((double)(x - t0) / 100.0);
-                }
-                if (v.empty()) continue;
-                std::sort(v.begin(), v.end());
-                med[k] += v[v.size() / 2];
-                mx[k] += v.back();
-                cnt[k]++;
-            }
-        }
-        fprintf(stderr, "step trace (us after the layer's first start; median / latest workgroup):\n");
-        for (int k = 0; k < 32; k++)
-            if (cnt[k]) fprintf(stderr, "  %2d: %7.2f %7.2f\n", k, med[k] / cnt[k], mx[k] / cnt[k]);
-        LBT_HIP(ctx, hipMemset(m->trace, 0, t.size() * 8));
-    }
-    return LBT_OK;
-}
-
 int ensure_sampler(lbt_model* m) {
     if (m->sstate) return LBT_OK;
     lbt_ctx* ctx = m->ctx;
@@ -839,22 +668,6 @@ int decode_steps(lbt_model* m, lbt_cache* c, int n, int slot0, const lbt_sample_
     lbt_ctx* ctx = m->ctx;
     if (n <= 0) return LBT_OK;
     int rc;
-    if (step_ready(m, c)) {
-        StepArgs a;
-        if ((rc = step_prepare(m, c, a))) return rc;
-        if ((rc = launch_set_state(ctx, m->state, c->len - 1, slot0))) return rc;
-        const lbt_config& cf = m->cfg;
-        for (int s = 0; s < n; s++) {
-            if ((rc = launch_decode_step(ctx, m->plan, m->dargs, ctx->stream))) return rc;
-            m->epochs += 5.0 * cf.num_hidden_layers;
-            if ((rc = model_head(m, m->x, 1, (float)cf.rms_norm_eps, sp ? m->logits : nullptr, m->key, nullptr)))
-                return rc;
-            if ((rc = sample_key(m, sp))) return rc;
-        }
-        c->len += n;
-        m->last_n = 1;
-        return LBT_OK;
-    }
     if (ctx->prof || ctx->tune.no_graph) {
         for (int s = 0; s < n; s++) {
             if ((rc = forward_dev(m, c, nullptr, 1, false, sp != nullptr, m->tok_out + slot0 + s))) return rc;
@@ -1105,10 +918,6 @@ void lbt_model_free(lbt_model* m) {
     if (!m) return;
     hipStreamSynchronize(m->ctx->stream);
     if (m->step_exec) hipGraphExecDestroy(m->step_exec);
-    if (m->ptab) hipFree(m->ptab);
-    if (m->ll) hipFree(m->ll);
-    if (m->trace) hipFree(m->trace);
-    if (m->dargs) hipFree(m->dargs);
     if (m->sstate) hipFree(m->sstate);
     if (m->sscratch) hipFree(m->sscratch);
     void* bufs[] = {m->wbuf, m->fbuf, m->embed, m->cos_t, m->sin_t, m->x,   m->q,       m->k,
@@ -1226,7 +1035,6 @@ int lbt_model_generate_greedy(lbt_model* m, const uint32_t* prompt, size_t n, si
     }
     hipError_t e = hipStreamSynchronize(ctx->stream);
     if (!rc && e != hipSuccess) rc = hip_err(ctx, e, "generate");
-    if (!rc) rc = step_check(m);
     if (!rc) {
         float a = 0, b = 0;
         hipEventElapsedTime(&a, e0, e1);
@@ -1262,7 +1070,6 @@ int lbt_model_decode_greedy(lbt_model* m, lbt_cache* c, uint32_t first, size_t s
     hipEventRecord(e1, ctx->stream);
     hipError_t e = hipStreamSynchronize(ctx->stream);
     if (!rc && e != hipSuccess) rc = hip_err(ctx, e, "decode");
-    if (!rc) rc = step_check(m);
     if (!rc) {
         float a = 0;
         hipEventElapsedTime(&a, e0, e1);
@@ -1320,7 +1127,6 @@ int lbt_model_decode_sample(lbt_model* m, lbt_cache* c, uint32_t first, size_t s
     hipEventRecord(e1, ctx->stream);
     hipError_t e = hipStreamSynchronize(ctx->stream);
     if (!rc && e != hipSuccess) rc = hip_err(ctx, e, "decode");
-    if (!rc) rc = step_check(m);
     if (!rc) {
         float a = 0;
         hipEventElapsedTime(&a, e0, e1);
@@ -1368,18 +1174,6 @@ int lbt_model_set_head(lbt_model* m, int kind) {
     }
     if (kind != m->head_kind) drop_step_graph(m);
     m->head_kind = kind;
-    return LBT_OK;
-}
-
-int lbt_model_set_decode(lbt_model* m, int kind) {
-    if (!m) return LBT_E_INVALID;
-    if (kind != 0 && kind != 1)
-        return set_err(m->ctx, LBT_E_INVALID, "set_decode: kind must be 0 (one dispatch) or 1 (multi-kernel)");
-#if !LBT_WITH_STEP
-    if (kind == 0)
-        return set_err(m->ctx, LBT_E_INVALID, "set_decode: the one-dispatch step is not in this build (LBT_WITH_STEP=1)");
-#endif
-    m->decode_kind = kind;
     return LBT_OK;
 }
 

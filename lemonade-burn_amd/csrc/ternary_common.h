@@ -5,11 +5,6 @@
 #include "lbt_device.h"
 #include "lbt_internal.h"
 
-// Optional phase stamps of the activation prologue (debug builds of the GEMV).
-#ifndef LBT_QTR
-#define LBT_QTR(i)
-#endif
-
 namespace lbt {
 
 struct GemvArgs {
@@ -192,14 +187,11 @@ __device__ __forceinline__ void quantize_row_regs(RowRegs<EPT>& r, int cols, int
     const int tid = (int)threadIdx.x;
     const bool act = tid < NT;
     row_norm<EPT, NT, NORM>(r, cols, norm_w, eps, red);
-    LBT_QTR(4)
     float am = 0.0f;
 #pragma unroll
     for (int e = 0; e < EPT; e++) am = fmaxf(am, fabsf(r.v[e]));
-    LBT_QTR(5)
     am = block_max_n<NT>(am, red + 16);
     const float scale = 127.0f / fmaxf(am, 1e-5f);
-    LBT_QTR(6)
     int s = 0;
 #pragma unroll
     for (int g = 0; g < EPT / 4; g++) {
@@ -209,7 +201,6 @@ __device__ __forceinline__ void quantize_row_regs(RowRegs<EPT>& r, int cols, int
             *(uint32_t*)(dst + pos(i0)) = quant4(&r.v[4 * g], scale, s);
         }
     }
-    LBT_QTR(7)
     if constexpr (DEFER_QS) {
         s = wave_sum_i(s);
         if ((tid & 63) == 0 && act) ((int*)(red + 32))[tid >> 6] = s;
@@ -217,7 +208,6 @@ __device__ __forceinline__ void quantize_row_regs(RowRegs<EPT>& r, int cols, int
         return;
     }
     s = block_sum_i_n<NT>(s, (int*)(red + 32));
-    LBT_QTR(8)
     if (tid == 0) {
         *sa = scale;
         *qs = s;

@@ -24,36 +24,6 @@
 //     gate/up rows (model.rs:362-363).
 #include <hip/hip_runtime.h>
 
-#ifdef LBT_GEMV_TRACE
-// Debug build only: per-workgroup wall-clock stamps of the GEMV phases.
-__device__ unsigned long long lbt_gemv_trace[4096 * 16];
-#ifndef LBT_TRACE_IN
-#define LBT_TRACE_IN (-1)
-#endif
-#define GTR(i) \
-    if ((LBT_TRACE_IN < 0 || LBT_TRACE_IN == IN) && threadIdx.x == 0 && blockIdx.y == 0 && blockIdx.x < 4096) \
-        lbt_gemv_trace[blockIdx.x * 16 + (i)] = wall_clock64();
-#define GCLK(i)
-extern "C" int lbt_debug_gemv_trace(unsigned long long* out) {
-    return (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(lbt_gemv_trace), sizeof(lbt_gemv_trace));
-}
-extern "C" int lbt_debug_gemv_clear() {
-    void* p;
-    if (hipGetSymbolAddress(&p, HIP_SYMBOL(lbt_gemv_trace)) != hipSuccess) return -1;
-    return (int)hipMemset(p, 0, sizeof(lbt_gemv_trace));
-}
-#if LBT_TRACE_IN == 2
-#define LBT_CTR(i) \
-    if (threadIdx.x == 0 && blockIdx.y == 0 && blockIdx.x < 4096) lbt_gemv_trace[blockIdx.x * 16 + (i)] = wall_clock64();
-#endif
-#if LBT_TRACE_IN < 0
-#define LBT_QTR(i) \
-    if (threadIdx.x == 0 && blockIdx.y == 0 && blockIdx.x < 4096) lbt_gemv_trace[blockIdx.x * 16 + (i)] = wall_clock64();
-#endif
-#else
-#define GTR(i)
-#define GCLK(i)
-#endif
 
 #include "lbt_device.h"
 #include "lbt_internal.h"
@@ -130,8 +100,6 @@ __global__ __launch_bounds__(kThreads) void tgemv_kernel(GemvArgs a) {
     __shared__ int qs[T];
     __shared__ int part[TILES][4][R][T];
 
-    GTR(0)
-    GCLK(10)
     const int tid = threadIdx.x, w = tid >> 6, ln = tid & 63;
     const int rg = ln / L, j = ln % L;
     const int t0 = blockIdx.y * T;
@@ -172,12 +140,10 @@ __global__ __launch_bounds__(kThreads) void tgemv_kernel(GemvArgs a) {
         }
     }
 
-    GTR(1)
     if constexpr (kAttn) {
         __shared__ AttnTab tab;
         attn.ns = attn_splits((a.pos_dev ? *a.pos_dev : a.pos0) + 1);
         attn_row_finish(attn, arow, rrow, tab);
-        GTR(5)
         quantize_row_regs(rrow, a.cols, a.kp, norm_w, a.eps, xq, [C](int i) { return perm_pos(i, C); }, &sa[0],
                           &qs[0], red);
     } else if constexpr (kRegs) {
@@ -190,7 +156,6 @@ __global__ __launch_bounds__(kThreads) void tgemv_kernel(GemvArgs a) {
         build_acts<T, IN, EPT>(a, t0, xq, sa, qs, red);
     }
     __syncthreads();
-    GTR(2)
 
 #pragma unroll
     for (int k = 0; k < TILES; k++) {
@@ -230,7 +195,6 @@ __global__ __launch_bounds__(kThreads) void tgemv_kernel(GemvArgs a) {
                 wv[k][i] = (valid[k] && c < C) ? ld_stream(rowp[k] + c) : make_uint4(0, 0, 0, 0);
             }
         }
-        if (k == 0) { GTR(3) }
 #pragma unroll
         for (int t = 0; t < T; t++) acc[t] = xor_sum_down_i<L / 2>(acc[t]);
         if (j == 0) {
@@ -245,8 +209,6 @@ __global__ __launch_bounds__(kThreads) void tgemv_kernel(GemvArgs a) {
 #pragma unroll
     for (int k = 0; k < TILES; k++)
         epilogue<R, T, OUT>(a, (blockIdx.x * TILES + k) * R, t0, part[k], sa, qs, tid - k * 64);
-    GTR(4)
-    GCLK(11)
 }
 
 // Standalone quantizer: one workgroup per row, writes q [m, kp] (zero padded),

@@ -19,38 +19,6 @@
 //   * epilogues are the shared ones of ternary_common.h.
 #include <hip/hip_runtime.h>
 
-#ifdef LBT_GEMV_TRACE
-// Trace builds only (the library built with -DLBT_GEMV_TRACE): wall-clock
-// stamps (100 MHz) of the phases of the workgroups of the last launch whose
-// (OUT, IN) matches lbt_gemvcu_sel, 16 slots per workgroup.
-__device__ unsigned long long lbt_gemvcu_trace[1024 * 16];
-__device__ int lbt_gemvcu_sel[2];
-__device__ int lbt_gemvcu_on;  // written and read by thread 0 of each workgroup only
-#define CTR(i)                                                       \
-    if (threadIdx.x == 0 && blockIdx.x < 1024 && lbt_gemvcu_on != 0) \
-        lbt_gemvcu_trace[blockIdx.x * 16 + (i)] = wall_clock64();
-#define LBT_QTR(i) CTR(i)
-// the same stamp by the first lane of the last wavefront
-#define CTR_LAST(i)                                                                                      \
-    if (threadIdx.x == kCuThreads - 64 && blockIdx.x < 1024 &&                                          \
-        lbt_gemvcu_sel[0] == OUT && lbt_gemvcu_sel[1] == IN)                                              \
-        lbt_gemvcu_trace[blockIdx.x * 16 + (i)] = wall_clock64();
-extern "C" int lbt_debug_gemvcu_select(int out_mode, int in_mode) {
-    const int v[2] = {out_mode, in_mode};
-    return (int)hipMemcpyToSymbol(HIP_SYMBOL(lbt_gemvcu_sel), v, sizeof(v));
-}
-extern "C" int lbt_debug_gemvcu_trace(unsigned long long* out) {
-    return (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(lbt_gemvcu_trace), sizeof(lbt_gemvcu_trace));
-}
-extern "C" int lbt_debug_gemvcu_clear() {
-    void* p;
-    if (hipGetSymbolAddress(&p, HIP_SYMBOL(lbt_gemvcu_trace)) != hipSuccess) return -1;
-    return (int)hipMemset(p, 0, sizeof(lbt_gemvcu_trace));
-}
-#else
-#define CTR(i)
-#define CTR_LAST(i)
-#endif
 
 #include "lbt_device.h"
 #include "lbt_internal.h"
@@ -126,11 +94,6 @@ __global__ __launch_bounds__(kCuThreads) void tgemv_cu_kernel(GemvArgs a, int rp
     const int C = a.C;
     const int vr0 = blockIdx.x * rpw;
     const bool rvalid = rs < rpw && vr0 + rs < a.total_rows;
-#ifdef LBT_GEMV_TRACE
-    if (threadIdx.x == 0) lbt_gemvcu_on = lbt_gemvcu_sel[0] == OUT && lbt_gemvcu_sel[1] == IN;
-#endif
-    CTR(0)
-    CTR_LAST(13)
 
     // the activation row's loads first
     RowRegs<EPT> row;
@@ -151,7 +114,6 @@ __global__ __launch_bounds__(kCuThreads) void tgemv_cu_kernel(GemvArgs a, int rp
 
     // then every weight load of this workgroup, once every wavefront's row
     // loads are queued ahead of them (a bare barrier: no wait for the data)
-    CTR_LAST(14)
     __builtin_amdgcn_s_barrier();
     uint4 wv[CPL];
     {
@@ -168,7 +130,6 @@ __global__ __launch_bounds__(kCuThreads) void tgemv_cu_kernel(GemvArgs a, int rp
             wv[i] = ld_stream(rowp + (c < C ? c : C - 1));
         }
     }
-    CTR(1)
 
     // prologue: (attention combine,) RMSNorm + ActQuant into the permuted LDS image
     if constexpr (IN == kInAttn) {
@@ -181,7 +142,6 @@ __global__ __launch_bounds__(kCuThreads) void tgemv_cu_kernel(GemvArgs a, int rp
         }
         __syncthreads();
         if (PW == 16 || w < PW) attn_row_combine<EPT, 4, PNT>(attn, arow, row, tab);
-        CTR(3)
     }
     if constexpr (PW == 16)
         quantize_row_regs<EPT, kCuThreads, -1, true>(row, a.cols, a.kp, norm_w, a.eps, xq,
@@ -193,7 +153,6 @@ __global__ __launch_bounds__(kCuThreads) void tgemv_cu_kernel(GemvArgs a, int rp
         quant_row_waves<EPT, PW, 0>(row, a.cols, a.kp, norm_w, a.eps, xq, [C](int i) { return perm_pos(i, C); },
                                     &sa_s, red);
     __syncthreads();
-    CTR(9)
     // sum(q): the wavefronts' partials left by the quantizer
     int qsum = 0;
     {
@@ -238,7 +197,6 @@ __global__ __launch_bounds__(kCuThreads) void tgemv_cu_kernel(GemvArgs a, int rp
     int acc = (accs[0] + (accs[1] >> 2)) + ((accs[2] >> 4) + accs[3]);
     acc = xor_sum_down_i<L / 2>(acc);  // every lane of the row holds its sum
     const int dot = acc - qsum;
-    CTR(10)
 
     // epilogue by the row's first lane, no LDS pass: a row pair (2p, 2p + 1)
     // lies in one wavefront (L <= 32 for the paired outputs), the odd row's
@@ -251,11 +209,6 @@ __global__ __launch_bounds__(kCuThreads) void tgemv_cu_kernel(GemvArgs a, int rp
     } else {
         if (out_row) store_single<OUT>(a, 0, vr0 + rs, dot, sa_s);
     }
-#ifdef LBT_GEMV_TRACE
-    CTR(11)
-    __builtin_amdgcn_s_waitcnt(0);
-    CTR(12)
-#endif
 }
 
 namespace {

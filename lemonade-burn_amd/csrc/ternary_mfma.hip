@@ -27,23 +27,6 @@
 
 #include "ternary_common.h"
 
-#ifdef LBT_GEMM_TRACE
-// Debug build only: per-workgroup wall-clock stamps of the GEMM phases.
-__device__ unsigned long long lbt_gemm_trace[4096 * 8];
-#define MTR(i)                                                       \
-    {                                                                \
-        const unsigned b = blockIdx.y * gridDim.x + blockIdx.x;      \
-        if (threadIdx.x == 0 && b < 4096) {                          \
-            lbt_gemm_trace[b * 8 + (i)] = wall_clock64();            \
-            if ((i) == 0 || (i) == 4) lbt_gemm_trace[b * 8 + 5 + (i) / 4] = clock64(); \
-        }                                                            \
-    }
-extern "C" int lbt_debug_gemm_trace(unsigned long long* out) {
-    return (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(lbt_gemm_trace), sizeof(lbt_gemm_trace));
-}
-#else
-#define MTR(i)
-#endif
 
 namespace lbt {
 
@@ -545,7 +528,6 @@ void tgemm2_kernel(GemvArgs a) {
     const int m0 = ty * BM, n0 = tx * BN;
     const int kp = a.kp, M = a.m;
     const int nsteps = kp / RB;
-    MTR(0)
     // a full wavefront block of one matrix takes the lean epilogue; its
     // per-token values are loaded now and divided once the loads of the
     // first slices are out (they arrive during the main loop's prologue)
@@ -652,12 +634,10 @@ void tgemm2_kernel(GemvArgs a) {
         a_issue(pi, p);
         b_issue(pi, bw[p]);
     }
-    MTR(1)
     if constexpr (OUT == kOutF32 || OUT == kOutF32Add || OUT == kOutI32)
         if (fast) epi32_pre<OUT, MS>(a, tok0, swm, et, true);
     wait_vm(std::integral_constant<int, NB + (ST - 1) * (NA + NB)>{});
     __builtin_amdgcn_s_barrier();
-    MTR(2)
     a_read(0, aop[0]);
 
     // Step p (ring slot p % ST and operand buffer p % 2 as constants: no
@@ -716,23 +696,14 @@ void tgemm2_kernel(GemvArgs a) {
     for (int k = 0; k < ST; k++)
 #pragma unroll
         for (int i = 0; i < NB; i++) asm volatile("" ::"v"(bw[k][i]));
-    MTR(3)
 
     if constexpr (OUT == kOutF32 || OUT == kOutF32Add || OUT == kOutI32) {
         if (fast) {
             epi32_full<OUT, MS, NS>(a, acc, tok0, mt0, ro0, et);
-#ifdef LBT_GEMM_TRACE
-            __builtin_amdgcn_s_waitcnt(0);
-#endif
-            MTR(4)
             return;
         }
     }
     mfma_epilogue<OUT, TM>(a, acc, tok0, row0);
-#ifdef LBT_GEMM_TRACE
-    __builtin_amdgcn_s_waitcnt(0);
-#endif
-    MTR(4)
 }
 
 // Prefill GEMM with one workgroup per CU of 8 or more wavefronts (at least

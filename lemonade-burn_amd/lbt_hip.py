@@ -108,7 +108,6 @@ SIGNATURES = {
     "lbt_sample_dev": (i32, [vp, vp, sz, sz, vp, vp, vp]),
     "lbt_model_read_hidden": (i32, [vp, vp, sz]),
     "lbt_model_set_head": (i32, [vp, i32]),
-    "lbt_model_set_decode": (i32, [vp, i32]),
     "lbt_batch_new": (i32, [vp, i32, i32, C.POINTER(vp)]),
     "lbt_batch_free": (None, [vp]),
     "lbt_batch_len": (i32, [vp, i32]),
@@ -384,10 +383,6 @@ class Model:
         h = C.c_void_p()
         self.ctx.check(self.ctx.lib.lbt_cache_new(self.h, C.byref(h)))
         return Cache(self, h)
-
-    def set_decode(self, kind: int):
-        """0: all layers of a decode token in one dispatch (default); 1: one dispatch per kernel (graph)."""
-        self.ctx.check(self.ctx.lib.lbt_model_set_decode(self.h, kind))
 
     def set_head(self, kind: int):
         """0 = the exact tied bf16 head, 1 = the opt-in int8 head (q8head.rs), 2 = the

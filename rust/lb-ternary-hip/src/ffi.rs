@@ -71,7 +71,7 @@ pub struct LbtConfig {
 }
 
 /// Per-class device time of the kernels launched while profiling is on
-/// (0 decode GEMV, 1 GEMM, 2 LM head, 3 attention, 4 other, 5 one-dispatch step).
+/// (0 decode GEMV, 1 GEMM, 2 LM head, 3 attention, 4 other).
 #[repr(C)]
 #[derive(Clone, Copy, Debug, Default)]
 pub struct LbtProf {
@@ -311,7 +311,6 @@ extern "C" {
         ms_decode: *mut f32,
     ) -> c_int;
     pub fn lbt_model_set_head(m: *mut LbtModel, kind: c_int) -> c_int;
-    pub fn lbt_model_set_decode(m: *mut LbtModel, kind: c_int) -> c_int;
     pub fn lbt_model_read_hidden(m: *mut LbtModel, out: *mut f32, n: usize) -> c_int;
 
     // ---- batched decode and the continuous-batching scheduler

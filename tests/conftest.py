@@ -26,14 +26,6 @@ def ctx():
     c.close()
 
 
-def step_built() -> bool:
-    """Whether the library was built with the one-dispatch decode step
-    (LBT_WITH_STEP=1; off by default, it is slower than the graph step)."""
-    import lbt_hip
-
-    return "+step" in lbt_hip.load_library().lbt_version().decode()
-
-
 def announce(msg: str):
     """Names the case on stdout before a GPU step, so a fault is attributable."""
     print(f"[gpu-case] {msg}", flush=True)

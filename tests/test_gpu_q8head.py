@@ -159,7 +159,6 @@ def test_graph_step_survives_head_switches_and_regrowth(ctx):
                         d["max_pos"])
     announce("graph step across head switches and regrowth")
     m = lbt_hip.Model.synthetic(ctx, hip_cfg, 21)
-    m.set_decode(1)
 
     def oracle_tokens(head, prompt, steps):
         om = orc.OracleModel(or_cfg, 21)

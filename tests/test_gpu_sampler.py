@@ -10,7 +10,7 @@ import pytest
 
 import lbt_hip
 import lbt_oracle as orc
-from conftest import announce, step_built
+from conftest import announce
 
 pytestmark = pytest.mark.gpu
 
@@ -112,15 +112,11 @@ def run_model(m, om, params, seed, prompt, steps):
 
 
 @pytest.mark.parametrize("params", [(0.8, 0.9, 0), (1.2, 1.0, 20), (0.0, 1.0, 0), (0.6, 0.7, 5)])
-@pytest.mark.parametrize("path", ["graph", "eager", "step"])
+@pytest.mark.parametrize("path", ["graph", "eager"])
 def test_model_sampling_matches_oracle(ctx, ctx_with, params, path):
-    if path == "step" and not step_built():
-        pytest.skip("one-dispatch step not built (LBT_WITH_STEP=1)")
     c_ = ctx_with(LBT_NO_GRAPH="1") if path == "eager" else ctx
     announce(f"model sampling {path} {params}")
     m = lbt_hip.Model.synthetic(c_, lbt_hip.make_config(**CFG), 31)
-    if path == "step":
-        m.set_decode(0)
     om = orc.OracleModel(orc.config(**CFG), 31)
     prompt = np.array([5, 99, 400, 7, 12, 800], np.uint32)
     for seed in (1, 0xDEADBEEF12345, 2**63 + 7):
