@@ -120,8 +120,10 @@ int lbt_ternary_linear_dev(lbt_ctx* ctx, const lbt_weight* const* ws, size_t n, 
  * round256(m * padded(cols)) + 8 m must be <= 4 MiB (LBT_E_INVALID beyond,
  * e.g. about 600 rows at cols = 6912); profiling must be off.  Results equal
  * lbt_ternary_linear_dev's bit for bit.  Every call on a device shares that
- * device's scratch: calls that overlap on one device (several contexts or
- * host threads) race. */
+ * device's scratch; calls are ordered per device (one at a time on the host,
+ * each stream waiting on the device for the previous call of another
+ * stream), except under stream capture, where no cross-stream wait is
+ * recorded and captured calls overlapping other streams' calls race. */
 int lbt_ternary_linear_dev_noalloc(lbt_ctx* ctx, const lbt_weight* const* ws, size_t n, const float* x,
                                    size_t m, size_t cols, float* const* outs);
 

@@ -996,7 +996,12 @@ __global__ __launch_bounds__(kThreads) void lmhead_mfma_kernel(const uint16_t* W
         const int nb = cols / 64;
         // untracked loads (inline asm) with explicit waits: the compiler's
         // own tracking of these loop-carried buffers waits for every load in
-        // flight, which left no block of loads ahead of the MFMAs
+        // flight, which left no block of loads ahead of the MFMAs.  The
+        // compiler does not know these registers are written late: a copy or
+        // spill of one between its load and land() would read stale data, so
+        // the kernel must stay free of scratch (tests/test_build_checks.py
+        // compiles it and checks the resource report) and every buffer stays
+        // live until land() has waited for it.
         constexpr int NL = 4 * NV + 8;  // 16-byte loads per lane and block
         u32x4 bw[2][NV][4], ah[2][4], al[2][4];
         auto gl = [](u32x4& d, const uint4* p) {
@@ -1106,9 +1111,11 @@ constexpr int kHeadMfmaNV = 2;
 int launch_bf16_mfma_head(lbt_ctx* ctx, const uint16_t* w, int rows, int cols, const float* x, int m,
                           const float* norm_w, float eps, float* logits, unsigned long long* key, float* xn,
                           uint16_t* xs, size_t xs_bytes) {
-    if (m < 2 || m > 64 || !xn || cols % 64 || cols > 16 * kThreads)
-        return set_err(ctx, LBT_E_INVALID, "bf16 matrix-core head: 2..64 rows, cols a multiple of 64");
-    const int tt = m <= 32 ? 1 : 2, mp = 32 * tt;
+    // heads of up to 32 rows stay on the f32 kernel (faster there), so only
+    // the two-token-tile instantiation exists
+    if (m < 33 || m > 64 || !xn || cols % 64 || cols > 16 * kThreads)
+        return set_err(ctx, LBT_E_INVALID, "bf16 matrix-core head: 33..64 rows, cols a multiple of 64");
+    constexpr int tt = 2, mp = 32 * tt;
     if ((size_t)2 * mp * cols * 2 > xs_bytes) return set_err(ctx, LBT_E_INVALID, "bf16 matrix-core head: scratch");
     uint16_t* xh = xs;
     uint16_t* xl = xs + (size_t)mp * cols;
@@ -1118,12 +1125,8 @@ int launch_bf16_mfma_head(lbt_ctx* ctx, const uint16_t* w, int rows, int cols, c
     hipLaunchKernelGGL(bf16_split_kernel, dim3(mp), dim3(kThreads), 0, ctx->stream, xn, m, cols, xh, xl);
     const int rows_per_wg = 32 * kHeadMfmaNV * (4 / tt);
     const dim3 grid((unsigned)((rows + rows_per_wg - 1) / rows_per_wg));
-    if (tt == 1)
-        hipExtLaunchKernelGGL((lmhead_mfma_kernel<1, kHeadMfmaNV>), grid, dim3(kThreads), 0, ctx->stream, e0, e1, 0, w,
-                              rows, cols, xh, xl, m, logits, key);
-    else
-        hipExtLaunchKernelGGL((lmhead_mfma_kernel<2, kHeadMfmaNV>), grid, dim3(kThreads), 0, ctx->stream, e0, e1, 0, w,
-                              rows, cols, xh, xl, m, logits, key);
+    hipExtLaunchKernelGGL((lmhead_mfma_kernel<tt, kHeadMfmaNV>), grid, dim3(kThreads), 0, ctx->stream, e0, e1, 0, w,
+                          rows, cols, xh, xl, m, logits, key);
     LBT_HIP(ctx, hipGetLastError());
     prof_commit(ctx, e0, e1, kProfHead, (double)rows * cols * 2.0);
     return LBT_OK;

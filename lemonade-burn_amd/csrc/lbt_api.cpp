@@ -471,7 +471,10 @@ int lbt_ternary_linear_dev_noalloc(lbt_ctx* ctx, const lbt_weight* const* ws, si
     op.scratch = ctx->noalloc;
     op.scratch_bytes = ctx->noalloc_bytes;
     for (size_t i = 0; i < n; i++) op.out[i] = outs[i];
-    return launch_ternary(ctx, op);
+    // the device's scratch is shared by every context: calls are ordered
+    const int rc2 = noalloc_ordered(ctx->device, ctx->stream, [&] { return launch_ternary(ctx, op); });
+    if (rc2 == LBT_E_DEVICE && ctx->err.empty()) return set_err(ctx, rc2, "lbt_ternary_linear_dev_noalloc: ordering");
+    return rc2;
 }
 
 int lbt_ternary_linear(lbt_ctx* ctx, const lbt_weight* const* ws, size_t n, const float* x, size_t m, size_t cols,

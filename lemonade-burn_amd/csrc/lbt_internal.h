@@ -1,6 +1,7 @@
 // lbt_internal.h -- host-side internals shared by the C ABI, the model loop
 // and the kernel launchers.
 #pragma once
+#include <functional>
 #include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -252,6 +253,10 @@ int act_scratch(lbt_ctx* ctx, const TernaryOp& op, size_t bytes, void** out);
 // Device address of this device's static no-alloc scratch (noalloc.hip),
 // looked up once per device; called by lbt_ctx_create with the device current.
 int noalloc_scratch_init(int device, void** out, size_t* bytes);
+// Runs `launch` (stream `s`) in this device's order of no-alloc calls
+// (noalloc.hip): one at a time on the host, each after the previous call's
+// kernels on the device.
+int noalloc_ordered(int device, hipStream_t s, const std::function<int()>& launch);
 int launch_fill_u64(lbt_ctx* ctx, unsigned long long* p, int n, unsigned long long v);
 // Streaming device copy (16-byte granules, byte tail).
 int launch_copy(lbt_ctx* ctx, void* dst, const void* src, size_t bytes);

@@ -246,9 +246,17 @@ struct lbt_model {
     // graph of one decode step (embed from the argmax key .. LM head), valid
     // for the cache buffers and workspace it was captured with
     int* state = nullptr;  // device {position - 1, output slot, barrier epoch, spare}
-    hipGraphExec_t step_exec = nullptr;
+    // Captured steps are kept per key (buffers, head kind, sampling
+    // parameters) for as long as the buffers they name live: a head switch or
+    // a sampling step captures its own graph beside the others instead of
+    // destroying and re-capturing one.
     static constexpr int kStepKey = 11;
-    const void* step_key[kStepKey] = {};
+    static constexpr int kStepGraphs = 8;
+    struct StepGraph {
+        const void* key[kStepKey];
+        hipGraphExec_t exec;
+    };
+    std::vector<StepGraph> steps;
     // device sampler (sample.hip) of the sampling decode loop: the sampler
     // state and the candidate scratch of one row
     unsigned long long* sstate = nullptr;
@@ -390,14 +398,16 @@ int model_alloc(lbt_model* m) {
     return LBT_OK;
 }
 
-// The captured decode-step graph holds the addresses of the workspace, the
-// token slots and one cache: it is destroyed (after the stream has drained)
-// before any of them is freed, so no live graph ever refers to freed memory.
+// A captured decode-step graph holds the addresses of the workspace, the
+// token slots and one cache: every graph is destroyed (after the stream has
+// drained) before any of them is freed, so no live graph ever refers to
+// freed memory.  Switching the head or the sampling parameters frees nothing
+// and destroys nothing.
 void drop_step_graph(lbt_model* m) {
-    if (!m->step_exec) return;
+    if (m->steps.empty()) return;
     hipStreamSynchronize(m->ctx->stream);
-    hipGraphExecDestroy(m->step_exec);
-    m->step_exec = nullptr;
+    for (auto& g : m->steps) hipGraphExecDestroy(g.exec);
+    m->steps.clear();
 }
 
 int grow_tok_out(lbt_model* m, int need) {
@@ -693,8 +703,11 @@ int decode_steps(lbt_model* m, lbt_cache* c, int n, int slot0, const lbt_sample_
                                             (const void*)(uintptr_t)tb,
                                             (const void*)(uintptr_t)pb,
                                             (const void*)(uintptr_t)(sp ? sp->top_k : 0)};
-    if (!m->step_exec || memcmp(key, m->step_key, sizeof(key)) != 0) {
-        drop_step_graph(m);
+    hipGraphExec_t exec = nullptr;
+    for (auto& sg : m->steps)
+        if (memcmp(key, sg.key, sizeof(key)) == 0) exec = sg.exec;
+    if (!exec) {
+        if ((int)m->steps.size() >= lbt_model::kStepGraphs) drop_step_graph(m);
         hipGraph_t g = nullptr;
         LBT_HIP(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
         const int len = c->len;
@@ -707,16 +720,16 @@ int decode_steps(lbt_model* m, lbt_cache* c, int n, int slot0, const lbt_sample_
             return rc;
         }
         if (e != hipSuccess) return hip_err(ctx, e, "capture decode step");
-        e = hipGraphInstantiate(&m->step_exec, g, nullptr, nullptr, 0);
+        e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
         hipGraphDestroy(g);
-        if (e != hipSuccess) {
-            m->step_exec = nullptr;
-            return hip_err(ctx, e, "instantiate decode step");
-        }
-        memcpy(m->step_key, key, sizeof(key));
+        if (e != hipSuccess) return hip_err(ctx, e, "instantiate decode step");
+        lbt_model::StepGraph sg;
+        memcpy(sg.key, key, sizeof(key));
+        sg.exec = exec;
+        m->steps.push_back(sg);
     }
     if ((rc = launch_set_state(ctx, m->state, c->len - 1, slot0))) return rc;
-    for (int s = 0; s < n; s++) LBT_HIP(ctx, hipGraphLaunch(m->step_exec, ctx->stream));
+    for (int s = 0; s < n; s++) LBT_HIP(ctx, hipGraphLaunch(exec, ctx->stream));
     c->len += n;
     m->last_n = 1;
     return LBT_OK;
@@ -917,7 +930,7 @@ int lbt_model_load(lbt_ctx* ctx, const char* dir, lbt_model** out) {
 void lbt_model_free(lbt_model* m) {
     if (!m) return;
     hipStreamSynchronize(m->ctx->stream);
-    if (m->step_exec) hipGraphExecDestroy(m->step_exec);
+    drop_step_graph(m);
     if (m->sstate) hipFree(m->sstate);
     if (m->sscratch) hipFree(m->sscratch);
     void* bufs[] = {m->wbuf, m->fbuf, m->embed, m->cos_t, m->sin_t, m->x,   m->q,       m->k,
@@ -1172,8 +1185,7 @@ int lbt_model_set_head(lbt_model* m, int kind) {
         m->q8 = q;
         m->q8s = qs;
     }
-    if (kind != m->head_kind) drop_step_graph(m);
-    m->head_kind = kind;
+    m->head_kind = kind;  // the step graphs are keyed by it
     return LBT_OK;
 }
 

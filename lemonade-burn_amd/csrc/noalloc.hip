@@ -10,8 +10,13 @@
 // code the array's name is a host-side stand-in, not a device address.
 // Every call on a device shares the array and leaves its contents behind;
 // the quantizer writes every byte a later kernel reads (padding included),
-// so nothing needs clearing.  Calls that overlap on one device (two
-// contexts' streams, several host threads) race.
+// so nothing needs clearing.  Calls on one device are ordered: each call runs
+// under the device's host mutex and, when the previous call came from
+// another stream, first makes its stream wait (on the device) for that call's
+// completion event.  Under stream capture no event is waited for or recorded
+// (a captured stream cannot wait on work outside its capture): captured calls
+// that overlap other streams' calls on the device race.
+#include <functional>
 #include <mutex>
 
 #include "lbt_internal.h"
@@ -26,6 +31,14 @@ static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 std::mutex g_mu;
 void* g_ptr[kMaxDevices] = {};
 
+// per device: the order of calls
+struct DevOrder {
+    std::mutex mu;
+    hipEvent_t done = nullptr;      // recorded after the last call's kernels
+    hipStream_t last = nullptr;     // the stream of the last call
+};
+DevOrder g_order[kMaxDevices];
+
 }  // namespace
 
 namespace lbt {
@@ -38,10 +51,28 @@ int noalloc_scratch_init(int device, void** out, size_t* bytes) {
     if (!g_ptr[device]) {
         void* p = nullptr;
         if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return LBT_E_DEVICE;
+        hipEvent_t ev = nullptr;
+        if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess) return LBT_E_DEVICE;
+        g_order[device].done = ev;
         g_ptr[device] = p;
     }
     *out = g_ptr[device];
     *bytes = kNoAllocScratchBytes;
+    return LBT_OK;
+}
+
+int noalloc_ordered(int device, hipStream_t s, const std::function<int()>& launch) {
+    if (device < 0 || device >= kMaxDevices || !g_order[device].done) return LBT_E_DEVICE;
+    DevOrder& o = g_order[device];
+    std::lock_guard<std::mutex> lk(o.mu);
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cs) != hipSuccess) return LBT_E_DEVICE;
+    const bool capturing = cs != hipStreamCaptureStatusNone;
+    if (!capturing && o.last && o.last != s && hipStreamWaitEvent(s, o.done, 0) != hipSuccess) return LBT_E_DEVICE;
+    const int rc = launch();
+    if (rc || capturing) return rc;
+    if (hipEventRecord(o.done, s) != hipSuccess) return LBT_E_DEVICE;
+    o.last = s;
     return LBT_OK;
 }
 

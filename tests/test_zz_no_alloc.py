@@ -1,6 +1,7 @@
 """lbt_ternary_linear_dev_noalloc (the entry point that allocates nothing: its
 several-row activations live in a static per-device scratch) against
-lbt_ternary_linear_dev, bit for bit, through the C ABI: two calls in a row,
+lbt_ternary_linear_dev and the oracle (ActQuant + ternary_gemm_multi's f32
+epilogue), bit for bit, through the C ABI: two calls in a row,
 the second smaller (fewer rows, a narrower padded width whose padding the
 first call's rows had filled), the MFMA and the single-token paths, and the
 size limit."""
@@ -57,11 +58,15 @@ def run(ctx, fn, ws, x):
         d.free()
 
 
-def weights(ctx, rng, shapes, cols):
+def weights(ctx, rng, shapes, cols, keep=None):
+    """Uploaded ternary matrices; `keep` collects (packed, rows, scale) for the oracle."""
     out = []
     for rows, s in shapes:
         t = rng.choice(np.array([-1, 0, 1], np.int8), size=(rows, cols), p=[0.3, 0.4, 0.3])
-        out.append(ctx.upload(orc.pack(t), rows, cols, s))
+        packed = orc.pack(t)
+        out.append(ctx.upload(packed, rows, cols, s))
+        if keep is not None:
+            keep.append((packed, rows, s))
     return out
 
 
@@ -70,12 +75,16 @@ def test_noalloc_equals_linear_dev_twice(ctx, cases):
     rng = np.random.default_rng(11)
     for i, (m, cols) in enumerate(cases):
         announce(f"noalloc call {i}: m={m} cols={cols}")
-        ws = weights(ctx, rng, [(2560, 0.9), (640, 1.1), (640, 1.3)][: 3 if i == 0 else 1], cols)
+        kept = []
+        ws = weights(ctx, rng, [(2560, 0.9), (640, 1.1), (640, 1.3)][: 3 if i == 0 else 1], cols, kept)
         x = rng.standard_normal((m, cols)).astype(np.float32)
         got = run(ctx, ctx.lib.lbt_ternary_linear_dev_noalloc, ws, x)
         ref = run(ctx, ctx.lib.lbt_ternary_linear_dev, ws, x)
-        for g, r in zip(got, ref):
+        q, s_a, qsum = orc.quantize_acts(x)
+        for g, r, (packed, rows, s_w) in zip(got, ref, kept):
             assert np.array_equal(g, r), f"call {i} m={m} cols={cols}"
+            exp = orc.gemm_f32(packed, rows, cols, s_w, q, s_a, qsum)
+            assert np.array_equal(g, exp), f"oracle, call {i} m={m} cols={cols}"
         for w in ws:
             w.free()
 
