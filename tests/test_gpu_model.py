@@ -208,7 +208,7 @@ def test_full_2b_prompt64_decode_matches_oracle(ctx):
     (uniform-random tokens, one per position) check the decode logits at
     distinct inputs: within 1e-3 rel / 1e-2 abs of the oracle (in fact bit
     for bit) and the same argmax at every position, with the smallest
-    top-1/top-2 margin printed."""
+    top-1/top-2 margin above that tolerance."""
     steps, forced = 128, 64
     hip_cfg = lbt_hip.make_config()
     or_cfg = orc.config()
