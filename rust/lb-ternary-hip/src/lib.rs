@@ -14,11 +14,17 @@
 //!   the 1-3 matrices sharing an input, the bf16 linear of the tied head;
 //! * [`model::HipBitNet`] is `BitNet::{load, new_cache, forward}`
 //!   (model.rs:149-374) with the whole token loop on the device, plus the
-//!   device-side greedy and sampling loops of the server (main.rs:102-160).
+//!   device-side greedy and sampling loops of the server (main.rs:102-160);
+//! * with the `burn` feature, [`bitnet::BitNet`] / [`bitnet::KvCache`] carry
+//!   the reference's exact signatures (`load(&Path, &Device)`,
+//!   `new_cache() -> KvCache`, `forward(..) -> Tensor<2>`), so lb-server and
+//!   lb-run switch by one `use` line.
 //!
 //! Errors are `Err(String)` with the library's message (the reference's CPU
 //! kernels assert; its CubeCL crate returned `Result<_, String>`).
 
+#[cfg(feature = "burn")]
+pub mod bitnet;
 pub mod ffi;
 pub mod model;
 

@@ -133,3 +133,49 @@ def test_mapping_examples():
     assert c_type_to_rust("float* const* outs") == "*const *mut f32"
     assert c_type_to_rust("lbt_ctx** out") == "*mut *mut LbtCtx"
     assert c_type_to_rust("const char* r") == "*const c_char"
+
+
+# ---- the `burn` facade: lb_model::BitNet's own signatures --------------------
+# The reference's declarations (crates/lb-model/src/model.rs:149, :234, :305)
+# and the calls lb-server / lb-run make (lb-server/src/main.rs:104-107,153,
+# lb-model/src/bin/lb-run.rs:94-106), normalised: what the facade must accept.
+REF_SIGS = {
+    "load": "pub fn load(dir: &Path, device: &Device) -> Result<Self>",
+    "new_cache": "pub fn new_cache(&self) -> KvCache",
+    "forward": "pub fn forward(&self, tokens: &[u32], cache: &mut KvCache, all_logits: bool) -> Tensor<2>",
+}
+REF_MODEL = Path("/root/reference/crates/lb-model/src/model.rs")
+
+
+def facade_sigs():
+    text = (REPO / "rust" / "lb-ternary-hip" / "src" / "bitnet.rs").read_text()
+    body = text[text.index("impl BitNet {"):]
+    out = {}
+    for m in re.finditer(r"(pub fn (\w+)\((.*?)\)\s*->\s*([^{]+?))\s*\{", body, flags=re.S):
+        out[m.group(2)] = " ".join(m.group(1).split())
+    return out
+
+
+def norm(sig: str) -> str:
+    # anyhow::Result and Result are the same type in lb-model (use anyhow::Result)
+    return sig.replace("anyhow::Result", "Result")
+
+
+def test_burn_facade_has_the_reference_signatures():
+    got = facade_sigs()
+    for name, sig in REF_SIGS.items():
+        assert norm(got[name]) == sig, (name, got[name])
+    text = (REPO / "rust" / "lb-ternary-hip" / "src" / "bitnet.rs").read_text()
+    assert re.search(r"pub struct KvCache \{[^}]*pub len: usize,[^}]*pub cap: usize,", text, flags=re.S)
+
+
+def test_reference_signatures_are_current():
+    """REF_SIGS restates the reference's declarations (checked where the
+    reference tree is present; it is not on the GPU box)."""
+    if not REF_MODEL.exists():
+        import pytest
+
+        pytest.skip("reference tree not present")
+    text = " ".join(REF_MODEL.read_text().split())
+    for sig in REF_SIGS.values():
+        assert sig in text, sig
