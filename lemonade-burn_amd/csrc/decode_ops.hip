@@ -660,6 +660,154 @@ __global__ __launch_bounds__(NT) void lmhead_batch_kernel(const void* W, const f
     }
 }
 
+// The bf16 head of several tokens with the weight stream kept in flight:
+// one wavefront per SIMD (256 threads, 16 token rows in LDS), each taking R
+// rows at a time; the raw bf16 chunks of its next R rows load (untracked
+// loads, explicit waits) while the current ones compute, and a chunk is
+// widened to f32 once for all 16 tokens.  Every (token, row) accumulator
+// takes its products in the order of lmhead_batch_kernel (chunk i, then
+// element e) and the accumulators reduce by the same recursive halving, so
+// the logits are those of lmhead_batch_kernel and of the one-token head bit
+// for bit.
+template <int R, int NCH, int TG, int NT>
+__global__ __launch_bounds__(NT) void lmhead_stream_kernel(const uint16_t* W, int rows, int cols, const float* xn,
+                                                           int m, int tile_rows, float* logits,
+                                                           unsigned long long* key) {
+    constexpr int A = R * TG, NW = NT / 64;
+    static_assert(A == 32 || A == 64, "32 or 64 accumulators per lane");
+    extern __shared__ __align__(16) float xs[];  // [TG][cols]
+    const int ngroups = (m + TG - 1) / TG;
+    const int grp = blockIdx.x % ngroups, tile = blockIdx.x / ngroups;
+    const int t0 = grp * TG, nt = m - t0 < TG ? m - t0 : TG;
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int nchunks = cols >> 3;
+    const int r_begin = tile * tile_rows, r_end = r_begin + tile_rows < rows ? r_begin + tile_rows : rows;
+    const int nblk = r_end > r_begin + w * R ? (r_end - r_begin - w * R + NW * R - 1) / (NW * R) : 0;
+    // the first block's weights go out before the token rows are staged
+    u32x4 B0[R][NCH], B1[R][NCH];
+    auto issue = [&](int b, u32x4 (&d)[R][NCH]) {
+        const int rb = r_begin + w * R + b * NW * R;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const int row = rb + r < r_end ? rb + r : r_begin;  // past the end: a row of the tile (unused)
+            const uint4* wr = (const uint4*)(W + (size_t)row * cols);
+#pragma unroll
+            for (int i = 0; i < NCH; i++) {
+                const int c = lane + 64 * i;
+                d[r][i] = ld_u4_async_nt(wr + (c < nchunks ? c : 0));
+            }
+        }
+    };
+    // all but the block issued last have landed (loads complete in issue order)
+    auto land = [&](u32x4 (&d)[R][NCH]) {
+        vm_wait<R * NCH>();
+#pragma unroll
+        for (int r = 0; r < R; r++)
+#pragma unroll
+            for (int i = 0; i < NCH; i++) pin(d[r][i]);
+    };
+    // this lane's (token, row) after the reduction: accumulator (lane >> 1) & 31
+    // (A = 32, lane pairs hold the same sum) or lane (A = 64)
+    const int my_a = A == 32 ? ((lane >> 1) & 31) : lane;
+    const int my_t = my_a / R, my_r = my_a % R;
+    const bool writer = A == 64 || (lane & 1) == 0;
+    unsigned long long best = 0ull;  // of token my_t
+    auto compute = [&](int b, const u32x4 (&d)[R][NCH]) {
+        float acc[A];
+#pragma unroll
+        for (int q = 0; q < A; q++) acc[q] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NCH; i++) {
+            const int c = lane + 64 * i;
+            if (c < nchunks) {
+                float wf[R][8];
+#pragma unroll
+                for (int r = 0; r < R; r++) {
+                    const u32x4 v = d[r][i];
+                    wf[r][0] = bf_lo(v.x);
+                    wf[r][1] = bf_hi(v.x);
+                    wf[r][2] = bf_lo(v.y);
+                    wf[r][3] = bf_hi(v.y);
+                    wf[r][4] = bf_lo(v.z);
+                    wf[r][5] = bf_hi(v.z);
+                    wf[r][6] = bf_lo(v.w);
+                    wf[r][7] = bf_hi(v.w);
+                }
+#pragma unroll
+                for (int t = 0; t < TG; t++) {
+                    const float* xt = xs + t * cols;
+                    const float4 x0 = *(const float4*)(xt + 8 * c);
+                    const float4 x1 = *(const float4*)(xt + 8 * c + 4);
+                    const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+                    for (int r = 0; r < R; r++)
+#pragma unroll
+                        for (int e = 0; e < 8; e++)
+                            acc[t * R + r] = __builtin_fmaf(wf[r][e], xv[e], acc[t * R + r]);
+                }
+            }
+        }
+        float a;
+        {
+            float h16[16], h8[8], h4[4], h2[2], h1[1];
+            if constexpr (A == 64) {
+                float h32[32];
+                halve<32>(acc, h32);
+                halve<16>(h32, h16);
+            } else {
+                halve<32>(acc, h16);
+            }
+            halve<A == 64 ? 8 : 16>(h16, h8);
+            halve<A == 64 ? 4 : 8>(h8, h4);
+            halve<A == 64 ? 2 : 4>(h4, h2);
+            halve<A == 64 ? 1 : 2>(h2, h1);
+            a = A == 64 ? h1[0] : xor_add<1>(h1[0]);
+        }
+        const int row = r_begin + w * R + b * NW * R + my_r;
+        if (writer && my_t < nt && row < r_end) {
+            if (logits) logits[(size_t)(t0 + my_t) * rows + row] = a;
+            const unsigned long long k = argmax_key(a, (uint32_t)row);
+            best = k > best ? k : best;
+        }
+    };
+    // the first block's weights go out before the token rows are staged
+    issue(0, B0);
+    for (int i = tid * 4; i < nt * cols; i += NT * 4)
+        *(float4*)(xs + i) = *(const float4*)(xn + (size_t)t0 * cols + i);
+    for (int i = nt * cols + tid; i < TG * cols; i += NT) xs[i] = 0.0f;  // unused token rows
+    __syncthreads();
+    // loads, waits and pins are unconditional (no copy of a register still
+    // being loaded); blocks past the last are loaded and not used
+    for (int b = 0; b < nblk; b += 2) {
+        issue(b + 1, B1);
+        land(B0);
+        compute(b, B0);
+        issue(b + 2, B0);
+        land(B1);
+        if (b + 1 < nblk) compute(b + 1, B1);
+    }
+    vm_wait<0>();
+#pragma unroll
+    for (int r = 0; r < R; r++)
+#pragma unroll
+        for (int i = 0; i < NCH; i++) {
+            keep(B0[r][i]);
+            keep(B1[r][i]);
+        }
+    // one atomic per (workgroup, token): the lanes' keys meet in LDS
+    __syncthreads();
+    constexpr int KW = A == 64 ? 64 : 32;  // keys per wavefront
+    unsigned long long* wbest = (unsigned long long*)xs;  // [NW][KW]
+    if (writer) wbest[w * KW + (A == 64 ? lane : (lane >> 1))] = best;
+    __syncthreads();
+    if (key && tid < nt) {
+        unsigned long long bk = 0ull;
+        for (int i = 0; i < NW * KW; i++)
+            if (i % KW / R == tid) bk = wbest[i] > bk ? wbest[i] : bk;
+        if (bk) atomicMax(&key[t0 + tid], bk);
+    }
+}
+
 __global__ void set_state_kernel(int* state, int pos, int slot) {
     if (threadIdx.x == 0) {
         state[0] = pos;
@@ -900,8 +1048,29 @@ int launch_head(lbt_ctx* ctx, const void* w, const float* rscale, int rows, int 
     hipExtLaunchKernelGGL((lmhead_batch_kernel<kR, kLmChunks, TGv, Q8v, NTv>), dim3(tiles * ngroups), dim3(NTv), lds, \
                           ctx->stream, e0, e1, 0, w, rscale, rows, cols, xn, m, tile_rows, logits, key)
         if (big) {
-            if (q8) LBT_HEAD_LAUNCH(16, true, 512);
-            else LBT_HEAD_LAUNCH(16, false, 512);
+            if (q8) {
+                LBT_HEAD_LAUNCH(16, true, 512);
+            } else if (!ctx->tune.head_batch_classic) {
+                // one wavefront per SIMD, weights a block ahead: ~one workgroup per CU
+                constexpr int SR = 2, SNT = 512;  // rows per block, threads
+                int st = ctx->cus / ngroups;
+                if (st < 1) st = 1;
+                int str = (rows + st - 1) / st;
+                str = (str + (SNT / 64) * SR - 1) / ((SNT / 64) * SR) * ((SNT / 64) * SR);
+                st = (rows + str - 1) / str;
+                static bool attr2 = false;
+                if (!attr2) {
+                    (void)hipFuncSetAttribute((const void*)lmhead_stream_kernel<SR, kLmChunks, 16, SNT>,
+                                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+                    (void)hipGetLastError();
+                    attr2 = true;
+                }
+                hipExtLaunchKernelGGL((lmhead_stream_kernel<SR, kLmChunks, 16, SNT>), dim3(st * ngroups), dim3(SNT),
+                                      lds, ctx->stream, e0, e1, 0, (const uint16_t*)w, rows, cols, xn, m, str, logits,
+                                      key);
+            } else {
+                LBT_HEAD_LAUNCH(16, false, 512);
+            }
         } else {
             if (q8) LBT_HEAD_LAUNCH(kTG, true, kThreads);
             else LBT_HEAD_LAUNCH(kTG, false, kThreads);

@@ -34,6 +34,7 @@ LbtTuning read_tuning() {
         t.attn_wide = v ? (atoi(v) != 0 ? 1 : 0) : -1;
     }
     t.head_tg8 = getenv("LBT_HEAD_TG8") != nullptr;
+    t.head_batch_classic = getenv("LBT_HEAD_BATCH_CLASSIC") != nullptr;
     t.gemv_pw = num("LBT_GEMV_PW", 4) == 16 ? 16 : 4;
     t.gemv_pwo = num("LBT_GEMV_PWO", 16) == 4 ? 4 : 16;
     return t;

@@ -19,7 +19,7 @@ HIPCC = "/opt/rocm/bin/hipcc"
 
 # source file -> (mangled kernel name prefix, region checked)
 KERNELS = {
-    "decode_ops.hip": [("_ZN3lbt18lmhead_mfma_kernel", "all"), ("_ZN3lbt13lmhead_kernel", "all"),
+    "decode_ops.hip": [("_ZN3lbt18lmhead_mfma_kernel", "all"), ("_ZN3lbt13lmhead_kernel", "all"), ("_ZN3lbt20lmhead_stream_kernel", "all"),
                        ("_ZN3lbt13q8head_kernel", "all")],
     "ternary_mfma.hip": [("_ZN3lbt13tgemm2_kernel", "mfma"), ("_ZN3lbt13tgemm3_kernel", "mfma")],
 }

@@ -147,7 +147,10 @@ def test_multi_matches_separate_bit_for_bit(ctx):
 
 def test_bf16_linear(ctx):
     rng = np.random.default_rng(9)
-    for rows, cols, m in [(37, 2584, 1), (1000, 2560, 3), (128256 // 8, 2560, 1)]:
+    # m >= 9: the batched head's 16-token groups (lmhead_stream_kernel), ragged
+    # groups and row tiles included
+    for rows, cols, m in [(37, 2584, 1), (1000, 2560, 3), (128256 // 8, 2560, 1), (1000, 2560, 9),
+                          (3001, 2560, 37), (8000, 2560, 64)]:
         announce(f"bf16 {rows}x{cols} m={m}")
         wf = (rng.standard_normal((rows, cols)) * 0.05).astype(np.float32)
         wb = orc.f32_to_bf16(wf).reshape(rows, cols)
@@ -305,3 +308,20 @@ def test_memcpy_d2d_sizes(ctx):
         assert np.array_equal(got, exp)
         lib.lbt_dev_free(ctx.h, a)
         lib.lbt_dev_free(ctx.h, b)
+
+
+def test_batched_bf16_head_kernels_agree(ctx, ctx_with):
+    """The batched bf16 head on the weight-streaming kernel (default) and on
+    lmhead_batch_kernel (LBT_HEAD_BATCH_CLASSIC) give the same logits bit for
+    bit, at the 2B head's width for 16..64 rows."""
+    rng = np.random.default_rng(31)
+    rows, cols = 20000, 2560
+    wb = orc.f32_to_bf16((rng.standard_normal((rows, cols)) * 0.05).astype(np.float32)).reshape(rows, cols)
+    c2 = ctx_with(LBT_HEAD_BATCH_CLASSIC="1")
+    w1, w2 = ctx.bf16_upload(wb), c2.bf16_upload(wb)
+    for m in (16, 33, 64):
+        announce(f"batched head kernels m={m}")
+        x = rng.standard_normal((m, cols)).astype(np.float32)
+        assert np.array_equal(ctx.bf16_linear(w1, x), c2.bf16_linear(w2, x)), m
+    w1.free()
+    w2.free()
