@@ -677,7 +677,11 @@ __global__ __launch_bounds__(NT) void lmhead_stream_kernel(const uint16_t* W, in
     static_assert(A == 32 || A == 64, "32 or 64 accumulators per lane");
     extern __shared__ __align__(16) float xs[];  // [TG][cols]
     const int ngroups = (m + TG - 1) / TG;
-    const int grp = blockIdx.x % ngroups, tile = blockIdx.x / ngroups;
+    // the token groups of a row tile are ntiles apart in the grid: with ntiles
+    // a multiple of 8 they sit on one XCD (workgroup b on XCD b mod 8) and
+    // share its L2's copy of the tile's weights
+    const int ntiles = (int)gridDim.x / ngroups;
+    const int grp = blockIdx.x / ntiles, tile = blockIdx.x % ntiles;
     const int t0 = grp * TG, nt = m - t0 < TG ? m - t0 : TG;
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const int nchunks = cols >> 3;
