@@ -37,6 +37,8 @@ LbtTuning read_tuning() {
     t.head_batch_classic = getenv("LBT_HEAD_BATCH_CLASSIC") != nullptr;
     t.gemv_pw = num("LBT_GEMV_PW", 4) == 16 ? 16 : 4;
     t.gemv_pwo = num("LBT_GEMV_PWO", 16) == 4 ? 4 : 16;
+    t.gemm_ksplit = (int)num("LBT_GEMM_KSPLIT", 0);
+    if (t.gemm_ksplit < 0 || t.gemm_ksplit > 16) t.gemm_ksplit = 0;
     return t;
 }
 
@@ -184,6 +186,7 @@ void lbt_ctx_destroy(lbt_ctx* ctx) {
     for (auto e : ctx->free_events) hipEventDestroy(e);
     if (ctx->ws) hipFree(ctx->ws);
     if (ctx->qws) hipFree(ctx->qws);
+    if (ctx->kws) hipFree(ctx->kws);
     if (ctx->sws) hipFree(ctx->sws);
     hipStreamDestroy(ctx->stream);
     delete ctx;

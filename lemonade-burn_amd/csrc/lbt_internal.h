@@ -28,6 +28,7 @@ struct LbtTuning {
     bool head_batch_classic = false;  // LBT_HEAD_BATCH_CLASSIC: batched bf16 head on lmhead_batch_kernel (16-token groups)
     int gemv_pw = 4;          // LBT_GEMV_PW=16: single-token GEMV prologue (f32 rows) on all 16 wavefronts (default 4)
     int gemv_pwo = 16;        // LBT_GEMV_PWO=4: ... of the o projection (attention-combine rows) on four (default 16)
+    int gemm_ksplit = 0;      // LBT_GEMM_KSPLIT: k ranges of the pipelined GEMM's small grids (0 auto, 1 off)
 };
 
 struct lbt_ctx {
@@ -52,6 +53,10 @@ struct lbt_ctx {
     // grow-only device scratch of the prefill GEMM (quantized activations)
     void* qws = nullptr;
     size_t qws_bytes = 0;
+    // grow-only split-k scratch: kKsplitTiles tile counters (zero between
+    // launches) then the partial tiles
+    void* kws = nullptr;
+    size_t kws_bytes = 0;
     // grow-only scratch of lbt_sample_dev
     void* sws = nullptr;
     size_t sws_bytes = 0;

@@ -33,6 +33,13 @@ struct GemvArgs {
     const float* sin_t;
     uint16_t* kc;
     uint16_t* vc;
+    // split-k GEMM: the k steps are cut into ksplit ranges (gridDim.z); each
+    // workgroup stores its int32 partial tile to kpart and the last of a
+    // tile's workgroups (counter kcnt[tile], left at zero) adds them up and
+    // runs the epilogue
+    int ksplit;
+    int* kcnt;
+    int* kpart;
 };
 
 // Element i (0..2) of a 3-array of uniform values by selects between scalar

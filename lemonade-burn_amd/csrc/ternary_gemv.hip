@@ -296,6 +296,7 @@ hipError_t launch_t(const GemvArgs& a, int nch, int tiles, int in_mode, int out_
 
 int make_gemv_args(lbt_ctx* ctx, const TernaryOp& op, GemvArgs& a) {
     a = GemvArgs{};
+    a.ksplit = 1;
     const int nmat = op.nmat;
     if (nmat < 1 || nmat > 3 || op.cols <= 0 || op.m <= 0) return set_err(ctx, LBT_E_INVALID, "ternary: bad shape");
     if (op.out_mode == kOutRelu2 && (nmat != 2 || op.rows[0] != op.rows[1]))

@@ -505,6 +505,52 @@ __device__ __forceinline__ void g2_tile(int& tx, int& ty) {
     ty = band * G + r % gsz;
 }
 
+// Split-k: the partial int32 tile of every workgroup goes to kpart with
+// device-coherent stores ([tile][range][wavefront][ms][s][r][lane], so each
+// store instruction writes 256 contiguous bytes); once they are acknowledged
+// the workgroup counts itself in at kcnt[tile].  The last one to arrive
+// resets the counter, reads the other ranges' partials (device-coherent
+// loads) and adds them to its own: integer sums, so the result has the same
+// bits in any arrival order.  Returns whether this workgroup is the last.
+template <int MS, int NS>
+__device__ __forceinline__ bool split_reduce(const GemvArgs& a, v16i (&acc)[MS][NS], int tx, int ty, int w, int lane) {
+    constexpr int CW = MS * NS * 1024;  // ints per wavefront
+    __shared__ int last;
+    const int tile = ty * (int)gridDim.x + tx, zs = (int)blockIdx.z, ks = a.ksplit;
+    int* base = a.kpart + (size_t)tile * ks * (4 * CW) + w * CW + lane;
+    int* mine = base + (size_t)zs * (4 * CW);
+#pragma unroll
+    for (int ms = 0; ms < MS; ms++)
+#pragma unroll
+        for (int s = 0; s < NS; s++)
+#pragma unroll
+            for (int r = 0; r < 16; r++)
+                __hip_atomic_store(mine + ((ms * NS + s) * 16 + r) * 64, acc[ms][s][r], __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int old = __hip_atomic_fetch_add(a.kcnt + tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last = old == ks - 1;
+        if (old == ks - 1) __hip_atomic_store(a.kcnt + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!last) return false;
+    for (int z = 0; z < ks; z++) {
+        if (z == zs) continue;
+        const int* src = base + (size_t)z * (4 * CW);
+#pragma unroll
+        for (int ms = 0; ms < MS; ms++)
+#pragma unroll
+            for (int s = 0; s < NS; s++)
+#pragma unroll
+                for (int r = 0; r < 16; r++)
+                    acc[ms][s][r] += __hip_atomic_load(src + ((ms * NS + s) * 16 + r) * 64, __ATOMIC_RELAXED,
+                                                       __HIP_MEMORY_SCOPE_AGENT);
+    }
+    return true;
+}
+
 template <int OUT, int MS, int NS, int KB, int ST = kG2Stages>
 // Two wavefronts per SIMD: without the bound the compiler moved the
 // accumulators to AGPRs beyond 256 registers (one wavefront per SIMD, 20%
@@ -527,7 +573,9 @@ void tgemm2_kernel(GemvArgs a) {
     g2_tile(tx, ty);
     const int m0 = ty * BM, n0 = tx * BN;
     const int kp = a.kp, M = a.m;
-    const int nsteps = kp / RB;
+    // this workgroup's k steps: range blockIdx.z of a.ksplit
+    const int nk = kp / RB, zs = (int)blockIdx.z;
+    const int ps0 = (int)((long)nk * zs / a.ksplit), ps1 = (int)((long)nk * (zs + 1) / a.ksplit);
     // a full wavefront block of one matrix takes the lean epilogue; its
     // per-token values are loaded now and divided once the loads of the
     // first slices are out (they arrive during the main loop's prologue)
@@ -627,10 +675,10 @@ void tgemm2_kernel(GemvArgs a) {
     // end re-load the last one: cache hits into a stage nobody reads, so the
     // count of loads in flight is the same on every step), then the A
     // operands of step 0.
-    const int plast = nsteps - 1;
+    const int plast = ps1 - 1;
 #pragma unroll
     for (int p = 0; p < ST; p++) {
-        const int pi = p < plast ? p : plast;
+        const int pi = ps0 + p < plast ? ps0 + p : plast;
         a_issue(pi, p);
         b_issue(pi, bw[p]);
     }
@@ -680,10 +728,10 @@ void tgemm2_kernel(GemvArgs a) {
     // unrolled over a multiple of both the ring (slot) and the operand
     // double buffer (cur), so both are constants in every step
     constexpr int U = ST % 2 == 0 ? ST : 2 * ST;
-    for (int p = 0; p < nsteps; p += U)
+    for (int p = ps0; p < ps1; p += U)
         seq_while(std::make_integer_sequence<int, U>{}, [&](auto ic) {
             constexpr int i = decltype(ic)::value;
-            if (p + i >= nsteps) return false;
+            if (p + i >= ps1) return false;
             step(p + i, std::integral_constant<int, i % ST>{}, std::integral_constant<int, i & 1>{});
             return true;
         });
@@ -697,6 +745,7 @@ void tgemm2_kernel(GemvArgs a) {
 #pragma unroll
         for (int i = 0; i < NB; i++) asm volatile("" ::"v"(bw[k][i]));
 
+    if (a.ksplit > 1 && !split_reduce<MS, NS>(a, acc, tx, ty, w, lane)) return;
     if constexpr (OUT == kOutF32 || OUT == kOutF32Add || OUT == kOutI32) {
         if (fast) {
             epi32_full<OUT, MS, NS>(a, acc, tok0, mt0, ro0, et);
@@ -1019,6 +1068,53 @@ int qws_reserve(lbt_ctx* ctx, size_t bytes, void** out) {
     return LBT_OK;
 }
 
+namespace {
+constexpr int kKsplitTiles = 1024;  // tile counters of the split-k scratch
+constexpr int kKsplitMax = 3;        // k ranges per tile
+constexpr int kKsplitMinSteps = 16;  // 128-k steps per range
+
+// k ranges for a pipelined-GEMM grid of `tiles` workgroups of `tile_ints`
+// int32 accumulators over nk steps: as many as the two workgroup slots of
+// every CU hold, at most kKsplitMax and at least kKsplitMinSteps steps each
+// (the partials' hand-off costs ~2-3 us, so only long k pays: 2560 x 6912
+// at M = 128 14.0 -> 10.6 us with 3 ranges, at M = 256 14.6 -> 12.6 us;
+// 6912 x 2560 at M = 128, 20 steps, 8.4 -> 10.2 us with 2, so 1 there;
+// wavefront groups splitting k inside a workgroup were no faster); 1 where
+// the call brings its own scratch (the allocation-free entry point) or a
+// stream capture is under way with too small a split-k scratch.  Sets
+// a.ksplit / kcnt / kpart.
+int pick_ksplit(lbt_ctx* ctx, const TernaryOp& op, GemvArgs& a, long tiles, int tile_ints, int nk) {
+    a.ksplit = 1;
+    if (op.scratch || tiles > kKsplitTiles) return LBT_OK;
+    int ks = ctx->tune.gemm_ksplit;
+    if (ks == 0) {
+        const long fill = 2L * ctx->cus / tiles;
+        ks = (int)(fill < kKsplitMax ? fill : kKsplitMax);
+        if (ks > nk / kKsplitMinSteps) ks = nk / kKsplitMinSteps;
+    }
+    if (ks > nk) ks = nk;
+    if (ks < 2) return LBT_OK;
+    const size_t need = (size_t)kKsplitTiles * 4 + (size_t)tiles * ks * tile_ints * 4;
+    if (need > ctx->kws_bytes) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(ctx->stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return LBT_OK;
+        if (ctx->kws) {
+            hipStreamSynchronize(ctx->stream);
+            hipFree(ctx->kws);
+            ctx->kws = nullptr;
+            ctx->kws_bytes = 0;
+        }
+        LBT_HIP(ctx, hipMalloc(&ctx->kws, need));
+        LBT_HIP(ctx, hipMemsetAsync(ctx->kws, 0, (size_t)kKsplitTiles * 4, ctx->stream));
+        ctx->kws_bytes = need;
+    }
+    a.ksplit = ks;
+    a.kcnt = (int*)ctx->kws;
+    a.kpart = (int*)ctx->kws + kKsplitTiles;
+    return LBT_OK;
+}
+}  // namespace
+
 int act_scratch(lbt_ctx* ctx, const TernaryOp& op, size_t bytes, void** out) {
     if (!op.scratch) return qws_reserve(ctx, bytes, out);
     if (bytes > op.scratch_bytes) return set_err(ctx, LBT_E_INVALID, "ternary: activations exceed the given scratch");
@@ -1116,9 +1212,16 @@ int launch_ternary_mfma(lbt_ctx* ctx, const TernaryOp& op_in) {
         else
             e = launch_tiles3<1, 8, 4, 1, 1, kG3Stages>(a, op.out_mode, g3, ctx->stream, e0, e1);
     } else if (gmode != 4 && (t128 >= 200 || gmode == 5)) {
-        e = launch_tiles2<2, 2, 1>(a, op.out_mode, g128, ctx->stream, e0, e1);
+        // grids that leave workgroup slots idle split k (gridDim.z ranges)
+        dim3 g = g128;
+        if ((rc = pick_ksplit(ctx, op, a, t128, 4 * 4 * 1024, a.kp / 128))) return rc;
+        g.z = (unsigned)a.ksplit;
+        e = launch_tiles2<2, 2, 1>(a, op.out_mode, g, ctx->stream, e0, e1);
     } else {
-        e = launch_tiles2<1, 1, 1>(a, op.out_mode, g64, ctx->stream, e0, e1);
+        dim3 g = g64;
+        if ((rc = pick_ksplit(ctx, op, a, (long)g64.x * g64.y, 4 * 1024, a.kp / 128))) return rc;
+        g.z = (unsigned)a.ksplit;
+        e = launch_tiles2<1, 1, 1>(a, op.out_mode, g, ctx->stream, e0, e1);
     }
     if (e != hipSuccess) return hip_err(ctx, e, "ternary GEMM launch");
     prof_commit(ctx, e0, e1, kProfGemm, 2.0 * op.m * (double)total * a.kp);

@@ -66,6 +66,27 @@ def test_ragged_tiles_one_workgroup_per_cu(ctx_with, rows, cols, m, mode):
     w.free()
 
 
+@pytest.mark.parametrize("rows,cols,m", [(130, 2560, 129), (300, 1280, 257), (256, 6912, 96), (1000, 2560, 70),
+                                         (77, 1024, 200)])
+@pytest.mark.parametrize("mode,ks", [("4", "2"), ("4", "3"), ("4", "7"), ("5", "2"), ("5", "5")])
+def test_split_k_ranges(ctx_with, rows, cols, m, mode, ks):
+    # k cut into ks ranges (workgroups of one tile meet at a counter; the
+    # last adds the int32 partials): the same integers and f32 bits as one
+    # range, three calls in a row (the counters return to zero), the last on
+    # fewer tokens
+    ctx = ctx_with(LBT_GEMM_MODE=mode, LBT_GEMM_KSPLIT=ks)
+    announce(f"prefill split-k mode {mode} ks {ks} {rows}x{cols} m={m}")
+    t, scale, x = golden_case(rows, cols, m, rows + cols + m)
+    p = orc.pack(t)
+    w = ctx.upload(p, rows, cols, float(scale))
+    for mm in (m, m, m - 33):
+        q, sa, su = orc.quantize_acts(x[:mm])
+        assert np.array_equal(ctx.gemm_i32(w, q, su), q[:, :cols].astype(np.int64) @ t.T.astype(np.int64))
+        (y,) = ctx.ternary_linear([w], x[:mm])
+        assert np.array_equal(y, orc.gemm_f32(p, rows, cols, scale, q, sa, su))
+    w.free()
+
+
 @pytest.mark.parametrize("rows,cols", [(6912, 2560), (2560, 6912), (640, 2560), (13824, 2560)])
 @pytest.mark.parametrize("m", [2, 7, 16, 17, 32, 48, 64])
 def test_few_token_gemm_bitexact(ctx, rows, cols, m):
