@@ -87,6 +87,29 @@ def test_split_k_ranges(ctx_with, rows, cols, m, mode, ks):
     w.free()
 
 
+def test_split_k_alternating_inputs(ctx_with):
+    # the default split of 2560 x 6912 at M = 128 (three k ranges), twelve
+    # calls alternating two inputs: each call's partials land at the same
+    # scratch addresses as the previous call's, so a reader that saw an
+    # earlier call's values (a stale cache line on its XCD) would fail here
+    ctx = ctx_with(LBT_GEMM_KSPLIT="3")
+    rows, cols, m = 2560, 6912, 128
+    announce(f"prefill split-k alternating inputs {rows}x{cols} m={m}")
+    rng = np.random.default_rng(77)
+    t = ternary_iid(rng, rows, cols)
+    p = orc.pack(t)
+    w = ctx.upload(p, rows, cols, 1.0)
+    xs = [rng.standard_normal((m, cols)).astype(np.float32) for _ in range(2)]
+    want = []
+    for x in xs:
+        q, sa, su = orc.quantize_acts(x)
+        want.append(orc.gemm_f32(p, rows, cols, 1.0, q, sa, su))
+    for i in range(12):
+        (y,) = ctx.ternary_linear([w], xs[i % 2])
+        assert np.array_equal(y, want[i % 2]), f"call {i}"
+    w.free()
+
+
 @pytest.mark.parametrize("rows,cols", [(6912, 2560), (2560, 6912), (640, 2560), (13824, 2560)])
 @pytest.mark.parametrize("m", [2, 7, 16, 17, 32, 48, 64])
 def test_few_token_gemm_bitexact(ctx, rows, cols, m):
