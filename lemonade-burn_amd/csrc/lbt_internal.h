@@ -53,10 +53,9 @@ struct lbt_ctx {
     // grow-only device scratch of the prefill GEMM (quantized activations)
     void* qws = nullptr;
     size_t qws_bytes = 0;
-    // grow-only split-k scratch: kKsplitTiles tile counters (zero between
-    // launches) then the partial tiles
+    // split-k scratch of the prefill GEMM, allocated once: tile counters
+    // (zero between launches), then the partial tiles
     void* kws = nullptr;
-    size_t kws_bytes = 0;
     // grow-only scratch of lbt_sample_dev
     void* sws = nullptr;
     size_t sws_bytes = 0;

@@ -1072,6 +1072,11 @@ namespace {
 constexpr int kKsplitTiles = 1024;  // tile counters of the split-k scratch
 constexpr int kKsplitMax = 3;        // k ranges per tile
 constexpr int kKsplitMinSteps = 16;  // 128-k steps per range
+// The split-k scratch, allocated once per context at this size and never
+// moved (a captured graph may hold its address): the counters and the
+// partial tiles of up to 512 workgroups of 128 x 128 tiles, what the
+// automatic split asks for at most (two workgroups per CU).
+constexpr size_t kKsplitBytes = (size_t)kKsplitTiles * 4 + (size_t)512 * 16384 * 4;
 
 // k ranges for a pipelined-GEMM grid of `tiles` workgroups of `tile_ints`
 // int32 accumulators over nk steps: as many as the two workgroup slots of
@@ -1079,13 +1084,14 @@ constexpr int kKsplitMinSteps = 16;  // 128-k steps per range
 // (the partials' hand-off costs ~2-3 us, so only long k pays: 2560 x 6912
 // at M = 128 14.0 -> 10.6 us with 3 ranges, at M = 256 14.6 -> 12.6 us;
 // 6912 x 2560 at M = 128, 20 steps, 8.4 -> 10.2 us with 2, so 1 there;
-// wavefront groups splitting k inside a workgroup were no faster); 1 where
-// the call brings its own scratch (the allocation-free entry point) or a
-// stream capture is under way with too small a split-k scratch.  Sets
-// a.ksplit / kcnt / kpart.
-int pick_ksplit(lbt_ctx* ctx, const TernaryOp& op, GemvArgs& a, long tiles, int tile_ints, int nk) {
+// wavefront groups splitting k inside a workgroup were no faster), and no
+// more than the scratch holds; 1 where the call brings its own scratch (the
+// allocation-free entry point), or the scratch is not there yet and a stream
+// capture is under way or the allocation fails (the split is only a
+// speed-up).  Sets a.ksplit / kcnt / kpart.
+void pick_ksplit(lbt_ctx* ctx, const TernaryOp& op, GemvArgs& a, long tiles, int tile_ints, int nk) {
     a.ksplit = 1;
-    if (op.scratch || tiles > kKsplitTiles) return LBT_OK;
+    if (op.scratch || tiles > kKsplitTiles) return;
     int ks = ctx->tune.gemm_ksplit;
     if (ks == 0) {
         const long fill = 2L * ctx->cus / tiles;
@@ -1093,25 +1099,26 @@ int pick_ksplit(lbt_ctx* ctx, const TernaryOp& op, GemvArgs& a, long tiles, int 
         if (ks > nk / kKsplitMinSteps) ks = nk / kKsplitMinSteps;
     }
     if (ks > nk) ks = nk;
-    if (ks < 2) return LBT_OK;
-    const size_t need = (size_t)kKsplitTiles * 4 + (size_t)tiles * ks * tile_ints * 4;
-    if (need > ctx->kws_bytes) {
+    while (ks > 1 && (size_t)kKsplitTiles * 4 + (size_t)tiles * ks * tile_ints * 4 > kKsplitBytes) ks--;
+    if (ks < 2) return;
+    if (!ctx->kws) {
         hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-        if (hipStreamIsCapturing(ctx->stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return LBT_OK;
-        if (ctx->kws) {
-            hipStreamSynchronize(ctx->stream);
-            hipFree(ctx->kws);
-            ctx->kws = nullptr;
-            ctx->kws_bytes = 0;
+        if (hipStreamIsCapturing(ctx->stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return;
+        void* p = nullptr;
+        if (hipMalloc(&p, kKsplitBytes) != hipSuccess) {
+            (void)hipGetLastError();
+            return;
         }
-        LBT_HIP(ctx, hipMalloc(&ctx->kws, need));
-        LBT_HIP(ctx, hipMemsetAsync(ctx->kws, 0, (size_t)kKsplitTiles * 4, ctx->stream));
-        ctx->kws_bytes = need;
+        if (hipMemsetAsync(p, 0, (size_t)kKsplitTiles * 4, ctx->stream) != hipSuccess) {
+            (void)hipGetLastError();
+            hipFree(p);
+            return;
+        }
+        ctx->kws = p;
     }
     a.ksplit = ks;
     a.kcnt = (int*)ctx->kws;
     a.kpart = (int*)ctx->kws + kKsplitTiles;
-    return LBT_OK;
 }
 }  // namespace
 
@@ -1214,12 +1221,12 @@ int launch_ternary_mfma(lbt_ctx* ctx, const TernaryOp& op_in) {
     } else if (gmode != 4 && (t128 >= 200 || gmode == 5)) {
         // grids that leave workgroup slots idle split k (gridDim.z ranges)
         dim3 g = g128;
-        if ((rc = pick_ksplit(ctx, op, a, t128, 4 * 4 * 1024, a.kp / 128))) return rc;
+        pick_ksplit(ctx, op, a, t128, 4 * 4 * 1024, a.kp / 128);
         g.z = (unsigned)a.ksplit;
         e = launch_tiles2<2, 2, 1>(a, op.out_mode, g, ctx->stream, e0, e1);
     } else {
         dim3 g = g64;
-        if ((rc = pick_ksplit(ctx, op, a, (long)g64.x * g64.y, 4 * 1024, a.kp / 128))) return rc;
+        pick_ksplit(ctx, op, a, (long)g64.x * g64.y, 4 * 1024, a.kp / 128);
         g.z = (unsigned)a.ksplit;
         e = launch_tiles2<1, 1, 1>(a, op.out_mode, g, ctx->stream, e0, e1);
     }
