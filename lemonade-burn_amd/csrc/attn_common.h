@@ -282,6 +282,54 @@ __device__ __forceinline__ void halve_slots(const float (&v)[K], float (&o)[K / 
     }
 }
 
+// q . k of one key for the GH heads of a group: lane cc of the key's LK lanes
+// holds its 8 dims of each head (permuted by its head slot, q8[j] = head
+// j ^ hh) and the key's 8 bf16 values kv; fused multiply-adds in dim order,
+// then the first log2(GH) butterfly steps by recursive halving (lane cc ends
+// with head hh = cc / (LK / GH)), the rest as a butterfly.  Returns head hh's
+// score (every lane of the key active).
+template <int LK, int GH>
+__device__ __forceinline__ float attn_group_score(const u32x4& kv, const float (&q8)[GH][8]) {
+    const uint32_t wv[4] = {kv.x, kv.y, kv.z, kv.w};
+    float a[GH];
+#pragma unroll
+    for (int h = 0; h < GH; h++) {
+        a[h] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            a[h] = __builtin_fmaf(q8[h][2 * e], bf16_to_f32((uint16_t)(wv[e] & 0xffffu)), a[h]);
+            a[h] = __builtin_fmaf(q8[h][2 * e + 1], bf16_to_f32((uint16_t)(wv[e] >> 16)), a[h]);
+        }
+    }
+    if constexpr (GH == 1) {
+        return xor_sum_down<LK / 2>(a[0]);
+    } else if constexpr (GH == 2) {
+        float h1[1];
+        halve_slots<LK / 2>(a, h1);
+        return xor_sum_down<LK / 4>(h1[0]);
+    } else {
+        static_assert(GH == 4, "1, 2 or 4 heads per group");
+        float h2[2], h1[1];
+        halve_slots<LK / 2>(a, h2);
+        halve_slots<LK / 4>(h2, h1);
+        return xor_sum_down<LK / 8>(h1[0]);
+    }
+}
+
+// acc[h][e] += p[h] * v[8 cc + e] for the 8 bf16 values of one V row chunk.
+template <int GH>
+__device__ __forceinline__ void attn_group_pv(const u32x4& vv, const float (&pj)[GH], float (&acc)[GH][8]) {
+    const uint32_t wv[4] = {vv.x, vv.y, vv.z, vv.w};
+#pragma unroll
+    for (int h = 0; h < GH; h++) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            acc[h][2 * e] = __builtin_fmaf(pj[h], bf16_to_f32((uint16_t)(wv[e] & 0xffffu)), acc[h][2 * e]);
+            acc[h][2 * e + 1] = __builtin_fmaf(pj[h], bf16_to_f32((uint16_t)(wv[e] >> 16)), acc[h][2 * e + 1]);
+        }
+    }
+}
+
 template <int LK, int GH, int KU>
 __device__ __forceinline__ void attention_split_group(const float* q, int g, int nh, int s, int p, const uint16_t* K0,
                                                       const uint16_t* V0, float scaling, float* o, float* ml,
@@ -348,32 +396,7 @@ __device__ __forceinline__ void attention_split_group(const float* q, int g, int
 #pragma unroll
         for (int u = 0; u < KU; u++) {
             const int k = b0 + u * NK + w * GW + kslot;
-            const uint32_t wv[4] = {kbuf[u].x, kbuf[u].y, kbuf[u].z, kbuf[u].w};
-            float a[GH];
-#pragma unroll
-            for (int h = 0; h < GH; h++) {
-                a[h] = 0.0f;
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    a[h] = __builtin_fmaf(q8[h][2 * e], bf16_to_f32((uint16_t)(wv[e] & 0xffffu)), a[h]);
-                    a[h] = __builtin_fmaf(q8[h][2 * e + 1], bf16_to_f32((uint16_t)(wv[e] >> 16)), a[h]);
-                }
-            }
-            float r;
-            if constexpr (GH == 1) {
-                r = xor_sum_down<LK / 2>(a[0]);
-            } else if constexpr (GH == 2) {
-                float h1[1];
-                halve_slots<LK / 2>(a, h1);
-                r = xor_sum_down<LK / 4>(h1[0]);
-            } else {
-                static_assert(GH == 4, "1, 2 or 4 heads per group");
-                float h2[2], h1[1];
-                halve_slots<LK / 2>(a, h2);
-                halve_slots<LK / 4>(h2, h1);
-                r = xor_sum_down<LK / 8>(h1[0]);
-            }
-            const float sv = r * scaling;
+            const float sv = attn_group_score<LK, GH>(kbuf[u], q8) * scaling;
             const bool kin = k < cnt;
             if (kin && cc % LPH == 0) sc[k * GH + hh] = sv;
             mxo = fmaxf(mxo, kin ? sv : -__builtin_inff());
@@ -436,7 +459,6 @@ __device__ __forceinline__ void attention_split_group(const float* q, int g, int
 #pragma unroll
         for (int u = 0; u < KU; u++) {
             const int k = b0 + grp + u * NK;
-            const uint32_t wv[4] = {vbuf[u].x, vbuf[u].y, vbuf[u].z, vbuf[u].w};
             float pj[GH];
             if constexpr (GH == 4) {
                 const float4 t = *(const float4*)(sc + k * 4);
@@ -448,14 +470,7 @@ __device__ __forceinline__ void attention_split_group(const float* q, int g, int
 #pragma unroll
                 for (int h = 0; h < GH; h++) pj[h] = sc[k * GH + h];
             }
-#pragma unroll
-            for (int h = 0; h < GH; h++) {
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    acc[h][2 * e] = __builtin_fmaf(pj[h], bf16_to_f32((uint16_t)(wv[e] & 0xffffu)), acc[h][2 * e]);
-                    acc[h][2 * e + 1] = __builtin_fmaf(pj[h], bf16_to_f32((uint16_t)(wv[e] >> 16)), acc[h][2 * e + 1]);
-                }
-            }
+            attn_group_pv<GH>(vbuf[u], pj, acc);
         }
     };
     for (int b0 = 0;; b0 += 2 * STEP) {
@@ -489,6 +504,188 @@ __device__ __forceinline__ void attention_split_group(const float* q, int g, int
         ml[((size_t)s * nh + g * GH + h) * 2] =
             fmaxf(fmaxf(sh.rmax[h][0], sh.rmax[h][1]), fmaxf(sh.rmax[h][2], sh.rmax[h][3]));
         ml[((size_t)s * nh + g * GH + h) * 2 + 1] = (sh.rsum[h][0] + sh.rsum[h][1]) + (sh.rsum[h][2] + sh.rsum[h][3]);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// The split of attention_split_group<LK, GH, .> on ONE wavefront, with the
+// same partials bit for bit: the four wavefronts of that workgroup become
+// four virtual wavefronts of this one, and no barrier is needed, so the
+// wavefronts of a workgroup are independent (row, KV head, split) tasks --
+// a long prefill runs four times as many of its short split chains at a
+// time.  The order, as in the workgroup form:
+//   * key k's score by the LK lanes (kslot = k mod 64/LK) of pass k / (64/LK),
+//     attn_group_score; virtual wavefront v = (k / (64/LK)) mod 4 of the
+//     workgroup form is the one that held key k, so each lane keeps one
+//     running max per v and the head max is the max of the four wave maxima;
+//   * exponentials of keys u = 64 v + lane, +256, ... summed per virtual
+//     thread in that order, each virtual wavefront's sums reduced by
+//     wave_sum, l = (l_0 + l_1) + (l_2 + l_3);
+//   * PV: key group grp = 4 v + lane / LK (16 groups of LK lanes) accumulates
+//     keys grp, grp + 16, ... by attn_group_pv; per virtual wavefront the
+//     groups combine by xor_sum_up<LK>, o = (o_0 + o_1) + (o_2 + o_3).
+// Keys past cnt read zero (bounded buffer loads) and get p = 0 (fma(0, 0,
+// acc) = acc, acc never -0), so the padding differs from the workgroup form
+// without changing a bit.  Cached K/V loads (prefill rows re-read them).
+// sc: this wavefront's [ceil16(ks)][GH] score / exponential buffer in LDS.
+template <int LK, int GH>
+__device__ __forceinline__ void attention_split_wave(const float* q, int g, int nh, int s, int p, const uint16_t* K0,
+                                                     const uint16_t* V0, float scaling, float* o, float* ml,
+                                                     float* sc) {
+    static_assert(LK == 16 && GH == 4, "four keys per pass (head_dim 128), four query heads per KV head");
+    constexpr int HD = LK * 8, KPP = 64 / LK, LPH = LK / GH, NG = kThreads / LK;
+    const int vis = p + 1;
+    const int ks = attn_split_keys(vis);
+    const int ns = (vis + ks - 1) / ks;
+    if (s >= ns) return;
+    const int j0 = s * ks, cnt = vis - j0 < ks ? vis - j0 : ks;
+    const int lane = (int)threadIdx.x & 63, kslot = lane / LK, cc = lane % LK, hh = cc / LPH;
+    const __amdgpu_buffer_rsrc_t kr = buf_rsrc(K0 + (size_t)j0 * HD, (uint32_t)cnt * HD * 2u);
+    const __amdgpu_buffer_rsrc_t vr = buf_rsrc(V0 + (size_t)j0 * HD, (uint32_t)cnt * HD * 2u);
+    const uint32_t loff = (uint32_t)(kslot * HD + 8 * cc) * 2u;  // this lane's chunk of its key / V row
+    float q8[GH][8];
+#pragma unroll
+    for (int j = 0; j < GH; j++) {
+        const float* qj = q + (size_t)(g * GH + (j ^ hh)) * HD + 8 * cc;
+        const f32x4 a = *(const f32x4*)qj, b = *(const f32x4*)(qj + 4);
+        q8[j][0] = a.x, q8[j][1] = a.y, q8[j][2] = a.z, q8[j][3] = a.w;
+        q8[j][4] = b.x, q8[j][5] = b.y, q8[j][6] = b.z, q8[j][7] = b.w;
+    }
+    // scores: passes of KPP keys, in batches of 4 passes (4 loads in flight)
+    constexpr int PB = 4;
+
+    const int npass = (cnt + KPP - 1) / KPP;
+    float mxo[4] = {-__builtin_inff(), -__builtin_inff(), -__builtin_inff(), -__builtin_inff()};
+#pragma unroll 1
+    for (int pb = 0; pb < npass; pb += PB) {
+        u32x4 kb[PB];
+#pragma unroll
+        for (int i = 0; i < PB; i++)
+            kb[i] = __builtin_bit_cast(
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, loff, (uint32_t)((pb + i) * KPP) * HD * 2u, 0));
+#pragma unroll
+        for (int i = 0; i < PB; i++) {
+            const int k = (pb + i) * KPP + kslot;
+            const float sv = attn_group_score<LK, GH>(kb[i], q8) * scaling;
+            const bool kin = k < cnt;
+            if (kin && cc % LPH == 0) sc[k * GH + hh] = sv;
+            // pass pb + i of this wavefront is pass (pb + i) / 4 of virtual wavefront (pb + i) mod 4
+            mxo[i & 3] = fmaxf(mxo[i & 3], kin ? sv : -__builtin_inff());
+        }
+    }
+    // the head max over the four virtual wavefronts' running maxima (a max
+    // does not depend on the order; only the sign of a zero max could, and
+    // exp(s - m) and every later value are the same with either)
+    float m[GH];
+    {
+        const float mx = fmaxf(fmaxf(mxo[0], mxo[1]), fmaxf(mxo[2], mxo[3]));
+#pragma unroll
+        for (int h = 0; h < GH; h++) m[h] = wave_max(hh == h ? mx : -__builtin_inff());
+    }
+    asm volatile("" ::: "memory");  // the score stores before the reads below (LDS is in order per wavefront)
+    // exponentials; keys cnt .. ext16 - 1 get p = 0
+    const int ext = (cnt + NG - 1) / NG * NG;
+    float lsum[GH];
+    {
+        float ls[4][GH];
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            float ps[GH];
+#pragma unroll
+            for (int h = 0; h < GH; h++) ps[h] = 0.0f;
+            if (64 * v >= ext) {  // no key: the sums are +0 (uniform branch)
+#pragma unroll
+                for (int h = 0; h < GH; h++) ls[v][h] = 0.0f;
+                continue;
+            }
+            for (int u = 64 * v + lane; u < ext; u += kThreads) {
+                float* sp = sc + u * GH;
+                float e[GH];
+                if (u < cnt) {
+#pragma unroll
+                    for (int h = 0; h < GH; h++) {
+                        e[h] = lbt_expf(sp[h] - m[h]);
+                        ps[h] = ps[h] + e[h];
+                    }
+                } else {
+#pragma unroll
+                    for (int h = 0; h < GH; h++) e[h] = 0.0f;
+                }
+#pragma unroll
+                for (int h = 0; h < GH; h++) sp[h] = e[h];
+            }
+#pragma unroll
+            for (int h = 0; h < GH; h++) ls[v][h] = wave_sum(ps[h]);
+        }
+#pragma unroll
+        for (int h = 0; h < GH; h++) lsum[h] = (ls[0][h] + ls[1][h]) + (ls[2][h] + ls[3][h]);
+    }
+    asm volatile("" ::: "memory");  // the exponential stores before the PV reads
+    // PV per virtual wavefront v: this lane's group 4 v + kslot takes keys
+    // 16 u + 4 v + kslot, u ascending; the groups then combine as
+    // xor_sum_up<LK> does ((g0 + g1) + (g2 + g3): steps 16, then 32), here by
+    // recursive halving, which leaves lane (kslot, cc) the sum for head
+    // hv = (kslot >> 1) + 2 (kslot & 1), dims 8 cc .. 8 cc + 7
+    const int nu = ext / NG;
+    auto pv_v = [&](int v, float (&r)[8]) {
+        constexpr int VB = 4;
+        float acc[GH][8];
+#pragma unroll
+        for (int h = 0; h < GH; h++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) acc[h][e] = 0.0f;
+#pragma unroll 1
+        for (int ub = 0; ub < nu; ub += VB) {
+            u32x4 vb[VB];
+#pragma unroll
+            for (int i = 0; i < VB; i++)
+                vb[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                      vr, loff, (uint32_t)((ub + i) * NG + 4 * v) * HD * 2u, 0));
+#pragma unroll
+            for (int i = 0; i < VB; i++) {
+                if (ub + i >= nu) break;
+                const int k = (ub + i) * NG + 4 * v + kslot;
+                const float4 t = *(const float4*)(sc + k * 4);
+                const float pj[GH] = {t.x, t.y, t.z, t.w};
+                attn_group_pv<GH>(vb[i], pj, acc);
+            }
+        }
+        float flat[GH * 8], h16[16];
+#pragma unroll
+        for (int h = 0; h < GH; h++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) flat[h * 8 + e] = acc[h][e];
+        halve<16, GH * 8>(flat, h16);
+        halve<32, 16>(h16, r);
+    };
+    float r[8], o01[8], o23[8];
+    pv_v(0, r);
+#pragma unroll
+    for (int e = 0; e < 8; e++) o01[e] = r[e];
+    pv_v(1, r);
+#pragma unroll
+    for (int e = 0; e < 8; e++) o01[e] = o01[e] + r[e];
+    pv_v(2, r);
+#pragma unroll
+    for (int e = 0; e < 8; e++) o23[e] = r[e];
+    pv_v(3, r);
+    {
+        const int hv = (kslot >> 1) + 2 * (kslot & 1);
+        float* od = o + (size_t)s * nh * HD + (size_t)(g * GH + hv) * HD + 8 * cc;
+        float fv[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) fv[e] = o01[e] + (o23[e] + r[e]);
+        *(f32x4*)od = f32x4{fv[0], fv[1], fv[2], fv[3]};
+        *(f32x4*)(od + 4) = f32x4{fv[4], fv[5], fv[6], fv[7]};
+    }
+    if (lane < GH) {
+        const int h = lane;
+        float mh = m[0], lh = lsum[0];
+#pragma unroll
+        for (int j = 1; j < GH; j++)
+            if (h == j) mh = m[j], lh = lsum[j];
+        ml[((size_t)s * nh + g * GH + h) * 2] = mh;
+        ml[((size_t)s * nh + g * GH + h) * 2 + 1] = lh;
     }
 }
 

@@ -71,6 +71,29 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(const float* q, int
                             mlt, sc, sh);
 }
 
+// One wavefront per (query row, KV head, key split), four per workgroup:
+// attention_split_wave, the grouped kernel's partials bit for bit without a
+// barrier.  Task i = blockIdx.x * 4 + wavefront is (row, KV head, split)
+// with the split fastest; nsg splits per (row, KV head) in the grid (the
+// most any row has); scw floats of LDS scores per wavefront.
+template <int LK, int GH>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void attention_wave_kernel(const float* q, int nh, int kvh, RowPos rp,
+                                                                  const uint16_t* kc, const uint16_t* vc, int cap,
+                                                                  float scaling, float* o, float* ml, int m, int nsg,
+                                                                  int scw) {
+    extern __shared__ __align__(16) float sc[];  // [4][scw]
+    const int w = (int)threadIdx.x >> 6;
+    const long i = (long)blockIdx.x * 4 + w;
+    const int s = (int)(i % nsg);
+    const long r = i / nsg;
+    const int g = (int)(r % kvh), t = (int)(r / kvh);
+    if (t >= m) return;
+    const int H = nh * LK * 8;
+    const size_t kvoff = row_cache_offset(rp, t) + (size_t)g * cap * LK * 8;
+    attention_split_wave<LK, GH>(q + (size_t)t * H, g, nh, s, row_position(rp, t), kc + kvoff, vc + kvoff, scaling,
+                                 o + (size_t)t * kAttnSplits * H, ml + (size_t)t * kAttnSplits * nh * 2, sc + w * scw);
+}
+
 // The same splits with one workgroup per (KV head, key split, query row)
 // taking all GH query heads of the KV head.  Grid (kvh * splits, m).
 // wide: eight key passes in flight per split of more than 64 keys (grids of
@@ -962,6 +985,31 @@ int launch_attention(lbt_ctx* ctx, const float* q, int m, int nh, int kvh, int h
     const size_t lds = grouped ? (size_t)gh * attn_group_score_keys(attn_split_keys(rp.vis_max), hd / 8) * sizeof(float)
                                : (size_t)attn_split_keys(rp.vis_max) * sizeof(float);
     if (lds > 64 * 1024) return set_err(ctx, LBT_E_RANGE, "attention: context too long for the LDS score buffer");
+    // rows of one sequence at consecutive positions (a prefill) with at
+    // least 8 (row, KV head, split) tasks per CU: one wavefront per task
+    // where the shape allows (2B, 2048-token prefill: attention 41.5 ->
+    // 21.7 ms; at 64 and 128 tokens the workgroup per task stays faster,
+    // 0.25 against 0.42 ms and 0.38 against 0.43 ms).  LBT_ATTN_WAVE=1 / 0
+    // forces it on / off for grouped attention.
+    const int aw = ctx->tune.attn_wave;
+    const long wave_tasks = (long)m * kvh * attn_splits(rp.vis_max);
+    if (grouped && gh == 4 && hd == 128 &&
+        (aw > 0 || (aw < 0 && m > 1 && !rp.tok_pos && !rp.pos_dev && wave_tasks >= 8L * ctx->cus))) {
+        const int nsg = attn_splits(rp.vis_max);
+        const int scw = (attn_split_keys(rp.vis_max) + 15) / 16 * 16 * 4;
+        const size_t wl = (size_t)4 * scw * sizeof(float);
+        const long tasks = wave_tasks;
+        if (wl <= 64 * 1024 && (tasks + 3) / 4 < (1L << 31)) {
+            hipEvent_t e0, e1;
+            prof_pair(ctx, &e0, &e1);
+            hipExtLaunchKernelGGL((attention_wave_kernel<16, 4>), dim3((unsigned)((tasks + 3) / 4)), dim3(kThreads), wl,
+                                  ctx->stream, e0, e1, 0, q, nh, kvh, rp, kc, vc, cap, scaling, o, ml, m, nsg, scw);
+            const hipError_t e = hipGetLastError();
+            if (e != hipSuccess) return hip_err(ctx, e, "attention_wave_kernel launch");
+            prof_commit(ctx, e0, e1, kProfAttn, 2.0 * kvh * (double)rp.vis_max * hd * 2.0 * m);
+            return LBT_OK;
+        }
+    }
     hipEvent_t e0, e1;
     prof_pair(ctx, &e0, &e1);
     // as many splits as the longest visible row has (rows with fewer exit

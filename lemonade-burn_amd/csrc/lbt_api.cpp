@@ -30,6 +30,10 @@ LbtTuning read_tuning() {
     t.small_ns = (int)num("LBT_GEMM_SMALL_NS", 0);
     t.small_pf = num("LBT_GEMM_SMALL_PF", 1) != 0;
     {
+        const char* v = getenv("LBT_ATTN_WAVE");
+        t.attn_wave = v ? (atoi(v) != 0 ? 1 : 0) : -1;
+    }
+    {
         const char* v = getenv("LBT_ATTN_WIDE");
         t.attn_wide = v ? (atoi(v) != 0 ? 1 : 0) : -1;
     }

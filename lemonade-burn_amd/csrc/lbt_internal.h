@@ -23,6 +23,7 @@ struct LbtTuning {
     int small_ms = 1;         // LBT_GEMM_SMALL_MS: cap of its token tiles (16 * ms)
     int small_ns = 0;         // LBT_GEMM_SMALL_NS: 1 / 2 forces its row tile (0 auto)
     bool small_pf = true;     // LBT_GEMM_SMALL_PF=0: no epilogue prefetch
+    int attn_wave = -1;       // LBT_ATTN_WAVE=1/0: one wavefront per (row, KV head, split) on/off (-1: prefill rows)
     int attn_wide = -1;       // LBT_ATTN_WIDE=1/0: eight-pass K/V pipeline of the grouped attention on/off (-1: by grid size)
     bool head_tg8 = false;           // LBT_HEAD_TG8: 8-token groups in the batched LM head
     bool head_batch_classic = false;  // LBT_HEAD_BATCH_CLASSIC: batched bf16 head on lmhead_batch_kernel (16-token groups)

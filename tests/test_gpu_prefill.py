@@ -199,6 +199,49 @@ def test_model_prefill_mfma_matches_oracle_and_gemv(ctx, ctx_with, n):
     om.free()
 
 
+@pytest.mark.parametrize("n,force", [(1100, None), (130, "1"), (9, "1")])
+def test_model_long_prefill_attention_matches_oracle(ctx, ctx_with, n, force):
+    # the one-wavefront-per-split attention kernel (4 query heads per KV
+    # head, head_dim 128): by default past 1024 tokens (splits of more than
+    # 64 keys), forced on short prompts; logits bit-exact to the oracle
+    cfg = dict(hidden=512, intermediate=1536, heads=4, kv_heads=1, layers=2, vocab=1000, max_pos=2048)
+    announce(f"model long prefill n={n} wave={force}")
+    c0 = ctx_with(LBT_ATTN_WAVE=force) if force else ctx
+    m = lbt_hip.Model.synthetic(c0, lbt_hip.make_config(**cfg), 5)
+    om = orc.OracleModel(orc.config(**cfg), 5)
+    toks = (np.arange(n) * 37 % cfg["vocab"]).astype(np.uint32)
+    c = m.new_cache()
+    got = m.forward(toks, c, all_logits=True)
+    want = om.forward(toks, all_logits=True)
+    assert np.array_equal(got[-64:], want[-64:])
+    assert np.array_equal(got, want)
+    c.free()
+    m.free()
+    om.free()
+
+
+@pytest.mark.parametrize("n", [2, 63, 65, 700, 1024, 1025, 1040, 4096, 4100])
+def test_prefill_attention_kernels_agree(ctx, ctx_with, n):
+    # the 2B shape's attention (20 query heads over 5 KV heads, head_dim 128)
+    # at prefill lengths across the split-size steps (64-key splits up to
+    # 1024 keys, then ceil(vis / 16); past 4096 two keys per virtual thread):
+    # one wavefront per split against the workgroup-per-split kernel (both
+    # forced), logits and KV cache bit for bit
+    cfg = lbt_hip.make_config(layers=1, vocab=1000, max_pos=4224)
+    announce(f"prefill attention wavefront vs workgroup kernel n={n}")
+    toks = np.random.default_rng(n + 7).integers(0, 1000, n).astype(np.uint32)
+    outs = []
+    for c in (ctx_with(LBT_ATTN_WAVE="1"), ctx_with(LBT_ATTN_WAVE="0")):
+        m = lbt_hip.Model.synthetic(c, cfg, 17)
+        cache = m.new_cache()
+        logits = m.forward(toks, cache, all_logits=True)
+        outs.append((logits, cache.read(0, False), cache.read(0, True)))
+        cache.free()
+        m.free()
+    for a, b in zip(outs[0], outs[1]):
+        assert np.array_equal(a, b)
+
+
 @pytest.mark.parametrize("mode", ["4", "5", "6", "7", "8"])
 def test_model_prefill_every_gemm_tiling_matches_oracle(ctx_with, mode):
     # every epilogue (q/k/v + RoPE + KV append, residual add, relu^2*up) through
