@@ -153,6 +153,37 @@ def sched_throughput(model, cfg, slots: int = 16, requests: int = 32, prompt_len
             "tok_s": round(total / wall, 1), "wall_s": round(wall, 3)}
 
 
+def long_prefill(model, ctx, cfg, lengths=(512, 2048)) -> list:
+    """Prefill of one long prompt (uniform-random ids) on the 2B-shaped model:
+    host wall time of lbt_model_forward (argmax of the last row) between two
+    synchronizations, best of three after a warm-up, and the device time of
+    its attention, GEMM and head kernels from one profiled run."""
+    res = []
+    for n in lengths:
+        toks = np.random.default_rng(n).integers(0, cfg.vocab_size, n).astype(np.uint32)
+        ts = []
+        for _ in range(4):
+            c = model.new_cache()
+            ctx.sync()
+            t0 = time.perf_counter()
+            model.forward_argmax(toks, c)
+            ctx.sync()
+            ts.append(time.perf_counter() - t0)
+            c.free()
+        ctx.prof_read(reset=True)
+        ctx.prof_enable(True)
+        c = model.new_cache()
+        model.forward_argmax(toks, c)
+        ctx.sync()
+        c.free()
+        p = ctx.prof_read(reset=True)
+        ctx.prof_enable(False)
+        best = min(ts[1:])
+        res.append({"tokens": n, "ms": round(best * 1e3, 2), "tok_s": round(n / best, 1),
+                    "attn_ms": round(p["attn"]["ms"], 2), "gemm_ms": round(p["gemm"]["ms"], 2)})
+    return res
+
+
 def prefill_gemm(ctx, reps: int = 10) -> list:
     """The prefill GEMM benchmark: the prefill GEMM (int8 MFMA) on the FFN shapes
     2560->6912 and 6912->2560 at M = 128, 512, 2048 tokens; seeded ternary
@@ -418,6 +449,7 @@ def main() -> int:
                     help="only the config-1/2 per-shape GEMV figures (the workload profiled for them)")
     ap.add_argument("--int8-head-only", action="store_true",
                     help="only the opt-in int8 LM head decode figure (the workload profiled for its kernel)")
+    ap.add_argument("--no-long-prefill", action="store_true", help="skip the 512 / 2048-token prefills")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the config-3 prefill GEMM sweep (the workload profiled for the MFMA counters)")
     ap.add_argument("--batched-only", action="store_true",
@@ -542,6 +574,8 @@ def main() -> int:
         line["int8_head_decode"] = int8_head_decode(model, ctx, prompt)
     if not args.no_sampled:
         line["sampled_decode"] = sampled_decode(model, prompt)
+    if not args.no_long_prefill:
+        line["long_prefill"] = long_prefill(model, ctx, cfg)
     if not args.no_batched:
         line["batched_decode"] = [batched_decode(model, cfg, bsz) for bsz in (16, 64)]
         line["batched_decode_mfma_head"] = batched_mfma_head(model, cfg)
