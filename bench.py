@@ -450,6 +450,8 @@ def main() -> int:
     ap.add_argument("--int8-head-only", action="store_true",
                     help="only the opt-in int8 LM head decode figure (the workload profiled for its kernel)")
     ap.add_argument("--no-long-prefill", action="store_true", help="skip the 512 / 2048-token prefills")
+    ap.add_argument("--long-prefill-only", action="store_true",
+                    help="only the 512 / 2048-token prefills (the workload profiled for the prefill attention)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the config-3 prefill GEMM sweep (the workload profiled for the MFMA counters)")
     ap.add_argument("--batched-only", action="store_true",
@@ -475,6 +477,14 @@ def main() -> int:
         model = lbt_hip.Model.synthetic(ctx, cfg, SEED)
         print(json.dumps({"batched_decode": [batched_decode(model, cfg, b) for b in (16, 64)],
                           "batched_decode_mfma_head": batched_mfma_head(model, cfg)}), flush=True)
+        return 0
+    if args.long_prefill_only:
+        import lbt_hip
+
+        ctx = lbt_hip.Ctx(0)
+        cfg = lbt_hip.make_config()
+        model = lbt_hip.Model.synthetic(ctx, cfg, SEED)
+        print(json.dumps({"long_prefill": long_prefill(model, ctx, cfg)}), flush=True)
         return 0
     if args.int8_head_only:
         import lbt_hip
