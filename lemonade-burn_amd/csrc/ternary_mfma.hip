@@ -223,6 +223,7 @@ struct Epi32Tok {
     static constexpr int N = (MS + 1) / 2;
     int qs[N];
     float inv[N];
+    int pos[N];  // the token's position (q/k/v outputs only)
 };
 
 template <int OUT, int MS>
@@ -235,6 +236,8 @@ __device__ __forceinline__ void epi32_pre(const GemvArgs& a, int tok0, float swm
         if (!divide) {
             t.qs[i] = gload(a.qsum + tok);
             t.inv[i] = a.qscale ? gload(a.qscale + tok) : 1.0f;  // s_a until divided
+            if constexpr (OUT == kOutQKV)
+                t.pos[i] = a.tok_pos ? gload(a.tok_pos + tok) : (a.pos_dev ? gload(a.pos_dev) : a.pos0) + tok;
         } else {
             t.inv[i] = OUT == kOutI32 ? 0.0f : 1.0f / (t.inv[i] * swm);
         }
@@ -294,6 +297,85 @@ __device__ __forceinline__ void epi32_full(const GemvArgs& a, v16i (&acc)[MS][NS
                     __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), ob, off, 0, 2);
                 }
             }
+    }
+}
+
+// The q/k/v output (RoPE on q and k, bf16 K/V cache append) of a wavefront
+// block whose 32 NS virtual rows lie in one matrix and whose tokens are all
+// below M: store_pair's values and float expressions, with its per-element
+// work hoisted -- sum(q), 1/(s_a*s_w) and the position come per token from
+// t (loaded and divided before the main loop), the row's matrix, head and
+// dim once per lane, and every cos / sin load of a 32-token block issued
+// before that block's stores (store_pair's loads wait behind the previous
+// pair's stores, which might alias them).  A V pair (rows r, r + 1) goes out
+// as one 32-bit store of the two bf16 values.
+template <int MS, int NS>
+__device__ __forceinline__ void epi32_qkv(const GemvArgs& a, v16i (&acc)[MS][NS], int tok0, int row0,
+                                          const Epi32Tok<MS>& t) {
+    using L = DLayout<32>;
+    constexpr int R = L::R;
+    const int lane = (int)threadIdx.x & 63, lr = L::row(lane);
+    const bool even = (lr & 1) == 0;
+    const int hd = a.hd, h2 = hd >> 1;
+    int mat[NS], r0[NS];
+#pragma unroll
+    for (int s = 0; s < NS; s++) resolve_row<kOutQKV>(a, row0 + s * 32 + (lr & ~1), mat[s], r0[s]);
+#pragma unroll
+    for (int ms = 0; ms < MS; ms++) {
+        int qs[R], pos[R];
+        float inv[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const int src = (ms & 1) * 32 + L::tok(lane, r);
+            qs[r] = __shfl(t.qs[ms >> 1], src, 64);
+            inv[r] = __shfl(t.inv[ms >> 1], src, 64);
+            pos[r] = __shfl(t.pos[ms >> 1], src, 64);
+        }
+#pragma unroll
+        for (int s = 0; s < NS; s++) {
+            float y0[R], y1[R];
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const int d0 = acc[ms][s][r] - qs[r];
+                const int d1 = __shfl_xor(d0, 1);
+                y0[r] = (float)d0 * inv[r];
+                y1[r] = (float)d1 * inv[r];
+            }
+            if (!even) continue;
+            const int g = r0[s] / hd, dd = r0[s] % hd;
+            if (mat[s] == 2) {
+#pragma unroll
+                for (int r = 0; r < R; r++) {
+                    const int tok = tok0 + ms * 32 + L::tok(lane, r);
+                    const size_t coff = a.tok_pos ? (size_t)tok * a.seq_stride : 0;
+                    uint16_t* dst = a.vc + coff + ((size_t)g * a.cap + pos[r]) * hd + dd;
+                    gstore((uint32_t*)dst, (uint32_t)f32_to_bf16(y0[r]) | ((uint32_t)f32_to_bf16(y1[r]) << 16));
+                }
+                continue;
+            }
+            float c[R], sn[R];
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                c[r] = gload(a.cos_t + (size_t)pos[r] * h2 + dd);
+                sn[r] = gload(a.sin_t + (size_t)pos[r] * h2 + dd);
+            }
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const int tok = tok0 + ms * 32 + L::tok(lane, r);
+                const float z0 = y0[r] * c[r] + (-y1[r]) * sn[r];
+                const float z1 = y1[r] * c[r] + y0[r] * sn[r];
+                if (mat[s] == 0) {
+                    float* q = (float*)a.out[0] + (size_t)tok * a.rows[0];
+                    gstore(q + r0[s], z0);
+                    gstore(q + r0[s] + h2, z1);
+                } else {
+                    const size_t coff = a.tok_pos ? (size_t)tok * a.seq_stride : 0;
+                    uint16_t* dst = a.kc + coff + ((size_t)g * a.cap + pos[r]) * hd + dd;
+                    gstore(dst, f32_to_bf16(z0));
+                    gstore(dst + h2, f32_to_bf16(z1));
+                }
+            }
+        }
     }
 }
 
@@ -592,6 +674,13 @@ void tgemm2_kernel(GemvArgs a) {
         swm = mt0 == 0 ? a.sw[0] : (mt0 == 1 ? a.sw[1] : a.sw[2]);
         fast = tok0 + MS * TM <= M && row0 + NS * TM <= a.total_rows && mt0 == mt1 && (long)M * ldm < (1L << 30);
         if (fast) epi32_pre<OUT, MS>(a, tok0, swm, et, false);
+    } else if constexpr (OUT == kOutQKV) {
+        int mt1, ro1;
+        resolve_row<OUT>(a, row0, mt0, ro0);
+        resolve_row<OUT>(a, row0 + NS * TM - 1, mt1, ro1);
+        swm = mt0 == 0 ? a.sw[0] : (mt0 == 1 ? a.sw[1] : a.sw[2]);
+        fast = tok0 + MS * TM <= M && row0 + NS * TM <= a.total_rows && mt0 == mt1;
+        if (fast) epi32_pre<OUT, MS>(a, tok0, swm, et, false);
     }
 
     // weights: row tile s of this wave, row l32; packed uint4 2b + g of a step
@@ -682,7 +771,7 @@ void tgemm2_kernel(GemvArgs a) {
         a_issue(pi, p);
         b_issue(pi, bw[p]);
     }
-    if constexpr (OUT == kOutF32 || OUT == kOutF32Add || OUT == kOutI32)
+    if constexpr (OUT == kOutF32 || OUT == kOutF32Add || OUT == kOutI32 || OUT == kOutQKV)
         if (fast) epi32_pre<OUT, MS>(a, tok0, swm, et, true);
     wait_vm(std::integral_constant<int, NB + (ST - 1) * (NA + NB)>{});
     __builtin_amdgcn_s_barrier();
@@ -749,6 +838,11 @@ void tgemm2_kernel(GemvArgs a) {
     if constexpr (OUT == kOutF32 || OUT == kOutF32Add || OUT == kOutI32) {
         if (fast) {
             epi32_full<OUT, MS, NS>(a, acc, tok0, mt0, ro0, et);
+            return;
+        }
+    } else if constexpr (OUT == kOutQKV) {
+        if (fast) {
+            epi32_qkv<MS, NS>(a, acc, tok0, row0, et);
             return;
         }
     }
@@ -837,6 +931,13 @@ void tgemm3_kernel(GemvArgs a) {
         swm = mt0 == 0 ? a.sw[0] : (mt0 == 1 ? a.sw[1] : a.sw[2]);
         fast = tok0 + MS * TM <= M && row0 + NS * TM <= a.total_rows && mt0 == mt1 && (long)M * ldm < (1L << 30);
         if (fast) epi32_pre<OUT, MS>(a, tok0, swm, et, false);
+    } else if constexpr (OUT == kOutQKV) {
+        int mt1, ro1;
+        resolve_row<OUT>(a, row0, mt0, ro0);
+        resolve_row<OUT>(a, row0 + NS * TM - 1, mt1, ro1);
+        swm = mt0 == 0 ? a.sw[0] : (mt0 == 1 ? a.sw[1] : a.sw[2]);
+        fast = tok0 + MS * TM <= M && row0 + NS * TM <= a.total_rows && mt0 == mt1;
+        if (fast) epi32_pre<OUT, MS>(a, tok0, swm, et, false);
     }
     const uint4* brow[NS];
 #pragma unroll
@@ -900,7 +1001,7 @@ const int plast = nsteps - 1;
         a_issue(pi, p);
         b_issue(pi, bw[p]);
     }
-    if constexpr (OUT == kOutF32 || OUT == kOutF32Add || OUT == kOutI32)
+    if constexpr (OUT == kOutF32 || OUT == kOutF32Add || OUT == kOutI32 || OUT == kOutQKV)
         if (fast) epi32_pre<OUT, MS>(a, tok0, swm, et, true);
 
     // Step p: slice p and weights p landed (own loads), barrier (every
@@ -959,6 +1060,11 @@ const int plast = nsteps - 1;
     if constexpr (OUT == kOutF32 || OUT == kOutF32Add || OUT == kOutI32) {
         if (fast) {
             epi32_full<OUT, MS, NS>(a, acc, tok0, mt0, ro0, et);
+            return;
+        }
+    } else if constexpr (OUT == kOutQKV) {
+        if (fast) {
+            epi32_qkv<MS, NS>(a, acc, tok0, row0, et);
             return;
         }
     }
@@ -1056,8 +1162,8 @@ hipError_t launch_small(const GemvArgs& a, int out_mode, bool pf, dim3 grid, hip
 int qws_reserve(lbt_ctx* ctx, size_t bytes, void** out) {
     if (bytes > ctx->qws_bytes) {
         if (ctx->qws) {
-            hipStreamSynchronize(ctx->stream);
-            hipFree(ctx->qws);
+            (void)hipStreamSynchronize(ctx->stream);
+            (void)hipFree(ctx->qws);
             ctx->qws = nullptr;
             ctx->qws_bytes = 0;
         }
@@ -1111,7 +1217,7 @@ void pick_ksplit(lbt_ctx* ctx, const TernaryOp& op, GemvArgs& a, long tiles, int
         }
         if (hipMemsetAsync(p, 0, (size_t)kKsplitTiles * 4, ctx->stream) != hipSuccess) {
             (void)hipGetLastError();
-            hipFree(p);
+            (void)hipFree(p);
             return;
         }
         ctx->kws = p;

@@ -63,6 +63,31 @@ def test_batch_matches_single_sequence_oracle(ctx, shape, nseq):
     m.free()
 
 
+def test_batch_96_matches_fewtoken_epilogue(ctx_with):
+    """96 sequences: the batched GEMMs take the pipelined MFMA tiles, whose
+    full wavefront blocks use the lean q/k/v epilogue (per-sequence positions
+    and cache rows); logits and greedy tokens equal those of the few-token
+    kernel (LBT_GEMM_MODE=6, the general epilogue) bit for bit."""
+    hip_cfg, _ = cfgs()
+    announce("batch 96 sequences: pipelined tiles vs few-token kernel")
+    outs = []
+    for c in (ctx_with(LBT_GEMM_MODE="4"), ctx_with(LBT_GEMM_MODE="6")):
+        m = lbt_hip.Model.synthetic(c, hip_cfg, 57)
+        b = m.new_batch(96, 256)
+        rng = np.random.default_rng(96)
+        nxt = []
+        for s in range(96):
+            prompt = rng.integers(0, hip_cfg.vocab_size, 1 + (5 * s) % 9).astype(np.uint32)
+            nxt.append(b.prefill(s, prompt))
+        logits, nx = b.forward(np.array(nxt, np.uint32))
+        toks, _ = b.decode_greedy(nx, 4)
+        outs.append((logits, nx, toks))
+        b.free()
+        m.free()
+    for a, b_ in zip(outs[0], outs[1]):
+        assert np.array_equal(a, b_)
+
+
 @pytest.mark.parametrize("wide", [False, True])
 def test_batch_long_context_matches_oracle(ctx, ctx_with, wide):
     """Prompts of 1100+ tokens (65-key and longer splits: the four- and, with
