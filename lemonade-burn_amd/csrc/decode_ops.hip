@@ -88,10 +88,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     extern __shared__ __align__(16) float sc[];  // [4][scw]
     const int w = (int)threadIdx.x >> 6;
     const long i = (long)blockIdx.x * 4 + w;
+    if (i >= (long)m * kvh * nsg) return;  // the last workgroup's spare wavefronts
     const int t = (int)(i % m);
     const long r = i / m;
     const int g = (int)(r % kvh), s = (int)(r / kvh);
-    if (t >= m) return;
     const int H = nh * LK * 8;
     const size_t kvoff = row_cache_offset(rp, t) + (size_t)g * cap * LK * 8;
     attention_split_wave<LK, GH>(q + (size_t)t * H, g, nh, s, row_position(rp, t), kc + kvoff, vc + kvoff, scaling,
@@ -992,7 +992,7 @@ int launch_attention(lbt_ctx* ctx, const float* q, int m, int nh, int kvh, int h
     // rows of one sequence at consecutive positions (a prefill) with at
     // least 8 (row, KV head, split) tasks per CU: one wavefront per task
     // where the shape allows (2B, 2048-token prefill: attention 41.5 ->
-    // 21.7 ms; at 64 and 128 tokens the workgroup per task stays faster,
+    // 18.9 ms; at 64 and 128 tokens the workgroup per task stays faster,
     // 0.25 against 0.42 ms and 0.38 against 0.43 ms).  LBT_ATTN_WAVE=1 / 0
     // forces it on / off for grouped attention.
     const int aw = ctx->tune.attn_wave;
