@@ -42,6 +42,7 @@ LbtTuning read_tuning() {
     t.gemv_pw = num("LBT_GEMV_PW", 4) == 16 ? 16 : 4;
     t.gemv_pwo = num("LBT_GEMV_PWO", 16) == 4 ? 4 : 16;
     t.gemm_ksplit = (int)num("LBT_GEMM_KSPLIT", 0);
+    t.quant_wide = getenv("LBT_QUANT_WIDE") != nullptr;
     if (t.gemm_ksplit < 0 || t.gemm_ksplit > 16) t.gemm_ksplit = 0;
     return t;
 }

@@ -29,6 +29,7 @@ struct LbtTuning {
     bool head_batch_classic = false;  // LBT_HEAD_BATCH_CLASSIC: batched bf16 head on lmhead_batch_kernel (16-token groups)
     int gemv_pw = 4;          // LBT_GEMV_PW=16: single-token GEMV prologue (f32 rows) on all 16 wavefronts (default 4)
     int gemv_pwo = 16;        // LBT_GEMV_PWO=4: ... of the o projection (attention-combine rows) on four (default 16)
+    bool quant_wide = false;  // LBT_QUANT_WIDE: row quantizer on 1024 threads (quantize_wide_kernel) instead of 4 wavefronts
     int gemm_ksplit = 0;      // LBT_GEMM_KSPLIT: k ranges of the pipelined GEMM's small grids (0 auto, 1 off)
 };
 
@@ -171,6 +172,10 @@ int launch_ternary_gemv_cu(lbt_ctx* ctx, const TernaryOp& op);
 int launch_ternary_mfma(lbt_ctx* ctx, const TernaryOp& op);
 
 // Standalone (rms)norm + quantize of m rows into global q [m, kp], scale, sum.
+// RMSNorm + ActQuant of m rows on one 256-thread workgroup each (rows up to
+// 256 * 28 padded columns, 16-byte aligned, k % 4 == 0).
+int launch_quantize_pw(lbt_ctx* ctx, const float* x, const float* norm_w, float eps, int m, int k, int kp,
+                       int8_t* q, float* scale, int32_t* sum);
 int launch_quantize(lbt_ctx* ctx, const float* x, const float* norm_w, float eps, int m, int k, int8_t* q,
                     float* scale, int32_t* sum);
 

@@ -384,6 +384,8 @@ int launch_quantize(lbt_ctx* ctx, const float* x, const float* norm_w, float eps
     if (m <= 0) return LBT_OK;
     const int kp = (int)padded_cols((size_t)k);
     const bool wide = k % 4 == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)norm_w & 15) == 0 && kp <= 8 * 1024;
+    if (wide && kp <= 256 * 28 && !ctx->tune.quant_wide)
+        return launch_quantize_pw(ctx, x, norm_w, eps, m, k, kp, q, scale, sum);
     if (wide && kp <= 4 * 1024)
         hipLaunchKernelGGL(quantize_wide_kernel<4>, dim3(m), dim3(1024), 0, ctx->stream, x, norm_w, eps, k, kp, q,
                            scale, sum);

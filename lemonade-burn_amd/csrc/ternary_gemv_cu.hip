@@ -79,6 +79,43 @@ __device__ __forceinline__ void quant_row_waves(RowRegs<EPT>& r, int cols, int k
     }
 }
 
+// RMSNorm (norm_w set) + ActQuant of row blockIdx.x into q / scale / sum on
+// one 256-thread workgroup: the GEMV prologue's quant_row_waves on its four
+// wavefronts, so the values of quantize_wide_kernel (canonical sum of
+// squares; max and integer sums order free) with shorter reduction chains.
+template <int EPT>
+__global__ __launch_bounds__(256) void quantize_pw_kernel(const float* x, const float* norm_w, float eps, int k,
+                                                          int kp, int8_t* q, float* scale, int32_t* sum) {
+    __shared__ __align__(16) float red[kRedFloats];
+    const int row = blockIdx.x;
+    RowRegs<EPT> r;
+    const float* nw = norm_w ? launder(norm_w) : nullptr;
+    row_load_buf<EPT, 256>(x + (size_t)row * k, k, nw, r);
+    if (nw)
+        quant_row_waves<EPT, 4, 1>(r, k, kp, nw, eps, q + (size_t)row * kp, [](int i) { return i; }, &scale[row], red);
+    else
+        quant_row_waves<EPT, 4, 0>(r, k, kp, nw, eps, q + (size_t)row * kp, [](int i) { return i; }, &scale[row], red);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int* ps = (const int*)(red + 32);
+        sum[row] = (ps[0] + ps[1]) + (ps[2] + ps[3]);
+    }
+}
+
+int launch_quantize_pw(lbt_ctx* ctx, const float* x, const float* norm_w, float eps, int m, int k, int kp,
+                       int8_t* q, float* scale, int32_t* sum) {
+    if (kp <= 256 * 12)
+        hipLaunchKernelGGL(quantize_pw_kernel<12>, dim3(m), dim3(256), 0, ctx->stream, x, norm_w, eps, k, kp, q,
+                           scale, sum);
+    else if (kp <= 256 * 28)
+        hipLaunchKernelGGL(quantize_pw_kernel<28>, dim3(m), dim3(256), 0, ctx->stream, x, norm_w, eps, k, kp, q,
+                           scale, sum);
+    else
+        return set_err(ctx, LBT_E_INVALID, "quantize: row too long for the four-wavefront quantizer");
+    LBT_HIP(ctx, hipGetLastError());
+    return LBT_OK;
+}
+
 // PW: wavefronts of the activation prologue (16: all, EPT elements per
 // thread; 4: the first four, EPT elements per thread of 256).
 template <int L, int CPL, int IN, int OUT, int EPT, int PW>
