@@ -911,7 +911,7 @@ int or_model_forward(or_model* m, const uint32_t* tokens, size_t n, int all_logi
     float scaling = powf((float)hd, -0.5f);
 
     float* x = (float*)malloc(n * H * sizeof(float));
-    float* nrm = (float*)malloc(n * I * sizeof(float));
+    float* nrm = (float*)malloc(n * (I > H ? I : H) * sizeof(float)); /* normed rows of either width */
     float* q = (float*)malloc(n * H * sizeof(float));
     float* kk = (float*)malloc(n * kvh * hd * sizeof(float));
     float* vv = (float*)malloc(n * kvh * hd * sizeof(float));

@@ -220,6 +220,24 @@ def test_model_long_prefill_attention_matches_oracle(ctx, ctx_with, n, force):
     om.free()
 
 
+def test_model_prefill_wide_hidden_matches_oracle(ctx):
+    # hidden 4096: the q/k/v GEMM at 128 tokens has 32 k steps over 192
+    # 64 x 64 tiles, so it splits k in two (the RoPE / KV-append epilogue
+    # after the partials' hand-off), and the attention takes the
+    # one-wavefront-per-split kernel; logits bit-exact to the oracle
+    cfg = dict(hidden=4096, intermediate=1024, heads=32, kv_heads=8, layers=1, vocab=1000, max_pos=512)
+    announce("model prefill hidden 4096, 128 tokens")
+    m = lbt_hip.Model.synthetic(ctx, lbt_hip.make_config(**cfg), 9)
+    om = orc.OracleModel(orc.config(**cfg), 9)
+    toks = (np.arange(128) * 13 % cfg["vocab"]).astype(np.uint32)
+    c = m.new_cache()
+    got = m.forward(toks, c, all_logits=True)
+    assert np.array_equal(got, om.forward(toks, all_logits=True))
+    c.free()
+    m.free()
+    om.free()
+
+
 @pytest.mark.parametrize("n", [2, 63, 65, 700, 1024, 1025, 1040, 4096, 4100])
 def test_prefill_attention_kernels_agree(ctx, ctx_with, n):
     # the 2B shape's attention (20 query heads over 5 KV heads, head_dim 128)
