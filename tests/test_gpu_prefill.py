@@ -220,6 +220,25 @@ def test_model_long_prefill_attention_matches_oracle(ctx, ctx_with, n, force):
     om.free()
 
 
+def test_model_chunked_long_prefill_matches_oracle(ctx):
+    # a 1100-token prompt in two chunks (700 then 400 tokens): the second
+    # chunk's rows start at position 700 over a cache the first wrote, on the
+    # one-wavefront-per-split attention; logits bit-exact to the oracle's
+    # same two calls
+    cfg = dict(hidden=512, intermediate=1536, heads=4, kv_heads=1, layers=2, vocab=1000, max_pos=2048)
+    announce("model chunked long prefill 700 + 400")
+    m = lbt_hip.Model.synthetic(ctx, lbt_hip.make_config(**cfg), 6)
+    om = orc.OracleModel(orc.config(**cfg), 6)
+    toks = (np.arange(1100) * 41 % cfg["vocab"]).astype(np.uint32)
+    c = m.new_cache()
+    for part in (toks[:700], toks[700:]):
+        got = m.forward(part, c, all_logits=True)
+        assert np.array_equal(got, om.forward(part, all_logits=True))
+    c.free()
+    m.free()
+    om.free()
+
+
 def test_model_prefill_wide_hidden_matches_oracle(ctx):
     # hidden 4096: the q/k/v GEMM at 128 tokens has 32 k steps over 192
     # 64 x 64 tiles, so it splits k in two (the RoPE / KV-append epilogue
