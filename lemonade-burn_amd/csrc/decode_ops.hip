@@ -86,7 +86,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
                                                                   float scaling, float* o, float* ml, int m, int nsg,
                                                                   int scw) {
     extern __shared__ __align__(16) float sc[];  // [4][scw]
-    const int w = (int)threadIdx.x >> 6;
+    // uniform per wavefront, and known to be: the task's row, KV head and
+    // split then sit in scalar registers, and so do the K / V buffer
+    // descriptors built from them (a descriptor the compiler cannot prove
+    // uniform turns every buffer load into a waterfall loop)
+    const int w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
     const long i = (long)blockIdx.x * 4 + w;
     if (i >= (long)m * kvh * nsg) return;  // the last workgroup's spare wavefronts
     const int t = (int)(i % m);
