@@ -848,6 +848,14 @@ int lbt_model_load(lbt_ctx* ctx, const char* dir, lbt_model** out) {
     const JVal* fmt = meta ? meta->get("format") : nullptr;
     if (!fmt || fmt->kind != JVal::Str || fmt->str != "lemonade-burn-ternary")
         return set_err(ctx, LBT_E_IO, path + " is not a lemonade-burn ternary file");
+    // a JSON number that is a whole byte count or dimension (no sign, no
+    // fraction, below 2^53: what a double holds exactly)
+    auto as_size = [](const JVal& v, size_t& o) {
+        if (v.kind != JVal::Num || !(v.num >= 0.0) || v.num >= 9007199254740992.0 || v.num != (double)(uint64_t)v.num)
+            return false;
+        o = (size_t)v.num;
+        return true;
+    };
     std::map<std::string, StTensor> tensors;
     for (auto& kv : hdr.obj) {
         if (kv.first == "__metadata__") continue;
@@ -858,9 +866,14 @@ int lbt_model_load(lbt_ctx* ctx, const char* dir, lbt_model** out) {
         if (!dt || !sh || !of || of->arr.size() != 2) return set_err(ctx, LBT_E_IO, "bad tensor entry " + kv.first);
         StTensor st;
         st.dtype = dt->str;
-        for (auto& d : sh->arr) st.shape.push_back((size_t)d.num);
-        size_t b = (size_t)of->arr[0].num, e = (size_t)of->arr[1].num;
-        if (b > e || e > data_size) return set_err(ctx, LBT_E_IO, "bad offsets for " + kv.first);
+        for (auto& d : sh->arr) {
+            size_t n = 0;
+            if (!as_size(d, n)) return set_err(ctx, LBT_E_IO, "bad shape for " + kv.first);
+            st.shape.push_back(n);
+        }
+        size_t b = 0, e = 0;
+        if (!as_size(of->arr[0], b) || !as_size(of->arr[1], e) || b > e || e > data_size)
+            return set_err(ctx, LBT_E_IO, "bad offsets for " + kv.first);
         st.data = data0 + b;
         st.bytes = e - b;
         tensors[kv.first] = st;
@@ -919,8 +932,9 @@ int lbt_model_load(lbt_ctx* ctx, const char* dir, lbt_model** out) {
     auto ei = tensors.find("model.embed_tokens.weight");
     // model.rs:203-206
     if (ei == tensors.end() || ei->second.dtype != "BF16" || ei->second.shape.size() != 2 ||
-        ei->second.shape[0] != (size_t)c.vocab_size || ei->second.shape[1] != (size_t)c.hidden_size)
-        return fail(LBT_E_IO, "embed_tokens: unexpected dtype/shape");
+        ei->second.shape[0] != (size_t)c.vocab_size || ei->second.shape[1] != (size_t)c.hidden_size ||
+        ei->second.bytes != (size_t)c.vocab_size * (size_t)c.hidden_size * 2)
+        return fail(LBT_E_IO, "embed_tokens: unexpected dtype/shape/size");
     if (hipMemcpy(m->embed, ei->second.data, ei->second.bytes, hipMemcpyHostToDevice) != hipSuccess)
         return fail(LBT_E_DEVICE, "upload embedding");
     *out = m.release();

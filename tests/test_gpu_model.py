@@ -200,6 +200,45 @@ def test_load_lb_convert_file(ctx, tmp_path, intermediate):
         lbt_hip.Model.load(ctx, tmp_path)
 
 
+def test_load_rejects_malformed_files(ctx, tmp_path):
+    """A model file whose header does not describe its data is refused with an
+    error, before anything is copied: an embedding whose data_offsets span
+    more bytes than its shape, a negative or fractional offset, a shape that
+    is not a whole number, and a file cut short."""
+    hip_cfg, or_cfg = cfgs()
+    announce("model_load malformed files")
+    write_lbt_file(tmp_path, or_cfg, 34)
+    path = tmp_path / "model.lbt.safetensors"
+    raw = path.read_bytes()
+    hlen = int.from_bytes(raw[:8], "little")
+    hdr = json.loads(raw[8:8 + hlen])
+    data = raw[8 + hlen:]
+
+    def write(h, d=data):
+        hb = json.dumps(h).encode()
+        hb += b" " * (-len(hb) % 8)
+        path.write_bytes(len(hb).to_bytes(8, "little") + hb + d)
+
+    emb = "model.embed_tokens.weight"
+    b0, e0 = hdr[emb]["data_offsets"]
+    cases = {
+        "embedding offsets past its shape": {emb: dict(hdr[emb], data_offsets=[b0, len(data)] if e0 < len(data)
+                                                     else [0, e0])},
+        "negative offset": {emb: dict(hdr[emb], data_offsets=[-8, e0])},
+        "fractional offset": {emb: dict(hdr[emb], data_offsets=[b0 + 0.5, e0])},
+        "fractional shape": {emb: dict(hdr[emb], shape=[or_cfg.vocab + 0.5, or_cfg.hidden])},
+    }
+    for name, change in cases.items():
+        write(dict(hdr, **change))
+        with pytest.raises(lbt_hip.LbtError):
+            lbt_hip.Model.load(ctx, tmp_path)
+    write(hdr, data[: len(data) // 2])
+    with pytest.raises(lbt_hip.LbtError, match="offsets"):
+        lbt_hip.Model.load(ctx, tmp_path)
+    write(hdr)
+    lbt_hip.Model.load(ctx, tmp_path).free()
+
+
 def test_full_2b_prompt64_decode_matches_oracle(ctx):
     """The decode benchmark workload: 2B4T-shaped model, 64-token uniform-random prompt,
     128 greedy decode steps on the device (graph-replayed step): tokens
