@@ -246,6 +246,7 @@ int lbt_memcpy_d2d(lbt_ctx* ctx, void* dst, const void* src, size_t bytes) {
 static int weight_new(lbt_ctx* ctx, const uint8_t* src, bool src_dev, size_t rows, size_t cols, float scale,
                       lbt_weight** out) {
     if (!ctx || !out || !src || rows == 0 || cols == 0) return set_err(ctx, LBT_E_INVALID, "weight: bad arguments");
+    if (rows > kMaxDim || cols > kMaxDim) return set_err(ctx, LBT_E_INVALID, "weight: dimension above 2^30");
     *out = nullptr;
     lbt_weight* w = new lbt_weight();
     w->ctx = ctx;
@@ -295,18 +296,22 @@ const uint8_t* lbt_weight_device_ptr(const lbt_weight* w) { return w ? w->d : nu
 // ---- quantization ------------------------------------------------------------
 int lbt_quantize_acts_dev(lbt_ctx* ctx, const float* x, size_t m, size_t k, int8_t* q, float* scale, int32_t* sum) {
     if (!ctx || k == 0) return set_err(ctx, LBT_E_INVALID, "quantize: bad arguments");
+    if (m > kMaxDim || k > kMaxDim) return set_err(ctx, LBT_E_INVALID, "quantize: dimension above 2^30");
     return launch_quantize(ctx, x, nullptr, 0.0f, (int)m, (int)k, q, scale, sum);
 }
 
 int lbt_rmsnorm_quantize_dev(lbt_ctx* ctx, const float* x, const float* norm_w, float eps, size_t m, size_t k,
                              int8_t* q, float* scale, int32_t* sum) {
     if (!ctx || k == 0 || !norm_w) return set_err(ctx, LBT_E_INVALID, "rmsnorm_quantize: bad arguments");
+    if (m > kMaxDim || k > kMaxDim) return set_err(ctx, LBT_E_INVALID, "rmsnorm_quantize: dimension above 2^30");
     return launch_quantize(ctx, x, norm_w, eps, (int)m, (int)k, q, scale, sum);
 }
 
 int lbt_quantize_acts(lbt_ctx* ctx, const float* x, size_t m, size_t k, int8_t* q, float* scale, int32_t* sum) {
     if (!ctx || k == 0) return set_err(ctx, LBT_E_INVALID, "quantize: bad arguments");
+    if (m > kMaxDim || k > kMaxDim) return set_err(ctx, LBT_E_INVALID, "quantize: dimension above 2^30");
     if (m == 0) return LBT_OK;
+    if (m > kMaxDim) return set_err(ctx, LBT_E_INVALID, "row count above 2^30");
     const size_t kp = padded_cols(k);
     Carve cv;
     size_t ox = cv.add(m * k * 4), oq = cv.add(m * kp), os = cv.add(m * 4), ou = cv.add(m * 4);
@@ -329,6 +334,7 @@ int lbt_quantize_acts(lbt_ctx* ctx, const float* x, size_t m, size_t k, int8_t* 
 int lbt_gemm_i32_dev(lbt_ctx* ctx, const lbt_weight* w, const int8_t* q, const int32_t* sum, size_t m, int32_t* out) {
     if (!ctx || !w) return set_err(ctx, LBT_E_INVALID, "gemm_i32: bad arguments");
     if (m == 0) return LBT_OK;
+    if (m > kMaxDim) return set_err(ctx, LBT_E_INVALID, "row count above 2^30");
     TernaryOp op = make_op(&w, 1, m);
     op.in_mode = kInPreQ;
     op.out_mode = kOutI32;
@@ -341,6 +347,7 @@ int lbt_gemm_i32_dev(lbt_ctx* ctx, const lbt_weight* w, const int8_t* q, const i
 int lbt_gemm_i32(lbt_ctx* ctx, const lbt_weight* w, const int8_t* q, const int32_t* sum, size_t m, int32_t* out) {
     if (!ctx || !w) return set_err(ctx, LBT_E_INVALID, "gemm_i32: bad arguments");
     if (m == 0) return LBT_OK;
+    if (m > kMaxDim) return set_err(ctx, LBT_E_INVALID, "row count above 2^30");
     Carve cv;
     size_t oq = cv.add(m * w->kp), os = cv.add(m * 4), oo = cv.add(m * w->rows * 4);
     void* ws;
@@ -361,6 +368,7 @@ int lbt_gemm_multi_dev(lbt_ctx* ctx, const lbt_weight* const* ws, size_t n, cons
     int rc = check_ws(ctx, ws, n, 0, false);
     if (rc) return rc;
     if (m == 0) return LBT_OK;
+    if (m > kMaxDim) return set_err(ctx, LBT_E_INVALID, "row count above 2^30");
     TernaryOp op = make_op(ws, n, m);
     op.in_mode = kInPreQ;
     op.out_mode = kOutF32;
@@ -376,6 +384,7 @@ int lbt_gemm_multi(lbt_ctx* ctx, const lbt_weight* const* ws, size_t n, const in
     int rc = check_ws(ctx, ws, n, 0, false);
     if (rc) return rc;
     if (m == 0) return LBT_OK;
+    if (m > kMaxDim) return set_err(ctx, LBT_E_INVALID, "row count above 2^30");
     const size_t kp = ws[0]->kp;
     Carve cv;
     size_t oq = cv.add(m * kp), osc = cv.add(m * 4), osu = cv.add(m * 4);
@@ -404,6 +413,7 @@ int lbt_ternary_linear_dev(lbt_ctx* ctx, const lbt_weight* const* ws, size_t n, 
     int rc = check_ws(ctx, ws, n, cols, true);
     if (rc) return rc;
     if (m == 0) return LBT_OK;
+    if (m > kMaxDim) return set_err(ctx, LBT_E_INVALID, "row count above 2^30");
     TernaryOp op = make_op(ws, n, m);
     op.in_mode = kInF32;
     op.out_mode = kOutF32;
@@ -461,6 +471,7 @@ int lbt_ternary_linear_dev_noalloc(lbt_ctx* ctx, const lbt_weight* const* ws, si
     int rc = check_ws(ctx, ws, n, cols, true);
     if (rc) return rc;
     if (m == 0) return LBT_OK;
+    if (m > kMaxDim) return set_err(ctx, LBT_E_INVALID, "row count above 2^30");
     const size_t kp = ws[0]->kp;
     const size_t need = ((m * kp + 255) & ~(size_t)255) + m * 8;
     if (need > ctx->noalloc_bytes) {
@@ -491,6 +502,7 @@ int lbt_ternary_linear(lbt_ctx* ctx, const lbt_weight* const* ws, size_t n, cons
     int rc = check_ws(ctx, ws, n, cols, true);
     if (rc) return rc;
     if (m == 0) return LBT_OK;
+    if (m > kMaxDim) return set_err(ctx, LBT_E_INVALID, "row count above 2^30");
     Carve cv;
     size_t ox = cv.add(m * cols * 4);
     size_t oo[3];
@@ -514,6 +526,7 @@ int lbt_ternary_linear(lbt_ctx* ctx, const lbt_weight* const* ws, size_t n, cons
 int lbt_bf16_upload(lbt_ctx* ctx, const uint16_t* w, size_t rows, size_t cols, lbt_bf16** out) {
     if (!ctx || !w || !out || rows == 0 || cols == 0 || cols % 8)
         return set_err(ctx, LBT_E_INVALID, "bf16_upload: bad arguments (cols must be a multiple of 8)");
+    if (rows > kMaxDim || cols > kMaxDim) return set_err(ctx, LBT_E_INVALID, "bf16_upload: dimension above 2^30");
     *out = nullptr;
     lbt_bf16* b = new lbt_bf16();
     b->ctx = ctx;
@@ -547,6 +560,7 @@ int lbt_bf16_linear_dev(lbt_ctx* ctx, const lbt_bf16* w, const float* x, size_t 
 int lbt_bf16_linear(lbt_ctx* ctx, const lbt_bf16* w, const float* x, size_t m, float* out) {
     if (!ctx || !w) return set_err(ctx, LBT_E_INVALID, "bf16_linear: bad arguments");
     if (m == 0) return LBT_OK;
+    if (m > kMaxDim) return set_err(ctx, LBT_E_INVALID, "row count above 2^30");
     Carve cv;
     size_t ox = cv.add(m * w->cols * 4), oo = cv.add(m * w->rows * 4);
     void* wsp;
@@ -611,6 +625,7 @@ int lbt_q8head_linear_dev(lbt_ctx* ctx, const lbt_q8head* h, const float* x, siz
 int lbt_q8head_linear(lbt_ctx* ctx, const lbt_q8head* h, const float* x, size_t m, float* out) {
     if (!ctx || !h) return set_err(ctx, LBT_E_INVALID, "q8head_linear: bad arguments");
     if (m == 0) return LBT_OK;
+    if (m > kMaxDim) return set_err(ctx, LBT_E_INVALID, "row count above 2^30");
     Carve cv;
     size_t ox = cv.add(m * h->cols * 4), oo = cv.add(m * h->rows * 4);
     void* wsp;

@@ -215,6 +215,9 @@ int launch_embed(lbt_ctx* ctx, const uint16_t* embed, int hidden, int vocab, con
 // at most kAttnSplits splits per (row, query head).
 constexpr int kAttnSplits = 16;
 constexpr int kAttnMinKeys = 64;
+// the largest row count, column count or token count the entry points take
+// (sizes reach the kernels as int; products of two stay within 64 bits)
+constexpr size_t kMaxDim = (size_t)1 << 30;
 constexpr int kAttnMaxHeads = 64;  // heads of the split combine
 __host__ __device__ __forceinline__ int attn_split_keys(int vis) {
     const int ks = (vis + kAttnSplits - 1) / kAttnSplits;

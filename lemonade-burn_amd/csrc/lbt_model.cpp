@@ -327,6 +327,9 @@ int validate_config(lbt_ctx* ctx, const lbt_config& c) {
     if (c.hidden_size <= 0 || c.intermediate_size <= 0 || c.num_attention_heads <= 0 || c.num_key_value_heads <= 0 ||
         c.num_hidden_layers <= 0 || c.vocab_size <= 0 || c.max_position_embeddings <= 0)
         return set_err(ctx, LBT_E_INVALID, "config: non-positive dimension");
+    for (int32_t d : {c.hidden_size, c.intermediate_size, c.num_attention_heads, c.num_key_value_heads,
+                      c.num_hidden_layers, c.vocab_size, c.max_position_embeddings})
+        if ((size_t)d > kMaxDim) return set_err(ctx, LBT_E_INVALID, "config: dimension above 2^30");
     if (c.hidden_size % c.num_attention_heads || c.num_attention_heads % c.num_key_value_heads)
         return set_err(ctx, LBT_E_INVALID, "config: heads do not divide");
     const int hd = c.hidden_size / c.num_attention_heads;
@@ -464,9 +467,9 @@ int ensure_cap(lbt_cache* cc, int need) {
     const lbt_config& c = m->cfg;
     if (need > c.max_position_embeddings)
         return set_err(ctx, LBT_E_RANGE, "context length " + std::to_string(c.max_position_embeddings) + " exceeded");
-    int cap = 1;
-    while (cap < need) cap <<= 1;
-    if (cap < 256) cap = 256;
+    int cap = 256;
+    while (cap < need && cap < (1 << 30)) cap <<= 1;
+    if (cap < need) cap = need;
     if (cap > c.max_position_embeddings) cap = c.max_position_embeddings;
     const size_t kvh = (size_t)c.num_key_value_heads, hd = (size_t)m->hd, L = (size_t)c.num_hidden_layers;
     uint16_t *nk = nullptr, *nv = nullptr;
@@ -487,6 +490,18 @@ int ensure_cap(lbt_cache* cc, int need) {
     cc->v = nv;
     cc->cap = cap;
     return LBT_OK;
+}
+
+// Room in the cache for `a` + `b` more positions (sizes as the caller gave
+// them, checked before any narrowing): the context-length error past
+// max_position_embeddings, else ensure_cap.
+int ensure_room(lbt_cache* cc, size_t a, size_t b = 0) {
+    const lbt_config& c = cc->m->cfg;
+    const size_t room = (size_t)c.max_position_embeddings - (size_t)cc->len;
+    if (a > room || b > room - a)
+        return set_err(cc->m->ctx, LBT_E_RANGE,
+                       "context length " + std::to_string(c.max_position_embeddings) + " exceeded");
+    return ensure_cap(cc, cc->len + (int)(a + b));
 }
 
 // KV cache rows of a forward pass: layer l of sequence 0 starts at
@@ -757,13 +772,17 @@ int read_config(lbt_ctx* ctx, const std::string& dir, lbt_config& c) {
                           "num_hidden_layers", "vocab_size", "max_position_embeddings"};
     int32_t* dst[] = {&c.hidden_size, &c.intermediate_size, &c.num_attention_heads, &c.num_key_value_heads,
                       &c.num_hidden_layers, &c.vocab_size, &c.max_position_embeddings};
+    // dimensions: whole numbers that an int32 holds (the range check of
+    // each dimension follows in validate_config)
     for (int i = 0; i < 7; i++) {
         if (!num(keys[i], d)) return set_err(ctx, LBT_E_IO, std::string("config.json: missing ") + keys[i]);
+        if (!(d >= -2147483648.0 && d <= 2147483647.0) || d != (double)(int64_t)d)
+            return set_err(ctx, LBT_E_INVALID, std::string("config.json: ") + keys[i] + " is not a whole number");
         *dst[i] = (int32_t)d;
     }
     if (!num("rms_norm_eps", c.rms_norm_eps)) return set_err(ctx, LBT_E_IO, "config.json: missing rms_norm_eps");
     if (!num("rope_theta", c.rope_theta)) return set_err(ctx, LBT_E_IO, "config.json: missing rope_theta");
-    c.bos_token_id = num("bos_token_id", d) ? (uint32_t)d : 0u;
+    c.bos_token_id = num("bos_token_id", d) && d >= 0.0 && d <= 4294967295.0 ? (uint32_t)d : 0u;
     const JVal* act = j.get("hidden_act");
     const JVal* tied = j.get("tie_word_embeddings");
     // model.rs:151-153
@@ -1011,7 +1030,7 @@ int lbt_model_forward(lbt_model* m, const uint32_t* tokens, size_t n, lbt_cache*
     if (!m || !c || !tokens || n == 0) return set_err(m ? m->ctx : nullptr, LBT_E_INVALID, "forward: bad arguments");
     lbt_ctx* ctx = m->ctx;
     int rc;
-    if ((rc = ensure_cap(c, c->len + (int)n))) return rc;
+    if ((rc = ensure_room(c, n))) return rc;
     if ((rc = ensure_ws(m, (int)n))) return rc;
     if ((rc = upload_tokens(m, tokens, n))) return rc;
     if ((rc = forward_dev(m, c, m->toks, (int)n, all_logits != 0, true, nullptr))) return rc;
@@ -1027,7 +1046,7 @@ int lbt_model_forward_argmax(lbt_model* m, const uint32_t* tokens, size_t n, lbt
     if (!m || !c || !tokens || n == 0 || !next) return set_err(m ? m->ctx : nullptr, LBT_E_INVALID, "bad arguments");
     lbt_ctx* ctx = m->ctx;
     int rc;
-    if ((rc = ensure_cap(c, c->len + (int)n))) return rc;
+    if ((rc = ensure_room(c, n))) return rc;
     if ((rc = ensure_ws(m, (int)n))) return rc;
     if ((rc = upload_tokens(m, tokens, n))) return rc;
     if ((rc = forward_dev(m, c, m->toks, (int)n, false, false, nullptr))) return rc;
@@ -1043,7 +1062,7 @@ int lbt_model_generate_greedy(lbt_model* m, const uint32_t* prompt, size_t n, si
     if (!m || !c || !prompt || n == 0 || !out_tokens) return set_err(m ? m->ctx : nullptr, LBT_E_INVALID, "bad arguments");
     lbt_ctx* ctx = m->ctx;
     int rc;
-    if ((rc = ensure_cap(c, c->len + (int)n + (int)steps))) return rc;
+    if ((rc = ensure_room(c, n, steps))) return rc;
     if ((rc = ensure_ws(m, (int)n))) return rc;
     if ((rc = grow_tok_out(m, (int)steps + 1))) return rc;
     if ((rc = upload_tokens(m, prompt, n))) return rc;
@@ -1083,7 +1102,7 @@ int lbt_model_decode_greedy(lbt_model* m, lbt_cache* c, uint32_t first, size_t s
     lbt_ctx* ctx = m->ctx;
     if (first >= (uint32_t)m->cfg.vocab_size) return set_err(ctx, LBT_E_INVALID, "token id out of range");
     int rc;
-    if ((rc = ensure_cap(c, c->len + (int)steps))) return rc;
+    if ((rc = ensure_room(c, steps))) return rc;
     if ((rc = ensure_ws(m, 1))) return rc;
     if ((rc = grow_tok_out(m, (int)steps + 1))) return rc;
     LBT_HIP(ctx, hipMemcpyAsync(m->toks, &first, 4, hipMemcpyHostToDevice, ctx->stream));
@@ -1115,7 +1134,7 @@ int lbt_model_forward_sample(lbt_model* m, const uint32_t* tokens, size_t n, lbt
         return set_err(m ? m->ctx : nullptr, LBT_E_INVALID, "bad arguments");
     lbt_ctx* ctx = m->ctx;
     int rc;
-    if ((rc = ensure_cap(c, c->len + (int)n))) return rc;
+    if ((rc = ensure_room(c, n))) return rc;
     if ((rc = ensure_ws(m, (int)n))) return rc;
     if ((rc = ensure_sampler(m))) return rc;
     if ((rc = upload_tokens(m, tokens, n))) return rc;
@@ -1137,7 +1156,7 @@ int lbt_model_decode_sample(lbt_model* m, lbt_cache* c, uint32_t first, size_t s
     lbt_ctx* ctx = m->ctx;
     if (first >= (uint32_t)m->cfg.vocab_size) return set_err(ctx, LBT_E_INVALID, "token id out of range");
     int rc;
-    if ((rc = ensure_cap(c, c->len + (int)steps))) return rc;
+    if ((rc = ensure_room(c, steps))) return rc;
     if ((rc = ensure_ws(m, 1))) return rc;
     if ((rc = grow_tok_out(m, (int)steps + 1))) return rc;
     if ((rc = ensure_sampler(m))) return rc;
@@ -1287,7 +1306,7 @@ int lbt_batch_prefill(lbt_batch* b, int seq, const uint32_t* tokens, size_t n, u
         return set_err(b ? b->m->ctx : nullptr, LBT_E_INVALID, "bad arguments");
     lbt_model* m = b->m;
     lbt_ctx* ctx = m->ctx;
-    if (b->len[seq] + (int)n > b->cap) return set_err(ctx, LBT_E_RANGE, "batch: sequence capacity exceeded");
+    if (n > (size_t)(b->cap - b->len[seq])) return set_err(ctx, LBT_E_RANGE, "batch: sequence capacity exceeded");
     int rc;
     if ((rc = ensure_ws(m, (int)n))) return rc;
     if ((rc = upload_tokens(m, tokens, n))) return rc;
@@ -1333,7 +1352,7 @@ int lbt_batch_prefill_sample(lbt_batch* b, int seq, const uint32_t* tokens, size
         return set_err(b ? b->m->ctx : nullptr, LBT_E_INVALID, "bad arguments");
     lbt_model* m = b->m;
     lbt_ctx* ctx = m->ctx;
-    if (b->len[seq] + (int)n > b->cap) return set_err(ctx, LBT_E_RANGE, "batch: sequence capacity exceeded");
+    if (n > (size_t)(b->cap - b->len[seq])) return set_err(ctx, LBT_E_RANGE, "batch: sequence capacity exceeded");
     int rc;
     if ((rc = ensure_ws(m, (int)n))) return rc;
     if ((rc = batch_sampler(b))) return rc;

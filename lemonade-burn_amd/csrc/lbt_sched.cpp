@@ -75,7 +75,8 @@ void lbt_sched_free(lbt_sched* s) {
 int lbt_sched_submit(lbt_sched* s, const uint32_t* prompt, size_t n, size_t max_new, uint32_t stop, uint64_t* id) {
     if (!s || !prompt || n == 0 || max_new == 0 || !id) return lbt::set_err(ctx_of(s), LBT_E_INVALID, "bad arguments");
     // the prompt, then max_new - 1 decode steps (the first token is the prefill's)
-    if (n + max_new - 1 > (size_t)s->cap) return lbt::set_err(ctx_of(s), LBT_E_RANGE, "sched: request exceeds slot capacity");
+    if (n > (size_t)s->cap || max_new - 1 > (size_t)s->cap - n)
+        return lbt::set_err(ctx_of(s), LBT_E_RANGE, "sched: request exceeds slot capacity");
     for (size_t i = 0; i < n; i++)
         if (prompt[i] >= (uint32_t)s->vocab) return lbt::set_err(ctx_of(s), LBT_E_INVALID, "token id out of range");
     lbt_sched::Req r;

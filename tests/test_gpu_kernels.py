@@ -267,6 +267,62 @@ def test_invalid_arguments_return_errors(ctx):
     w.free()
 
 
+def test_oversized_arguments_return_errors(ctx):
+    # sizes the kernels could not index (int rows, columns and token counts;
+    # 32-bit cache positions) are refused at the C ABI with an error, before
+    # any memory behind the pointers is touched
+    import lbt_hip
+
+    lib, h = ctx.lib, ctx.h
+    E_RANGE = {v: k for k, v in lbt_hip.ERRORS.items()}["LBT_E_RANGE"]
+    big, huge = 1 << 31, (1 << 64) - 1
+    w = ctx.upload(np.full((4, 32), 0x55, np.uint8), 4, 128, 1.0)
+    x = np.zeros((1, 128), np.float32)
+    out = np.zeros((1, 4), np.float32)
+    wa = (C.c_void_p * 1)(w.h)
+    oa = (C.c_void_p * 1)(out.ctypes.data)
+    q = np.zeros((1, 128), np.int8)
+    s = np.zeros(1, np.float32)
+    su = np.zeros(1, np.int32)
+    dummy = C.c_void_p(x.ctypes.data)
+    h2 = C.c_void_p()
+    calls = {
+        "ternary_linear_dev m": lambda: lib.lbt_ternary_linear_dev(h, wa, 1, dummy, big, 128, oa),
+        "ternary_linear m": lambda: lib.lbt_ternary_linear(h, wa, 1, dummy, big, 128, oa),
+        "gemm_i32_dev m": lambda: lib.lbt_gemm_i32_dev(h, w.h, q.ctypes.data, su.ctypes.data, big, out.ctypes.data),
+        "quantize_acts_dev m": lambda: lib.lbt_quantize_acts_dev(h, dummy, big, 128, q.ctypes.data, s.ctypes.data,
+                                                                 su.ctypes.data),
+        "quantize_acts k": lambda: lib.lbt_quantize_acts(h, dummy, 1, big, q.ctypes.data, s.ctypes.data,
+                                                         su.ctypes.data),
+        "weight_upload rows": lambda: lib.lbt_weight_upload(h, dummy, big, 128, C.c_float(1.0), C.byref(h2)),
+        "bf16_upload rows": lambda: lib.lbt_bf16_upload(h, dummy, big, 128, C.byref(h2)),
+    }
+    for name, call in calls.items():
+        assert call() != 0, name
+    w.free()
+    cfg = dict(hidden=256, intermediate=512, heads=4, kv_heads=2, layers=1, vocab=100, max_pos=64)
+    m = lbt_hip.Model.synthetic(ctx, lbt_hip.make_config(**cfg), 3)
+    c = m.new_cache()
+    toks = np.array([1, 2, 3], np.uint32)
+    nxt = np.zeros(4, np.uint32)
+    assert lib.lbt_model_forward(m.h, toks.ctypes.data, (1 << 32) + 3, c.h, 0, None) == E_RANGE
+    assert lib.lbt_model_forward_argmax(m.h, toks.ctypes.data, huge, c.h, nxt.ctypes.data) == E_RANGE
+    assert lib.lbt_model_generate_greedy(m.h, toks.ctypes.data, 3, huge, c.h, nxt.ctypes.data, None,
+                                         None) == E_RANGE
+    assert lib.lbt_model_decode_greedy(m.h, c.h, 1, huge, nxt.ctypes.data, None) == E_RANGE
+    assert len(c) == 0
+    b = m.new_batch(2, 32)
+    assert lib.lbt_batch_prefill(b.h, 0, toks.ctypes.data, (1 << 32) + 3, nxt.ctypes.data) == E_RANGE
+    assert b.len(0) == 0
+    b.free()
+    # a valid call afterwards still gives the oracle's logits
+    om = orc.OracleModel(orc.config(**cfg), 3)
+    assert np.array_equal(m.forward(toks, c, all_logits=True), om.forward(toks, all_logits=True))
+    om.free()
+    c.free()
+    m.free()
+
+
 @pytest.mark.gpu
 def test_fused_prologue_edge_cases_match_oracle(ctx):
     # the reference's quantizer edge cases (NaN -> 0, +-inf, denormals, ties,

@@ -204,7 +204,8 @@ def test_load_rejects_malformed_files(ctx, tmp_path):
     """A model file whose header does not describe its data is refused with an
     error, before anything is copied: an embedding whose data_offsets span
     more bytes than its shape, a negative or fractional offset, a shape that
-    is not a whole number, and a file cut short."""
+    is not a whole number, a file cut short, and config.json dimensions that
+    are not whole numbers an int32 holds, or not positive."""
     hip_cfg, or_cfg = cfgs()
     announce("model_load malformed files")
     write_lbt_file(tmp_path, or_cfg, 34)
@@ -237,6 +238,16 @@ def test_load_rejects_malformed_files(ctx, tmp_path):
         lbt_hip.Model.load(ctx, tmp_path)
     write(hdr)
     lbt_hip.Model.load(ctx, tmp_path).free()
+    conf = tmp_path / "config.json"
+    good = conf.read_text()
+    for bad in ('"hidden_size": 1e20', '"hidden_size": 128.5', '"vocab_size": -3'):
+        key = bad.split(":")[0]
+        j = json.loads(good)
+        j[key.strip('"')] = json.loads(bad.split(":", 1)[1])
+        conf.write_text(json.dumps(j))
+        with pytest.raises(lbt_hip.LbtError):
+            lbt_hip.Model.load(ctx, tmp_path)
+    conf.write_text(good)
 
 
 def test_full_2b_prompt64_decode_matches_oracle(ctx):
