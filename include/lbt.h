@@ -16,6 +16,10 @@
  *   - One context per host thread (like the reference's single model worker
  *     thread, crates/lb-server/src/main.rs:92-100); a context is not
  *     thread-safe.
+ *   - Sizes (rows, columns, token counts, config dimensions) above 2^30 are
+ *     refused with LBT_E_INVALID; token and step counts past the cache's
+ *     room (max_position_embeddings, or a batch slot's capacity) with
+ *     LBT_E_RANGE.  Both before any memory behind the pointers is read.
  */
 #ifndef LBT_H
 #define LBT_H
