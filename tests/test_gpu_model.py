@@ -125,6 +125,31 @@ def test_cache_growth_keeps_contents(ctx):
     om.free()
 
 
+def test_decode_fills_context_exactly(ctx):
+    # max_position_embeddings 300: the cache grows 256 -> 300 (clamped, not a
+    # power of two) under the graph-replayed step, the greedy run ends with
+    # the cache exactly full and the tokens equal the oracle's; one position
+    # more is a context-length error that leaves the cache as it was
+    hip_cfg, or_cfg = cfgs(max_pos=300)
+    announce("decode to max_position_embeddings 300")
+    m = lbt_hip.Model.synthetic(ctx, hip_cfg, 6)
+    om = orc.OracleModel(or_cfg, 6)
+    prompt = (np.arange(10) * 13 % or_cfg.vocab).astype(np.uint32)
+    cache = m.new_cache()
+    toks, _, _ = m.generate_greedy(prompt, 290, cache)
+    exp = [int(om.forward(prompt)[0].argmax())]
+    for _ in range(290):
+        exp.append(int(om.forward([exp[-1]])[0].argmax()))
+    assert list(toks) == exp
+    assert len(cache) == 300
+    with pytest.raises(lbt_hip.LbtError):
+        m.forward(np.array([exp[-1]], np.uint32), cache)
+    assert len(cache) == 300
+    cache.free()
+    m.free()
+    om.free()
+
+
 def test_context_limit_is_an_error(ctx):
     hip_cfg, _ = cfgs(max_pos=64, layers=1)
     m = lbt_hip.Model.synthetic(ctx, hip_cfg, 1)
