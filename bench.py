@@ -284,9 +284,21 @@ def gemv_shapes(ctx, reps: int = 4) -> dict:
         run(was[:4])  # code objects, clocks
         cold = run(was * reps)
         warm = run([was[0]] * 256)
+        # the host-pointer entry point (the reference's slice API): the row
+        # copied in, the product, the outputs copied back and the stream
+        # synchronized, per call by the host clock (PCIe-inclusive; warm
+        # matrix)
+        y = np.zeros(rows, np.float32)
+        ha = (C.c_void_p * 1)(y.ctypes.data)
+        for _ in range(8):
+            ctx.check(lib.lbt_ternary_linear(ctx.h, was[0], 1, x.ctypes.data, 1, cols, ha))
+        t0 = time.perf_counter()
+        for _ in range(200):
+            ctx.check(lib.lbt_ternary_linear(ctx.h, was[0], 1, x.ctypes.data, 1, cols, ha))
+        host = (time.perf_counter() - t0) / 200 * 1e6
         bytes_ = packed.nbytes + cols * 4
         rec = {"rows": rows, "cols": cols, "copies": ncopy}
-        for k, us in (("cold", cold), ("warm", warm)):
+        for k, us in (("cold", cold), ("warm", warm), ("host_pointers", host)):
             gbs = bytes_ / (us * 1e-6) / 1e9
             rec[k] = {"us": round(us, 3), "GBs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
         out[name] = rec
